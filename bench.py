@@ -1,0 +1,173 @@
+#!/usr/bin/env python3
+"""Benchmark: HelixML SSM forward hot path on one MI355X.
+
+Metric: Mamba selective-scan fwd tokens/s + achieved HBM GB/s (% of peak), 1 GPU.
+Default workload = BASELINE config 2: fused selective scan, batch 8 x L 2048 x d_inner 1536 x
+d_state 16, fp32, inputs resident in HBM, 3 rotating input sets (1.2 GB) so the 256 MB MALL
+cannot serve a step from the previous one. A "step" is one hx_selective_scan_fwd call over one
+batch. Prints ONE JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--workload c2|c4|c4s4|c4s4d|c3scan] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from helixml_amd import _ffi, ssm  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
+
+
+def scan_bytes(bt, L, dim, N, es, with_z=True, with_D=True):
+    """Algorithmic HBM bytes of one fused scan: read u, delta, (z), B, C once, write out once,
+    plus A (and D). State never leaves registers."""
+    streams = 3 + (1 if with_z else 0)  # u, delta, out, z
+    return streams * bt * L * dim * es + 2 * bt * L * N * es + dim * N * 4 + (dim * 4 if with_D else 0)
+
+
+def make_scan_inputs(bt, L, dim, N, gen, dev, dtype):
+    """BASELINE config-2 distributions."""
+    f = torch.float32
+    u = torch.randn((bt, L, dim), generator=gen, device=dev, dtype=f)
+    delta = torch.randn((bt, L, dim), generator=gen, device=dev, dtype=f) * 0.5 - 4.0
+    z = torch.randn((bt, L, dim), generator=gen, device=dev, dtype=f)
+    B = torch.randn((bt, L, N), generator=gen, device=dev, dtype=f)
+    C = torch.randn((bt, L, N), generator=gen, device=dev, dtype=f)
+    A = -torch.exp(torch.log(torch.arange(1, N + 1, device=dev, dtype=f))).repeat(dim, 1).contiguous()
+    D = torch.randn((dim,), generator=gen, device=dev, dtype=f)
+    cast = lambda t: t.to(dtype).contiguous()
+    return dict(u=cast(u), delta=cast(delta), A=A, B=cast(B), C=cast(C), D=D, z=cast(z))
+
+
+def time_steps(fn, sets, steps, warmup):
+    """Runs `warmup` untimed steps then exactly `steps` timed steps, rotating over `sets` input sets;
+    HIP events on the stream the kernels are launched on (torch's current stream, which is the
+    stream handed to the C ABI). Returns ms per step."""
+    for i in range(warmup):
+        fn(i % sets)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i % sets)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_baseline_scan(x_dev, sample_batches):
+    """The CPU oracle (C restatement, port of the reference's CPU arithmetic) on a bounded
+    sample of the same workload: the first `sample_batches` batch rows of input set 0."""
+    import oracle  # test/bench infrastructure only
+    host = {k: (v[:sample_batches].float().cpu().numpy() if v.dim() == 3 else v.float().cpu().numpy())
+            for k, v in x_dev.items()}
+    bt, L, dim = host["u"].shape
+    t0 = time.perf_counter()
+    out1 = oracle.selective_scan(**host)
+    t1 = time.perf_counter()
+    threads = min(oracle.max_threads(), 16)
+    t2 = time.perf_counter()
+    oracle.selective_scan_omp(**host, threads=threads)
+    t3 = time.perf_counter()
+    toks = bt * L
+    return dict(value=toks / (t1 - t0), unit="tokens/s", cores=1, kind="port",
+                sample=f"batch rows 0..{bt - 1} of config 2 input set 0 ({bt}x{L}x{dim}x16), "
+                       f"single-threaded C oracle, {t1 - t0:.2f} s",
+                omp=dict(value=toks / (t3 - t2), threads=threads, seconds=round(t3 - t2, 3))), out1
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c2", choices=["c2", "c2bf16", "c4"])
+    ap.add_argument("--variant", type=int, default=0, help="scan kernel variant (hx_set_scan_variant)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the scan shards by channel with "
+                                   "no exchange (see DESIGN.md); multi-GPU runs are not part of it",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    dev = torch.device("cuda:0")
+    _ffi.call("hx_init", 0)
+    if args.variant:
+        ssm.set_scan_variant(args.variant)
+
+    if args.workload in ("c2", "c2bf16"):
+        bt, L, dim, N = 8, 2048, 1536, 16
+        dtype = torch.bfloat16 if args.workload == "c2bf16" else torch.float32
+        workload = "selective_scan_fwd config2 (batch 8, L 2048, d_inner 1536, d_state 16)"
+    else:
+        bt, L, dim, N = 1, 65536, 2048, 16
+        dtype = torch.float32
+        workload = "selective_scan_fwd config4 scan (batch 1, L 65536, d_inner 2048, d_state 16)"
+    es = 2 if dtype == torch.bfloat16 else 4
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x48454C49)
+    nsets = 3 if bt * L * dim * es * 4 < 2**31 else 2
+    sets = [make_scan_inputs(bt, L, dim, N, gen, dev, dtype) for _ in range(nsets)]
+    outs = [torch.empty_like(s["u"]) for s in sets]
+
+    def step(i):
+        ssm.selective_scan_fwd(**sets[i], out=outs[i])
+
+    ms = time_steps(step, nsets, args.steps, args.warmup)
+    tokens = bt * L
+    nbytes = scan_bytes(bt, L, dim, N, es)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+
+    cpu = None
+    parity = None
+    if not args.no_cpu and args.workload in ("c2", "c2bf16"):
+        step(0)
+        torch.cuda.synchronize()
+        sample = 8
+        cpu, ref = cpu_baseline_scan(sets[0], sample)
+        g = outs[0][:sample].float().cpu().numpy()
+        r = ref.astype(np.float64)
+        floor = 1e-3 * np.abs(r).max()
+        parity = float((np.abs(g - r) / np.maximum(np.abs(r), floor)).max())
+
+    rec = {
+        "metric": "Mamba selective-scan fwd tokens/s + achieved HBM GB/s (% of peak), 1 GPU",
+        "value": tokens * 1e3 / ms,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32" if dtype == torch.float32 else "bf16-storage/fp32-compute",
+        "data": "synthetic (BASELINE config distributions, seeded torch generator)",
+        "config": {"workload": workload, "batch": bt, "seq_len": L, "d_inner": dim, "d_state": N,
+                   "storage": "fp32" if es == 4 else "bf16", "input_sets": nsets},
+        "hbm_gbs": achieved,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "algorithmic_bytes": nbytes, "kernel_ms": ms},
+        "cpu_baseline": cpu,
+        "parity_max_rel_err": parity,
+    }
+    print(json.dumps(rec))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,90 @@
+// hx_common.h — shared host/device helpers for libhelix_hip.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "helix_hip.h"
+
+namespace hx {
+
+// ------------------------------------------------------------------ error plumbing (host)
+// Sets the calling thread's last-error text and returns `code`. Every C entry point reports
+// failures through this, so hx_last_error() always names the check that failed.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+#define HX_HIP_CHECK(expr)                                                                   \
+    do {                                                                                     \
+        hipError_t hx_e_ = (expr);                                                           \
+        if (hx_e_ != hipSuccess)                                                             \
+            return ::hx::set_error(HX_ERR_BACKEND, "%s failed: %s (%s:%d)", #expr,           \
+                                   hipGetErrorString(hx_e_), __FILE__, __LINE__);            \
+    } while (0)
+
+// Checks the launch that was just issued.
+#define HX_LAUNCH_CHECK() HX_HIP_CHECK(hipGetLastError())
+
+#define HX_REQUIRE(cond, code, ...)                                                          \
+    do {                                                                                     \
+        if (!(cond)) return ::hx::set_error((code), __VA_ARGS__);                            \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned(const void* p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+// ------------------------------------------------------------------ device helpers
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Storage <-> fp32. bf16 is stored as raw uint16 (upper half of an fp32); conversion to
+// storage rounds to nearest even.
+template <typename T> struct Storage;
+template <> struct Storage<float> {
+    __device__ static inline float load(const float* p) { return *p; }
+    __device__ static inline void store(float* p, float v) { *p = v; }
+};
+template <> struct Storage<uint16_t> {
+    __device__ static inline float load(const uint16_t* p) {
+        return __uint_as_float(static_cast<uint32_t>(*p) << 16);
+    }
+    __device__ static inline uint16_t round(float v) {
+        uint32_t x = __float_as_uint(v);
+        if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x007fffffu))  // NaN stays NaN
+            return static_cast<uint16_t>((x >> 16) | 0x40u);
+        x += 0x7fffu + ((x >> 16) & 1u);
+        return static_cast<uint16_t>(x >> 16);
+    }
+    __device__ static inline void store(uint16_t* p, float v) { *p = round(v); }
+};
+
+__device__ inline float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// exp2 on the transcendental unit (v_exp_f32). Inputs here are finite; underflow flushes to 0.
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ inline float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// softplus(x) = log(1 + e^x), x > 20 -> x. log1p is evaluated as log(u) * e / (u - 1) with
+// u = 1 + e (Goldberg, "What every computer scientist should know about floating-point
+// arithmetic", 1991, Thm. 4), which keeps full relative accuracy for small e^x.
+__device__ inline float softplus(float x) {
+    float e = fast_exp2(x * kLog2e);
+    float u = 1.0f + e;
+    float lg = fast_log2(u) * kLn2;
+    float r = (u == 1.0f) ? e : lg * (e * fast_rcp(u - 1.0f));
+    return x > 20.0f ? x : r;
+}
+
+// silu(z) = z / (1 + e^-z)   (backend-cpu/src/lib.rs:1158-1162)
+__device__ inline float silu(float z) { return z * fast_rcp(1.0f + fast_exp2(-z * kLog2e)); }
+
+}  // namespace hx

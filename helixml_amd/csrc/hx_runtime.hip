@@ -1,0 +1,86 @@
+// hx_runtime.hip — device selection, allocation, copies and error reporting for the C ABI.
+#include <cstdarg>
+#include <cstring>
+
+#include "hx_common.h"
+
+namespace hx {
+
+namespace {
+thread_local char g_last_error[1024] = {0};
+}
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+void clear_error() { g_last_error[0] = 0; }
+
+}  // namespace hx
+
+extern "C" {
+
+int hx_version(void) { return (0 << 16) | (1 << 8) | 0; }
+
+const char* hx_last_error(void) { return hx::g_last_error; }
+
+int hx_init(int device) {
+    int n = 0;
+    HX_HIP_CHECK(hipGetDeviceCount(&n));
+    HX_REQUIRE(device >= 0 && device < n, HX_ERR_INVALID_INPUT,
+               "hx_init: device %d out of range (%d visible)", device, n);
+    HX_HIP_CHECK(hipSetDevice(device));
+    hx::clear_error();
+    return HX_OK;
+}
+
+int hx_malloc(void** ptr, size_t bytes) {
+    HX_REQUIRE(ptr != nullptr, HX_ERR_INVALID_INPUT, "hx_malloc: null out-pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return HX_OK;
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e != hipSuccess) {
+        *ptr = nullptr;
+        return hx::set_error(HX_ERR_ALLOCATION, "hx_malloc(%zu bytes): %s", bytes,
+                             hipGetErrorString(e));
+    }
+    return HX_OK;
+}
+
+int hx_free(void* ptr) {
+    if (ptr == nullptr) return HX_OK;
+    HX_HIP_CHECK(hipFree(ptr));
+    return HX_OK;
+}
+
+int hx_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return HX_OK;
+    HX_REQUIRE(dst && src, HX_ERR_INVALID_INPUT, "hx_memcpy_h2d: null pointer");
+    HX_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return HX_OK;
+}
+
+int hx_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return HX_OK;
+    HX_REQUIRE(dst && src, HX_ERR_INVALID_INPUT, "hx_memcpy_d2h: null pointer");
+    HX_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return HX_OK;
+}
+
+int hx_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return HX_OK;
+    HX_REQUIRE(dst && src, HX_ERR_INVALID_INPUT, "hx_memcpy_d2d: null pointer");
+    HX_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, hx::as_stream(stream)));
+    return HX_OK;
+}
+
+int hx_sync(void) {
+    HX_HIP_CHECK(hipDeviceSynchronize());
+    return HX_OK;
+}
+
+}  // extern "C"

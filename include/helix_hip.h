@@ -1,0 +1,153 @@
+/*
+ * helix_hip.h — C ABI of libhelix_hip.so, the MI355X (gfx950) backend for HelixML's
+ * state-space-model forward path.
+ *
+ * This is the drop-in boundary a Rust `crates/backend-hip` binds with an `extern "C"` block
+ * (the binding is shown in INTEGRATION.md). Every entry point takes plain pointers, sizes and
+ * enums: no HIP, torch or C++ types cross it. Device buffers are allocated by the caller
+ * (hx_malloc, or any HIP allocation on the same device); the library never allocates on the
+ * caller's behalf except in hx_malloc. A `stream` argument is a hipStream_t passed as void*
+ * (NULL = the legacy default stream). All compute entry points are stream-ordered and
+ * asynchronous; they validate shapes on the host before any launch and return a status code.
+ * No C++ exception or panic crosses this boundary.
+ *
+ * Layout conventions (row-major, contiguous, the reference's [tokens, channels] order,
+ * crates/nn/src/lib.rs:121-123 and :889):
+ *   u, delta, z, out : [batch, seqlen, dim]      (channels contiguous)
+ *   B, C (selective) : [batch, seqlen, dstate]
+ *   A                : [dim, dstate]  fp32
+ *   D, dt_bias       : [dim]          fp32
+ *   state            : [batch, dim, dstate] fp32
+ */
+#ifndef HELIX_HIP_H
+#define HELIX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. One per tensor_core::TensorError variant
+ * (reference crates/tensor-core/src/error.rs:7-37), so the Rust side maps them 1:1. */
+typedef enum {
+    HX_OK = 0,
+    HX_ERR_SHAPE_MISMATCH = 1,     /* TensorError::ShapeMismatch      (error.rs:9)  */
+    HX_ERR_INVALID_DIMENSION = 2,  /* TensorError::InvalidDimension   (error.rs:12) */
+    HX_ERR_DEVICE_MISMATCH = 3,    /* TensorError::DeviceMismatch     (error.rs:15) */
+    HX_ERR_DTYPE_MISMATCH = 4,     /* TensorError::DTypeMismatch      (error.rs:18) */
+    HX_ERR_UNSUPPORTED = 5,        /* TensorError::UnsupportedOperation (error.rs:21) */
+    HX_ERR_ALLOCATION = 6,         /* TensorError::AllocationFailed   (error.rs:24) */
+    HX_ERR_BACKEND = 7,            /* TensorError::BackendError       (error.rs:27) */
+    HX_ERR_INVALID_INPUT = 9       /* TensorError::InvalidInput       (error.rs:36) */
+} hx_status;
+
+/* Storage dtypes. Arithmetic and recurrent state are always fp32.
+ * (tensor_core::DType has no BF16, crates/tensor-core/src/dtype.rs:8-37; HX_BF16 is the
+ * storage format the north-star config 3 asks for.) */
+typedef enum { HX_F32 = 0, HX_BF16 = 1 } hx_dtype;
+
+/* ------------------------------------------------------------------ runtime */
+/* Library version, (major << 16) | (minor << 8) | patch. */
+int hx_version(void);
+/* Selects and initialises `device`. Replaces nothing in the reference (its Device enum has no
+ * ROCm variant, tensor-core/src/device.rs:8-25); the Rust side calls it from HipTensor's ctor. */
+int hx_init(int device);
+/* Device allocation / free / copies; back HipTensor storage (the reference's
+ * Tensor::to_device, tensor-core/src/tensor.rs:54, and CpuTensor's owned ndarray). */
+int hx_malloc(void** ptr, size_t bytes);
+int hx_free(void* ptr);
+int hx_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int hx_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int hx_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* Waits for all work on the device. */
+int hx_sync(void);
+/* Text of the last error raised on the calling thread ("" if none). Becomes the message of
+ * TensorError::BackendError / the variant matching the status. */
+const char* hx_last_error(void);
+
+/* ------------------------------------------------------------------ fused selective scan */
+/* Fused Mamba selective-scan forward, one pass over HBM.
+ * Replaces the composite the reference spells as nn::ssm::MambaBlock::selective_ssm
+ * (crates/nn/src/ssm.rs:474-483, which delegates to S4Block::forward_ssm, ssm.rs:138-186) with
+ * the selective semantics the reference's own discretisation implies (Abar = exp(dt*A),
+ * ssm.rs:108-116; Bbar = dt*B, ssm.rs:127-130) and SiLU gating (backend-cpu/src/lib.rs:1158-1162):
+ *   dt    = softplus(delta + dt_bias)        (softplus only if delta_softplus != 0)
+ *   h[n]  = exp(dt*A[d,n]) * h[n] + dt*u*B[b,t,n]
+ *   y     = sum_n C[b,t,n]*h[n] + D[d]*u
+ *   out   = y * silu(z)                       (if z != NULL)
+ * dtype selects the storage type of u, delta, z, B, C and out; A, D, dt_bias, state are fp32.
+ * init_state (nullable) seeds h; last_state (nullable) receives h after the last step. */
+int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
+                          int dtype, int delta_softplus,
+                          const void* u, const void* delta, const float* A,
+                          const void* B, const void* C, const float* D,
+                          const void* z, const float* dt_bias,
+                          void* out, const float* init_state, float* last_state,
+                          void* stream);
+
+/* Single-step recurrent decode (state update only), for token-by-token generation:
+ * the same arithmetic as one time step of hx_selective_scan_fwd with seqlen 1, updating
+ * `state` [batch, dim, dstate] in place. u, delta, z, out: [batch, dim]; B, C: [batch, dstate].
+ * No reference counterpart beyond the per-step body of ssm.rs:166-182. */
+int hx_selective_state_update(int64_t batch, int64_t dim, int64_t dstate,
+                              int dtype, int delta_softplus,
+                              float* state, const void* u, const void* delta, const float* A,
+                              const void* B, const void* C, const float* D,
+                              const void* z, const float* dt_bias, void* out,
+                              void* stream);
+
+/* ------------------------------------------------------------------ S4 recurrences */
+/* Reference-faithful nn::ssm::S4Block::forward_ssm (crates/nn/src/ssm.rs:138-186) with
+ * discretize(dt) (ssm.rs:103-135): a[n] = exp(dt*a_real[n])*cos(dt*a_imag[n]), Bd = dt*B,
+ * one state h[dstate] SHARED by all channels:
+ *   h = a (.) h + Bd . x[:, t];   y[t][m] = (C . h)[m] + D[m] * x[m][t]
+ * x: [d_model, seqlen] row-major (column t is u_t, ssm.rs:168-169).
+ * y: memory [seqlen, d_model] (CpuTensor::stack(..., 1) of per-step vectors writes rows in time
+ *    order, backend-cpu/src/lib.rs:277-296; the shape field it reports is [d_model, seqlen]).
+ * gate (nullable) [d_model]: y[t][m] *= gate[m] — fuses nn::ssm::MambaBlock's gating
+ *    (ssm.rs:460-461, broadcast_to repeat-rows, backend-cpu/src/lib.rs:1388-1404).
+ * B: [dstate, d_model], C: [d_model, dstate], D: [d_model]. dstate <= 64. */
+int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, float dt,
+                  const float* x, const float* a_real, const float* a_imag,
+                  const float* B, const float* C, const float* D, const float* gate,
+                  float* y, void* stream);
+
+/* S4D diagonal complex recurrence (per-channel state, S4D discretisation with the same
+ * ZOH-on-A / Euler-on-B choice as ssm.rs:108-130), the complex form of what
+ * S4Block::discretize computes and then drops (A_d_imag, ssm.rs:121-125):
+ *   Abar[d,n] = exp(dt[d]*(a_re[d,n] + i*a_im[d,n])), Bbar = dt[d]*B[d,n] (complex)
+ *   h[d,n] = Abar*h + Bbar*x[b,t,d];  y[b,t,d] = 2*Re(sum_n C[d,n]*h[d,n]) + D[d]*x[b,t,d]
+ * x, y: [batch, seqlen, dim] fp32. a_re, a_im, B_re, B_im, C_re, C_im: [dim, dstate]; dt, D: [dim]. */
+int hx_s4d_complex_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
+                       const float* x, const float* dt,
+                       const float* a_re, const float* a_im,
+                       const float* B_re, const float* B_im,
+                       const float* C_re, const float* C_im,
+                       const float* D, float* y, void* stream);
+
+/* ------------------------------------------------------------------ dense */
+/* nn::Linear::forward (crates/nn/src/lib.rs:120-134): Y[r][o] = sum_k X[r][k]*W[o][k] + bias[o],
+ * W in the reference's [out_features, in_features] layout; bias nullable.
+ * act: 0 = none, 1 = SiLU fused on the output (nn::MambaBlock::forward_mamba's
+ * Linear -> silu, lib.rs:894-900). fp32 storage and accumulate. */
+int hx_linear_f32(int64_t rows, int64_t in_features, int64_t out_features,
+                  const float* X, const float* W, const float* bias, int act,
+                  float* Y, void* stream);
+
+/* CpuTensor::matmul 2-D x 2-D (crates/backend-cpu/src/lib.rs:644-678): Y = A[M,K] . B[K,N]. */
+int hx_matmul_f32(int64_t M, int64_t K, int64_t N, const float* A, const float* B, float* Y,
+                  void* stream);
+
+/* ------------------------------------------------------------------ tuning */
+/* Selects the selective-scan kernel variant for later calls in this process: 0 = auto (default),
+ * 1/2/4/8 = the fast kernel with that many waves per block (16/W states per wave), -1 = the
+ * generic one-thread-per-channel kernel. A measurement knob with no reference counterpart;
+ * results are identical within fp32 rounding for every variant. */
+int hx_set_scan_variant(int variant);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HELIX_HIP_H */

@@ -1,0 +1,262 @@
+"""CPU oracle for the SSM forward path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+this package; the product library (``helixml_amd``, ``libhelix_hip.so``) never does.
+
+``liboracle.so`` (built from ``hx_oracle.c`` / ``hx_oracle_omp.c`` by ``make -C oracle``) holds
+the plain-C restatement of the reference's CPU arithmetic; this module wraps it for numpy.
+``numpy_*`` functions are a second, independent float64 restatement used to cross-check the C
+one (tests/test_oracle.py).
+
+Pinning status of each function (how tests/test_oracle.py pins it):
+  matmul, linear        reference KATs ones[2,3].ones[3,4] == 3 and ones+ones == 2
+                        (backend-cpu/src/lib.rs:1733-1758), numpy float64
+  silu                  closed form x*sigmoid(x), special values
+  s4_ref_fwd            zero input, impulse response, step response (geometric series),
+                        linearity, B=0 -> D*u, a=1 -> prefix sum, numpy float64 brute force
+  ssm_mamba_fwd         composition: matmul + s4_ref_fwd + gate (each pinned above)
+  mamba_mlp             composition of linear/silu, numpy float64
+  rmsnorm               closed form on constant rows, numpy float64
+  selective_scan(_f64)  B=0/C=0 -> D*u*silu(z); A=0 -> prefix sum; N=1 constant inputs ->
+                        geometric series; split-sequence == whole (state hand-off);
+                        decode steps == prefill; f32 vs f64; numpy float64
+  s4d_complex           impulse response 2*Re(sum C Abar^t Bbar), constant-input steady state
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_lib = None
+
+_f = ctypes.c_float
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_p = ctypes.c_void_p
+
+
+def build() -> Path:
+    """Compiles liboracle.so with the Makefile next to this file."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        sig = {
+            "oracle_matmul": [_i64, _i64, _i64, _p, _p, _p],
+            "oracle_silu": [_i64, _p, _p],
+            "oracle_linear": [_i64, _i64, _i64, _p, _p, _p, _int, _p],
+            "oracle_mamba_mlp": [_i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p],
+            "oracle_rmsnorm": [_i64, _i64, _p, _p, _f, _p],
+            "oracle_s4_ref_fwd": [_i64, _i64, _i64, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+            "oracle_ssm_mamba_fwd": [_i64, _i64, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+            "oracle_selective_scan": [_i64, _i64, _i64, _i64, _int] + [_p] * 11,
+            "oracle_selective_scan_f64": [_i64, _i64, _i64, _i64, _int] + [_p] * 11,
+            "oracle_selective_state_update": [_i64, _i64, _i64, _int] + [_p] * 10,
+            "oracle_s4d_complex": [_i64, _i64, _i64, _i64] + [_p] * 10,
+            "oracle_selective_scan_omp": [_i64, _i64, _i64, _i64, _int] + [_p] * 9 + [_int],
+            "oracle_max_threads": [],
+        }
+        for name, args in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _int if name == "oracle_max_threads" else None
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ------------------------------------------------------------------ C restatement wrappers
+
+def matmul(A, B):
+    A, B = _f32(A), _f32(B)
+    M, K = A.shape
+    K2, N = B.shape
+    assert K == K2
+    Y = np.empty((M, N), np.float32)
+    lib().oracle_matmul(M, K, N, _ptr(A), _ptr(B), _ptr(Y))
+    return Y
+
+
+def silu(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().oracle_silu(x.size, _ptr(x), _ptr(y))
+    return y
+
+
+def linear(X, W, bias=None, act=0):
+    X, W, bias = _f32(X), _f32(W), _f32(bias)
+    R, IN = X.shape
+    OUT = W.shape[0]
+    Y = np.empty((R, OUT), np.float32)
+    lib().oracle_linear(R, IN, OUT, _ptr(X), _ptr(W), _ptr(bias), act, _ptr(Y))
+    return Y
+
+
+def mamba_mlp(X, Wg, bg, Wo, bo):
+    X, Wg, bg, Wo, bo = map(_f32, (X, Wg, bg, Wo, bo))
+    R, dm = X.shape
+    di = Wg.shape[0]
+    tmp = np.empty((R, di), np.float32)
+    Y = np.empty((R, dm), np.float32)
+    lib().oracle_mamba_mlp(R, dm, di, _ptr(X), _ptr(Wg), _ptr(bg), _ptr(Wo), _ptr(bo), _ptr(tmp), _ptr(Y))
+    return Y
+
+
+def rmsnorm(X, w, eps):
+    X, w = _f32(X), _f32(w)
+    R, Dm = X.shape
+    Y = np.empty_like(X)
+    lib().oracle_rmsnorm(R, Dm, _ptr(X), _ptr(w), eps, _ptr(Y))
+    return Y
+
+
+def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1):
+    """x [M, L] -> y memory [L, M] (see hx_oracle.c)."""
+    x, a_real, a_imag, B, C, D, gate = map(_f32, (x, a_real, a_imag, B, C, D, gate))
+    M, L = x.shape
+    N = a_real.shape[0]
+    y = np.empty((L, M), np.float32)
+    work = np.empty(3 * N + M, np.float32)
+    lib().oracle_s4_ref_fwd(M, N, L, dt, _ptr(x), _ptr(a_real), _ptr(a_imag), _ptr(B), _ptr(C),
+                            _ptr(D), _ptr(gate), _ptr(y), _ptr(work))
+    return y
+
+
+def ssm_mamba_fwd(X, delta_proj, a_real, a_imag, B, C, D, gate, dt=0.1):
+    X, delta_proj, a_real, a_imag, B, C, D, gate = map(_f32, (X, delta_proj, a_real, a_imag, B, C, D, gate))
+    M = X.shape[0]
+    N = a_real.shape[0]
+    y = np.empty((M, M), np.float32)
+    work = np.empty(M * M + 3 * N + M, np.float32)
+    lib().oracle_ssm_mamba_fwd(M, N, dt, _ptr(X), _ptr(delta_proj), _ptr(a_real), _ptr(a_imag),
+                               _ptr(B), _ptr(C), _ptr(D), _ptr(gate), _ptr(y), _ptr(work))
+    return y
+
+
+def selective_scan(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_softplus=True,
+                   init_state=None, return_last_state=False, f64=False):
+    """u, delta, z: [Bt, L, Dd]; A [Dd, N]; B, C [Bt, L, N]; D, dt_bias [Dd]."""
+    u, delta, A, B, C, D, z, dt_bias, init_state = map(_f32, (u, delta, A, B, C, D, z, dt_bias, init_state))
+    Bt, L, Dd = u.shape
+    N = A.shape[1]
+    if f64:
+        out = np.empty((Bt, L, Dd), np.float64)
+        last = np.empty((Bt, Dd, N), np.float64) if return_last_state else None
+        fn = lib().oracle_selective_scan_f64
+    else:
+        out = np.empty((Bt, L, Dd), np.float32)
+        last = np.empty((Bt, Dd, N), np.float32) if return_last_state else None
+        fn = lib().oracle_selective_scan
+    fn(Bt, L, Dd, N, int(bool(delta_softplus)), _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C),
+       _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(out), _ptr(init_state), _ptr(last))
+    return (out, last) if return_last_state else out
+
+
+def selective_state_update(state, u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_softplus=True):
+    """One decode step; returns (out [Bt, Dd], new_state [Bt, Dd, N])."""
+    state = np.array(state, dtype=np.float32, copy=True)
+    u, delta, A, B, C, D, z, dt_bias = map(_f32, (u, delta, A, B, C, D, z, dt_bias))
+    Bt, Dd = u.shape
+    N = A.shape[1]
+    out = np.empty((Bt, Dd), np.float32)
+    lib().oracle_selective_state_update(Bt, Dd, N, int(bool(delta_softplus)), _ptr(state), _ptr(u),
+                                        _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z),
+                                        _ptr(dt_bias), _ptr(out))
+    return out, state
+
+
+def selective_scan_omp(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_softplus=True, threads=0):
+    u, delta, A, B, C, D, z, dt_bias = map(_f32, (u, delta, A, B, C, D, z, dt_bias))
+    Bt, L, Dd = u.shape
+    N = A.shape[1]
+    out = np.empty((Bt, L, Dd), np.float32)
+    lib().oracle_selective_scan_omp(Bt, L, Dd, N, int(bool(delta_softplus)), _ptr(u), _ptr(delta),
+                                    _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(dt_bias),
+                                    _ptr(out), int(threads))
+    return out
+
+
+def max_threads() -> int:
+    return lib().oracle_max_threads()
+
+
+def s4d_complex(x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D=None):
+    x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D = map(_f32, (x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D))
+    Bt, L, Dd = x.shape
+    N = a_re.shape[1]
+    y = np.empty((Bt, L, Dd), np.float64)
+    lib().oracle_s4d_complex(Bt, L, Dd, N, _ptr(x), _ptr(dt), _ptr(a_re), _ptr(a_im), _ptr(B_re),
+                             _ptr(B_im), _ptr(C_re), _ptr(C_im), _ptr(D), _ptr(y))
+    return y
+
+
+# ------------------------------------------------------------------ independent float64 restatements
+
+def numpy_selective_scan(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_softplus=True,
+                         init_state=None):
+    """Vectorised over (batch, channel, state), float64; returns (out, last_state)."""
+    u = np.asarray(u, np.float64)
+    dl = np.asarray(delta, np.float64)
+    if dt_bias is not None:
+        dl = dl + np.asarray(dt_bias, np.float64)[None, None, :]
+    if delta_softplus:
+        dl = np.where(dl > 20.0, dl, np.log1p(np.exp(np.minimum(dl, 20.0))))
+    A = np.asarray(A, np.float64)
+    B = np.asarray(B, np.float64)
+    C = np.asarray(C, np.float64)
+    Bt, L, Dd = u.shape
+    N = A.shape[1]
+    h = np.zeros((Bt, Dd, N)) if init_state is None else np.asarray(init_state, np.float64).copy()
+    out = np.empty((Bt, L, Dd))
+    for t in range(L):
+        dA = np.exp(dl[:, t, :, None] * A[None])                          # [Bt, Dd, N]
+        h = dA * h + (dl[:, t, :] * u[:, t, :])[:, :, None] * B[:, t, None, :]
+        y = np.einsum("bdn,bn->bd", h, C[:, t, :])
+        if D is not None:
+            y = y + np.asarray(D, np.float64)[None] * u[:, t, :]
+        if z is not None:
+            zz = np.asarray(z, np.float64)[:, t, :]
+            y = y * zz / (1.0 + np.exp(-zz))
+        out[:, t, :] = y
+    return out, h
+
+
+def numpy_s4_ref(x, a_real, a_imag, B, C, D, gate=None, dt=0.1):
+    """float64 restatement of S4Block::forward_ssm (ssm.rs:138-186); y memory [L, M]."""
+    x = np.asarray(x, np.float64)
+    M, L = x.shape
+    a = np.exp(np.asarray(a_real, np.float64) * dt) * np.cos(np.asarray(a_imag, np.float64) * dt)
+    Bd = np.asarray(B, np.float64) * dt
+    C = np.asarray(C, np.float64)
+    D = np.asarray(D, np.float64)
+    h = np.zeros(a.shape[0])
+    y = np.empty((L, M))
+    for t in range(L):
+        h = a * h + Bd @ x[:, t]
+        y[t] = C @ h + D * x[:, t]
+    if gate is not None:
+        y = y * np.asarray(gate, np.float64)[None, :]
+    return y

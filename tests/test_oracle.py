@@ -1,0 +1,330 @@
+"""Pins the CPU oracle (oracle/hx_oracle.c) before anything is compared against it.
+
+Each oracle function is checked against the reference's own known-answer tests where they exist
+(backend-cpu/src/lib.rs:1733-1758), closed forms, invariants and an independent float64 numpy
+restatement — chosen so a dropped term, a wrong sign/index or a transposed operand fails.
+The planted-mistake tests at the end show the checks do fail on such mistakes.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests.util import rel_err
+
+F = np.float32
+
+
+# ------------------------------------------------------------------ CpuTensor primitives
+
+def test_reference_kat_matmul_ones():
+    # backend-cpu/src/lib.rs:1747-1758: ones[2,3] . ones[3,4] == 3 everywhere (to 1e-6)
+    y = oracle.matmul(np.ones((2, 3), F), np.ones((3, 4), F))
+    assert y.shape == (2, 4)
+    assert np.all(np.abs(y - 3.0) < 1e-6)
+
+
+def test_reference_kat_linear_ones_plus_bias():
+    # Linear with W = ones[4,3] (out, in) on ones[2,3]: 3 + bias (ones+ones == 2 KAT: lib.rs:1733-1744)
+    y = oracle.linear(np.ones((2, 3), F), np.ones((4, 3), F), np.ones(4, F))
+    assert np.all(y == 4.0)
+    assert np.all(oracle.linear(np.ones((2, 3), F), np.zeros((4, 3), F), np.ones(4, F)) + 1.0 == 2.0)
+
+
+def test_matmul_vs_numpy_f64():
+    rng = np.random.default_rng(1)
+    A = rng.standard_normal((17, 33), dtype=F)
+    B = rng.standard_normal((33, 9), dtype=F)
+    assert rel_err(oracle.matmul(A, B), A.astype(np.float64) @ B.astype(np.float64)) < 1e-4
+
+
+def test_matmul_is_sequential_f32_ijk():
+    # a value where summation order matters in f32: 1e8 + 1 - 1e8 (k ascending) == 0 in f32
+    A = np.array([[1e8, 1.0, -1e8]], F)
+    B = np.ones((3, 1), F)
+    assert oracle.matmul(A, B)[0, 0] == np.float32(np.float32(np.float32(1e8) + 1.0) - np.float32(1e8))
+
+
+def test_silu_closed_form():
+    x = np.array([0.0, 1.0, -1.0, 30.0, -30.0, 5.5], F)
+    y = oracle.silu(x)
+    ref = x.astype(np.float64) / (1.0 + np.exp(-x.astype(np.float64)))
+    assert y[0] == 0.0
+    assert rel_err(y, ref) < 1e-6
+    assert abs(y[3] - 30.0) < 1e-5
+
+
+def test_linear_and_mlp_vs_numpy():
+    rng = np.random.default_rng(2)
+    X = rng.uniform(-1, 1, (10, 8)).astype(F)
+    Wg = rng.standard_normal((16, 8), dtype=F)
+    bg = rng.standard_normal(16, dtype=F)
+    Wo = rng.standard_normal((8, 16), dtype=F)
+    bo = rng.standard_normal(8, dtype=F)
+    X64 = X.astype(np.float64)
+    H = X64 @ Wg.T.astype(np.float64) + bg
+    S = H / (1 + np.exp(-H))
+    Y = S @ Wo.T.astype(np.float64) + bo
+    assert rel_err(oracle.mamba_mlp(X, Wg, bg, Wo, bo), Y) < 1e-5
+
+
+def test_rmsnorm_constant_rows():
+    x = np.full((3, 8), 2.0, F)
+    y = oracle.rmsnorm(x, np.ones(8, F), 1e-6)
+    assert rel_err(y, np.full((3, 8), 2.0 / np.sqrt(4.0 + 1e-6))) < 1e-6
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 32), dtype=F)
+    w = rng.standard_normal(32, dtype=F)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + 1e-5) * w
+    assert rel_err(oracle.rmsnorm(x, w, 1e-5), ref) < 1e-5
+
+
+# ------------------------------------------------------------------ S4 reference mode
+
+def s4_params(M, N, seed, a_real=None, a_imag=None, D=None):
+    rng = np.random.default_rng(seed)
+    return dict(
+        a_real=np.zeros(N, F) if a_real is None else a_real.astype(F),
+        a_imag=rng.standard_normal(N, dtype=F) if a_imag is None else a_imag.astype(F),
+        B=(rng.standard_normal((N, M)) * 0.1).astype(F),
+        C=(rng.standard_normal((M, N)) * 0.1).astype(F),
+        D=rng.standard_normal(M, dtype=F) if D is None else D.astype(F),
+    )
+
+
+def test_s4_zero_input_zero_output():
+    p = s4_params(6, 4, 0)
+    y = oracle.s4_ref_fwd(np.zeros((6, 9), F), **p)
+    assert y.shape == (9, 6) and np.all(y == 0)
+
+
+def test_s4_impulse_response_closed_form():
+    M, N, L, j = 5, 4, 12, 2
+    p = s4_params(M, N, 1, a_real=np.full(4, -0.5), a_imag=np.pi * np.arange(4))
+    x = np.zeros((M, L), F)
+    x[j, 0] = 1.0
+    y = oracle.s4_ref_fwd(x, **p)
+    dt = 0.1
+    a = np.exp(-0.5 * dt) * np.cos(np.pi * np.arange(N) * dt)
+    Bd = p["B"].astype(np.float64) * dt
+    for t in range(L):
+        ref = p["C"].astype(np.float64) @ (a ** t * Bd[:, j])
+        if t == 0:
+            ref[j] += p["D"][j]
+        assert rel_err(y[t], ref) < 1e-5, t
+
+
+def test_s4_step_response_geometric_series():
+    M, N, L, j = 4, 3, 40, 1
+    p = s4_params(M, N, 2, a_real=np.array([-1.0, -2.0, -0.3]), a_imag=np.array([0.0, 3.0, 7.0]))
+    x = np.zeros((M, L), F)
+    x[j, :] = 1.0
+    y = oracle.s4_ref_fwd(x, **p)
+    dt = 0.1
+    a = np.exp(p["a_real"] * dt) * np.cos(p["a_imag"] * dt)
+    Bd = p["B"].astype(np.float64)[:, j] * dt
+    for t in range(L):
+        h = (1 - a ** (t + 1)) / (1 - a) * Bd
+        ref = p["C"].astype(np.float64) @ h
+        ref[j] += p["D"][j]
+        assert rel_err(y[t], ref) < 1e-5
+
+
+def test_s4_a_equal_one_is_prefix_sum():
+    M, N, L = 6, 5, 30
+    p = s4_params(M, N, 3, a_real=np.zeros(N), a_imag=np.zeros(N))
+    x = np.random.default_rng(4).standard_normal((M, L)).astype(F)
+    y = oracle.s4_ref_fwd(x, **p)
+    H = np.cumsum((p["B"].astype(np.float64) * 0.1) @ x.astype(np.float64), axis=1)  # [N, L]
+    ref = (p["C"].astype(np.float64) @ H).T + (p["D"][:, None] * x).T
+    assert rel_err(y, ref) < 1e-5
+
+
+def test_s4_b_zero_gives_feedthrough_and_gate():
+    M, N, L = 7, 4, 11
+    p = s4_params(M, N, 5)
+    p["B"] = np.zeros_like(p["B"])
+    x = np.random.default_rng(6).standard_normal((M, L)).astype(F)
+    gate = np.random.default_rng(7).standard_normal(M).astype(F)
+    y = oracle.s4_ref_fwd(x, gate=gate, **p)
+    assert np.array_equal(y, ((p["D"][:, None] * x).T * gate[None, :]).astype(F))
+
+
+def test_s4_linearity_and_numpy_bruteforce():
+    M, N, L = 8, 4, 16
+    p = s4_params(M, N, 8, a_real=np.full(N, -0.5), a_imag=np.pi * np.arange(N))
+    rng = np.random.default_rng(9)
+    x1 = rng.standard_normal((M, L)).astype(F)
+    x2 = rng.standard_normal((M, L)).astype(F)
+    y12 = oracle.s4_ref_fwd(x1 + 2 * x2, **p)
+    assert rel_err(y12, oracle.s4_ref_fwd(x1, **p).astype(np.float64) + 2 * oracle.s4_ref_fwd(x2, **p)) < 1e-4
+    assert rel_err(oracle.s4_ref_fwd(x1, **p), oracle.numpy_s4_ref(x1, **p)) < 1e-5
+
+
+def test_ssm_mamba_is_matmul_then_s4_then_gate():
+    M, N = 12, 4
+    rng = np.random.default_rng(10)
+    X = rng.standard_normal((M, M)).astype(F)
+    dp = (rng.standard_normal((M, M)) * 0.1).astype(F)
+    gate = (rng.standard_normal(M) * 0.1).astype(F)
+    p = s4_params(M, N, 11)
+    y = oracle.ssm_mamba_fwd(X, dp, gate=gate, **p)
+    delta = oracle.matmul(X, dp)
+    assert np.array_equal(y, oracle.s4_ref_fwd(delta, gate=gate, **p))
+    ref = oracle.numpy_s4_ref(X.astype(np.float64) @ dp.astype(np.float64), gate=gate, **p)
+    assert rel_err(y, ref) < 1e-4
+
+
+# ------------------------------------------------------------------ selective scan
+
+def inputs(bt, L, dim, N, seed, **kw):
+    from tests.util import scan_inputs
+    return scan_inputs(bt, L, dim, N, seed, **kw)
+
+
+def test_scan_b_zero_is_gated_feedthrough():
+    x = inputs(2, 9, 5, 4, 0)
+    x["B"][:] = 0
+    out = oracle.selective_scan(**x)
+    u, z = x["u"].astype(np.float64), x["z"].astype(np.float64)
+    assert rel_err(out, x["D"] * u * z / (1 + np.exp(-z))) < 1e-6
+    x2 = inputs(2, 9, 5, 4, 0)
+    x2["C"][:] = 0
+    assert rel_err(oracle.selective_scan(**x2), x["D"] * u * z / (1 + np.exp(-z))) < 1e-6
+
+
+def test_scan_a_zero_is_prefix_sum():
+    x = inputs(2, 25, 6, 8, 1, with_z=False)
+    x["A"][:] = 0
+    out = oracle.selective_scan(**x)
+    dl = x["delta"].astype(np.float64)
+    dl = np.log1p(np.exp(dl))
+    du = dl * x["u"]                                                     # [b, L, d]
+    H = np.cumsum(du[..., None] * x["B"][:, :, None, :].astype(np.float64), axis=1)   # [b, L, d, n]
+    ref = np.einsum("bldn,bln->bld", H, x["C"].astype(np.float64)) + x["D"] * x["u"]
+    assert rel_err(out, ref) < 1e-5
+
+
+def test_scan_single_state_geometric_series():
+    L, dl, A, u, Bv, Cv = 50, 0.2, -1.5, 0.7, 1.3, -0.9
+    f = lambda v, shape: np.full(shape, v, F)
+    out = oracle.selective_scan(f(u, (1, L, 1)), f(dl, (1, L, 1)), f(A, (1, 1)), f(Bv, (1, L, 1)),
+                                f(Cv, (1, L, 1)), delta_softplus=False)
+    a = np.exp(dl * A)
+    t = np.arange(L)
+    ref = Cv * dl * u * Bv * (1 - a ** (t + 1)) / (1 - a)
+    assert rel_err(out[0, :, 0], ref) < 1e-5
+
+
+def test_scan_split_sequence_equals_whole():
+    x = inputs(2, 40, 7, 16, 2, with_bias=True)
+    out, last = oracle.selective_scan(**x, return_last_state=True)
+    k = 17
+    first = {n: (v[:, :k] if n in ("u", "delta", "B", "C", "z") else v) for n, v in x.items()}
+    second = {n: (v[:, k:] if n in ("u", "delta", "B", "C", "z") else v) for n, v in x.items()}
+    o1, s1 = oracle.selective_scan(**first, return_last_state=True)
+    o2, s2 = oracle.selective_scan(**second, init_state=s1, return_last_state=True)
+    assert np.array_equal(np.concatenate([o1, o2], 1), out)
+    assert np.array_equal(s2, last)
+
+
+def test_scan_decode_steps_equal_prefill():
+    x = inputs(3, 12, 5, 16, 3)
+    out, last = oracle.selective_scan(**x, return_last_state=True)
+    state = np.zeros((3, 5, 16), F)
+    for t in range(12):
+        o, state = oracle.selective_state_update(state, x["u"][:, t], x["delta"][:, t], x["A"],
+                                                 x["B"][:, t], x["C"][:, t], x["D"], x["z"][:, t])
+        assert np.array_equal(o, out[:, t])
+    assert np.array_equal(state, last)
+
+
+def test_scan_f32_f64_and_numpy_agree():
+    x = inputs(2, 300, 9, 16, 4, with_bias=True, s4d_real_A=False)
+    o32 = oracle.selective_scan(**x)
+    o64, s64 = oracle.selective_scan(**x, f64=True, return_last_state=True)
+    on, sn = oracle.numpy_selective_scan(**x)
+    assert rel_err(on, o64) < 1e-10
+    assert rel_err(sn, s64) < 1e-10
+    assert rel_err(o32, o64) < 1e-4
+
+
+def test_scan_omp_matches_serial():
+    x = inputs(2, 64, 33, 16, 5)
+    assert np.array_equal(oracle.selective_scan_omp(**x, threads=3), oracle.selective_scan(**x))
+
+
+def test_scan_softplus_threshold():
+    # delta_raw > 20 passes through unchanged: h = exp(d*A) h + d*u*B with d = delta_raw
+    L = 3
+    f = lambda v, shape: np.full(shape, v, F)
+    out = oracle.selective_scan(f(1.0, (1, L, 1)), f(25.0, (1, L, 1)), f(-0.01, (1, 1)),
+                                f(1.0, (1, L, 1)), f(1.0, (1, L, 1)))
+    out_np = oracle.selective_scan(f(1.0, (1, L, 1)), f(25.0, (1, L, 1)), f(-0.01, (1, 1)),
+                                   f(1.0, (1, L, 1)), f(1.0, (1, L, 1)), delta_softplus=False)
+    assert np.array_equal(out, out_np)
+
+
+# ------------------------------------------------------------------ S4D complex
+
+def s4d_params(dim, N, seed):
+    rng = np.random.default_rng(seed)
+    return dict(
+        dt=np.full(dim, 0.1, F),
+        a_re=np.full((dim, N), -0.5, F),
+        a_im=np.tile((np.pi * np.arange(N)).astype(F), (dim, 1)),
+        B_re=rng.standard_normal((dim, N)).astype(F), B_im=rng.standard_normal((dim, N)).astype(F),
+        C_re=rng.standard_normal((dim, N)).astype(F), C_im=rng.standard_normal((dim, N)).astype(F),
+        D=rng.standard_normal(dim).astype(F),
+    )
+
+
+def test_s4d_impulse_response():
+    dim, N, L = 3, 4, 20
+    p = s4d_params(dim, N, 0)
+    x = np.zeros((1, L, dim), F)
+    x[0, 0, :] = 1.0
+    y = oracle.s4d_complex(x, **p)
+    q = {k: v.astype(np.float64) for k, v in p.items()}
+    Ab = np.exp(q["dt"][:, None] * (q["a_re"] + 1j * q["a_im"]))
+    Bb = q["dt"][:, None] * (q["B_re"] + 1j * q["B_im"])
+    Cc = q["C_re"] + 1j * q["C_im"]
+    for t in range(L):
+        ref = 2 * np.real((Cc * Ab ** t * Bb).sum(-1)) + (p["D"] if t == 0 else 0)
+        assert rel_err(y[0, t], ref) < 1e-6
+
+
+def test_s4d_constant_input_steady_state():
+    dim, N, L = 2, 3, 400
+    p = s4d_params(dim, N, 1)
+    x = np.ones((1, L, dim), F)
+    y = oracle.s4d_complex(x, **p)
+    q = {k: v.astype(np.float64) for k, v in p.items()}
+    Ab = np.exp(q["dt"][:, None] * (q["a_re"] + 1j * q["a_im"]))
+    Bb = q["dt"][:, None] * (q["B_re"] + 1j * q["B_im"])
+    Cc = q["C_re"] + 1j * q["C_im"]
+    ss = 2 * np.real((Cc * Bb / (1 - Ab)).sum(-1)) + p["D"]
+    assert rel_err(y[0, -1], ss) < 1e-6
+
+
+# ------------------------------------------------------------------ planted mistakes (the checks bite)
+
+def test_planted_mistakes_are_caught():
+    x = inputs(1, 50, 4, 16, 6)
+    good = oracle.selective_scan(**x)
+    ref, _ = oracle.numpy_selective_scan(**x)
+    assert rel_err(good, ref) < 1e-4
+    # dropped D term
+    assert rel_err(oracle.selective_scan(**{**x, "D": None}), ref) > 1e-2
+    # B and C transposed
+    assert rel_err(oracle.selective_scan(**{**x, "B": x["C"], "C": x["B"]}), ref) > 1e-2
+    # sign of A flipped (on a short sequence so it stays finite)
+    short = {n: (v[:, :8] if n in ("u", "delta", "B", "C", "z") else v) for n, v in x.items()}
+    ref_s, _ = oracle.numpy_selective_scan(**short)
+    assert rel_err(oracle.selective_scan(**{**short, "A": -short["A"]}), ref_s) > 1e-3
+    # S4: wrong decay (cos replaced by 1) is caught by the closed form
+    M, N, L = 4, 4, 10
+    p = s4_params(M, N, 12, a_real=np.full(N, -0.5), a_imag=np.pi * np.arange(N))
+    x1 = np.random.default_rng(13).standard_normal((M, L)).astype(F)
+    wrong = dict(p, a_imag=np.zeros(N, F))
+    assert rel_err(oracle.s4_ref_fwd(x1, **wrong), oracle.numpy_s4_ref(x1, **p)) > 1e-2

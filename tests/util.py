@@ -1,0 +1,55 @@
+"""Shared test helpers: seeded inputs and the tolerance metric.
+
+Tolerance metric (used by every parity test):
+    rel = max_i |g_i - r_i| / max(|r_i|, 1e-3 * max_j |r_j|)
+i.e. elementwise relative error with a denominator floor at 1e-3 of the output's infinity
+norm, so near-zero outputs do not blow the ratio up. Bars: fp32 storage 1e-4, bf16 storage
+2e-2, both against the fp32 CPU oracle on identical inputs.
+"""
+import numpy as np
+
+TOL_F32 = 1e-4
+TOL_BF16 = 2e-2
+
+
+def rel_err(g, r) -> float:
+    g = np.asarray(g, np.float64)
+    r = np.asarray(r, np.float64)
+    if r.size == 0:
+        return 0.0
+    floor = 1e-3 * max(np.abs(r).max(), 1e-30)
+    return float((np.abs(g - r) / np.maximum(np.abs(r), floor)).max())
+
+
+def norm_err(g, r) -> float:
+    g = np.asarray(g, np.float64)
+    r = np.asarray(r, np.float64)
+    return float(np.abs(g - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+def bf16_round(x):
+    """Round-to-nearest-even to bf16, returned as float32 (what bf16 storage holds)."""
+    x = np.ascontiguousarray(x, np.float32)
+    b = x.view(np.uint32).astype(np.uint64)
+    b = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
+    return b.astype(np.uint32).view(np.float32)
+
+
+def scan_inputs(bt, L, dim, N, seed, with_z=True, with_D=True, with_bias=False, s4d_real_A=True):
+    """The BASELINE config-2 distributions: u, z ~ N(0,1); delta_raw = N(0,1)*0.5 - 4 (softplus
+    applied by the kernel); A[d,n] = -(n+1) (S4D-real init); B, C ~ N(0,1) per (batch, t, state);
+    D ~ N(0,1)."""
+    rng = np.random.default_rng(seed)
+    f = np.float32
+    u = rng.standard_normal((bt, L, dim), dtype=f)
+    delta = (rng.standard_normal((bt, L, dim), dtype=f) * f(0.5) - f(4.0)).astype(f)
+    if s4d_real_A:
+        A = -np.tile(np.arange(1, N + 1, dtype=f), (dim, 1))
+    else:
+        A = -np.exp(rng.standard_normal((dim, N), dtype=f)).astype(f)
+    B = rng.standard_normal((bt, L, N), dtype=f)
+    C = rng.standard_normal((bt, L, N), dtype=f)
+    D = rng.standard_normal(dim, dtype=f) if with_D else None
+    z = rng.standard_normal((bt, L, dim), dtype=f) if with_z else None
+    dt_bias = (rng.standard_normal(dim, dtype=f) * f(0.1)).astype(f) if with_bias else None
+    return dict(u=u, delta=delta, A=A, B=B, C=C, D=D, z=z, dt_bias=dt_bias)
