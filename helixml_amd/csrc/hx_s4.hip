@@ -2,9 +2,9 @@
 //
 // (1) Reference-mode S4Block::forward_ssm (crates/nn/src/ssm.rs:138-186): one state h[N] shared
 //     by all d_model channels, constant diagonal decay a[n] = exp(dt*a_real)*cos(dt*a_imag)
-//     (ssm.rs:113-120), Bd = dt*B (ssm.rs:130). It factors into three bandwidth-bound steps:
+//     (ssm.rs:113-120), Bd = dt*B (ssm.rs:130). It factors into three steps:
 //       U[t][n] = sum_m Bd[n][m] * x[m][t]            (column reduction over channels)
-//       H[t][n] = a[n]*H[t-1][n] + U[t][n]             (16 independent first-order scans)
+//       H[t][n] = a[n]*H[t-1][n] + U[t][n]             (16 independent first-order recurrences)
 //       y[t][m] = (sum_n C[m][n]*H[t][n] + D[m]*x[m][t]) * gate[m]
 //     x is [d_model, L] (time contiguous) and y is [L, d_model] (channels contiguous), so the
 //     output kernel transposes through LDS.
@@ -16,13 +16,20 @@ namespace {
 
 constexpr int kMaxState = 64;
 
+// Reference mode reproduces the reference's f32 operation order exactly, so its output is
+// bit-identical to CpuTensor's (the recurrence is ill-conditioned when |a| ~ 1, which the
+// reference's default init A_real = 0 gives, so any re-association drifts): every product and
+// sum is an unfused, individually rounded f32 operation (__fmul_rn / __fadd_rn), sums run in
+// the reference's index order, and a[n] is computed on the host with the same libm expf/cosf
+// the reference's Rust f32 methods call.
+
 // ---------------------------------------------------------------- ref mode, step 1
-// U[t][n] = sum_m (B[n][m]*dt) * x[m][t]. One thread per t, m ascending; B is read with
-// wave-uniform addresses (scalar loads).
+// U[t][n] = sum_m Bd[n][m] * x[m][t], m ascending (CpuTensor 2-D x 1-D matmul,
+// backend-cpu/src/lib.rs:728-735). One thread per t; Bd rows are wave-uniform (scalar loads).
 template <int NS>
 __global__ __launch_bounds__(256) void s4_input_proj_kernel(int64_t M, int64_t L, int64_t N,
-                                                            float dt, const float* __restrict__ x,
-                                                            const float* __restrict__ B,
+                                                            const float* __restrict__ x,
+                                                            const float* __restrict__ Bd,
                                                             float* __restrict__ U) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= L) return;
@@ -33,88 +40,52 @@ __global__ __launch_bounds__(256) void s4_input_proj_kernel(int64_t M, int64_t L
         const float xv = x[m * L + t];
 #pragma unroll
         for (int n = 0; n < NS; ++n)
-            if (n < N) acc[n] = fmaf(B[n * M + m] * dt, xv, acc[n]);
+            if (n < N) acc[n] = __fadd_rn(acc[n], __fmul_rn(Bd[n * M + m], xv));
     }
 #pragma unroll
     for (int n = 0; n < NS; ++n)
         if (n < N) U[t * N + n] = acc[n];
 }
 
+// Bd = B * dt (mul_scalar, ssm.rs:130), rounded once like the reference.
+__global__ void s4_scale_kernel(int64_t n, float dt, const float* __restrict__ B,
+                                float* __restrict__ Bd) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) Bd[i] = __fmul_rn(B[i], dt);
+}
+
 // ---------------------------------------------------------------- ref mode, step 2
-// Chunked first-order scan H[t] = a*H[t-1] + U[t] for each state n. Phase A: each chunk
-// scans from zero and records its end value; phase B: one thread per n carries across chunks;
-// phase C: each chunk adds a^(k+1) * carry_in to its local values.
-constexpr int kScanChunk = 256;
-
-__device__ inline float s4_decay(const float* a_real, const float* a_imag, int n, float dt) {
-    const float tr = a_real[n] * dt;
-    const float ti = a_imag[n] * dt;
-    return expf(tr) * cosf(ti);
-}
-
-__global__ __launch_bounds__(256) void s4_scan_local_kernel(int64_t L, int64_t N, float dt,
-                                                            const float* __restrict__ a_real,
-                                                            const float* __restrict__ a_imag,
-                                                            float* __restrict__ H,
-                                                            float* __restrict__ chunk_end) {
-    // thread = (chunk, n)
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t nchunks = (L + kScanChunk - 1) / kScanChunk;
-    if (gid >= nchunks * N) return;
-    const int64_t c = gid / N, n = gid % N;
-    const float a = s4_decay(a_real, a_imag, (int)n, dt);
-    const int64_t t0 = c * kScanChunk, t1 = min(L, t0 + kScanChunk);
-    float h = 0.0f;
-    for (int64_t t = t0; t < t1; ++t) {
-        h = fmaf(a, h, H[t * N + n]);
-        H[t * N + n] = h;
-    }
-    chunk_end[c * N + n] = h;
-}
-
-__global__ void s4_scan_carry_kernel(int64_t L, int64_t N, float dt,
-                                     const float* __restrict__ a_real,
-                                     const float* __restrict__ a_imag,
-                                     float* __restrict__ chunk_end) {
-    // In place: chunk_end[c] becomes the state entering chunk c.
+// H[t][n] = a[n]*H[t-1][n] + U[t][n] sequentially in t, one lane per state: s1 = a*h rounded,
+// then h = s1 + s2 rounded (ssm.rs:172-174). In place over U.
+__global__ __launch_bounds__(64) void s4_scan_seq_kernel(int64_t L, int64_t N,
+                                                         const float* __restrict__ a,
+                                                         float* __restrict__ H) {
     const int n = threadIdx.x;
     if (n >= N) return;
-    const float a = s4_decay(a_real, a_imag, n, dt);
-    const int64_t nchunks = (L + kScanChunk - 1) / kScanChunk;
-    // a^kScanChunk by repeated squaring (kScanChunk is a power of two)
-    float aT = a;
-    for (int s = 1; s < kScanChunk; s <<= 1) aT *= aT;
-    float carry = 0.0f;
-    for (int64_t c = 0; c < nchunks; ++c) {
-        const float e = chunk_end[c * N + n];
-        chunk_end[c * N + n] = carry;
-        carry = fmaf(aT, carry, e);
+    const float an = a[n];
+    float h = 0.0f;
+    int64_t t = 0;
+    // 8 steps per iteration: the loads of a batch issue together ahead of the dependent chain
+    for (; t + 8 <= L; t += 8) {
+        float s2[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s2[k] = H[(t + k) * N + n];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            h = __fadd_rn(__fmul_rn(an, h), s2[k]);
+            H[(t + k) * N + n] = h;
+        }
     }
-}
-
-__global__ __launch_bounds__(256) void s4_scan_fix_kernel(int64_t L, int64_t N, float dt,
-                                                          const float* __restrict__ a_real,
-                                                          const float* __restrict__ a_imag,
-                                                          float* __restrict__ H,
-                                                          const float* __restrict__ carry_in) {
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t nchunks = (L + kScanChunk - 1) / kScanChunk;
-    if (gid >= nchunks * N) return;
-    const int64_t c = gid / N, n = gid % N;
-    if (c == 0) return;
-    const float a = s4_decay(a_real, a_imag, (int)n, dt);
-    const float cin = carry_in[c * N + n];
-    const int64_t t0 = c * kScanChunk, t1 = min(L, t0 + kScanChunk);
-    float p = a;
-    for (int64_t t = t0; t < t1; ++t) {
-        H[t * N + n] = fmaf(p, cin, H[t * N + n]);
-        p *= a;
+    for (; t < L; ++t) {
+        h = __fadd_rn(__fmul_rn(an, h), H[t * N + n]);
+        H[t * N + n] = h;
     }
 }
 
 // ---------------------------------------------------------------- ref mode, step 3
-// y[t][m] = (sum_n C[m][n]*H[t][n] + D[m]*x[m][t]) * gate[m]. Tile = 64 channels x 32 steps:
-// x is read along t (row of x) into LDS, y written along m.
+// o[m] = sum_n C[m][n]*h[n] (n ascending, 2-D x 1-D matmul); y = o + D[m]*u[m]
+// (ssm.rs:177-179); y *= gate[m] (ssm.rs:460-461). Tile = 64 channels x 32 steps: x is read
+// along t (rows of x) into LDS and y written along m.
 constexpr int kTileM = 64, kTileT = 32;
 
 template <int NS>
@@ -130,7 +101,6 @@ __global__ __launch_bounds__(256) void s4_output_kernel(int64_t M, int64_t L, in
     const int64_t m0 = (int64_t)blockIdx.x * kTileM;
     const int64_t t0 = (int64_t)blockIdx.y * kTileT;
     const int tid = threadIdx.x;
-    // load x tile: 64 rows (m) x 32 cols (t), 8 passes of 256 threads
     for (int i = tid; i < kTileM * kTileT; i += 256) {
         const int mm = i / kTileT, tt = i % kTileT;
         const int64_t m = m0 + mm, t = t0 + tt;
@@ -148,16 +118,17 @@ __global__ __launch_bounds__(256) void s4_output_kernel(int64_t M, int64_t L, in
     float c[NS];
 #pragma unroll
     for (int n = 0; n < NS; ++n) c[n] = n < N ? C[m * N + n] : 0.0f;
-    const float dd = D ? D[m] : 0.0f;
+    const float dd = D[m];
     const float g = gate ? gate[m] : 1.0f;
     for (int tt = tid >> 6; tt < kTileT; tt += 4) {
         const int64_t t = t0 + tt;
         if (t >= L) break;
         float o = 0.0f;
 #pragma unroll
-        for (int n = 0; n < NS; ++n) o = fmaf(c[n], sh[tt][n], o);
-        float v = o + dd * sx[mm][tt];
-        if (gate) v *= g;
+        for (int n = 0; n < NS; ++n)
+            if (n < N) o = __fadd_rn(o, __fmul_rn(c[n], sh[tt][n]));
+        float v = __fadd_rn(o, __fmul_rn(dd, sx[mm][tt]));
+        if (gate) v = __fmul_rn(v, g);
         y[t * M + m] = v;
     }
 }
@@ -225,35 +196,46 @@ extern "C" int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, fl
     HX_REQUIRE(x && a_real && a_imag && B && C && D && y, HX_ERR_INVALID_INPUT,
                "s4_ref: x, a_real, a_imag, B, C, D and y must be non-NULL");
     hipStream_t s = as_stream(stream);
-    // H (L x N) is staged in y's tail? No: y is L x M and may be smaller than L x N when
-    // M < N. A scratch buffer is allocated per call.
-    float* H = nullptr;
-    float* ends = nullptr;
-    const int64_t nchunks = (seqlen + kScanChunk - 1) / kScanChunk;
-    HX_HIP_CHECK(hipMallocAsync((void**)&H, (size_t)seqlen * dstate * sizeof(float), s));
-    hipError_t e = hipMallocAsync((void**)&ends, (size_t)nchunks * dstate * sizeof(float), s);
-    if (e != hipSuccess) {
-        (void)hipFreeAsync(H, s);
-        return set_error(HX_ERR_ALLOCATION, "s4_ref: scratch allocation failed: %s",
-                         hipGetErrorString(e));
+
+    // discretize(dt) (ssm.rs:113-120) on the host with libm, exactly as the reference:
+    // tr = a_real*dt; ti = a_imag*dt; a = expf(tr) * cosf(ti). This synchronises with `stream`
+    // (the parameters are read back), which reference mode accepts for bit-faithfulness.
+    float ar[kMaxState], ai[kMaxState], a[kMaxState];
+    HX_HIP_CHECK(hipStreamSynchronize(s));
+    HX_HIP_CHECK(hipMemcpy(ar, a_real, dstate * sizeof(float), hipMemcpyDeviceToHost));
+    HX_HIP_CHECK(hipMemcpy(ai, a_imag, dstate * sizeof(float), hipMemcpyDeviceToHost));
+    for (int64_t n = 0; n < dstate; ++n) {
+        volatile float tr = ar[n] * dt;
+        volatile float ti = ai[n] * dt;
+        a[n] = expf(tr) * cosf(ti);
     }
+
+    // scratch: a [N] | Bd [N*M] | H [L*N]
+    const size_t n_a = 64, n_bd = (size_t)dstate * d_model, n_h = (size_t)seqlen * dstate;
+    float* scratch = nullptr;
+    HX_HIP_CHECK(hipMallocAsync((void**)&scratch, (n_a + n_bd + n_h) * sizeof(float), s));
+    float* a_dev = scratch;
+    float* Bd = scratch + n_a;
+    float* H = Bd + n_bd;
     int rc = HX_OK;
-    {
+    hipError_t e = hipMemcpyAsync(a_dev, a, dstate * sizeof(float), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);  // `a` is a stack buffer
+    if (e != hipSuccess) {
+        rc = set_error(HX_ERR_BACKEND, "s4_ref: upload of discretised A failed: %s",
+                       hipGetErrorString(e));
+    } else {
+        hipLaunchKernelGGL(s4_scale_kernel, dim3((unsigned)((n_bd + 255) / 256)), dim3(256), 0, s,
+                           (int64_t)n_bd, dt, B, Bd);
         dim3 g1((unsigned)((seqlen + 255) / 256));
         if (dstate <= 16)
             hipLaunchKernelGGL(s4_input_proj_kernel<16>, g1, dim3(256), 0, s, d_model, seqlen,
-                               dstate, dt, x, B, H);
+                               dstate, x, Bd, H);
         else
             hipLaunchKernelGGL(s4_input_proj_kernel<kMaxState>, g1, dim3(256), 0, s, d_model,
-                               seqlen, dstate, dt, x, B, H);
-        dim3 g2((unsigned)((nchunks * dstate + 255) / 256));
-        hipLaunchKernelGGL(s4_scan_local_kernel, g2, dim3(256), 0, s, seqlen, dstate, dt, a_real,
-                           a_imag, H, ends);
-        hipLaunchKernelGGL(s4_scan_carry_kernel, dim3(1), dim3(64), 0, s, seqlen, dstate, dt,
-                           a_real, a_imag, ends);
-        hipLaunchKernelGGL(s4_scan_fix_kernel, g2, dim3(256), 0, s, seqlen, dstate, dt, a_real,
-                           a_imag, H, ends);
-        dim3 g3((unsigned)((d_model + kTileM - 1) / kTileM), (unsigned)((seqlen + kTileT - 1) / kTileT));
+                               seqlen, dstate, x, Bd, H);
+        hipLaunchKernelGGL(s4_scan_seq_kernel, dim3(1), dim3(64), 0, s, seqlen, dstate, a_dev, H);
+        dim3 g3((unsigned)((d_model + kTileM - 1) / kTileM),
+                (unsigned)((seqlen + kTileT - 1) / kTileT));
         if (dstate <= 16)
             hipLaunchKernelGGL(s4_output_kernel<16>, g3, dim3(256), 0, s, d_model, seqlen, dstate,
                                x, H, C, D, gate, y);
@@ -264,8 +246,7 @@ extern "C" int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, fl
         if (le != hipSuccess)
             rc = set_error(HX_ERR_BACKEND, "s4_ref: launch failed: %s", hipGetErrorString(le));
     }
-    (void)hipFreeAsync(ends, s);
-    (void)hipFreeAsync(H, s);
+    (void)hipFreeAsync(scratch, s);
     return rc;
 }
 

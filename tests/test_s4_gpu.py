@@ -68,3 +68,14 @@ def test_s4d_complex_matches_oracle(dev, bt, L, dim, N):
     torch.cuda.synchronize()
     r = oracle.s4d_complex(x, **p)
     assert rel_err(g.cpu().numpy(), r) <= TOL_F32
+
+
+@pytest.mark.parametrize("M,N,L", [(64, 16, 100), (130, 16, 700), (33, 64, 70)])
+def test_s4_ref_bit_exact(dev, M, N, L):
+    """Reference mode reproduces CpuTensor's f32 op order, so it is bit-identical to the oracle,
+    including the ill-conditioned default init (A_real = 0, |a| ~ 1)."""
+    p = s4_inputs(M, N, L, seed=5 + M)
+    gate = (np.random.default_rng(2).standard_normal(M) * 0.1).astype(F)
+    g = ssm.s4_ref_fwd(**{k: dv(v, dev) for k, v in p.items()}, gate=dv(gate, dev)).cpu().numpy()
+    r = oracle.s4_ref_fwd(**p, gate=gate)
+    assert np.array_equal(g, r), f"max abs diff {np.abs(g - r).max()}"
