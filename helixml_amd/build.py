@@ -28,6 +28,10 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-munsafe-fp-atomics",
+    # multiply-adds fuse only within one expression (explicit fmaf elsewhere), and
+    # `#pragma clang fp contract(off)` is honoured where the reference's unfused f32 order must be
+    # reproduced
+    "-ffp-contract=on",
     # packed FP32 VALU ops are disabled: hipcc would otherwise form v_pk_* from scalar code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",

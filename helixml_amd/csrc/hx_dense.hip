@@ -3,11 +3,16 @@
 // nn::Linear::forward (crates/nn/src/lib.rs:120-134) computes X . W^T + bias with W stored
 // [out, in]; CpuTensor::matmul 2-D x 2-D (backend-cpu/src/lib.rs:644-678) computes A . B.
 // Both are small at the reference's shapes (d_model 64..512), so one LDS-tiled VALU kernel
-// with a 64x64 output tile and 4x4 register blocking covers them; fp32 accumulate.
+// with a 64x64 output tile and 4x4 register blocking covers them; fp32 accumulate in the
+// reference's k order, so results are bit-identical to CpuTensor's before the optional SiLU.
 #include "hx_common.h"
 
 namespace hx {
 namespace {
+
+// Reference order: each output is an f32 sum from 0.0 over k ascending of individually rounded
+// products (CpuTensor::matmul, backend-cpu/src/lib.rs:659-667), so no contraction into FMA.
+#pragma clang fp contract(off)
 
 constexpr int TM = 64, TN = 64, TK = 16;
 
@@ -20,6 +25,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int64_t M, int64_t K, int
                                                        const float* __restrict__ W,
                                                        const float* __restrict__ bias, int act,
                                                        float* __restrict__ Y) {
+#pragma clang fp contract(off)
     __shared__ float sa[TK][TM + 4];
     __shared__ float sb[TK][TN + 4];
     const int tid = threadIdx.x;
@@ -52,7 +58,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int64_t M, int64_t K, int
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+                for (int j = 0; j < 4; ++j) acc[i][j] = acc[i][j] + a[i] * b[j];
         }
         __syncthreads();
     }

@@ -16,6 +16,10 @@ namespace {
 
 constexpr int kMaxState = 64;
 
+// No multiply-add contraction anywhere in reference mode (hipcc defaults to contracting, and
+// __fmul_rn/__fadd_rn are plain operators here).
+#pragma clang fp contract(off)
+
 // Reference mode reproduces the reference's f32 operation order exactly, so its output is
 // bit-identical to CpuTensor's (the recurrence is ill-conditioned when |a| ~ 1, which the
 // reference's default init A_real = 0 gives, so any re-association drifts): every product and
@@ -31,6 +35,7 @@ __global__ __launch_bounds__(256) void s4_input_proj_kernel(int64_t M, int64_t L
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ Bd,
                                                             float* __restrict__ U) {
+#pragma clang fp contract(off)
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= L) return;
     float acc[NS];
@@ -60,6 +65,7 @@ __global__ void s4_scale_kernel(int64_t n, float dt, const float* __restrict__ B
 __global__ __launch_bounds__(64) void s4_scan_seq_kernel(int64_t L, int64_t N,
                                                          const float* __restrict__ a,
                                                          float* __restrict__ H) {
+#pragma clang fp contract(off)
     const int n = threadIdx.x;
     if (n >= N) return;
     const float an = a[n];
@@ -96,6 +102,7 @@ __global__ __launch_bounds__(256) void s4_output_kernel(int64_t M, int64_t L, in
                                                         const float* __restrict__ D,
                                                         const float* __restrict__ gate,
                                                         float* __restrict__ y) {
+#pragma clang fp contract(off)
     __shared__ float sx[kTileM][kTileT + 1];
     __shared__ float sh[kTileT][NS];
     const int64_t m0 = (int64_t)blockIdx.x * kTileM;

@@ -57,3 +57,16 @@ def test_exported_mamba_mlp_config1(dev):
     h = ssm.linear(dv(X, dev), dv(Wg, dev), dv(bg, dev), act=1)
     g = ssm.linear(h, dv(Wo, dev), dv(bo, dev)).cpu().numpy()
     assert rel_err(g, oracle.mamba_mlp(X, Wg, bg, Wo, bo)) <= TOL_F32
+
+
+@pytest.mark.parametrize("R,IN,OUT", [(100, 64, 128), (65, 70, 33)])
+def test_linear_and_matmul_bit_exact(dev, R, IN, OUT):
+    """Unfused products summed over k ascending from 0.0, then + bias: bit-identical to
+    CpuTensor::matmul (backend-cpu/src/lib.rs:659-667) and Linear::forward (nn/src/lib.rs:125-130)."""
+    rng = np.random.default_rng(R * IN)
+    X = rng.uniform(-1, 1, (R, IN)).astype(F)
+    W = rng.standard_normal((OUT, IN)).astype(F)
+    b = rng.standard_normal(OUT).astype(F)
+    assert np.array_equal(ssm.linear(dv(X, dev), dv(W, dev), dv(b, dev)).cpu().numpy(), oracle.linear(X, W, b))
+    Wt = np.ascontiguousarray(W.T)
+    assert np.array_equal(ssm.matmul(dv(X, dev), dv(Wt, dev)).cpu().numpy(), oracle.matmul(X, Wt))
