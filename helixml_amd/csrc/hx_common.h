@@ -68,6 +68,16 @@ template <> struct Storage<uint16_t> {
 
 __device__ inline float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
+// Workgroup barrier that orders LDS only. __syncthreads() is a workgroup-scope fence over all
+// address spaces, which on gfx9 makes every wave wait for its outstanding global loads and
+// stores (vmcnt(0)) at each barrier, defeating register prefetch of the next chunk. Kernels
+// that exchange data through LDS only use this instead.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // exp2 on the transcendental unit (v_exp_f32). Inputs here are finite; underflow flushes to 0.
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }

@@ -17,6 +17,8 @@
 // The state stays in VGPRs for the whole sequence; HBM is read once (u, delta, z) and written
 // once (out). This kernel is VALU/transcendental-bound at about 4 VALU + 1 v_exp per
 // state-update, which is why it runs on VALU and not MFMA.
+#include <type_traits>
+
 #include "hx_common.h"
 
 namespace hx {
@@ -26,6 +28,21 @@ template <typename T>
 __device__ inline float ld(const T* p) { return Storage<T>::load(p); }
 
 // ----------------------------------------------------------------------------- fast path
+// Vector of SPW consecutive storage elements read from LDS as fp32.
+template <int SPW>
+__device__ inline void lds_row(const float* p, float* v) {
+    if constexpr (SPW == 4) {
+        const float4 q = *reinterpret_cast<const float4*>(p);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else if constexpr (SPW == 2) {
+        const float2 q = *reinterpret_cast<const float2*>(p);
+        v[0] = q.x; v[1] = q.y;
+    } else {
+#pragma unroll
+        for (int k = 0; k < SPW; ++k) v[k] = p[k];
+    }
+}
+
 template <typename T, int W, int TCH, bool HAS_Z, bool SOFTPLUS>
 __global__ __launch_bounds__(64 * W) void scan_fwd_kernel(
     int64_t L, int64_t Dm,
@@ -34,15 +51,20 @@ __global__ __launch_bounds__(64 * W) void scan_fwd_kernel(
     const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
     const float* __restrict__ init_state, float* __restrict__ last_state) {
     constexpr int NS = 16;
-    constexpr int SPW = NS / W;    // states per wave
-    constexpr int SPS = TCH / W;   // pre/post steps per wave per chunk
+    constexpr int SPW = NS / W;        // states per wave
+    constexpr int SPS = TCH / W;       // pre/post steps per wave per chunk
+    constexpr int NT = 64 * W;         // threads
+    constexpr int BC = TCH * NS;       // B (or C) elements per chunk
+    constexpr int BCT = (2 * BC + NT - 1) / NT;  // B/C elements each thread stages per chunk
     static_assert(NS % W == 0 && TCH % W == 0, "bad tiling");
 
-    __shared__ float2 s_du[W > 1 ? TCH : 1][64];
-    __shared__ float s_part[W > 1 ? 2 : 1][W][W > 1 ? TCH : 1][64];
+    __shared__ float2 s_du[TCH][64];             // (dt, dt*u) per step and channel
+    __shared__ float s_part[2][W][TCH][64];      // per-wave partial readouts, double-buffered
+    __shared__ float s_bc[2][2][TCH][NS];        // [buf][B|C][step][state], double-buffered
 
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t b = blockIdx.y;
     const int64_t d = (int64_t)blockIdx.x * 64 + lane;
     const bool dvalid = d < Dm;
@@ -53,8 +75,8 @@ __global__ __launch_bounds__(64 * W) void scan_fwd_kernel(
     const T* __restrict__ dp = delta + row0;
     const T* __restrict__ zp = HAS_Z ? z + row0 : nullptr;
     T* __restrict__ op = out + row0;
-    const T* __restrict__ Bp = Bm + b * L * NS + w * SPW;  // wave-uniform
-    const T* __restrict__ Cp = Cm + b * L * NS + w * SPW;
+    const T* __restrict__ Bb = Bm + b * L * NS;
+    const T* __restrict__ Cb = Cm + b * L * NS;
 
     float A2[SPW], h[SPW];
 #pragma unroll
@@ -65,61 +87,87 @@ __global__ __launch_bounds__(64 * W) void scan_fwd_kernel(
     const float Dd = Dv ? Dv[dc] : 0.0f;
     const float bias = dt_bias ? dt_bias[dc] : 0.0f;
 
-    int buf = 0;
-    for (int64_t t0 = 0; t0 < L; t0 += TCH) {
-        // ---- pre: this wave's share of the chunk's per-element work
-        float uu[SPS], zz[SPS];
-        float2 q_reg[W == 1 ? TCH : 1];
+    // Register prefetch of one chunk: this wave's u/delta/z rows and this thread's share of B/C.
+    float pu[SPS], pd[SPS], pz[SPS], pbc[BCT];
+    auto fetch = [&](int64_t t0) {
 #pragma unroll
         for (int i = 0; i < SPS; ++i) {
-            const int s = (W > 1) ? (w + i * W) : i;
-            const int64_t t = t0 + s;
-            const bool tv = t < L;
-            const int64_t tc = tv ? t : L - 1;
-            uu[i] = ld(up + tc * Dm);
-            float dl = ld(dp + tc * Dm) + bias;
-            zz[i] = HAS_Z ? ld(zp + tc * Dm) : 0.0f;
+            const int64_t t = t0 + w + i * W;
+            const int64_t tc = t < L ? t : L - 1;
+            pu[i] = ld(up + tc * Dm);
+            pd[i] = ld(dp + tc * Dm);
+            pz[i] = HAS_Z ? ld(zp + tc * Dm) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < BCT; ++j) {
+            const int e = tid + j * NT;  // [B|C][step][state]
+            if (e < 2 * BC) {
+                const int which = e / BC, r = e % BC;
+                int64_t t = t0 + r / NS;
+                t = t < L ? t : L - 1;
+                const T* src = which ? Cb : Bb;
+                pbc[j] = ld(src + t * NS + (r % NS));
+            }
+        }
+    };
+    auto stage_bc = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < BCT; ++j) {
+            const int e = tid + j * NT;
+            if (e < 2 * BC) (&s_bc[buf][0][0][0])[e] = pbc[j];
+        }
+    };
+
+    fetch(0);
+    stage_bc(0);
+    int buf = 0;
+    for (int64_t t0 = 0; t0 < L; t0 += TCH) {
+        // ---- pre: this wave's share of the chunk's per-element work (prefetched inputs)
+        float uu[SPS], zz[SPS];
+#pragma unroll
+        for (int i = 0; i < SPS; ++i) {
+            const int s = w + i * W;
+            const bool tv = t0 + s < L;
+            uu[i] = pu[i];
+            zz[i] = pz[i];
+            float dl = pd[i] + bias;
             if (SOFTPLUS) dl = softplus(dl);
             dl = tv ? dl : 0.0f;  // steps past the end leave the state unchanged
-            const float2 q = make_float2(dl, dl * uu[i]);
-            if (W > 1) s_du[s][lane] = q;
-            else q_reg[i] = q;
+            s_du[s][lane] = make_float2(dl, dl * uu[i]);
         }
-        if (W > 1) __syncthreads();
+        // ---- prefetch the next chunk while this one computes
+        if (t0 + TCH < L) fetch(t0 + TCH);
+        lds_barrier();
 
         // ---- main: every wave advances its states through all TCH steps
-        float part[W == 1 ? TCH : 1];
 #pragma unroll
         for (int s = 0; s < TCH; ++s) {
-            const float2 q = (W > 1) ? s_du[s][lane] : q_reg[s];
-            const int64_t tc = (t0 + s < L) ? t0 + s : L - 1;
-            const T* Bs = Bp + tc * NS;
-            const T* Cs = Cp + tc * NS;
+            const float2 q = s_du[s][lane];
+            float bv[SPW], cv[SPW];
+            lds_row<SPW>(&s_bc[buf][0][s][w * SPW], bv);
+            lds_row<SPW>(&s_bc[buf][1][s][w * SPW], cv);
             float acc = 0.0f;
 #pragma unroll
             for (int k = 0; k < SPW; ++k) {
                 const float ab = fast_exp2(q.x * A2[k]);
-                h[k] = fmaf(ab, h[k], q.y * ld(Bs + k));
-                acc = fmaf(ld(Cs + k), h[k], acc);
+                h[k] = fmaf(ab, h[k], q.y * bv[k]);
+                acc = fmaf(cv[k], h[k], acc);
             }
-            if (W > 1) s_part[buf][w][s][lane] = acc;
-            else part[s] = acc;
+            s_part[buf][w][s][lane] = acc;
         }
-        if (W > 1) __syncthreads();
+        // B/C of the next chunk into the other buffer: every wave finished reading it (it was
+        // last read in the previous chunk's main loop, before this chunk's barrier).
+        if (t0 + TCH < L) stage_bc(buf ^ 1);
+        lds_barrier();
 
         // ---- post: this wave's share of readout, D skip, SiLU gate, store
 #pragma unroll
         for (int i = 0; i < SPS; ++i) {
-            const int s = (W > 1) ? (w + i * W) : i;
+            const int s = w + i * W;
             const int64_t t = t0 + s;
-            float y;
-            if (W > 1) {
-                y = 0.0f;
+            float y = 0.0f;
 #pragma unroll
-                for (int ww = 0; ww < W; ++ww) y += s_part[buf][ww][s][lane];
-            } else {
-                y = part[i];
-            }
+            for (int ww = 0; ww < W; ++ww) y += s_part[buf][ww][s][lane];
             y = fmaf(Dd, uu[i], y);
             if (HAS_Z) y *= silu(zz[i]);
             if (dvalid && t < L) Storage<T>::store(op + t * Dm, y);
@@ -129,6 +177,407 @@ __global__ __launch_bounds__(64 * W) void scan_fwd_kernel(
     if (last_state && dvalid) {
 #pragma unroll
         for (int k = 0; k < SPW; ++k) last_state[(b * Dm + d) * NS + w * SPW + k] = h[k];
+    }
+}
+
+// ----------------------------------------------------------------------------- state-lane path
+// One lane per (channel, state): a 16-lane DPP row holds the 16 states of one channel, a wave
+// holds 4 channels, a block of 4 waves 16 consecutive channels. Per chunk of 16 steps:
+//   * pre:  lane n of a row does the per-element work of step t0+n for its channel
+//           (softplus, dt*u) — each (t, d) exactly once;
+//   * main: step s broadcasts lane s's dt and dt*u across the row with DPP row_newbcast, which
+//           the compiler folds into the consuming v_mul (no extra instruction); B[t][n], C[t][n]
+//           come from an LDS tile of the block's batch row; per lane-step: v_mul, v_exp, v_mul,
+//           v_fma, v_mul = the minimum for the recurrence;
+//   * readout: the 16 per-state partials of each step are reduce-scattered across the row
+//           (recursive halving over DPP row_ror:8 / row_half_mirror / quad_perm), leaving lane n
+//           with y for step t0+n; then D*u, SiLU(z) and the store, again once per element.
+// 49152 channel-states of config 2 give 3072 waves, three per SIMD.
+
+template <int CTRL>
+__device__ inline float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+constexpr int kDppRor8 = 0x128;         // row_ror:8 (lane j <- lane j^8 within a row)
+constexpr int kDppHalfMirror = 0x141;   // row_half_mirror (lane j <- 7-j within each 8)
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
+template <int S> constexpr int kDppBcast = 0x150 + S;  // row_newbcast:S
+
+// Recursive-halving reduce-scatter over the 16 lanes of a DPP row: on return lane j holds
+// sum over the row's lanes of p[j].
+__device__ inline float row_reduce_scatter16(const float (&p)[16], int j) {
+    const bool hi8 = j & 8, hi4 = j & 4, hi2 = j & 2, hi1 = j & 1;
+    float q[8], r[4], v[2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float send = hi8 ? p[i] : p[i + 8];
+        const float keep = hi8 ? p[i + 8] : p[i];
+        q[i] = keep + dpp<kDppRor8>(send);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float send = hi4 ? q[i] : q[i + 4];
+        const float keep = hi4 ? q[i + 4] : q[i];
+        r[i] = keep + dpp<kDppHalfMirror>(send);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float send = hi2 ? r[i] : r[i + 2];
+        const float keep = hi2 ? r[i + 2] : r[i];
+        v[i] = keep + dpp<kDppXor2>(send);
+    }
+    const float send = hi1 ? v[0] : v[1];
+    const float keep = hi1 ? v[1] : v[0];
+    return keep + dpp<kDppXor1>(send);
+}
+
+template <int S>
+struct StepLoop {
+    template <typename F>
+    __device__ static inline void run(F&& f) {
+        StepLoop<S - 1>::run(f);
+        f(std::integral_constant<int, S - 1>{});
+    }
+};
+template <>
+struct StepLoop<0> {
+    template <typename F>
+    __device__ static inline void run(F&&) {}
+};
+
+template <typename T, int PF, bool HAS_Z, bool SOFTPLUS>
+__global__ __launch_bounds__(256) void scan_state_lane_kernel(
+    int64_t L, int64_t Dm, int ntiles,
+    const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
+    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
+    const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
+    const float* __restrict__ init_state, float* __restrict__ last_state) {
+    constexpr int NS = 16, TCH = 16, BSTR = TCH + 4;  // padded row: conflict-free b128 reads
+    __shared__ float s_bc[2][2][NS][BSTR];             // [buf][B|C][state][step]
+
+    // XCD-aware block order: hardware dispatches block ids round-robin over the 8 XCDs, so
+    // consecutive ids are renumbered to land on one XCD (neighbouring channel tiles share L2
+    // lines; the tiles of one batch row share its B/C).
+    const int nblk = gridDim.x * gridDim.y;
+    int id = blockIdx.x + gridDim.x * blockIdx.y;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+    const int tile = id % ntiles;
+    const int64_t b = id / ntiles;
+
+    const int tid = threadIdx.x;
+    const int n = tid & 15;                             // state == lane within the DPP row
+    const int64_t d = (int64_t)tile * 16 + (tid >> 4);  // channel of this row
+    const bool dvalid = d < Dm;
+    const int64_t dc = dvalid ? d : Dm - 1;
+
+    const int64_t col0 = b * L * Dm + dc;
+    const T* __restrict__ up = u + col0;
+    const T* __restrict__ dp = delta + col0;
+    const T* __restrict__ zp = HAS_Z ? z + col0 : nullptr;
+    T* __restrict__ op = out + col0;
+    const T* __restrict__ Bb = Bm + b * L * NS;
+    const T* __restrict__ Cb = Cm + b * L * NS;
+
+    const float A2 = A[dc * NS + n] * kLog2e;
+    float h = init_state ? init_state[(b * Dm + dc) * NS + n] : 0.0f;
+    const float Dd = Dv ? Dv[dc] : 0.0f;
+    const float bias = dt_bias ? dt_bias[dc] : 0.0f;
+
+    // Prefetch ring of PF chunks: slot k holds this lane's (t0+n, d) element of u/delta/z and one
+    // B and one C value of its chunk. Memory latency under load is several chunks of compute,
+    // so PF chunks stay in flight per wave.
+    float pu[PF], pd[PF], pz[PF], pb[PF], pc[PF];
+    const int64_t Lm1 = L - 1;
+    auto fetch = [&](int k, int64_t t0) {
+        const int64_t t = t0 + n < Lm1 ? t0 + n : Lm1;  // clamped: chunks past the end re-read row L-1
+        pu[k] = ld(up + t * Dm);
+        pd[k] = ld(dp + t * Dm);
+        pz[k] = HAS_Z ? ld(zp + t * Dm) : 0.0f;
+        const int64_t tb = t0 + (tid >> 4) < Lm1 ? t0 + (tid >> 4) : Lm1;
+        pb[k] = ld(Bb + tb * NS + n);
+        pc[k] = ld(Cb + tb * NS + n);
+    };
+    auto stage = [&](int k, int buf) {
+        s_bc[buf][0][n][tid >> 4] = pb[k];
+        s_bc[buf][1][n][tid >> 4] = pc[k];
+    };
+
+#pragma unroll
+    for (int k = 0; k < PF; ++k) fetch(k, (int64_t)k * TCH);
+    stage(0, 0);
+    lds_barrier();
+    for (int64_t tb0 = 0; tb0 < L; tb0 += PF * TCH) {
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+            const int64_t t0 = tb0 + k * TCH;
+            const int buf = k & 1;  // PF is even: the LDS buffer alternates chunk by chunk
+            // ---- pre: step t0+n of this row's channel (slot k was filled PF chunks ago)
+            const bool tv = t0 + n < L;
+            const float uu = pu[k], zz = pz[k];
+            float dl = pd[k] + bias;
+            if (SOFTPLUS) dl = softplus(dl);
+            dl = tv ? dl : 0.0f;  // steps past the end leave the state unchanged
+            const float du = dl * uu;
+
+            float bv[TCH], cv[TCH];
+#pragma unroll
+            for (int q = 0; q < TCH; q += 4) {
+                const float4 b4 = *reinterpret_cast<const float4*>(&s_bc[buf][0][n][q]);
+                const float4 c4 = *reinterpret_cast<const float4*>(&s_bc[buf][1][n][q]);
+                bv[q] = b4.x; bv[q + 1] = b4.y; bv[q + 2] = b4.z; bv[q + 3] = b4.w;
+                cv[q] = c4.x; cv[q + 1] = c4.y; cv[q + 2] = c4.z; cv[q + 3] = c4.w;
+            }
+            // B/C of the next chunk (slot k+1, fetched PF-1 chunks ago) into the other buffer,
+            // which every wave finished reading before the previous barrier.
+            stage((k + 1) % PF, buf ^ 1);
+            // refill slot k with the chunk PF ahead
+            fetch(k, t0 + PF * TCH);
+
+            // ---- main: 16 steps, state n
+            float p[TCH];
+            StepLoop<TCH>::run([&](auto sc) {
+                constexpr int s = decltype(sc)::value;
+                const float ab = fast_exp2(dpp<kDppBcast<s>>(dl) * A2);
+                h = fmaf(ab, h, dpp<kDppBcast<s>>(du) * bv[s]);
+                p[s] = cv[s] * h;
+            });
+
+            // ---- readout for step t0+n, then D skip, gate, store
+            float y = row_reduce_scatter16(p, n);
+            y = fmaf(Dd, uu, y);
+            if (HAS_Z) y *= silu(zz);
+            if (dvalid && tv) Storage<T>::store(op + (t0 + n) * Dm, y);
+            lds_barrier();
+            if (t0 + TCH >= L) break;
+        }
+    }
+    if (last_state && dvalid) last_state[(b * Dm + d) * NS + n] = h;
+}
+
+// ----------------------------------------------------------------------------- tile path
+// Memory side and math side are decoupled through LDS:
+//   * a block owns 64 consecutive channels of one batch row and walks time in chunks of TCH
+//     steps. u, delta, z are read and out is written as float4 tiles [TCH x 64]: 256-byte row
+//     segments, the pattern that streams best on this HBM (vs 16-64 B segments). Each thread
+//     owns one float4 (4 channels at one step) per chunk and does all per-element work for it:
+//     softplus and dt*u before the chunk, the readout sum, D*u, SiLU(z) and the store after it;
+//   * wave w owns states [w*SPW, (w+1)*SPW) of all 64 channels (lane = channel). dt and dt*u come
+//     from LDS; B and C of the wave's states are held in lane-distributed registers (every DPP
+//     row a full copy) and reach the multiplies through DPP row_newbcast, which the compiler
+//     folds into v_mul_f32_dpp, so delivering them costs no extra instruction or LDS traffic;
+//   * per-wave partial readouts are summed by the owning thread through LDS.
+// Loads run PF chunks ahead through a register ring.
+template <typename T> struct Vec4;
+template <> struct Vec4<float> {
+    using raw = float4;
+    __device__ static inline float4 load(const float* p) { return *reinterpret_cast<const float4*>(p); }
+    __device__ static inline void store(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+};
+template <> struct Vec4<uint16_t> {
+    using raw = uint2;
+    __device__ static inline float4 load(const uint16_t* p) {
+        const uint2 r = *reinterpret_cast<const uint2*>(p);
+        return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                           __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+    }
+    __device__ static inline void store(uint16_t* p, float4 v) {
+        using S = Storage<uint16_t>;
+        uint2 r;
+        r.x = (uint32_t)S::round(v.x) | ((uint32_t)S::round(v.y) << 16);
+        r.y = (uint32_t)S::round(v.z) | ((uint32_t)S::round(v.w) << 16);
+        *reinterpret_cast<uint2*>(p) = r;
+    }
+};
+
+__device__ inline float f4get(const float4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+template <typename T, int W, int TCH, int PF, bool HAS_Z, bool SOFTPLUS>
+__global__ __launch_bounds__(64 * W) void scan_tile_kernel(
+    int64_t L, int64_t Dm, int ntiles,
+    const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
+    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
+    const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
+    const float* __restrict__ init_state, float* __restrict__ last_state) {
+    constexpr int NS = 16;
+    constexpr int SPW = NS / W;            // states per wave
+    constexpr int NT = 64 * W;             // threads
+    constexpr int F4 = TCH * 16 / NT;      // float4 per thread per chunk per tensor
+    constexpr int NBC = TCH * SPW * 2;     // B/C values per wave per chunk
+    constexpr int QBC = NBC / 16;          // lane-distributed registers holding them
+    static_assert(NS % W == 0 && F4 >= 1 && F4 * NT == TCH * 16, "bad tiling");
+    static_assert(NBC % 16 == 0, "B/C values must fill whole DPP rows");
+
+    __shared__ float2 s_du[2][TCH][64];    // (dt, dt*u), double-buffered
+    __shared__ float s_part[W][TCH][64];   // per-wave partial readouts
+
+    // XCD-aware block order (block ids are dispatched round-robin over 8 XCDs): the tiles of
+    // one batch row, which share its B/C, land on one XCD.
+    const int nblk = gridDim.x;
+    int id = blockIdx.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+    const int tile = id % ntiles;
+    const int64_t b = id / ntiles;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t c0 = (int64_t)tile * 64;
+    const int64_t dl_ = c0 + lane;                 // this lane's channel in the math phase
+    const bool lvalid = dl_ < Dm;
+    const int64_t dlc = lvalid ? dl_ : Dm - 1;
+
+    // ---- per-thread float4 ownership (memory phase): element e = tid + j*NT of the tile
+    const int64_t rowbase = b * L * Dm;
+    int frow[F4];
+    int64_t fch[F4];
+    bool fvalid[F4];
+    float4 fbias[F4], fD[F4];
+#pragma unroll
+    for (int j = 0; j < F4; ++j) {
+        const int e = tid + j * NT;
+        frow[j] = e >> 4;
+        fch[j] = c0 + (e & 15) * 4;
+        fvalid[j] = fch[j] < Dm;  // Dm % 4 == 0: a float4 is wholly in or out
+        const int64_t cc = fvalid[j] ? fch[j] : 0;
+        fbias[j] = dt_bias ? *reinterpret_cast<const float4*>(dt_bias + cc) : make_float4(0, 0, 0, 0);
+        fD[j] = Dv ? *reinterpret_cast<const float4*>(Dv + cc) : make_float4(0, 0, 0, 0);
+    }
+
+    float A2[SPW], h[SPW];
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+        A2[k] = A[dlc * NS + w * SPW + k] * kLog2e;
+        h[k] = init_state ? init_state[(b * Dm + dlc) * NS + w * SPW + k] : 0.0f;
+    }
+
+    // ---- prefetch ring
+    float4 ru[PF][F4], rd[PF][F4], rz[PF][F4];
+    float rbc[PF][QBC];
+    const int64_t Lm1 = L - 1;
+    const int jr = lane & 15;  // position within the DPP row
+    auto fetch = [&](int k, int64_t t0) {
+#pragma unroll
+        for (int j = 0; j < F4; ++j) {
+            int64_t t = t0 + frow[j];
+            t = t < Lm1 ? t : Lm1;
+            const int64_t off = rowbase + t * Dm + (fvalid[j] ? fch[j] : 0);
+            ru[k][j] = Vec4<T>::load(u + off);
+            rd[k][j] = Vec4<T>::load(delta + off);
+            rz[k][j] = HAS_Z ? Vec4<T>::load(z + off) : make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < QBC; ++q) {
+            const int v = q * 16 + jr;         // value index: step s, B/C, state k
+            const int st = v / (2 * SPW);
+            const int bc = (v / SPW) & 1;
+            const int kk = v % SPW;
+            int64_t t = t0 + st;
+            t = t < Lm1 ? t : Lm1;
+            rbc[k][q] = ld((bc ? Cm : Bm) + (b * L + t) * NS + w * SPW + kk);
+        }
+    };
+
+#pragma unroll
+    for (int k = 0; k < PF; ++k) fetch(k, (int64_t)k * TCH);
+
+    for (int64_t tb0 = 0; tb0 < L; tb0 += PF * TCH) {
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+            const int64_t t0 = tb0 + k * TCH;
+            const int buf = k & 1;  // PF is even
+            // ---- pre (memory phase): dt and dt*u for this thread's float4s
+            float4 uu[F4], zz[F4];
+#pragma unroll
+            for (int j = 0; j < F4; ++j) {
+                uu[j] = ru[k][j];
+                zz[j] = rz[k][j];
+                const bool tv = t0 + frow[j] < L;
+                float dlv[4], duv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float x = f4get(rd[k][j], i) + f4get(fbias[j], i);
+                    if (SOFTPLUS) x = softplus(x);
+                    x = tv ? x : 0.0f;  // steps past the end leave the state unchanged
+                    dlv[i] = x;
+                    duv[i] = x * f4get(uu[j], i);
+                }
+                const int cl = ((tid + j * NT) & 15) * 4;
+                float4* p4 = reinterpret_cast<float4*>(&s_du[buf][frow[j]][cl]);
+                p4[0] = make_float4(dlv[0], duv[0], dlv[1], duv[1]);
+                p4[1] = make_float4(dlv[2], duv[2], dlv[3], duv[3]);
+            }
+            // B/C of this chunk, then refill the slot with the chunk PF ahead
+            float bc[QBC];
+#pragma unroll
+            for (int q = 0; q < QBC; ++q) bc[q] = rbc[k][q];
+            fetch(k, t0 + PF * TCH);
+            lds_barrier();
+
+            // ---- main (math phase): all TCH steps for this wave's states. The chunk's dt and
+            // dt*u are read in one batch and the partials written in one batch, so LDS latency is
+            // paid once per chunk instead of every few steps.
+            float2 q2[TCH];
+#pragma unroll
+            for (int s = 0; s < TCH; ++s) q2[s] = s_du[buf][s][lane];
+            // The decays exp2(dt*A) of a group of EG steps are issued together, ahead of the
+            // recurrence that consumes them, so the transcendental unit's latency overlaps.
+            constexpr int EG = 8;
+            float part[TCH];
+            StepLoop<TCH / EG>::run([&](auto gc) {
+                constexpr int g0 = decltype(gc)::value * EG;
+                float ab[EG][SPW];
+#pragma unroll
+                for (int e = 0; e < EG; ++e)
+#pragma unroll
+                    for (int kk = 0; kk < SPW; ++kk) ab[e][kk] = fast_exp2(q2[g0 + e].x * A2[kk]);
+                StepLoop<EG>::run([&](auto ec) {
+                    constexpr int s = g0 + decltype(ec)::value;
+                    float acc = 0.0f;
+                    StepLoop<SPW>::run([&](auto kc) {
+                        constexpr int kk = decltype(kc)::value;
+                        constexpr int vb = s * 2 * SPW + kk;        // B value index
+                        constexpr int vc = s * 2 * SPW + SPW + kk;  // C value index
+                        h[kk] = fmaf(ab[s - g0][kk], h[kk],
+                                     dpp<kDppBcast<vb % 16>>(bc[vb / 16]) * q2[s].y);
+                        acc += dpp<kDppBcast<vc % 16>>(bc[vc / 16]) * h[kk];
+                    });
+                    part[s] = acc;
+                });
+            });
+#pragma unroll
+            for (int s = 0; s < TCH; ++s) s_part[w][s][lane] = part[s];
+            lds_barrier();
+
+            // ---- post (memory phase): readout sum, D skip, gate, store
+#pragma unroll
+            for (int j = 0; j < F4; ++j) {
+                const int cl = ((tid + j * NT) & 15) * 4;
+                float4 y = make_float4(0, 0, 0, 0);
+#pragma unroll
+                for (int ww = 0; ww < W; ++ww) {
+                    const float4 pv = *reinterpret_cast<const float4*>(&s_part[ww][frow[j]][cl]);
+                    y.x += pv.x; y.y += pv.y; y.z += pv.z; y.w += pv.w;
+                }
+                y.x = fmaf(fD[j].x, uu[j].x, y.x);
+                y.y = fmaf(fD[j].y, uu[j].y, y.y);
+                y.z = fmaf(fD[j].z, uu[j].z, y.z);
+                y.w = fmaf(fD[j].w, uu[j].w, y.w);
+                if (HAS_Z) {
+                    y.x *= silu(zz[j].x); y.y *= silu(zz[j].y);
+                    y.z *= silu(zz[j].z); y.w *= silu(zz[j].w);
+                }
+                const int64_t t = t0 + frow[j];
+                if (fvalid[j] && t < L) Vec4<T>::store(out + rowbase + t * Dm + fch[j], y);
+            }
+            if (t0 + TCH >= L) break;
+        }
+    }
+    if (last_state && lvalid) {
+#pragma unroll
+        for (int k = 0; k < SPW; ++k) last_state[(b * Dm + dl_) * NS + w * SPW + k] = h[k];
     }
 }
 
@@ -247,6 +696,49 @@ int dispatch_fast(const ScanArgs& a) {
     return launch_fast<T, W, TCH, false, false>(a);
 }
 
+template <typename T, int W, int TCH, int PF, bool HAS_Z, bool SP>
+int launch_tile(const ScanArgs& a) {
+    const int ntiles = (int)((a.Dm + 63) / 64);
+    dim3 grid((unsigned)(ntiles * a.Bt));
+    hipLaunchKernelGGL((scan_tile_kernel<T, W, TCH, PF, HAS_Z, SP>), grid, dim3(64 * W), 0,
+                       a.stream, a.L, a.Dm, ntiles, (const T*)a.u, (const T*)a.delta, a.A,
+                       (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
+                       a.init_state, a.last_state);
+    HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+template <typename T, int W, int TCH, int PF>
+int dispatch_tile(const ScanArgs& a) {
+    const bool hz = a.z != nullptr;
+    if (hz && a.softplus) return launch_tile<T, W, TCH, PF, true, true>(a);
+    if (hz) return launch_tile<T, W, TCH, PF, true, false>(a);
+    if (a.softplus) return launch_tile<T, W, TCH, PF, false, true>(a);
+    return launch_tile<T, W, TCH, PF, false, false>(a);
+}
+
+template <typename T, bool HAS_Z, bool SP>
+int launch_state_lane(const ScanArgs& a) {
+    constexpr int PF = 4;
+    const int ntiles = (int)((a.Dm + 15) / 16);
+    dim3 grid((unsigned)ntiles, (unsigned)a.Bt);
+    hipLaunchKernelGGL((scan_state_lane_kernel<T, PF, HAS_Z, SP>), grid, dim3(256), 0, a.stream, a.L,
+                       a.Dm, ntiles, (const T*)a.u, (const T*)a.delta, a.A, (const T*)a.B,
+                       (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out, a.init_state,
+                       a.last_state);
+    HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+template <typename T>
+int dispatch_state_lane(const ScanArgs& a) {
+    const bool hz = a.z != nullptr;
+    if (hz && a.softplus) return launch_state_lane<T, true, true>(a);
+    if (hz) return launch_state_lane<T, true, false>(a);
+    if (a.softplus) return launch_state_lane<T, false, true>(a);
+    return launch_state_lane<T, false, false>(a);
+}
+
 template <typename T, int NMAX>
 int launch_generic(const ScanArgs& a) {
     const int64_t total = a.Bt * a.Dm;
@@ -281,12 +773,25 @@ int run_scan(const ScanArgs& a) {
     const bool fast_ok = a.N == 16 && aligned(a.B, 16 * es) && aligned(a.C, 16 * es);
     const int v = g_scan_variant;
     if (!fast_ok || v < 0) return dispatch_generic<T>(a);
+    const bool tile_ok = a.Dm % 4 == 0 && aligned(a.u, 16) && aligned(a.delta, 16) &&
+                         aligned(a.out, 16) && (!a.z || aligned(a.z, 16)) &&
+                         (!a.D || aligned(a.D, 16)) && (!a.dt_bias || aligned(a.dt_bias, 16)) &&
+                         a.Bt * ((a.Dm + 63) / 64) <= 0x7fffffff;
+    if (v == 0) {  // auto: the LDS-staged tile kernel where its float4 access is legal
+        if (tile_ok) return dispatch_tile<T, 4, 16, 2>(a);
+        return dispatch_fast<T, 8, 16>(a);
+    }
     switch (v) {
+        case 32: if (tile_ok) return dispatch_tile<T, 8, 32, 2>(a); break;
+        case 33: if (tile_ok) return dispatch_tile<T, 4, 16, 2>(a); break;
+        case 34: if (tile_ok) return dispatch_tile<T, 4, 32, 2>(a); break;
+        case 16: return dispatch_state_lane<T>(a);
         case 1: return dispatch_fast<T, 1, 16>(a);
         case 2: return dispatch_fast<T, 2, 16>(a);
         case 8: return dispatch_fast<T, 8, 16>(a);
         default: return dispatch_fast<T, 4, 16>(a);
     }
+    return dispatch_fast<T, 8, 16>(a);
 }
 
 int check_common(int64_t Bt, int64_t L, int64_t Dm, int64_t N, int dtype) {
@@ -337,9 +842,9 @@ extern "C" int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim,
 
 extern "C" int hx_set_scan_variant(int variant) {
     HX_REQUIRE(variant == 0 || variant == -1 || variant == 1 || variant == 2 || variant == 4 ||
-                   variant == 8,
-               HX_ERR_INVALID_INPUT, "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8",
-               variant);
+                   variant == 8 || variant == 16 || (variant >= 32 && variant <= 34),
+               HX_ERR_INVALID_INPUT,
+               "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8, 16, 32..34", variant);
     hx::g_scan_variant = variant;
     return HX_OK;
 }
