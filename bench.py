@@ -92,7 +92,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c2", choices=["c2", "c2bf16", "c4"])
+    ap.add_argument("--workload", default="c2", choices=["c2", "c2bf16", "c4", "copy"],
+                    help="copy = plain device copy of 512 MiB (HBM ceiling and counter calibration)")
     ap.add_argument("--variant", type=int, default=0, help="scan kernel variant (hx_set_scan_variant)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
@@ -109,6 +110,17 @@ def main():
     if args.variant:
         ssm.set_scan_variant(args.variant)
 
+    if args.workload == "copy":
+        n = 512 * 2**20 // 4
+        src = [torch.randn(n, device=dev) for _ in range(2)]
+        dst = [torch.empty_like(x) for x in src]
+        ms = time_steps(lambda i: dst[i].copy_(src[i]), 2, args.steps, args.warmup)
+        gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
+        print(json.dumps({"metric": "device copy GB/s (read + write)", "value": gbs, "unit": "GB/s",
+                          "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+                          "higher_is_better": True, "bytes_per_step": 2 * n * 4,
+                          "frac_of_8TBs": gbs / PEAK_HBM_GBS}))
+        return
     if args.workload in ("c2", "c2bf16"):
         bt, L, dim, N = 8, 2048, 1536, 16
         dtype = torch.bfloat16 if args.workload == "c2bf16" else torch.float32
@@ -144,6 +156,13 @@ def main():
         floor = 1e-3 * np.abs(r).max()
         parity = float((np.abs(g - r) / np.maximum(np.abs(r), floor)).max())
 
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "traffic.json")
+    if args.workload == "c2" and args.variant == 0 and os.path.exists(tfile):
+        # measured HBM bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)
+        rec_t = json.load(open(tfile)).get("scan_tile_kernel<float, 4, 16, 2, true, true>@config2")
+        traffic = rec_t["traffic_bytes"] if rec_t else None
+
     rec = {
         "metric": "Mamba selective-scan fwd tokens/s + achieved HBM GB/s (% of peak), 1 GPU",
         "value": tokens * 1e3 / ms,
@@ -161,7 +180,7 @@ def main():
                    "storage": "fp32" if es == 4 else "bf16", "input_sets": nsets},
         "hbm_gbs": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "algorithmic_bytes": nbytes, "kernel_ms": ms},
         "cpu_baseline": cpu,
         "parity_max_rel_err": parity,
