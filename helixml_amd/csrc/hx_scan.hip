@@ -394,7 +394,7 @@ __device__ inline float f4get(const float4& v, int i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
-template <typename T, int W, int TCH, int PF, bool HAS_Z, bool SOFTPLUS>
+template <typename T, int W, int TCH, int PF, bool HAS_Z, bool SOFTPLUS, bool SBC>
 __global__ __launch_bounds__(64 * W) void scan_tile_kernel(
     int64_t L, int64_t Dm, int ntiles,
     const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
@@ -406,12 +406,13 @@ __global__ __launch_bounds__(64 * W) void scan_tile_kernel(
     constexpr int NT = 64 * W;             // threads
     constexpr int F4 = TCH * 16 / NT;      // float4 per thread per chunk per tensor
     constexpr int NBC = TCH * SPW * 2;     // B/C values per wave per chunk
-    constexpr int QBC = NBC / 16;          // lane-distributed registers holding them
+    // lane-distributed registers holding them (SBC: B/C come through scalar loads instead)
+    constexpr int QBC = SBC ? 1 : NBC / 16;
     static_assert(NS % W == 0 && F4 >= 1 && F4 * NT == TCH * 16, "bad tiling");
     static_assert(NBC % 16 == 0, "B/C values must fill whole DPP rows");
 
     __shared__ float2 s_du[2][TCH][64];    // (dt, dt*u), double-buffered
-    __shared__ float s_part[W][TCH][64];   // per-wave partial readouts
+    __shared__ float s_part[2][W][TCH][64];  // per-wave partial readouts, double-buffered
 
     // XCD-aware block order (block ids are dispatched round-robin over 8 XCDs): the tiles of
     // one batch row, which share its B/C, land on one XCD.
@@ -431,7 +432,7 @@ __global__ __launch_bounds__(64 * W) void scan_tile_kernel(
 
     // ---- per-thread float4 ownership (memory phase): element e = tid + j*NT of the tile
     const int64_t rowbase = b * L * Dm;
-    int frow[F4];
+    int frow[F4], fcl[F4];
     int64_t fch[F4];
     bool fvalid[F4];
     float4 fbias[F4], fD[F4];
@@ -439,7 +440,8 @@ __global__ __launch_bounds__(64 * W) void scan_tile_kernel(
     for (int j = 0; j < F4; ++j) {
         const int e = tid + j * NT;
         frow[j] = e >> 4;
-        fch[j] = c0 + (e & 15) * 4;
+        fcl[j] = (e & 15) * 4;
+        fch[j] = c0 + fcl[j];
         fvalid[j] = fch[j] < Dm;  // Dm % 4 == 0: a float4 is wholly in or out
         const int64_t cc = fvalid[j] ? fch[j] : 0;
         fbias[j] = dt_bias ? *reinterpret_cast<const float4*>(dt_bias + cc) : make_float4(0, 0, 0, 0);
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(64 * W) void scan_tile_kernel(
         h[k] = init_state ? init_state[(b * Dm + dlc) * NS + w * SPW + k] : 0.0f;
     }
 
-    // ---- prefetch ring
+    // ---- prefetch ring (PF chunks in flight)
     float4 ru[PF][F4], rd[PF][F4], rz[PF][F4];
     float rbc[PF][QBC];
     const int64_t Lm1 = L - 1;
@@ -469,7 +471,7 @@ __global__ __launch_bounds__(64 * W) void scan_tile_kernel(
             rz[k][j] = HAS_Z ? Vec4<T>::load(z + off) : make_float4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int q = 0; q < QBC; ++q) {
+        for (int q = 0; q < (SBC ? 0 : QBC); ++q) {
             const int v = q * 16 + jr;         // value index: step s, B/C, state k
             const int st = v / (2 * SPW);
             const int bc = (v / SPW) & 1;
@@ -480,104 +482,390 @@ __global__ __launch_bounds__(64 * W) void scan_tile_kernel(
         }
     };
 
+    // pre: dt and dt*u of this thread's float4s of chunk t0 (ring slot k) into s_du[buf];
+    // keeps u and z for the chunk's post phase.
+    auto pre = [&](int k, int64_t t0, int buf, float4 (&uu)[F4], float4 (&zz)[F4]) {
 #pragma unroll
-    for (int k = 0; k < PF; ++k) fetch(k, (int64_t)k * TCH);
-
-    for (int64_t tb0 = 0; tb0 < L; tb0 += PF * TCH) {
+        for (int j = 0; j < F4; ++j) {
+            uu[j] = ru[k][j];
+            zz[j] = rz[k][j];
+            const bool tv = t0 + frow[j] < L;
+            float dlv[4], duv[4];
 #pragma unroll
-        for (int k = 0; k < PF; ++k) {
-            const int64_t t0 = tb0 + k * TCH;
-            const int buf = k & 1;  // PF is even
-            // ---- pre (memory phase): dt and dt*u for this thread's float4s
-            float4 uu[F4], zz[F4];
-#pragma unroll
-            for (int j = 0; j < F4; ++j) {
-                uu[j] = ru[k][j];
-                zz[j] = rz[k][j];
-                const bool tv = t0 + frow[j] < L;
-                float dlv[4], duv[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float x = f4get(rd[k][j], i) + f4get(fbias[j], i);
-                    if (SOFTPLUS) x = softplus(x);
-                    x = tv ? x : 0.0f;  // steps past the end leave the state unchanged
-                    dlv[i] = x;
-                    duv[i] = x * f4get(uu[j], i);
-                }
-                const int cl = ((tid + j * NT) & 15) * 4;
-                float4* p4 = reinterpret_cast<float4*>(&s_du[buf][frow[j]][cl]);
-                p4[0] = make_float4(dlv[0], duv[0], dlv[1], duv[1]);
-                p4[1] = make_float4(dlv[2], duv[2], dlv[3], duv[3]);
+            for (int i = 0; i < 4; ++i) {
+                float x = f4get(rd[k][j], i) + f4get(fbias[j], i);
+                if (SOFTPLUS) x = softplus(x);
+                x = tv ? x : 0.0f;  // steps past the end leave the state unchanged
+                dlv[i] = x;
+                duv[i] = x * f4get(uu[j], i);
             }
-            // B/C of this chunk, then refill the slot with the chunk PF ahead
-            float bc[QBC];
+            float4* p4 = reinterpret_cast<float4*>(&s_du[buf][frow[j]][fcl[j]]);
+            p4[0] = make_float4(dlv[0], duv[0], dlv[1], duv[1]);
+            p4[1] = make_float4(dlv[2], duv[2], dlv[3], duv[3]);
+        }
+    };
+    // post: readout sum over the waves' partials, D skip, gate, store for chunk t0.
+    auto post = [&](int64_t t0, int buf, const float4 (&uu)[F4], const float4 (&zz)[F4]) {
 #pragma unroll
-            for (int q = 0; q < QBC; ++q) bc[q] = rbc[k][q];
-            fetch(k, t0 + PF * TCH);
-            lds_barrier();
-
-            // ---- main (math phase): all TCH steps for this wave's states. The chunk's dt and
-            // dt*u are read in one batch and the partials written in one batch, so LDS latency is
-            // paid once per chunk instead of every few steps.
-            float2 q2[TCH];
+        for (int j = 0; j < F4; ++j) {
+            float4 y = make_float4(0, 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < TCH; ++s) q2[s] = s_du[buf][s][lane];
-            // The decays exp2(dt*A) of a group of EG steps are issued together, ahead of the
-            // recurrence that consumes them, so the transcendental unit's latency overlaps.
-            constexpr int EG = 8;
-            float part[TCH];
-            StepLoop<TCH / EG>::run([&](auto gc) {
-                constexpr int g0 = decltype(gc)::value * EG;
-                float ab[EG][SPW];
+            for (int ww = 0; ww < W; ++ww) {
+                const float4 pv = *reinterpret_cast<const float4*>(&s_part[buf][ww][frow[j]][fcl[j]]);
+                y.x += pv.x; y.y += pv.y; y.z += pv.z; y.w += pv.w;
+            }
+            y.x = fmaf(fD[j].x, uu[j].x, y.x);
+            y.y = fmaf(fD[j].y, uu[j].y, y.y);
+            y.z = fmaf(fD[j].z, uu[j].z, y.z);
+            y.w = fmaf(fD[j].w, uu[j].w, y.w);
+            if (HAS_Z) {
+                y.x *= silu(zz[j].x); y.y *= silu(zz[j].y);
+                y.z *= silu(zz[j].z); y.w *= silu(zz[j].w);
+            }
+            const int64_t t = t0 + frow[j];
+            if (fvalid[j] && t < L) Vec4<T>::store(out + rowbase + t * Dm + fch[j], y);
+        }
+    };
+    // main: all TCH steps of chunk (s_du[buf], B/C values bc) for this wave's states, partial
+    // readouts into s_part[buf]. dt, dt*u are read in one batch; the decays of a group of EG
+    // steps are issued together ahead of the recurrence that consumes them.
+    auto main_phase = [&](int buf, const float (&bc)[QBC], int64_t t0) {
+        float2 q2[TCH];
 #pragma unroll
-                for (int e = 0; e < EG; ++e)
+        for (int s = 0; s < TCH; ++s) q2[s] = s_du[buf][s][lane];
+        // SBC: this wave's B/C values are wave-uniform -> scalar loads into SGPRs, one group of
+        // EG steps loaded a group ahead, used directly as VALU operands.
+        const T* __restrict__ Bw = Bm + b * L * NS + w * SPW;
+        const T* __restrict__ Cw = Cm + b * L * NS + w * SPW;
+        const int smax = __builtin_amdgcn_readfirstlane(
+            (int)((Lm1 - t0) < (int64_t)(TCH - 1) ? (Lm1 - t0) : (int64_t)(TCH - 1)));
+        // group of EG steps: 8 decays in flight; with SBC, 2 x EG x SPW x 2 = 32 SGPRs of B/C
+        constexpr int EG = 8 / SPW >= 1 ? 8 / SPW : 1;
+        float sbv[2][EG][SPW], scv[2][EG][SPW];
+        auto load_group = [&](int slot, int g0) {
 #pragma unroll
-                    for (int kk = 0; kk < SPW; ++kk) ab[e][kk] = fast_exp2(q2[g0 + e].x * A2[kk]);
-                StepLoop<EG>::run([&](auto ec) {
-                    constexpr int s = g0 + decltype(ec)::value;
-                    float acc = 0.0f;
-                    StepLoop<SPW>::run([&](auto kc) {
-                        constexpr int kk = decltype(kc)::value;
-                        constexpr int vb = s * 2 * SPW + kk;        // B value index
-                        constexpr int vc = s * 2 * SPW + SPW + kk;  // C value index
-                        h[kk] = fmaf(ab[s - g0][kk], h[kk],
+            for (int e = 0; e < EG; ++e) {
+                const int ss = g0 + e < smax ? g0 + e : smax;
+                const int64_t off = (t0 + ss) * NS;
+#pragma unroll
+                for (int kk = 0; kk < SPW; ++kk) {
+                    sbv[slot][e][kk] = ld(Bw + off + kk);
+                    scv[slot][e][kk] = ld(Cw + off + kk);
+                }
+            }
+        };
+        if constexpr (SBC) load_group(0, 0);
+        // The decays exp2(dt*A) of a group of EG steps are issued together, ahead of the
+        // recurrence that consumes them, so the transcendental unit's latency overlaps.
+        float part[TCH];
+        StepLoop<TCH / EG>::run([&](auto gc) {
+            constexpr int gi = decltype(gc)::value;
+            constexpr int g0 = gi * EG;
+            if constexpr (SBC && g0 + EG < TCH) load_group((gi + 1) & 1, g0 + EG);
+            float ab[EG][SPW];
+#pragma unroll
+            for (int e = 0; e < EG; ++e)
+#pragma unroll
+                for (int kk = 0; kk < SPW; ++kk) ab[e][kk] = fast_exp2(q2[g0 + e].x * A2[kk]);
+            StepLoop<EG>::run([&](auto ec) {
+                constexpr int e = decltype(ec)::value;
+                constexpr int s = g0 + e;
+                float acc = 0.0f;
+                StepLoop<SPW>::run([&](auto kc) {
+                    constexpr int kk = decltype(kc)::value;
+                    constexpr int vb = s * 2 * SPW + kk;        // B value index
+                    constexpr int vc = s * 2 * SPW + SPW + kk;  // C value index
+                    if constexpr (SBC) {
+                        h[kk] = fmaf(ab[e][kk], h[kk], sbv[gi & 1][e][kk] * q2[s].y);
+                        acc = fmaf(scv[gi & 1][e][kk], h[kk], acc);
+                    } else {
+                        h[kk] = fmaf(ab[e][kk], h[kk],
                                      dpp<kDppBcast<vb % 16>>(bc[vb / 16]) * q2[s].y);
                         acc += dpp<kDppBcast<vc % 16>>(bc[vc / 16]) * h[kk];
-                    });
-                    part[s] = acc;
+                    }
                 });
+                part[s] = acc;
             });
+        });
 #pragma unroll
-            for (int s = 0; s < TCH; ++s) s_part[w][s][lane] = part[s];
-            lds_barrier();
+        for (int s = 0; s < TCH; ++s) s_part[buf][w][s][lane] = part[s];
+    };
 
-            // ---- post (memory phase): readout sum, D skip, gate, store
+    // Software pipeline, one barrier per chunk: iteration k runs post(k-1), main(k) and
+    // pre(k+1) in one barrier-free region (they touch different LDS buffers), so the scheduler
+    // overlaps their latencies.
 #pragma unroll
-            for (int j = 0; j < F4; ++j) {
-                const int cl = ((tid + j * NT) & 15) * 4;
-                float4 y = make_float4(0, 0, 0, 0);
+    for (int k = 0; k < PF; ++k) fetch(k, (int64_t)k * TCH);
+    float4 u_cur[F4], z_cur[F4], u_prev[F4], z_prev[F4];
+    float bc_cur[QBC];
+    pre(0, 0, 0, u_cur, z_cur);
 #pragma unroll
-                for (int ww = 0; ww < W; ++ww) {
-                    const float4 pv = *reinterpret_cast<const float4*>(&s_part[ww][frow[j]][cl]);
-                    y.x += pv.x; y.y += pv.y; y.z += pv.z; y.w += pv.w;
-                }
-                y.x = fmaf(fD[j].x, uu[j].x, y.x);
-                y.y = fmaf(fD[j].y, uu[j].y, y.y);
-                y.z = fmaf(fD[j].z, uu[j].z, y.z);
-                y.w = fmaf(fD[j].w, uu[j].w, y.w);
-                if (HAS_Z) {
-                    y.x *= silu(zz[j].x); y.y *= silu(zz[j].y);
-                    y.z *= silu(zz[j].z); y.w *= silu(zz[j].w);
-                }
-                const int64_t t = t0 + frow[j];
-                if (fvalid[j] && t < L) Vec4<T>::store(out + rowbase + t * Dm + fch[j], y);
-            }
-            if (t0 + TCH >= L) break;
-        }
+    for (int q = 0; q < QBC; ++q) bc_cur[q] = SBC ? 0.0f : rbc[0][q];
+    fetch(0, (int64_t)PF * TCH);
+    lds_barrier();
+    bool have_prev = false;
+    for (int64_t tb0 = 0; tb0 < L; tb0 += PF * TCH) {
+        // ring slots are compile-time indices: the PF chunks of one round are expanded by
+        // template recursion (a plain unrolled loop was left rolled by the compiler)
+        StepLoop<PF>::run([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            constexpr int kn = (k + 1) % PF;
+            const int64_t t0 = tb0 + k * TCH;
+            if (t0 >= L) return;  // uniform
+            constexpr int buf = k & 1;  // PF is even
+            if (have_prev) post(t0 - TCH, buf ^ 1, u_prev, z_prev);
+            main_phase(buf, bc_cur, t0);
+#pragma unroll
+            for (int j = 0; j < F4; ++j) { u_prev[j] = u_cur[j]; z_prev[j] = z_cur[j]; }
+            have_prev = true;
+            // next chunk: its slot kn was fetched PF-1 chunks ago; refill it afterwards
+            pre(kn, t0 + TCH, buf ^ 1, u_cur, z_cur);
+#pragma unroll
+            for (int q = 0; q < QBC; ++q) bc_cur[q] = SBC ? 0.0f : rbc[kn][q];
+            fetch(kn, t0 + TCH + (int64_t)PF * TCH);
+            lds_barrier();
+        });
+    }
+    // the last chunk's post (its partials are in the buffer main wrote last)
+    {
+        const int64_t nchunks = (L + TCH - 1) / TCH;
+        const int64_t tl = (nchunks - 1) * TCH;
+        post(tl, (int)((nchunks - 1) & 1), u_prev, z_prev);
     }
     if (last_state && lvalid) {
 #pragma unroll
         for (int k = 0; k < SPW; ++k) last_state[(b * Dm + dl_) * NS + w * SPW + k] = h[k];
+    }
+}
+
+// ----------------------------------------------------------------------------- wave-complete path
+// One wave owns 16 channels x all 16 states: DPP row r (16 lanes) holds states [4r, 4r+4) of the
+// wave's 16 channels, lane c of the row one channel. Nothing of the math crosses waves, so the
+// only block-level exchange is the memory staging:
+//   * a block = 4 waves = 64 channels reads u/delta/z and writes out as float4 tiles
+//     [16 steps x 64 ch] through LDS (256-byte row segments), one barrier per chunk;
+//   * per-element work (softplus, dt*u; D*u, SiLU(z)) runs once per element: lane (r, c) owns
+//     steps r, r+4, r+8, r+12 of channel c; the other rows get dt and dt*u by an all-gather over
+//     v_permlane16_swap / v_permlane32_swap (register transposes across rows, no LDS);
+//   * B[t][4r..4r+3] and C[t][4r..4r+3] of step t0+j sit in lane j of row r (one float4 load
+//     each per chunk) and reach the multiplies by DPP row_newbcast;
+//   * the per-row partial readouts are reduce-scattered across rows with the same swaps
+//     (12 swaps + 12 adds per 16 steps), leaving each lane the sums of its own 4 steps.
+__device__ inline void swap32(float& a, float& b) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+__device__ inline void swap16(float& a, float& b) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+// acc += (c broadcast from lane S of its DPP row) * h, one v_fmac_f32_dpp (the compiler folds
+// DPP into v_mul but not into v_fmac).
+template <int S>
+__device__ inline float fmac_bcast(float acc, float c, float h) {
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "+v"(acc)
+        : "v"(c), "v"(h), "n"(S));
+    return acc;
+}
+
+// Row-transposing reduce-scatter: P[j] holds this lane's partial for step q(j) where
+// q(i + 4*rr) = rr + 4*i; on return Y[i] is the sum over the 4 rows for step r + 4*i (r = own row).
+__device__ inline void rows_reduce_scatter(float (&P)[16], float (&Y)[4]) {
+    float Q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float a = P[i], b = P[i + 8];
+        swap32(a, b);  // rows 0,1: (P_i own, P_i of row+2); rows 2,3: (P_{i+8} of row-2, own)
+        Q[i] = a + b;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float a = Q[i], b = Q[i + 4];
+        swap16(a, b);
+        Y[i] = a + b;  // row r: sum for P index i + 4r
+    }
+}
+
+// Row all-gather: X[i] holds this lane's value for step r + 4*i (r = own row). On return
+// G[rr][i] holds the value of row rr's X[i] (same channel), i.e. step rr + 4*i.
+__device__ inline void rows_all_gather(const float (&X)[4], float (&G)[4][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float a = X[i], a2 = X[i];
+        swap16(a, a2);  // rows 0,1 -> a: row0's, a2: row1's; rows 2,3 -> a: row2's, a2: row3's
+        float b = a, b2 = a;
+        swap32(b, b2);  // b: (rows 0,1: row0's; rows 2,3: row0's) ; b2: row2's everywhere
+        float c = a2, c2 = a2;
+        swap32(c, c2);  // c: row1's; c2: row3's
+        G[0][i] = b;
+        G[1][i] = c;
+        G[2][i] = b2;
+        G[3][i] = c2;
+    }
+}
+
+template <typename T, int PF, bool HAS_Z, bool SOFTPLUS>
+__global__ __launch_bounds__(256) void scan_wave_kernel(
+    int64_t L, int64_t Dm, int ntiles,
+    const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
+    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
+    const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
+    const float* __restrict__ init_state, float* __restrict__ last_state) {
+    constexpr int NS = 16, TCH = 16, NT = 256;
+    constexpr int TS = 80;  // tile row stride (floats): rows r and r+1 of a wave hit disjoint banks
+    __shared__ float s_in[2][3][TCH][TS];  // [buf][u|delta|z][step][channel]
+    __shared__ float s_out[2][TCH][TS];
+
+    const int nblk = gridDim.x;
+    int id = blockIdx.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);  // XCD-aware order
+    const int tile = id % ntiles;
+    const int64_t b = id / ntiles;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int r = lane >> 4;   // row = state group
+    const int c = lane & 15;   // channel within the wave
+    const int64_t c0 = (int64_t)tile * 64;
+    const int cb = w * 16 + c;  // channel within the block tile
+    const int64_t d = c0 + cb;
+    const bool dvalid = d < Dm;
+    const int64_t dc = dvalid ? d : Dm - 1;
+
+    // memory phase ownership: float4 e = tid of each [16 x 64] tile
+    const int mrow = tid >> 4, mcl = (tid & 15) * 4;
+    const int64_t mch = c0 + mcl;
+    const bool mvalid = mch < Dm;  // Dm % 4 == 0
+    const int64_t rowbase = b * L * Dm;
+
+    float A2[4], h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        A2[k] = A[dc * NS + 4 * r + k] * kLog2e;
+        h[k] = init_state ? init_state[(b * Dm + dc) * NS + 4 * r + k] : 0.0f;
+    }
+    const float Dd = Dv ? Dv[dc] : 0.0f;
+    const float bias = dt_bias ? dt_bias[dc] : 0.0f;
+
+    // ring of PF chunks: the thread's float4 of u/delta/z, and this lane's B/C float4s
+    float4 ru[PF], rd[PF], rz[PF], rb[PF], rc[PF];
+    const int64_t Lm1 = L - 1;
+    auto fetch = [&](int k, int64_t t0) __attribute__((always_inline)) {
+        int64_t t = t0 + mrow;
+        t = t < Lm1 ? t : Lm1;
+        const int64_t off = rowbase + t * Dm + (mvalid ? mch : 0);
+        ru[k] = Vec4<T>::load(u + off);
+        rd[k] = Vec4<T>::load(delta + off);
+        rz[k] = HAS_Z ? Vec4<T>::load(z + off) : make_float4(0, 0, 0, 0);
+        int64_t tb = t0 + c;  // lane c of row r: step t0+c, states 4r..4r+3
+        tb = tb < Lm1 ? tb : Lm1;
+        rb[k] = Vec4<T>::load(Bm + (b * L + tb) * NS + 4 * r);
+        rc[k] = Vec4<T>::load(Cm + (b * L + tb) * NS + 4 * r);
+    };
+    auto stage_in = [&](int k, int buf) __attribute__((always_inline)) {
+        *reinterpret_cast<float4*>(&s_in[buf][0][mrow][mcl]) = ru[k];
+        *reinterpret_cast<float4*>(&s_in[buf][1][mrow][mcl]) = rd[k];
+        if (HAS_Z) *reinterpret_cast<float4*>(&s_in[buf][2][mrow][mcl]) = rz[k];
+    };
+    auto store_out = [&](int64_t t0, int buf) __attribute__((always_inline)) {
+        const int64_t t = t0 + mrow;
+        if (mvalid && t < L)
+            Vec4<T>::store(out + rowbase + t * Dm + mch,
+                           *reinterpret_cast<const float4*>(&s_out[buf][mrow][mcl]));
+    };
+
+    // math for one chunk: inputs from s_in[buf], outputs into s_out[buf]
+    auto compute = [&](int64_t t0, int buf, const float4& B4, const float4& C4) __attribute__((always_inline)) {
+        // pre: steps r + 4i of channel d
+        float uu[4], zz[4], dl[4], du[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int s = r + 4 * i;
+            uu[i] = s_in[buf][0][s][cb];
+            float x = s_in[buf][1][s][cb] + bias;
+            zz[i] = HAS_Z ? s_in[buf][2][s][cb] : 0.0f;
+            if (SOFTPLUS) x = softplus(x);
+            x = (t0 + s < L) ? x : 0.0f;  // steps past the end leave the state unchanged
+            dl[i] = x;
+            du[i] = x * uu[i];
+        }
+        float gdl[4][4], gdu[4][4];  // [row rr][i]: step rr + 4i
+        rows_all_gather(dl, gdl);
+        rows_all_gather(du, gdu);
+        const float bk[4] = {B4.x, B4.y, B4.z, B4.w};
+        const float ck[4] = {C4.x, C4.y, C4.z, C4.w};
+        // main: 16 steps, 4 states; P index j = i + 4*rr holds step rr + 4*i
+        float P[16];
+        StepLoop<4>::run([&](auto gc) {  // groups of 4 steps: 16 decays issued ahead
+            constexpr int g = decltype(gc)::value;
+            float ab[4][4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int s = 4 * g + e;
+                    ab[e][k] = fast_exp2(gdl[s & 3][s >> 2] * A2[k]);
+                }
+            StepLoop<4>::run([&](auto ec) {
+                constexpr int s = 4 * g + decltype(ec)::value;
+                const float dus = gdu[s & 3][s >> 2];
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    h[k] = fmaf(ab[s - 4 * g][k], h[k], dpp<kDppBcast<s>>(bk[k]) * dus);
+                    acc = fmac_bcast<s>(acc, ck[k], h[k]);
+                }
+                P[(s >> 2) + 4 * (s & 3)] = acc;  // j = i + 4*rr for s = rr + 4*i
+            });
+        });
+        float Y[4];
+        rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int s = r + 4 * i;
+            float y = fmaf(Dd, uu[i], Y[i]);
+            if (HAS_Z) y *= silu(zz[i]);
+            s_out[buf][s][cb] = y;
+        }
+    };
+
+    // pipeline: iteration k stages chunk k+1's inputs, stores chunk k-1's outputs, computes
+    // chunk k; one barrier per chunk.
+#pragma unroll
+    for (int k = 0; k < PF; ++k) fetch(k, (int64_t)k * TCH);
+    stage_in(0, 0);
+    float4 B4 = rb[0], C4 = rc[0];
+    fetch(0, (int64_t)PF * TCH);
+    lds_barrier();
+    for (int64_t tb0 = 0; tb0 < L; tb0 += PF * TCH) {
+        StepLoop<PF>::run([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            constexpr int kn = (k + 1) % PF;
+            constexpr int buf = k & 1;  // PF is even
+            const int64_t t0 = tb0 + k * TCH;
+            if (t0 >= L) return;  // uniform
+            stage_in(kn, buf ^ 1);
+            if (t0 > 0) store_out(t0 - TCH, buf ^ 1);
+            const float4 Bn = rb[kn], Cn = rc[kn];
+            fetch(kn, t0 + TCH + (int64_t)PF * TCH);
+            compute(t0, buf, B4, C4);
+            B4 = Bn;
+            C4 = Cn;
+            lds_barrier();
+        });
+    }
+    {
+        const int64_t nchunks = (L + TCH - 1) / TCH;
+        store_out((nchunks - 1) * TCH, (int)((nchunks - 1) & 1));
+    }
+    if (last_state && dvalid) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) last_state[(b * Dm + d) * NS + 4 * r + k] = h[k];
     }
 }
 
@@ -696,11 +984,11 @@ int dispatch_fast(const ScanArgs& a) {
     return launch_fast<T, W, TCH, false, false>(a);
 }
 
-template <typename T, int W, int TCH, int PF, bool HAS_Z, bool SP>
+template <typename T, int W, int TCH, int PF, bool HAS_Z, bool SP, bool SBC>
 int launch_tile(const ScanArgs& a) {
     const int ntiles = (int)((a.Dm + 63) / 64);
     dim3 grid((unsigned)(ntiles * a.Bt));
-    hipLaunchKernelGGL((scan_tile_kernel<T, W, TCH, PF, HAS_Z, SP>), grid, dim3(64 * W), 0,
+    hipLaunchKernelGGL((scan_tile_kernel<T, W, TCH, PF, HAS_Z, SP, SBC>), grid, dim3(64 * W), 0,
                        a.stream, a.L, a.Dm, ntiles, (const T*)a.u, (const T*)a.delta, a.A,
                        (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
                        a.init_state, a.last_state);
@@ -708,13 +996,34 @@ int launch_tile(const ScanArgs& a) {
     return HX_OK;
 }
 
-template <typename T, int W, int TCH, int PF>
+template <typename T, int W, int TCH, int PF, bool SBC>
 int dispatch_tile(const ScanArgs& a) {
     const bool hz = a.z != nullptr;
-    if (hz && a.softplus) return launch_tile<T, W, TCH, PF, true, true>(a);
-    if (hz) return launch_tile<T, W, TCH, PF, true, false>(a);
-    if (a.softplus) return launch_tile<T, W, TCH, PF, false, true>(a);
-    return launch_tile<T, W, TCH, PF, false, false>(a);
+    if (hz && a.softplus) return launch_tile<T, W, TCH, PF, true, true, SBC>(a);
+    if (hz) return launch_tile<T, W, TCH, PF, true, false, SBC>(a);
+    if (a.softplus) return launch_tile<T, W, TCH, PF, false, true, SBC>(a);
+    return launch_tile<T, W, TCH, PF, false, false, SBC>(a);
+}
+
+template <typename T, int PF, bool HAS_Z, bool SP>
+int launch_wave(const ScanArgs& a) {
+    const int ntiles = (int)((a.Dm + 63) / 64);
+    dim3 grid((unsigned)(ntiles * a.Bt));
+    hipLaunchKernelGGL((scan_wave_kernel<T, PF, HAS_Z, SP>), grid, dim3(256), 0, a.stream, a.L,
+                       a.Dm, ntiles, (const T*)a.u, (const T*)a.delta, a.A, (const T*)a.B,
+                       (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out, a.init_state,
+                       a.last_state);
+    HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+template <typename T, int PF>
+int dispatch_wave(const ScanArgs& a) {
+    const bool hz = a.z != nullptr;
+    if (hz && a.softplus) return launch_wave<T, PF, true, true>(a);
+    if (hz) return launch_wave<T, PF, true, false>(a);
+    if (a.softplus) return launch_wave<T, PF, false, true>(a);
+    return launch_wave<T, PF, false, false>(a);
 }
 
 template <typename T, bool HAS_Z, bool SP>
@@ -777,14 +1086,18 @@ int run_scan(const ScanArgs& a) {
                          aligned(a.out, 16) && (!a.z || aligned(a.z, 16)) &&
                          (!a.D || aligned(a.D, 16)) && (!a.dt_bias || aligned(a.dt_bias, 16)) &&
                          a.Bt * ((a.Dm + 63) / 64) <= 0x7fffffff;
-    if (v == 0) {  // auto: the LDS-staged tile kernel where its float4 access is legal
-        if (tile_ok) return dispatch_tile<T, 4, 16, 2>(a);
+    if (v == 0) {  // auto: the wave-complete kernel where its float4 access is legal
+        if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16)) return dispatch_wave<T, 2>(a);
+        if (tile_ok) return dispatch_tile<T, 8, 32, 2, false>(a);
         return dispatch_fast<T, 8, 16>(a);
     }
     switch (v) {
-        case 32: if (tile_ok) return dispatch_tile<T, 8, 32, 2>(a); break;
-        case 33: if (tile_ok) return dispatch_tile<T, 4, 16, 2>(a); break;
-        case 34: if (tile_ok) return dispatch_tile<T, 4, 32, 2>(a); break;
+        case 32: if (tile_ok) return dispatch_tile<T, 8, 32, 2, false>(a); break;
+        case 33: if (tile_ok) return dispatch_tile<T, 4, 16, 2, false>(a); break;
+        case 34: if (tile_ok) return dispatch_tile<T, 4, 32, 2, false>(a); break;
+        case 35: if (tile_ok) return dispatch_tile<T, 8, 32, 2, true>(a); break;
+        case 40: if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16)) return dispatch_wave<T, 2>(a); break;
+        case 36: if (tile_ok) return dispatch_tile<T, 4, 16, 2, true>(a); break;
         case 16: return dispatch_state_lane<T>(a);
         case 1: return dispatch_fast<T, 1, 16>(a);
         case 2: return dispatch_fast<T, 2, 16>(a);
@@ -842,9 +1155,9 @@ extern "C" int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim,
 
 extern "C" int hx_set_scan_variant(int variant) {
     HX_REQUIRE(variant == 0 || variant == -1 || variant == 1 || variant == 2 || variant == 4 ||
-                   variant == 8 || variant == 16 || (variant >= 32 && variant <= 34),
+                   variant == 8 || variant == 16 || (variant >= 32 && variant <= 36) || variant == 40,
                HX_ERR_INVALID_INPUT,
-               "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8, 16, 32..34", variant);
+               "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8, 16, 32..36, 40", variant);
     hx::g_scan_variant = variant;
     return HX_OK;
 }

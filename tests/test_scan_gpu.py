@@ -16,7 +16,7 @@ from tests.util import TOL_BF16, TOL_F32, bf16_round, rel_err, scan_inputs
 
 pytestmark = pytest.mark.gpu
 
-VARIANTS = [-1, 1, 2, 4, 8, 16, 32, 33, 34]
+VARIANTS = [-1, 1, 2, 4, 8, 16, 32, 33, 34, 35, 36, 40]
 
 
 def to_dev(x, dev, dtype=torch.float32):
@@ -64,7 +64,7 @@ def test_scan_matches_oracle(dev, shape, variant):
 @pytest.mark.parametrize("with_z", [True, False])
 @pytest.mark.parametrize("with_D", [True, False])
 @pytest.mark.parametrize("softplus", [True, False])
-@pytest.mark.parametrize("variant", [32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", [40, 32, 33, 16, 4, -1])
 def test_scan_optional_operands(dev, with_z, with_D, softplus, variant):
     ssm.set_scan_variant(variant)
     x = scan_inputs(2, 70, 96, 16, seed=7, with_z=with_z, with_D=with_D)
@@ -108,7 +108,7 @@ def test_scan_zero_length_returns_initial_state(dev):
     assert np.array_equal(s, init)
 
 
-@pytest.mark.parametrize("variant", [32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", [40, 32, 33, 16, 4, -1])
 @pytest.mark.parametrize("shape", [(2, 37, 70, 16), (1, 300, 256, 16)], ids=str)
 def test_scan_bf16_storage(dev, variant, shape):
     ssm.set_scan_variant(variant)
