@@ -83,6 +83,7 @@ SIGNATURES = {
     "hx_linear_f32": [_i64, _i64, _i64, _p, _p, _p, _int, _p, _p],
     "hx_matmul_f32": [_i64, _i64, _i64, _p, _p, _p, _p],
     "hx_set_scan_variant": [_int],
+    "hx_set_scan_segments": [_int],
 }
 
 _lib = None

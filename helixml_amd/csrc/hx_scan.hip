@@ -708,23 +708,43 @@ __device__ inline void rows_all_gather(const float (&X)[4], float (&G)[4][4]) {
     }
 }
 
-template <typename T, int PF, bool HAS_Z, bool SOFTPLUS>
+// Segments: for long sequences with few (batch, channel-tile) pairs the sequence is cut into
+// nseg segments of seg_len steps, each its own block. END_ONLY blocks run a segment from a zero
+// state and publish its end state and the segment's total dt (the decay over the segment is
+// exp(A * sum dt)); a carry kernel chains the segments' entry states; full blocks then run each
+// segment from its entry state (seg_init) and write the outputs.
+// Number of time segments for the wave kernel: 0 = automatic; set by hx_set_scan_segments.
+int g_scan_segments = 0;
+
+struct WaveSeg {
+    int64_t seg_len;
+    int nseg;
+    const float* seg_init;  // [nseg][B][D][16] entry states (full mode, nseg > 1)
+    float* seg_hend;        // [nseg][B][D][16] end state from zero (END_ONLY)
+    float* seg_sumdt;       // [nseg][B][D]     total dt of the segment (END_ONLY)
+};
+
+template <typename T, int PF, bool HAS_Z, bool SOFTPLUS, bool END_ONLY>
 __global__ __launch_bounds__(256) void scan_wave_kernel(
-    int64_t L, int64_t Dm, int ntiles,
+    int64_t L, int64_t Dm, int ntiles, int64_t Bt,
     const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
     const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
     const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
-    const float* __restrict__ init_state, float* __restrict__ last_state) {
-    constexpr int NS = 16, TCH = 16, NT = 256;
+    const float* __restrict__ init_state, float* __restrict__ last_state, WaveSeg sg) {
+    constexpr int NS = 16, TCH = 16;
     constexpr int TS = 80;  // tile row stride (floats): rows r and r+1 of a wave hit disjoint banks
+    constexpr bool USE_Z = HAS_Z && !END_ONLY;
     __shared__ float s_in[2][3][TCH][TS];  // [buf][u|delta|z][step][channel]
-    __shared__ float s_out[2][TCH][TS];
+    __shared__ float s_out[END_ONLY ? 1 : 2][TCH][TS];
 
     const int nblk = gridDim.x;
     int id = blockIdx.x;
     if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);  // XCD-aware order
     const int tile = id % ntiles;
-    const int64_t b = id / ntiles;
+    const int64_t b = (id / ntiles) % Bt;
+    const int seg = (int)(id / ntiles / Bt);
+    const int64_t tbeg = (int64_t)seg * sg.seg_len;
+    const int64_t tend = tbeg + sg.seg_len < L ? tbeg + sg.seg_len : L;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -744,39 +764,44 @@ __global__ __launch_bounds__(256) void scan_wave_kernel(
     const int64_t rowbase = b * L * Dm;
 
     float A2[4], h[4];
+    const float* h0 = END_ONLY ? nullptr
+                    : (sg.nseg > 1 ? sg.seg_init + (int64_t)seg * Bt * Dm * NS : init_state);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         A2[k] = A[dc * NS + 4 * r + k] * kLog2e;
-        h[k] = init_state ? init_state[(b * Dm + dc) * NS + 4 * r + k] : 0.0f;
+        h[k] = h0 ? h0[(b * Dm + dc) * NS + 4 * r + k] : 0.0f;
     }
     const float Dd = Dv ? Dv[dc] : 0.0f;
     const float bias = dt_bias ? dt_bias[dc] : 0.0f;
+    float sumdt = 0.0f;
 
     // ring of PF chunks: the thread's float4 of u/delta/z, and this lane's B/C float4s
     float4 ru[PF], rd[PF], rz[PF], rb[PF], rc[PF];
-    const int64_t Lm1 = L - 1;
+    const int64_t Lm1 = tend - 1;
     auto fetch = [&](int k, int64_t t0) __attribute__((always_inline)) {
         int64_t t = t0 + mrow;
         t = t < Lm1 ? t : Lm1;
         const int64_t off = rowbase + t * Dm + (mvalid ? mch : 0);
         ru[k] = Vec4<T>::load(u + off);
         rd[k] = Vec4<T>::load(delta + off);
-        rz[k] = HAS_Z ? Vec4<T>::load(z + off) : make_float4(0, 0, 0, 0);
+        rz[k] = USE_Z ? Vec4<T>::load(z + off) : make_float4(0, 0, 0, 0);
         int64_t tb = t0 + c;  // lane c of row r: step t0+c, states 4r..4r+3
         tb = tb < Lm1 ? tb : Lm1;
         rb[k] = Vec4<T>::load(Bm + (b * L + tb) * NS + 4 * r);
-        rc[k] = Vec4<T>::load(Cm + (b * L + tb) * NS + 4 * r);
+        rc[k] = END_ONLY ? make_float4(0, 0, 0, 0) : Vec4<T>::load(Cm + (b * L + tb) * NS + 4 * r);
     };
     auto stage_in = [&](int k, int buf) __attribute__((always_inline)) {
         *reinterpret_cast<float4*>(&s_in[buf][0][mrow][mcl]) = ru[k];
         *reinterpret_cast<float4*>(&s_in[buf][1][mrow][mcl]) = rd[k];
-        if (HAS_Z) *reinterpret_cast<float4*>(&s_in[buf][2][mrow][mcl]) = rz[k];
+        if (USE_Z) *reinterpret_cast<float4*>(&s_in[buf][2][mrow][mcl]) = rz[k];
     };
     auto store_out = [&](int64_t t0, int buf) __attribute__((always_inline)) {
-        const int64_t t = t0 + mrow;
-        if (mvalid && t < L)
-            Vec4<T>::store(out + rowbase + t * Dm + mch,
-                           *reinterpret_cast<const float4*>(&s_out[buf][mrow][mcl]));
+        if constexpr (!END_ONLY) {
+            const int64_t t = t0 + mrow;
+            if (mvalid && t < tend)
+                Vec4<T>::store(out + rowbase + t * Dm + mch,
+                               *reinterpret_cast<const float4*>(&s_out[buf][mrow][mcl]));
+        }
     };
 
     // math for one chunk: inputs from s_in[buf], outputs into s_out[buf]
@@ -788,11 +813,12 @@ __global__ __launch_bounds__(256) void scan_wave_kernel(
             const int s = r + 4 * i;
             uu[i] = s_in[buf][0][s][cb];
             float x = s_in[buf][1][s][cb] + bias;
-            zz[i] = HAS_Z ? s_in[buf][2][s][cb] : 0.0f;
+            zz[i] = USE_Z ? s_in[buf][2][s][cb] : 0.0f;
             if (SOFTPLUS) x = softplus(x);
-            x = (t0 + s < L) ? x : 0.0f;  // steps past the end leave the state unchanged
+            x = (t0 + s < tend) ? x : 0.0f;  // steps past the end leave the state unchanged
             dl[i] = x;
             du[i] = x * uu[i];
+            if (END_ONLY) sumdt += x;
         }
         float gdl[4][4], gdu[4][4];  // [row rr][i]: step rr + 4i
         rows_all_gather(dl, gdl);
@@ -818,39 +844,41 @@ __global__ __launch_bounds__(256) void scan_wave_kernel(
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     h[k] = fmaf(ab[s - 4 * g][k], h[k], dpp<kDppBcast<s>>(bk[k]) * dus);
-                    acc = fmac_bcast<s>(acc, ck[k], h[k]);
+                    if constexpr (!END_ONLY) acc = fmac_bcast<s>(acc, ck[k], h[k]);
                 }
                 P[(s >> 2) + 4 * (s & 3)] = acc;  // j = i + 4*rr for s = rr + 4*i
             });
         });
-        float Y[4];
-        rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i
+        if constexpr (!END_ONLY) {
+            float Y[4];
+            rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int s = r + 4 * i;
-            float y = fmaf(Dd, uu[i], Y[i]);
-            if (HAS_Z) y *= silu(zz[i]);
-            s_out[buf][s][cb] = y;
+            for (int i = 0; i < 4; ++i) {
+                const int s = r + 4 * i;
+                float y = fmaf(Dd, uu[i], Y[i]);
+                if (HAS_Z) y *= silu(zz[i]);
+                s_out[buf][s][cb] = y;
+            }
         }
     };
 
     // pipeline: iteration k stages chunk k+1's inputs, stores chunk k-1's outputs, computes
     // chunk k; one barrier per chunk.
 #pragma unroll
-    for (int k = 0; k < PF; ++k) fetch(k, (int64_t)k * TCH);
+    for (int k = 0; k < PF; ++k) fetch(k, tbeg + (int64_t)k * TCH);
     stage_in(0, 0);
     float4 B4 = rb[0], C4 = rc[0];
-    fetch(0, (int64_t)PF * TCH);
+    fetch(0, tbeg + (int64_t)PF * TCH);
     lds_barrier();
-    for (int64_t tb0 = 0; tb0 < L; tb0 += PF * TCH) {
-        StepLoop<PF>::run([&](auto kc) {
+    for (int64_t tb0 = tbeg; tb0 < tend; tb0 += PF * TCH) {
+        StepLoop<PF>::run([&](auto kc) __attribute__((always_inline)) {
             constexpr int k = decltype(kc)::value;
             constexpr int kn = (k + 1) % PF;
             constexpr int buf = k & 1;  // PF is even
             const int64_t t0 = tb0 + k * TCH;
-            if (t0 >= L) return;  // uniform
+            if (t0 >= tend) return;  // uniform
             stage_in(kn, buf ^ 1);
-            if (t0 > 0) store_out(t0 - TCH, buf ^ 1);
+            if (t0 > tbeg) store_out(t0 - TCH, END_ONLY ? 0 : buf ^ 1);
             const float4 Bn = rb[kn], Cn = rc[kn];
             fetch(kn, t0 + TCH + (int64_t)PF * TCH);
             compute(t0, buf, B4, C4);
@@ -859,13 +887,46 @@ __global__ __launch_bounds__(256) void scan_wave_kernel(
             lds_barrier();
         });
     }
-    {
-        const int64_t nchunks = (L + TCH - 1) / TCH;
-        store_out((nchunks - 1) * TCH, (int)((nchunks - 1) & 1));
-    }
-    if (last_state && dvalid) {
+    if constexpr (!END_ONLY) {
+        const int64_t nch = (tend - tbeg + TCH - 1) / TCH;
+        store_out(tbeg + (nch - 1) * TCH, (int)((nch - 1) & 1));
+        if (last_state && dvalid && seg == sg.nseg - 1) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) last_state[(b * Dm + d) * NS + 4 * r + k] = h[k];
+            for (int k = 0; k < 4; ++k) last_state[(b * Dm + d) * NS + 4 * r + k] = h[k];
+        }
+    } else {
+        // segment end state (from zero) and total dt; rows hold different steps of a channel
+        float t1 = sumdt, t2 = sumdt;
+        swap16(t1, t2);
+        float sa = t1 + t2;  // rows {0,1} pair and {2,3} pair
+        float t3 = sa, t4 = sa;
+        swap32(t3, t4);
+        sumdt = t3 + t4;
+        if (dvalid) {
+            float* he = sg.seg_hend + (int64_t)seg * Bt * Dm * NS;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) he[(b * Dm + d) * NS + 4 * r + k] = h[k];
+            if (r == 0) sg.seg_sumdt[((int64_t)seg * Bt + b) * Dm + d] = sumdt;
+        }
+    }
+}
+
+// Entry state of every segment: h_in[0] = init (or 0); h_in[k] = exp(A * sumdt[k-1]) * h_in[k-1]
+// + hend[k-1], per (b, d, n). Writes seg_init[k] for k = 0..nseg-1.
+__global__ __launch_bounds__(256) void scan_seg_carry_kernel(
+    int64_t Bt, int64_t Dm, int nseg, const float* __restrict__ A,
+    const float* __restrict__ init_state, const float* __restrict__ hend,
+    const float* __restrict__ sumdt, float* __restrict__ seg_init) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t per = Bt * Dm * 16;
+    if (gid >= per) return;
+    const int64_t bd = gid / 16, n = gid % 16;
+    const int64_t dd = bd % Dm;
+    const float a2 = A[dd * 16 + n] * kLog2e;
+    float hc = init_state ? init_state[gid] : 0.0f;
+    for (int k = 0; k < nseg; ++k) {
+        seg_init[(int64_t)k * per + gid] = hc;
+        hc = fmaf(fast_exp2(a2 * sumdt[(int64_t)k * Bt * Dm + bd]), hc, hend[(int64_t)k * per + gid]);
     }
 }
 
@@ -1005,16 +1066,56 @@ int dispatch_tile(const ScanArgs& a) {
     return launch_tile<T, W, TCH, PF, false, false, SBC>(a);
 }
 
-template <typename T, int PF, bool HAS_Z, bool SP>
-int launch_wave(const ScanArgs& a) {
+template <typename T, int PF, bool HAS_Z, bool SP, bool END_ONLY>
+int launch_wave_one(const ScanArgs& a, const WaveSeg& sg) {
     const int ntiles = (int)((a.Dm + 63) / 64);
-    dim3 grid((unsigned)(ntiles * a.Bt));
-    hipLaunchKernelGGL((scan_wave_kernel<T, PF, HAS_Z, SP>), grid, dim3(256), 0, a.stream, a.L,
-                       a.Dm, ntiles, (const T*)a.u, (const T*)a.delta, a.A, (const T*)a.B,
-                       (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out, a.init_state,
-                       a.last_state);
+    dim3 grid((unsigned)((int64_t)ntiles * a.Bt * sg.nseg));
+    hipLaunchKernelGGL((scan_wave_kernel<T, PF, HAS_Z, SP, END_ONLY>), grid, dim3(256), 0,
+                       a.stream, a.L, a.Dm, ntiles, a.Bt, (const T*)a.u, (const T*)a.delta, a.A,
+                       (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
+                       a.init_state, a.last_state, sg);
     HX_LAUNCH_CHECK();
     return HX_OK;
+}
+
+template <typename T, int PF, bool HAS_Z, bool SP>
+int launch_wave(const ScanArgs& a) {
+    // Segment the sequence when the (batch, 64-channel tile) pairs alone cannot fill the GPU.
+    const int64_t ntiles = (a.Dm + 63) / 64;
+    const int64_t pairs = ntiles * a.Bt;
+    int nseg = 1;
+    if (g_scan_segments > 0) {
+        nseg = g_scan_segments;
+    } else if (pairs < 256 && a.L >= 4096) {
+        const int64_t want = (512 + pairs - 1) / pairs;          // ~512 blocks
+        const int64_t cap = a.L / 1024;                           // segments >= 1024 steps
+        nseg = (int)(want < cap ? want : cap);
+        if (nseg < 1) nseg = 1;
+    }
+    int64_t seg_len = (a.L + nseg - 1) / nseg;
+    seg_len = (seg_len + 15) / 16 * 16;
+    nseg = (int)((a.L + seg_len - 1) / seg_len);
+    if (nseg <= 1) return launch_wave_one<T, PF, HAS_Z, SP, false>(a, WaveSeg{a.L, 1, nullptr, nullptr, nullptr});
+
+    const size_t per = (size_t)a.Bt * a.Dm * 16;
+    const size_t nfloat = (size_t)nseg * (2 * per + (size_t)a.Bt * a.Dm);
+    float* scratch = nullptr;
+    HX_HIP_CHECK(hipMallocAsync((void**)&scratch, nfloat * sizeof(float), a.stream));
+    float* hend = scratch;
+    float* seg_init = hend + (size_t)nseg * per;
+    float* sumdt = seg_init + (size_t)nseg * per;
+    int rc = launch_wave_one<T, PF, false, SP, true>(a, WaveSeg{seg_len, nseg, nullptr, hend, sumdt});
+    if (rc == HX_OK) {
+        hipLaunchKernelGGL(scan_seg_carry_kernel, dim3((unsigned)((per + 255) / 256)), dim3(256), 0,
+                           a.stream, a.Bt, a.Dm, nseg, a.A, a.init_state, hend, sumdt, seg_init);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess)
+            rc = set_error(HX_ERR_BACKEND, "scan carry launch failed: %s", hipGetErrorString(e));
+    }
+    if (rc == HX_OK)
+        rc = launch_wave_one<T, PF, HAS_Z, SP, false>(a, WaveSeg{seg_len, nseg, seg_init, nullptr, nullptr});
+    (void)hipFreeAsync(scratch, a.stream);
+    return rc;
 }
 
 template <typename T, int PF>
@@ -1159,6 +1260,13 @@ extern "C" int hx_set_scan_variant(int variant) {
                HX_ERR_INVALID_INPUT,
                "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8, 16, 32..36, 40", variant);
     hx::g_scan_variant = variant;
+    return HX_OK;
+}
+
+extern "C" int hx_set_scan_segments(int nseg) {
+    HX_REQUIRE(nseg >= 0 && nseg <= 4096, HX_ERR_INVALID_INPUT,
+               "hx_set_scan_segments: %d outside 0..4096", nseg);
+    hx::g_scan_segments = nseg;
     return HX_OK;
 }
 

@@ -170,3 +170,7 @@ def matmul(A, B, stream=None):
 
 def set_scan_variant(v: int) -> None:
     _ffi.call("hx_set_scan_variant", int(v))
+
+
+def set_scan_segments(n: int) -> None:
+    _ffi.call("hx_set_scan_segments", int(n))

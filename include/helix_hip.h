@@ -146,6 +146,11 @@ int hx_matmul_f32(int64_t M, int64_t K, int64_t N, const float* A, const float* 
  * generic one-thread-per-channel kernel. A measurement knob with no reference counterpart;
  * results are identical within fp32 rounding for every variant. */
 int hx_set_scan_variant(int variant);
+/* Number of time segments the long-sequence path splits a scan into (0 = automatic: only when
+ * the (batch, 64-channel) tiles cannot fill the GPU and seqlen >= 4096). Segments are scanned in
+ * parallel from a zero state, their entry states chained by a carry kernel, then rescanned with
+ * outputs. A measurement knob; results agree within fp32 rounding for every setting. */
+int hx_set_scan_segments(int nseg);
 
 #ifdef __cplusplus
 }

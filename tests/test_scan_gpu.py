@@ -168,3 +168,34 @@ def test_baseline_config2_full_size(dev):
     err = rel_err(g, r)
     print(f"config2 rel err {err:.3e}")
     assert err <= TOL_F32
+
+
+@pytest.fixture
+def _reset_segments(dev):
+    yield
+    ssm.set_scan_segments(0)
+
+
+@pytest.mark.parametrize("nseg", [2, 3, 7])
+@pytest.mark.parametrize("shape", [(2, 300, 128, 16), (1, 1000, 64, 16), (1, 77, 192, 16)], ids=str)
+def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape):
+    """Time-segmented path (segment end states from zero, carry chain, rescan from entry
+    states) against the sequential oracle, with an initial state and the final state checked."""
+    ssm.set_scan_segments(nseg)
+    x = scan_inputs(*shape, seed=nseg * 11 + shape[1], with_bias=True)
+    init = (np.random.default_rng(nseg).standard_normal((shape[0], shape[2], 16)) * 0.5).astype(np.float32)
+    r, rlast = oracle.selective_scan(**x, init_state=init, return_last_state=True)
+    g, glast = run_gpu(x, dev, init_state=init, last=True)
+    assert rel_err(g, r) <= TOL_F32
+    assert rel_err(glast, rlast) <= TOL_F32
+
+
+def test_baseline_config4_scan_full_size(dev):
+    """BASELINE config 4 scan (batch 1, L 65536, d_inner 2048, d_state 16, fp32): the automatic
+    segmented path against the (multi-threaded, arithmetic-identical) CPU oracle."""
+    x = scan_inputs(1, 65536, 2048, 16, seed=0xC4)
+    g = run_gpu(x, dev)
+    r = oracle.selective_scan_omp(**x)
+    err = rel_err(g, r)
+    print(f"config4 rel err {err:.3e}")
+    assert err <= TOL_F32
