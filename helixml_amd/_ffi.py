@@ -82,6 +82,11 @@ SIGNATURES = {
     "hx_s4d_complex_fwd": [_i64, _i64, _i64, _i64] + [_p] * 10 + [_p],
     "hx_linear_f32": [_i64, _i64, _i64, _p, _p, _p, _int, _p, _p],
     "hx_matmul_f32": [_i64, _i64, _i64, _p, _p, _p, _p],
+    "hx_gemm_bf16": [_i64, _i64, _i64, _p, _i64, _p, _i64, _p, _int, _int,
+                     _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p],
+    "hx_conv1d_silu": [_i64, _i64, _i64, _i64, _int, _p, _i64, _p, _p, _p, _p],
+    "hx_mamba_block_workspace_size": [_i64, _i64, _i64, _i64, _i64],
+    "hx_mamba_block_fwd": [_i64] * 7 + [_p] * 12 + [_sz, _p],
     "hx_set_scan_variant": [_int],
     "hx_set_scan_segments": [_int],
 }
@@ -100,7 +105,8 @@ def lib() -> ctypes.CDLL:
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_char_p if name == "hx_last_error" else _int
+            fn.restype = (ctypes.c_char_p if name == "hx_last_error" else
+                          _sz if name == "hx_mamba_block_workspace_size" else _int)
         _lib = L
     return _lib
 

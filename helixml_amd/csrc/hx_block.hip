@@ -1,0 +1,161 @@
+// hx_block.hip — the full Mamba block forward on gfx950:
+//   xz = x . W_in^T           (matrix-core GEMM, split into x | z)
+//   xc = SiLU(conv1d_causal(x) + conv_b)   (depthwise, kernel d_conv)
+//   dt_lo | B | C = xc . W_x^T  (GEMM, three outputs)
+//   dt = dt_lo . W_dt^T       (GEMM)
+//   y  = selective_scan(xc, dt, A, B, C, D, z, dt_bias, softplus)
+//   out = y . W_out^T         (GEMM)
+// The reference's exported MambaBlock::forward_mamba is Linear -> SiLU -> Linear
+// (crates/nn/src/lib.rs:888-906) and allocates A/B/C/D/delta_proj/B_proj/C_proj it never uses
+// (lib.rs:851-867); this is the block those parameters describe. bf16 storage, fp32 arithmetic.
+#include "hx_common.h"
+
+extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
+                            const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
+                            void* Y0, int64_t ld0, int64_t split1, void* Y1, int64_t ld1,
+                            int64_t split2, void* Y2, int64_t ld2, void* stream);
+
+namespace hx {
+namespace {
+
+// Causal depthwise conv over time + bias + SiLU, 4 channels per thread (8-byte bf16 / 16-byte
+// fp32 row accesses). y[b,t,d] = silu(bias[d] + sum_j w[d,j] * x[b, t-(K-1)+j, d]).
+template <typename T, int KW>
+__global__ __launch_bounds__(256) void conv1d_silu_kernel(int64_t Bt, int64_t L, int64_t Dm,
+                                                          const T* __restrict__ x, int64_t ldx,
+                                                          const float* __restrict__ w,
+                                                          const float* __restrict__ bias,
+                                                          T* __restrict__ y) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t D4 = Dm / 4;
+    if (gid >= Bt * L * D4) return;
+    const int64_t d4 = gid % D4;
+    const int64_t bt = gid / D4;  // b * L + t
+    const int64_t t = bt % L;
+    const int64_t d = d4 * 4;
+    float acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = bias ? bias[d + i] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < KW; ++j) {
+        const int64_t tt = t - (KW - 1) + j;
+        if (tt < 0) continue;
+        const T* xp = x + (bt - (KW - 1) + j) * ldx + d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(w[(d + i) * KW + j], Storage<T>::load(xp + i), acc[i]);
+    }
+    T* yp = y + bt * Dm + d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Storage<T>::store(yp + i, silu(acc[i]));
+}
+
+template <typename T>
+int launch_conv(int64_t Bt, int64_t L, int64_t Dm, int64_t KW, const void* x, int64_t ldx,
+                const float* w, const float* b, void* y, hipStream_t s) {
+    const int64_t total = Bt * L * (Dm / 4);
+    dim3 grid((unsigned)((total + 255) / 256));
+#define HX_CONV(K)                                                                            \
+    hipLaunchKernelGGL((conv1d_silu_kernel<T, K>), grid, dim3(256), 0, s, Bt, L, Dm,          \
+                       (const T*)x, ldx, w, b, (T*)y)
+    switch (KW) {
+        case 1: HX_CONV(1); break;
+        case 2: HX_CONV(2); break;
+        case 3: HX_CONV(3); break;
+        case 4: HX_CONV(4); break;
+        default: HX_CONV(8); break;
+    }
+#undef HX_CONV
+    HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+}  // namespace
+}  // namespace hx
+
+extern "C" int hx_conv1d_silu(int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+                              int dtype, const void* x, int64_t ldx, const float* weight,
+                              const float* bias, void* y, void* stream) {
+    using namespace hx;
+    HX_REQUIRE(batch >= 0 && seqlen >= 0 && dim >= 0, HX_ERR_INVALID_DIMENSION,
+               "conv1d_silu: negative size");
+    HX_REQUIRE(width >= 1 && width <= 4, HX_ERR_UNSUPPORTED, "conv1d_silu: width %lld (1..4)",
+               (long long)width);
+    HX_REQUIRE(dim % 4 == 0, HX_ERR_UNSUPPORTED, "conv1d_silu: dim %lld not a multiple of 4",
+               (long long)dim);
+    HX_REQUIRE(dtype == HX_F32 || dtype == HX_BF16, HX_ERR_DTYPE_MISMATCH, "conv1d_silu: dtype %d",
+               dtype);
+    if (batch == 0 || seqlen == 0 || dim == 0) return HX_OK;
+    HX_REQUIRE(x && weight && y && ldx >= dim, HX_ERR_INVALID_INPUT,
+               "conv1d_silu: x, weight, y required and ldx >= dim");
+    return dtype == HX_F32
+               ? launch_conv<float>(batch, seqlen, dim, width, x, ldx, weight, bias, y, as_stream(stream))
+               : launch_conv<uint16_t>(batch, seqlen, dim, width, x, ldx, weight, bias, y, as_stream(stream));
+}
+
+// Workspace layout (bf16 elements, M = batch*seqlen): xpart | z | xconv | dt | y  [M, d_inner]
+// each, dt_lo [M, dt_rank], B [M, N], C [M, N]; every region 256-byte aligned.
+namespace {
+inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+}  // namespace
+
+extern "C" size_t hx_mamba_block_workspace_size(int64_t batch, int64_t seqlen, int64_t d_inner,
+                                                int64_t dt_rank, int64_t dstate) {
+    const size_t M = (size_t)batch * seqlen;
+    return 5 * align256(M * d_inner * 2) + align256(M * dt_rank * 2) + 2 * align256(M * dstate * 2);
+}
+
+extern "C" int hx_mamba_block_fwd(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner,
+                                  int64_t dstate, int64_t dt_rank, int64_t d_conv,
+                                  const void* x, const void* w_in, const float* conv_w,
+                                  const float* conv_b, const void* w_x, const void* w_dt,
+                                  const float* dt_bias, const float* A, const float* D,
+                                  const void* w_out, void* out, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+    using namespace hx;
+    HX_REQUIRE(batch >= 0 && seqlen >= 0 && d_model > 0 && d_inner > 0 && dt_rank > 0,
+               HX_ERR_INVALID_DIMENSION, "mamba_block: bad sizes");
+    HX_REQUIRE(dstate == 16, HX_ERR_UNSUPPORTED, "mamba_block: dstate %lld (16 supported)",
+               (long long)dstate);
+    HX_REQUIRE(d_model % 8 == 0 && d_inner % 8 == 0 && dt_rank % 8 == 0, HX_ERR_UNSUPPORTED,
+               "mamba_block: d_model, d_inner and dt_rank must be multiples of 8");
+    if (batch == 0 || seqlen == 0) return HX_OK;
+    HX_REQUIRE(x && w_in && conv_w && w_x && w_dt && A && w_out && out && workspace,
+               HX_ERR_INVALID_INPUT, "mamba_block: a required pointer is NULL");
+    const size_t need = hx_mamba_block_workspace_size(batch, seqlen, d_inner, dt_rank, dstate);
+    HX_REQUIRE(workspace_bytes >= need, HX_ERR_INVALID_INPUT,
+               "mamba_block: workspace %zu bytes < %zu required", workspace_bytes, need);
+    const int64_t M = batch * seqlen;
+    char* p = (char*)workspace;
+    auto take = [&](size_t bytes) { void* r = p; p += align256(bytes); return r; };
+    void* xpart = take(M * d_inner * 2);
+    void* zbuf = take(M * d_inner * 2);
+    void* xconv = take(M * d_inner * 2);
+    void* dtb = take(M * d_inner * 2);
+    void* ybuf = take(M * d_inner * 2);
+    void* dtlo = take(M * dt_rank * 2);
+    void* Bb = take(M * dstate * 2);
+    void* Cb = take(M * dstate * 2);
+    int rc;
+    // in_proj: [M, d_model] x [2*d_inner, d_model]^T -> xpart | z
+    if ((rc = hx_gemm_bf16(M, 2 * d_inner, d_model, x, d_model, w_in, d_model, nullptr, 0, HX_BF16,
+                           xpart, d_inner, d_inner, zbuf, d_inner, 2 * d_inner, nullptr, 0, stream)))
+        return rc;
+    if ((rc = hx_conv1d_silu(batch, seqlen, d_inner, d_conv, HX_BF16, xpart, d_inner, conv_w,
+                             conv_b, xconv, stream)))
+        return rc;
+    // x_proj: [M, d_inner] x [dt_rank + 2N, d_inner]^T -> dt_lo | B | C
+    if ((rc = hx_gemm_bf16(M, dt_rank + 2 * dstate, d_inner, xconv, d_inner, w_x, d_inner, nullptr,
+                           0, HX_BF16, dtlo, dt_rank, dt_rank, Bb, dstate, dt_rank + dstate, Cb,
+                           dstate, stream)))
+        return rc;
+    // dt_proj: [M, dt_rank] x [d_inner, dt_rank]^T -> dt (dt_bias is added inside the scan)
+    if ((rc = hx_gemm_bf16(M, d_inner, dt_rank, dtlo, dt_rank, w_dt, dt_rank, nullptr, 0, HX_BF16,
+                           dtb, d_inner, d_inner, nullptr, 0, d_inner, nullptr, 0, stream)))
+        return rc;
+    if ((rc = hx_selective_scan_fwd(batch, seqlen, d_inner, dstate, HX_BF16, 1, xconv, dtb, A, Bb,
+                                    Cb, D, zbuf, dt_bias, ybuf, nullptr, nullptr, stream)))
+        return rc;
+    // out_proj: [M, d_inner] x [d_model, d_inner]^T -> out
+    return hx_gemm_bf16(M, d_model, d_inner, ybuf, d_inner, w_out, d_inner, nullptr, 0, HX_BF16, out,
+                        d_model, d_model, nullptr, 0, d_model, nullptr, 0, stream);
+}

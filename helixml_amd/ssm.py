@@ -168,6 +168,33 @@ def matmul(A, B, stream=None):
     return Y
 
 
+def gemm_bf16(X, W, bias=None, act=0, out_dtype=torch.bfloat16, splits=None, stream=None):
+    """Matrix-core GEMM Y = X . W^T (+ bias)(, SiLU) (hx_gemm_bf16). X [M, K], W [N, K] bf16
+    (row-major; X may be a row-strided view). splits=(s1[, s2]) returns the column blocks
+    [0, s1), [s1, s2), [s2, N) as separate contiguous tensors."""
+    M, K = X.shape
+    N = W.shape[0]
+    if W.shape[1] != K:
+        raise ShapeMismatch(f"expected {[K]}, got {[W.shape[1]]}")
+    if X.dtype != torch.bfloat16 or W.dtype != torch.bfloat16:
+        raise DTypeMismatch("gemm_bf16: X and W must be bfloat16")
+    if X.stride(1) != 1 or W.stride(1) != 1:
+        raise InvalidInput("gemm_bf16: X and W need unit column stride")
+    _need(bias, "bias", (N,), torch.float32)
+    cuts = [0] + list(splits or []) + [N]
+    outs = [torch.empty((M, cuts[i + 1] - cuts[i]), device=X.device, dtype=out_dtype)
+            for i in range(len(cuts) - 1)]
+    ys = outs + [None] * (3 - len(outs))
+    s1 = cuts[1] if len(cuts) > 2 else N
+    s2 = cuts[2] if len(cuts) > 3 else N
+    od = _STORAGE[out_dtype]
+    _ffi.call("hx_gemm_bf16", M, N, K, _ptr(X), X.stride(0), _ptr(W), W.stride(0), _ptr(bias),
+              int(act), od, _ptr(ys[0]), ys[0].shape[1], s1,
+              _ptr(ys[1]), ys[1].shape[1] if ys[1] is not None else 0, s2,
+              _ptr(ys[2]), ys[2].shape[1] if ys[2] is not None else 0, _stream(stream))
+    return outs[0] if len(outs) == 1 else tuple(outs)
+
+
 def set_scan_variant(v: int) -> None:
     _ffi.call("hx_set_scan_variant", int(v))
 

@@ -136,6 +136,42 @@ int hx_linear_f32(int64_t rows, int64_t in_features, int64_t out_features,
                   const float* X, const float* W, const float* bias, int act,
                   float* Y, void* stream);
 
+/* bf16 matrix-core GEMM for the Mamba block's projections: Y = X . W^T (+ bias)(, SiLU), the
+ * nn::Linear layout (crates/nn/src/lib.rs:120-134, weight [out, in]). X [M, K] (row stride ldx),
+ * W [N, K] (row stride ldw), bf16, 16-byte aligned rows; fp32 accumulate; out_dtype HX_F32 or
+ * HX_BF16. Columns [0, split1) go to Y0 (row stride ld0), [split1, split2) to Y1, [split2, N) to
+ * Y2 (split1 = split2 = N for a single output). act: 0 none, 1 SiLU. */
+int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
+                 const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
+                 void* Y0, int64_t ld0, int64_t split1, void* Y1, int64_t ld1,
+                 int64_t split2, void* Y2, int64_t ld2, void* stream);
+
+/* Causal depthwise conv1d over time + bias + SiLU (the Mamba block's conv, kernel `width` <= 4):
+ * y[b,t,d] = silu(bias[d] + sum_j weight[d,j] * x[b, t-width+1+j, d]) with zero padding.
+ * x: [batch, seqlen, dim] with row stride ldx (so it can be the x half of in_proj's output);
+ * y contiguous; dtype HX_F32 or HX_BF16 storage; weight [dim, width], bias [dim] fp32. */
+int hx_conv1d_silu(int64_t batch, int64_t seqlen, int64_t dim, int64_t width, int dtype,
+                   const void* x, int64_t ldx, const float* weight, const float* bias, void* y,
+                   void* stream);
+
+/* Full Mamba block forward, bf16 storage / fp32 arithmetic:
+ *   x|z = x . w_in^T; xc = SiLU(conv1d(x)); dt_lo|B|C = xc . w_x^T; dt = dt_lo . w_dt^T;
+ *   y = selective_scan(xc, dt, A, B, C, D, z, dt_bias, softplus); out = y . w_out^T.
+ * The block the reference's exported MambaBlock allocates parameters for
+ * (crates/nn/src/lib.rs:846-885) but whose forward is only Linear -> SiLU -> Linear (lib.rs:888-906).
+ * x, out [batch, seqlen, d_model] bf16; w_in [2*d_inner, d_model], w_x [dt_rank + 2*dstate,
+ * d_inner], w_dt [d_inner, dt_rank], w_out [d_model, d_inner] bf16; conv_w [d_inner, d_conv],
+ * conv_b, dt_bias, D [d_inner], A [d_inner, dstate] fp32. workspace: device memory of at least
+ * hx_mamba_block_workspace_size(...) bytes, owned by the caller. */
+size_t hx_mamba_block_workspace_size(int64_t batch, int64_t seqlen, int64_t d_inner,
+                                     int64_t dt_rank, int64_t dstate);
+int hx_mamba_block_fwd(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner,
+                       int64_t dstate, int64_t dt_rank, int64_t d_conv,
+                       const void* x, const void* w_in, const float* conv_w, const float* conv_b,
+                       const void* w_x, const void* w_dt, const float* dt_bias, const float* A,
+                       const float* D, const void* w_out, void* out, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* CpuTensor::matmul 2-D x 2-D (crates/backend-cpu/src/lib.rs:644-678): Y = A[M,K] . B[K,N]. */
 int hx_matmul_f32(int64_t M, int64_t K, int64_t N, const float* A, const float* B, float* Y,
                   void* stream);
