@@ -7,7 +7,10 @@ d_state 16, fp32, inputs resident in HBM, 3 rotating input sets (1.2 GB) so the 
 cannot serve a step from the previous one. A "step" is one hx_selective_scan_fwd call over one
 batch. Prints ONE JSON line.
 
-  python bench.py [--steps K] [--warmup W] [--workload c2|c4|c4s4|c4s4d|c3scan] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c2|c2bf16|c3|c4|copy] [--no-cpu]
+
+c3 = BASELINE config 3, the full Mamba block (in_proj, conv1d+SiLU, x_proj, dt_proj, fused scan,
+out_proj) at batch 4 x L 4096 x d_model 2048, bf16 storage; reported separately from the metric.
 """
 from __future__ import annotations
 
@@ -87,12 +90,94 @@ def cpu_baseline_scan(x_dev, sample_batches):
                 omp=dict(value=toks / (t3 - t2), threads=threads, seconds=round(t3 - t2, 3))), out1
 
 
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+
+
+def bench_block(args, dev):
+    """full Mamba block forward, bf16 storage / fp32 arithmetic. The step is one
+    hx_mamba_block_fwd call; a per-stage breakdown times each kernel on its own (same operands)."""
+    bt, L, dm, di, N, r, k = 4, 4096, 2048, 4096, 16, 128, 4
+    M = bt * L
+    gen = torch.Generator().manual_seed(0x48454C49)
+    bf = torch.bfloat16
+
+    def nrm(shape, fan):
+        return (torch.randn(shape, generator=gen) * (2.0 / fan) ** 0.5).to(dev, bf)
+
+    dt0 = torch.exp(torch.rand(di, generator=gen) * (np.log(0.1) - np.log(1e-3)) + np.log(1e-3))
+    prm = dict(w_in=nrm((2 * di, dm), dm),
+               conv_w=((torch.rand((di, k), generator=gen) * 2 - 1) / k ** 0.5).to(dev),
+               conv_b=((torch.rand(di, generator=gen) * 2 - 1) / k ** 0.5).to(dev),
+               w_x=nrm((r + 2 * N, di), di), w_dt=nrm((di, r), r),
+               dt_bias=(dt0 + torch.log(-torch.expm1(-dt0))).to(dev),
+               A=(-torch.arange(1, N + 1, dtype=torch.float32)).repeat(di, 1).to(dev),
+               D=torch.randn(di, generator=gen).to(dev), w_out=nrm((dm, di), di))
+    nsets = 2
+    xs = [torch.randn((bt, L, dm), generator=gen).to(dev, bf) for _ in range(nsets)]
+    outs = [torch.empty_like(x) for x in xs]
+    ws = torch.empty(ssm.mamba_block_workspace_size(bt, L, di, r, N), device=dev, dtype=torch.uint8)
+
+    def step(i):
+        ssm.mamba_block_fwd(xs[i], **prm, workspace=ws, out=outs[i])
+
+    ms = time_steps(step, nsets, args.steps, args.warmup)
+    flops = {"in_proj": 2 * M * 2 * di * dm, "x_proj": 2 * M * (r + 2 * N) * di,
+             "dt_proj": 2 * M * di * r, "out_proj": 2 * M * dm * di}
+    # per-stage breakdown on the block's own intermediates
+    x2 = xs[0].view(M, dm)
+    xz = ssm.gemm_bf16(x2, prm["w_in"], splits=(di,))
+    xc = ssm.conv1d_silu(xz[0].view(bt, L, di), prm["conv_w"], prm["conv_b"])
+    dbc = ssm.gemm_bf16(xc.view(M, di), prm["w_x"], splits=(r, r + N))
+    dt = ssm.gemm_bf16(dbc[0], prm["w_dt"])
+    Bm, Cm = dbc[1].view(bt, L, N), dbc[2].view(bt, L, N)
+    y = torch.empty((bt, L, di), device=dev, dtype=bf)
+    stages = {
+        "in_proj": lambda i: ssm.gemm_bf16(x2, prm["w_in"], splits=(di,)),
+        "conv1d_silu": lambda i: ssm.conv1d_silu(xz[0].view(bt, L, di), prm["conv_w"], prm["conv_b"], out=xc),
+        "x_proj": lambda i: ssm.gemm_bf16(xc.view(M, di), prm["w_x"], splits=(r, r + N)),
+        "dt_proj": lambda i: ssm.gemm_bf16(dbc[0], prm["w_dt"]),
+        "scan": lambda i: ssm.selective_scan_fwd(xc, dt.view(bt, L, di), prm["A"], Bm, Cm, prm["D"],
+                                                 xz[1].view(bt, L, di), prm["dt_bias"], out=y),
+        "out_proj": lambda i: ssm.gemm_bf16(y.view(M, di), prm["w_out"]),
+    }
+    breakdown = {}
+    for name, fn in stages.items():
+        sms = time_steps(fn, 1, max(args.steps // 2, 3), 2)
+        e = {"ms": sms}
+        if name in flops:
+            e["tflops"] = flops[name] / (sms * 1e-3) / 1e12
+        breakdown[name] = e
+    scan_bytes_ = scan_bytes(bt, L, di, N, 2)
+    breakdown["scan"]["hbm_gbs"] = scan_bytes_ / (breakdown["scan"]["ms"] * 1e-3) / 1e9
+    breakdown["conv1d_silu"]["hbm_gbs"] = 2 * M * di * 2 / (breakdown["conv1d_silu"]["ms"] * 1e-3) / 1e9
+    total_flops = sum(flops.values())
+    gemm_ms = sum(breakdown[n]["ms"] for n in flops)
+    rec = {
+        "metric": "Mamba block fwd tokens/s (config 3), 1 GPU",
+        "value": M * 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16-storage/fp32-compute",
+        "data": "synthetic (config-3 distributions, random-init weights, seeded)",
+        "config": {"workload": "mamba_block_fwd config3 (batch 4, L 4096, d_model 2048, d_inner 4096, "
+                               "d_state 16, dt_rank 128, conv 4)", "batch": bt, "seq_len": L,
+                   "d_model": dm, "d_inner": di, "d_state": N, "dt_rank": r, "d_conv": k},
+        "block_tflops": total_flops / (ms * 1e-3) / 1e12,
+        "roofline": {"bound": "mfma", "achieved": total_flops / (gemm_ms * 1e-3) / 1e12,
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": total_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                     "traffic": None, "algorithmic_flops": total_flops, "kernel_ms": gemm_ms},
+        "breakdown": breakdown,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(rec))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c2", choices=["c2", "c2bf16", "c4", "copy"],
+    ap.add_argument("--workload", default="c2", choices=["c2", "c2bf16", "c4", "c3", "copy"],
                     help="copy = plain device copy of 512 MiB (HBM ceiling and counter calibration)")
     ap.add_argument("--variant", type=int, default=0, help="scan kernel variant (hx_set_scan_variant)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -120,6 +205,9 @@ def main():
                           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
                           "higher_is_better": True, "bytes_per_step": 2 * n * 4,
                           "frac_of_8TBs": gbs / PEAK_HBM_GBS}))
+        return
+    if args.workload == "c3":
+        bench_block(args, dev)
         return
     if args.workload in ("c2", "c2bf16"):
         bt, L, dim, N = 8, 2048, 1536, 16
@@ -160,7 +248,7 @@ def main():
     tfile = os.path.join(ROOT, "profiles", "traffic.json")
     if args.workload == "c2" and args.variant == 0 and os.path.exists(tfile):
         # measured HBM bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)
-        rec_t = json.load(open(tfile)).get("scan_tile_kernel<float, 4, 16, 2, true, true>@config2")
+        rec_t = json.load(open(tfile)).get("scan_wave_kernel<float, 2, true, true, false>@config2")
         traffic = rec_t["traffic_bytes"] if rec_t else None
 
     rec = {

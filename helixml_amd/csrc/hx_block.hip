@@ -116,8 +116,8 @@ extern "C" int hx_mamba_block_fwd(int64_t batch, int64_t seqlen, int64_t d_model
                HX_ERR_INVALID_DIMENSION, "mamba_block: bad sizes");
     HX_REQUIRE(dstate == 16, HX_ERR_UNSUPPORTED, "mamba_block: dstate %lld (16 supported)",
                (long long)dstate);
-    HX_REQUIRE(d_model % 8 == 0 && d_inner % 8 == 0 && dt_rank % 8 == 0, HX_ERR_UNSUPPORTED,
-               "mamba_block: d_model, d_inner and dt_rank must be multiples of 8");
+    HX_REQUIRE(d_inner % 4 == 0, HX_ERR_UNSUPPORTED, "mamba_block: d_inner %lld not a multiple of 4",
+               (long long)d_inner);
     if (batch == 0 || seqlen == 0) return HX_OK;
     HX_REQUIRE(x && w_in && conv_w && w_x && w_dt && A && w_out && out && workspace,
                HX_ERR_INVALID_INPUT, "mamba_block: a required pointer is NULL");

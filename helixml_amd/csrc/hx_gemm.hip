@@ -2,6 +2,7 @@
 //
 // Y = X . W^T (+ bias), the nn::Linear layout (crates/nn/src/lib.rs:120-134: weight [out, in]):
 // X [M, K] and W [N, K] both K-contiguous bf16, fp32 accumulate, bf16 or fp32 output.
+// Rows whose start is not 16-byte aligned take an element-load variant of the same kernel.
 // Block tile 128 x 128 x 32, 4 waves in a 2 x 2 grid, each wave 64 x 64 = 2 x 2 tiles of
 // v_mfma_f32_32x32x16_bf16. Tiles are staged through LDS (double-buffered, rows padded by 16
 // bytes so the 16-byte fragment reads of 8 consecutive rows cover all 32 banks); global loads
@@ -27,9 +28,12 @@ struct GemmOut {
     int act;                 // 0 none, 1 SiLU
 };
 
+// 8 consecutive bf16 of row `row` from column `col`, zero outside [nrows, ncols). VEC: the row
+// start is 16-byte aligned (ld % 8 == 0, aligned base), so an in-bounds piece is one 16-byte load.
+template <bool VEC>
 __device__ inline uint4 load16_guard(const uint16_t* base, int64_t row, int64_t nrows, int64_t col,
                                      int64_t ncols, int64_t ld) {
-    if (row < nrows && col + 8 <= ncols) return *reinterpret_cast<const uint4*>(base + row * ld + col);
+    if (VEC && row < nrows && col + 8 <= ncols) return *reinterpret_cast<const uint4*>(base + row * ld + col);
     if (row >= nrows || col >= ncols) return make_uint4(0, 0, 0, 0);
     uint16_t v[8];
 #pragma unroll
@@ -37,6 +41,7 @@ __device__ inline uint4 load16_guard(const uint16_t* base, int64_t row, int64_t 
     return make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16));
 }
 
+template <bool VEC>
 __global__ __launch_bounds__(256) void gemm_bf16_nt_kernel(int64_t M, int64_t N, int64_t K,
                                                            const uint16_t* __restrict__ X,
                                                            int64_t ldx,
@@ -60,8 +65,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_kernel(int64_t M, int64_t N,
         for (int j = 0; j < 2; ++j) {
             const int e = tid + j * 256;
             const int row = e >> 2, kc = (e & 3) * 8;
-            ra[j] = load16_guard(X, m0 + row, M, k0 + kc, K, ldx);
-            rb[j] = load16_guard(W, n0 + row, N, k0 + kc, K, ldw);
+            ra[j] = load16_guard<VEC>(X, m0 + row, M, k0 + kc, K, ldx);
+            rb[j] = load16_guard<VEC>(W, n0 + row, N, k0 + kc, K, ldw);
         }
     };
     auto sstore = [&](int buf) __attribute__((always_inline)) {
@@ -156,8 +161,7 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     HX_REQUIRE(X && W && Y0, HX_ERR_INVALID_INPUT, "gemm_bf16: X, W and Y0 must be non-NULL");
     HX_REQUIRE(ldx >= K && ldw >= K && ld0 >= 0, HX_ERR_INVALID_DIMENSION,
                "gemm_bf16: leading dimensions smaller than K");
-    HX_REQUIRE(ldx % 8 == 0 && ldw % 8 == 0 && aligned(X, 16) && aligned(W, 16), HX_ERR_UNSUPPORTED,
-               "gemm_bf16: X and W need 16-byte aligned rows (ld %% 8 == 0)");
+    const bool vec = ldx % 8 == 0 && ldw % 8 == 0 && aligned(X, 16) && aligned(W, 16);
     if (split1 <= 0 || split1 > N) split1 = N;
     if (split2 < split1 || split2 > N) split2 = N;
     HX_REQUIRE(split1 == N || Y1, HX_ERR_INVALID_INPUT, "gemm_bf16: Y1 is NULL but split1 < N");
@@ -166,8 +170,12 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
                "gemm_bf16: M=%lld too large for the grid", (long long)M);
     GemmOut o{{Y0, Y1, Y2}, {ld0, ld1, ld2}, split1, split2, out_dtype == HX_BF16, act};
     dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-    hipLaunchKernelGGL(gemm_bf16_nt_kernel, grid, dim3(256), 0, as_stream(stream), M, N, K,
-                       (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
+    if (vec)
+        hipLaunchKernelGGL(gemm_bf16_nt_kernel<true>, grid, dim3(256), 0, as_stream(stream), M, N, K,
+                           (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
+    else  // rows not 16-byte aligned: element loads (odd K such as a small dt_rank)
+        hipLaunchKernelGGL(gemm_bf16_nt_kernel<false>, grid, dim3(256), 0, as_stream(stream), M, N, K,
+                           (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
     HX_LAUNCH_CHECK();
     return HX_OK;
 }

@@ -201,3 +201,108 @@ def set_scan_variant(v: int) -> None:
 
 def set_scan_segments(n: int) -> None:
     _ffi.call("hx_set_scan_segments", int(n))
+
+
+def conv1d_silu(x, weight, bias=None, out=None, stream=None):
+    """Causal depthwise conv1d + bias + SiLU (hx_conv1d_silu). x [batch, L, dim] (rows may be
+    strided, e.g. the x half of in_proj's output), weight [dim, width] fp32, bias [dim] fp32."""
+    bt, L, dim = x.shape
+    if x.dtype not in _STORAGE:
+        raise DTypeMismatch(f"x: storage dtype {x.dtype} is neither float32 nor bfloat16")
+    if x.stride(2) != 1 or x.stride(0) != L * x.stride(1):
+        raise InvalidInput("conv1d_silu: x needs unit channel stride and uniform row stride")
+    _need(weight, "weight", (dim, weight.shape[1]), torch.float32)
+    _need(bias, "bias", (dim,), torch.float32)
+    if out is None:
+        out = torch.empty((bt, L, dim), device=x.device, dtype=x.dtype)
+    _need(out, "out", (bt, L, dim), x.dtype)
+    _ffi.call("hx_conv1d_silu", bt, L, dim, weight.shape[1], _STORAGE[x.dtype], _ptr(x),
+              x.stride(1), _ptr(weight), _ptr(bias), _ptr(out), _stream(stream))
+    return out
+
+
+def mamba_block_workspace_size(batch, seqlen, d_inner, dt_rank, dstate) -> int:
+    return int(_ffi.lib().hx_mamba_block_workspace_size(batch, seqlen, d_inner, dt_rank, dstate))
+
+
+def mamba_block_fwd(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, workspace=None,
+                    out=None, stream=None):
+    """Full Mamba block forward (hx_mamba_block_fwd), bf16 storage. x [batch, L, d_model];
+    w_in [2*d_inner, d_model], w_x [dt_rank + 2*dstate, d_inner], w_dt [d_inner, dt_rank],
+    w_out [d_model, d_inner] bf16; conv_w [d_inner, d_conv], conv_b, dt_bias, D [d_inner],
+    A [d_inner, dstate] fp32. ``workspace``: a uint8 device tensor of at least
+    mamba_block_workspace_size(...) bytes (allocated here if None)."""
+    bt, L, dm = x.shape
+    di, dt_rank = w_dt.shape
+    N = A.shape[1]
+    bf = torch.bfloat16
+    _need(x, "x", (bt, L, dm), bf)
+    _need(w_in, "w_in", (2 * di, dm), bf)
+    _need(conv_w, "conv_w", (di, conv_w.shape[1]), torch.float32)
+    _need(conv_b, "conv_b", (di,), torch.float32)
+    _need(w_x, "w_x", (dt_rank + 2 * N, di), bf)
+    _need(w_dt, "w_dt", (di, dt_rank), bf)
+    _need(dt_bias, "dt_bias", (di,), torch.float32)
+    _need(A, "A", (di, N), torch.float32)
+    _need(D, "D", (di,), torch.float32)
+    _need(w_out, "w_out", (dm, di), bf)
+    ws_bytes = mamba_block_workspace_size(bt, L, di, dt_rank, N)
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+    if out is None:
+        out = torch.empty((bt, L, dm), device=x.device, dtype=bf)
+    _need(out, "out", (bt, L, dm), bf)
+    _ffi.call("hx_mamba_block_fwd", bt, L, dm, di, N, dt_rank, conv_w.shape[1], _ptr(x), _ptr(w_in),
+              _ptr(conv_w), _ptr(conv_b), _ptr(w_x), _ptr(w_dt), _ptr(dt_bias), _ptr(A), _ptr(D),
+              _ptr(w_out), _ptr(out), _ptr(workspace), workspace.numel() * workspace.element_size(),
+              _stream(stream))
+    return out
+
+
+class MambaBlock:
+    """Device-resident Mamba block with the reference constructor's arguments
+    (``MambaBlock::new(d_model, d_state, d_conv, expand)``, crates/nn/src/lib.rs:847) and the
+    parameters that constructor names (A, D, delta/B/C projections, in ("gate") and out
+    projections) laid out for the fused path: w_in = in_proj, w_x = x_proj (dt_lo | B | C rows),
+    w_dt = dt_proj, dt_rank = ceil(d_model / 16). ``forward`` is hx_mamba_block_fwd; the
+    workspace is kept between calls and regrown when a larger input arrives."""
+
+    def __init__(self, d_model, d_state=16, d_conv=4, expand=2, dt_rank=None, device="cuda",
+                 generator=None):
+        self.d_model, self.d_state, self.d_conv, self.expand = d_model, d_state, d_conv, expand
+        self.d_inner = d_model * expand
+        self.dt_rank = dt_rank or -(-d_model // 16)
+        di, r, N = self.d_inner, self.dt_rank, d_state
+        g = generator
+        f32, bf = torch.float32, torch.bfloat16
+
+        def normal(shape, std):
+            return (torch.randn(shape, generator=g) * std)
+
+        self.w_in = normal((2 * di, d_model), (2.0 / d_model) ** 0.5).to(device, bf)
+        self.conv_w = ((torch.rand((di, d_conv), generator=g) * 2 - 1) / d_conv ** 0.5).to(device, f32)
+        self.conv_b = ((torch.rand(di, generator=g) * 2 - 1) / d_conv ** 0.5).to(device, f32)
+        self.w_x = normal((r + 2 * N, di), (2.0 / di) ** 0.5).to(device, bf)
+        self.w_dt = normal((di, r), r ** -0.5).to(device, bf)
+        # dt = softplus(dt_proj + dt_bias) starts log-uniform in [1e-3, 1e-1]
+        dt0 = torch.exp(torch.rand(di, generator=g) * (torch.log(torch.tensor(0.1)) -
+                                                          torch.log(torch.tensor(1e-3)))
+                        + torch.log(torch.tensor(1e-3)))
+        self.dt_bias = (dt0 + torch.log(-torch.expm1(-dt0))).to(device, f32)
+        self.A = (-torch.arange(1, N + 1, dtype=f32)).repeat(di, 1).to(device)
+        self.D = torch.ones(di, dtype=f32).to(device)
+        self.w_out = normal((d_model, di), (2.0 / di) ** 0.5).to(device, bf)
+        self._ws = None
+
+    def parameters(self):
+        return dict(w_in=self.w_in, conv_w=self.conv_w, conv_b=self.conv_b, w_x=self.w_x,
+                    w_dt=self.w_dt, dt_bias=self.dt_bias, A=self.A, D=self.D, w_out=self.w_out)
+
+    def forward(self, x, out=None, stream=None):
+        bt, L, _ = x.shape
+        need = mamba_block_workspace_size(bt, L, self.d_inner, self.dt_rank, self.d_state)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, device=x.device, dtype=torch.uint8)
+        return mamba_block_fwd(x, workspace=self._ws, out=out, stream=stream, **self.parameters())
+
+    __call__ = forward

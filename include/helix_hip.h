@@ -138,7 +138,8 @@ int hx_linear_f32(int64_t rows, int64_t in_features, int64_t out_features,
 
 /* bf16 matrix-core GEMM for the Mamba block's projections: Y = X . W^T (+ bias)(, SiLU), the
  * nn::Linear layout (crates/nn/src/lib.rs:120-134, weight [out, in]). X [M, K] (row stride ldx),
- * W [N, K] (row stride ldw), bf16, 16-byte aligned rows; fp32 accumulate; out_dtype HX_F32 or
+ * W [N, K] (row stride ldw), bf16 (16-byte aligned rows take the fast 16-byte-load path, any
+ * other stride an element-load path); fp32 accumulate; out_dtype HX_F32 or
  * HX_BF16. Columns [0, split1) go to Y0 (row stride ld0), [split1, split2) to Y1, [split2, N) to
  * Y2 (split1 = split2 = N for a single output). act: 0 none, 1 SiLU. */
 int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
@@ -161,7 +162,8 @@ int hx_conv1d_silu(int64_t batch, int64_t seqlen, int64_t dim, int64_t width, in
  * (crates/nn/src/lib.rs:846-885) but whose forward is only Linear -> SiLU -> Linear (lib.rs:888-906).
  * x, out [batch, seqlen, d_model] bf16; w_in [2*d_inner, d_model], w_x [dt_rank + 2*dstate,
  * d_inner], w_dt [d_inner, dt_rank], w_out [d_model, d_inner] bf16; conv_w [d_inner, d_conv],
- * conv_b, dt_bias, D [d_inner], A [d_inner, dstate] fp32. workspace: device memory of at least
+ * conv_b, dt_bias, D [d_inner], A [d_inner, dstate] fp32. dstate 16, d_inner % 4 == 0, d_conv
+ * 1..4. workspace: device memory of at least
  * hx_mamba_block_workspace_size(...) bytes, owned by the caller. */
 size_t hx_mamba_block_workspace_size(int64_t batch, int64_t seqlen, int64_t d_inner,
                                      int64_t dt_rank, int64_t dstate);

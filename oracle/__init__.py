@@ -20,6 +20,11 @@ Pinning status of each function (how tests/test_oracle.py pins it):
   selective_scan(_f64)  B=0/C=0 -> D*u*silu(z); A=0 -> prefix sum; N=1 constant inputs ->
                         geometric series; split-sequence == whole (state hand-off);
                         decode steps == prefill; f32 vs f64; numpy float64
+  conv1d_silu           width 1 == silu(w*x+b); unit impulse -> time-reversed taps; causality
+                        (future inputs change nothing); numpy float64 np.convolve per channel
+  mamba_block           composition of linear + conv1d_silu + selective_scan (each pinned),
+                        bf16 rounding at the storage points; cross-checked against
+                        numpy_mamba_block (float64, same storage rounding)
   s4d_complex           impulse response 2*Re(sum C Abar^t Bbar), constant-input steady state
 """
 from __future__ import annotations
@@ -68,6 +73,7 @@ def lib() -> ctypes.CDLL:
             "oracle_s4d_complex": [_i64, _i64, _i64, _i64] + [_p] * 10,
             "oracle_selective_scan_omp": [_i64, _i64, _i64, _i64, _int] + [_p] * 9 + [_int],
             "oracle_max_threads": [],
+            "oracle_conv1d_silu": [_i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -213,6 +219,49 @@ def s4d_complex(x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D=None):
     return y
 
 
+def conv1d_silu(x, w, bias=None):
+    """x [Bt, L, Dd] (any row stride), w [Dd, W], bias [Dd] -> y [Bt, L, Dd] float32."""
+    x = np.asarray(x, np.float32)
+    Bt, L, Dd = x.shape
+    xs = np.ascontiguousarray(x)
+    w, bias = _f32(w), _f32(bias)
+    y = np.empty((Bt, L, Dd), np.float32)
+    lib().oracle_conv1d_silu(Bt, L, Dd, w.shape[1], _ptr(xs), Dd, _ptr(w), _ptr(bias), _ptr(y))
+    return y
+
+
+def bf16_round(a):
+    """Round-to-nearest-even to bfloat16, returned as float32 (the GPU path's storage format)."""
+    a = np.ascontiguousarray(a, np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(a), a, out)
+
+
+def mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, dt_rank, bf16=True):
+    """Mamba block forward: x [Bt, L, d_model] -> [Bt, L, d_model].
+    in_proj -> (x | z); SiLU(conv1d(x)); x_proj -> (dt_lo | B | C); dt = dt_lo . w_dt^T;
+    selective_scan(softplus(dt + dt_bias)); out_proj. Every intermediate the GPU stores in bf16 is
+    rounded to bf16 here too (``bf16=True``); arithmetic is f32."""
+    rnd = bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
+    Bt, L, dm = x.shape
+    di = w_dt.shape[0]
+    N = A.shape[1]
+    X = rnd(x).reshape(Bt * L, dm)
+    xz = linear(X, rnd(w_in))
+    xp = rnd(xz[:, :di]).reshape(Bt, L, di)
+    z = rnd(xz[:, di:]).reshape(Bt, L, di)
+    xc = rnd(conv1d_silu(xp, conv_w, conv_b))
+    dbc = linear(xc.reshape(Bt * L, di), rnd(w_x))
+    dtlo = rnd(dbc[:, :dt_rank])
+    Bm = rnd(dbc[:, dt_rank:dt_rank + N]).reshape(Bt, L, N)
+    Cm = rnd(dbc[:, dt_rank + N:]).reshape(Bt, L, N)
+    dt = rnd(linear(dtlo, rnd(w_dt))).reshape(Bt, L, di)
+    y = rnd(selective_scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True))
+    return rnd(linear(y.reshape(Bt * L, di), rnd(w_out))).reshape(Bt, L, dm)
+
+
 # ------------------------------------------------------------------ independent float64 restatements
 
 def numpy_selective_scan(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_softplus=True,
@@ -260,3 +309,36 @@ def numpy_s4_ref(x, a_real, a_imag, B, C, D, gate=None, dt=0.1):
     if gate is not None:
         y = y * np.asarray(gate, np.float64)[None, :]
     return y
+
+
+def numpy_conv1d_silu(x, w, bias=None):
+    """float64: per-channel full np.convolve with the reversed taps, first L outputs."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    Bt, L, Dd = x.shape
+    y = np.empty((Bt, L, Dd))
+    for b in range(Bt):
+        for d in range(Dd):
+            # causal: y[t] = sum_j w[j] x[t-W+1+j] == (x * w[::-1])[t] of the full convolution
+            y[b, :, d] = np.convolve(x[b, :, d], w[d, ::-1])[:L]
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)[None, None, :]
+    return y / (1.0 + np.exp(-y))
+
+
+def numpy_mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, dt_rank):
+    """float64 block with the same bf16 storage rounding points as ``mamba_block``."""
+    r = lambda a: bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
+    Bt, L, dm = x.shape
+    di = w_dt.shape[0]
+    N = A.shape[1]
+    xz = r(x).reshape(-1, dm) @ r(w_in).T
+    xp, z = r(xz[:, :di]).reshape(Bt, L, di), r(xz[:, di:]).reshape(Bt, L, di)
+    xc = r(numpy_conv1d_silu(xp, conv_w, conv_b))
+    dbc = xc.reshape(-1, di) @ r(w_x).T
+    dtlo = r(dbc[:, :dt_rank])
+    Bm = r(dbc[:, dt_rank:dt_rank + N]).reshape(Bt, L, N)
+    Cm = r(dbc[:, dt_rank + N:]).reshape(Bt, L, N)
+    dt = r(dtlo @ r(w_dt).T).reshape(Bt, L, di)
+    y, _ = numpy_selective_scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True)
+    return r(r(y).reshape(-1, di) @ r(w_out).T).reshape(Bt, L, dm)

@@ -267,3 +267,24 @@ void oracle_s4d_complex(int64_t Bt, int64_t L, int64_t Dd, int64_t N, const floa
             }
         }
 }
+
+/* ---------------------------------------------------------------- Mamba block pieces */
+
+/* Causal depthwise conv1d over time + bias + SiLU, the block's short convolution (Gu & Dao 2023,
+ * Fig. 3; the reference allocates d_conv but never convolves, nn/src/lib.rs:847-885).
+ * y[b,t,d] = silu(bias[d] + sum_{j<W} w[d,j] * x[b, t-W+1+j, d]), zero for t-W+1+j < 0;
+ * j ascending, f32. x row stride ldx (elements), y contiguous [Bt, L, Dd]. */
+void oracle_conv1d_silu(int64_t Bt, int64_t L, int64_t Dd, int64_t W, const float* x, int64_t ldx,
+                        const float* w, const float* bias, float* y) {
+    for (int64_t b = 0; b < Bt; ++b)
+        for (int64_t t = 0; t < L; ++t)
+            for (int64_t d = 0; d < Dd; ++d) {
+                float acc = bias ? bias[d] : 0.0f;
+                for (int64_t j = 0; j < W; ++j) {
+                    int64_t tt = t - (W - 1) + j;
+                    if (tt < 0) continue;
+                    acc += w[d * W + j] * x[(b * L + tt) * ldx + d];
+                }
+                y[(b * L + t) * Dd + d] = silu_ref(acc);
+            }
+}

@@ -47,3 +47,14 @@ def test_gemm_bf16_out_splits_and_strided_input(dev):
     got = np.concatenate([a.float().cpu().numpy(), b.float().cpu().numpy(), c.float().cpu().numpy()], 1)
     assert a.shape == (M, 128) and b.shape == (M, 16) and c.shape == (M, 16)
     assert rel_err(got, r) <= 2 ** -8  # one bf16 rounding of the output
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 40, 4), (130, 70, 13), (33, 256, 36)])
+def test_gemm_unaligned_rows(dev, M, N, K):
+    # K not a multiple of 8: rows are not 16-byte aligned, the element-load variant runs
+    g = torch.Generator().manual_seed(K)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    W = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)
+    y = ssm.gemm_bf16(X, W, out_dtype=torch.float32)
+    err = norm_err(y.cpu().numpy(), ref(X, W))
+    assert err <= 1e-5, err

@@ -309,6 +309,63 @@ def test_s4d_constant_input_steady_state():
 
 # ------------------------------------------------------------------ planted mistakes (the checks bite)
 
+# ------------------------------------------------------------------ Mamba block pieces
+
+def test_conv1d_width1_closed_form():
+    rng = np.random.default_rng(30)
+    x = rng.standard_normal((2, 7, 5)).astype(F)
+    w = rng.standard_normal((5, 1)).astype(F)
+    b = rng.standard_normal(5).astype(F)
+    pre = x.astype(np.float64) * w[:, 0] + b
+    assert rel_err(oracle.conv1d_silu(x, w, b), pre / (1 + np.exp(-pre))) < 1e-6
+
+
+def test_conv1d_impulse_gives_reversed_taps_and_is_causal():
+    W, L = 4, 9
+    w = np.arange(1, 2 * W + 1, dtype=F).reshape(2, W) * F(0.25)
+    x = np.zeros((1, L, 2), F)
+    x[0, 3, :] = 1.0
+    y = oracle.conv1d_silu(x, w)[0].astype(np.float64)
+    sil = lambda v: v / (1 + np.exp(-v))  # noqa: E731
+    for d in range(2):
+        for t in range(L):
+            j = t - 3  # the impulse at time 3 meets tap W-1-j at output t
+            expect = w[d, W - 1 - j] if 0 <= j < W else 0.0
+            assert abs(y[t, d] - sil(expect)) < 1e-6, (d, t)
+    # causality: changing x at t >= 5 leaves outputs before 5 untouched
+    x2 = x.copy()
+    x2[0, 5:, :] = 7.0
+    assert np.array_equal(oracle.conv1d_silu(x2, w)[0, :5], oracle.conv1d_silu(x, w)[0, :5])
+
+
+def test_conv1d_vs_numpy_convolve():
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((3, 20, 6)).astype(F)
+    w = rng.standard_normal((6, 4)).astype(F)
+    b = rng.standard_normal(6).astype(F)
+    assert rel_err(oracle.conv1d_silu(x, w, b), oracle.numpy_conv1d_silu(x, w, b)) < 1e-5
+
+
+def test_bf16_round_matches_torch():
+    import torch
+    rng = np.random.default_rng(32)
+    a = (rng.standard_normal(4096) * 10.0 ** rng.integers(-20, 20, 4096)).astype(F)
+    a[:4] = [0.0, -0.0, np.inf, -np.inf]
+    want = torch.from_numpy(a).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(oracle.bf16_round(a), want)
+
+
+def test_mamba_block_vs_numpy_f64():
+    from tests.util import block_inputs
+    p = block_inputs(2, 24, 16, 32, 16, 8, 4, seed=33)
+    y = oracle.mamba_block(**p, dt_rank=8)
+    r = oracle.numpy_mamba_block(**p, dt_rank=8)
+    assert y.shape == (2, 24, 16)
+    # both round the same storage points to bf16; a one-ulp bf16 flip of an intermediate is the
+    # largest legitimate difference
+    assert rel_err(y, r) < 2e-2
+
+
 def test_planted_mistakes_are_caught():
     x = inputs(1, 50, 4, 16, 6)
     good = oracle.selective_scan(**x)
@@ -328,3 +385,13 @@ def test_planted_mistakes_are_caught():
     x1 = np.random.default_rng(13).standard_normal((M, L)).astype(F)
     wrong = dict(p, a_imag=np.zeros(N, F))
     assert rel_err(oracle.s4_ref_fwd(x1, **wrong), oracle.numpy_s4_ref(x1, **p)) > 1e-2
+    # conv taps applied in forward instead of reversed order
+    xc = np.random.default_rng(14).standard_normal((1, 12, 3)).astype(F)
+    wc = np.random.default_rng(15).standard_normal((3, 4)).astype(F)
+    assert rel_err(oracle.conv1d_silu(xc, wc[:, ::-1]), oracle.numpy_conv1d_silu(xc, wc)) > 1e-2
+    # block: x and z halves of in_proj swapped
+    from tests.util import block_inputs
+    pb = block_inputs(1, 16, 16, 32, 16, 8, 4, seed=16)
+    rb = oracle.numpy_mamba_block(**pb, dt_rank=8)
+    swapped = dict(pb, w_in=np.concatenate([pb["w_in"][32:], pb["w_in"][:32]]))
+    assert rel_err(oracle.mamba_block(**swapped, dt_rank=8), rb) > 1e-1

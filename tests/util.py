@@ -53,3 +53,25 @@ def scan_inputs(bt, L, dim, N, seed, with_z=True, with_D=True, with_bias=False, 
     z = rng.standard_normal((bt, L, dim), dtype=f) if with_z else None
     dt_bias = (rng.standard_normal(dim, dtype=f) * f(0.1)).astype(f) if with_bias else None
     return dict(u=u, delta=delta, A=A, B=B, C=C, D=D, z=z, dt_bias=dt_bias)
+
+
+def block_inputs(bt, L, dm, di, N, dt_rank, k, seed):
+    """Config-3 distributions at any size: x ~ N(0,1); projection weights ~ N(0, sqrt(2/fan_in));
+    conv taps/bias ~ U(-1/sqrt(k), 1/sqrt(k)); dt_bias = softplus^-1 of a log-uniform dt in
+    [1e-3, 1e-1]; A = -(n+1) (S4D-real); D ~ N(0,1). All float32 (bf16 values where stored bf16)."""
+    rng = np.random.default_rng(seed)
+    f = np.float32
+    nrm = lambda shape, fan: rng.standard_normal(shape, dtype=f) * f(np.sqrt(2.0 / fan))  # noqa: E731
+    dt0 = np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), di))
+    return dict(
+        x=bf16_round(rng.standard_normal((bt, L, dm), dtype=f)),
+        w_in=bf16_round(nrm((2 * di, dm), dm)),
+        conv_w=rng.uniform(-1, 1, (di, k)).astype(f) / f(np.sqrt(k)),
+        conv_b=rng.uniform(-1, 1, di).astype(f) / f(np.sqrt(k)),
+        w_x=bf16_round(nrm((dt_rank + 2 * N, di), di)),
+        w_dt=bf16_round(nrm((di, dt_rank), dt_rank)),
+        dt_bias=(dt0 + np.log(-np.expm1(-dt0))).astype(f),
+        A=-np.tile(np.arange(1, N + 1, dtype=f), (di, 1)),
+        D=rng.standard_normal(di).astype(f),
+        w_out=bf16_round(nrm((dm, di), di)),
+    )
