@@ -7,10 +7,13 @@ d_state 16, fp32, inputs resident in HBM, 3 rotating input sets (1.2 GB) so the 
 cannot serve a step from the previous one. A "step" is one hx_selective_scan_fwd call over one
 batch. Prints ONE JSON line.
 
-  python bench.py [--steps K] [--warmup W] [--workload c2|c2bf16|c3|c4|copy] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c2|c2bf16|c3|c4|c4s4|c4s4exact|c4s4d|copy]
+                  [--no-cpu]
 
 c3 = BASELINE config 3, the full Mamba block (in_proj, conv1d+SiLU, x_proj, dt_proj, fused scan,
 out_proj) at batch 4 x L 4096 x d_model 2048, bf16 storage; reported separately from the metric.
+c4s4 / c4s4exact / c4s4d = BASELINE config 4's S4 recurrence (d 2048, N 16, L 65536): reference
+mode time-parallel, reference mode bit-exact, and the S4D diagonal complex form.
 """
 from __future__ import annotations
 
@@ -172,12 +175,64 @@ def bench_block(args, dev):
     print(json.dumps(rec))
 
 
+def bench_s4(args, dev):
+    """BASELINE config 4, S4 recurrence at d_model 2048, N 16, L 65536, fp32: A_real = -0.5,
+    A_imag = pi*n, dt = 0.1; B, C ~ N(0, 0.1); D ~ N(0, 1); x ~ N(0, 1). Algorithmic bytes: x read
+    once, y written once (1.074 GB)."""
+    M, N, L = 2048, 16, 65536
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x53345334)
+    f = torch.float32
+    nbytes = 2 * M * L * 4
+    if args.workload in ("c4s4", "c4s4exact"):
+        xs = [torch.randn((M, L), generator=gen, device=dev, dtype=f) for _ in range(2)]
+        prm = dict(a_real=torch.full((N,), -0.5, device=dev),
+                   a_imag=torch.pi * torch.arange(N, device=dev, dtype=f),
+                   B=torch.randn((N, M), generator=gen, device=dev) * 0.1,
+                   C=torch.randn((M, N), generator=gen, device=dev) * 0.1,
+                   D=torch.randn((M,), generator=gen, device=dev))
+        par = args.workload == "c4s4"
+
+        def step(i):
+            ssm.s4_ref_fwd(xs[i], **prm, parallel=par)
+
+        workload = ("S4Block::forward_ssm reference mode, " + ("time-parallel" if par else "bit-exact")
+                    + " (d_model 2048, N 16, L 65536, A = -0.5 + i*pi*n, dt 0.1)")
+    else:
+        xs = [torch.randn((1, L, M), generator=gen, device=dev, dtype=f) for _ in range(2)]
+        prm = dict(dt=torch.full((M,), 0.1, device=dev), a_re=torch.full((M, N), -0.5, device=dev),
+                   a_im=(torch.pi * torch.arange(N, device=dev, dtype=f)).repeat(M, 1).contiguous(),
+                   B_re=torch.randn((M, N), generator=gen, device=dev) * 0.1,
+                   B_im=torch.randn((M, N), generator=gen, device=dev) * 0.1,
+                   C_re=torch.randn((M, N), generator=gen, device=dev) * 0.1,
+                   C_im=torch.randn((M, N), generator=gen, device=dev) * 0.1,
+                   D=torch.randn((M,), generator=gen, device=dev))
+
+        def step(i):
+            ssm.s4d_complex_fwd(xs[i], **prm)
+
+        workload = "S4D diagonal complex recurrence (batch 1, L 65536, d 2048, N 16, A = -0.5 + i*pi*n)"
+    ms = time_steps(step, 2, args.steps, args.warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "S4 recurrence tokens/s (config 4), 1 GPU", "value": L * 1e3 / ms, "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (config-4 S4 parameters, seeded)",
+        "config": {"workload": workload, "d_model": M, "d_state": N, "seq_len": L},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": gbs / PEAK_HBM_GBS, "traffic": None, "algorithmic_bytes": nbytes,
+                     "kernel_ms": ms},
+        "cpu_baseline": None}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c2", choices=["c2", "c2bf16", "c4", "c3", "copy"],
+    ap.add_argument("--workload", default="c2",
+                    choices=["c2", "c2bf16", "c4", "c3", "c4s4", "c4s4exact", "c4s4d", "copy"],
                     help="copy = plain device copy of 512 MiB (HBM ceiling and counter calibration)")
     ap.add_argument("--variant", type=int, default=0, help="scan kernel variant (hx_set_scan_variant)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -208,6 +263,9 @@ def main():
         return
     if args.workload == "c3":
         bench_block(args, dev)
+        return
+    if args.workload in ("c4s4", "c4s4exact", "c4s4d"):
+        bench_s4(args, dev)
         return
     if args.workload in ("c2", "c2bf16"):
         bt, L, dim, N = 8, 2048, 1536, 16

@@ -79,6 +79,7 @@ SIGNATURES = {
     "hx_selective_scan_fwd": [_i64, _i64, _i64, _i64, _int, _int] + [_p] * 11 + [_p],
     "hx_selective_state_update": [_i64, _i64, _i64, _int, _int] + [_p] * 10 + [_p],
     "hx_s4_ref_fwd": [_i64, _i64, _i64, _f] + [_p] * 8 + [_p],
+    "hx_s4_ref_fwd_parallel": [_i64, _i64, _i64, _f] + [_p] * 8 + [_p],
     "hx_s4d_complex_fwd": [_i64, _i64, _i64, _i64] + [_p] * 10 + [_p],
     "hx_linear_f32": [_i64, _i64, _i64, _p, _p, _p, _int, _p, _p],
     "hx_matmul_f32": [_i64, _i64, _i64, _p, _p, _p, _p],
@@ -89,6 +90,8 @@ SIGNATURES = {
     "hx_mamba_block_fwd": [_i64] * 7 + [_p] * 12 + [_sz, _p],
     "hx_set_scan_variant": [_int],
     "hx_set_scan_segments": [_int],
+    "hx_set_s4d_path": [_int],
+    "hx_set_s4d_segments": [_int],
 }
 
 _lib = None

@@ -18,53 +18,128 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
 namespace hx {
 namespace {
 
-// Causal depthwise conv over time + bias + SiLU, 4 channels per thread (8-byte bf16 / 16-byte
-// fp32 row accesses). y[b,t,d] = silu(bias[d] + sum_j w[d,j] * x[b, t-(K-1)+j, d]).
-template <typename T, int KW>
-__global__ __launch_bounds__(256) void conv1d_silu_kernel(int64_t Bt, int64_t L, int64_t Dm,
+// Causal depthwise conv over time + bias + SiLU. A thread owns CPT adjacent channels (16 bytes
+// of a row when VEC) and TT consecutive steps; it keeps the last KW input rows in registers, so
+// each input row is read once plus a KW-1 row halo per run of TT steps. Block = 256 threads
+// across channels; grid.x = batch x step-runs, grid.y = channel blocks.
+// y[b,t,d] = silu(bias[d] + sum_j w[d,j] * x[b, t-(KW-1)+j, d]), zero before t = 0.
+template <typename T, int CPT, bool VEC>
+struct ConvRow {
+    __device__ static inline void load(const T* p, float (&v)[CPT]) {
+        if constexpr (VEC && sizeof(T) == 2 && CPT == 8) {
+            const uint4 q = *reinterpret_cast<const uint4*>(p);
+            const uint32_t wds[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[2 * i] = __uint_as_float(wds[i] << 16);
+                v[2 * i + 1] = __uint_as_float(wds[i] & 0xffff0000u);
+            }
+        } else if constexpr (VEC && sizeof(T) == 4 && CPT == 4) {
+            const float4 q = *reinterpret_cast<const float4*>(p);
+            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) v[i] = Storage<T>::load(p + i);
+        }
+    }
+    __device__ static inline void store(T* p, const float (&v)[CPT]) {
+        if constexpr (VEC && sizeof(T) == 2 && CPT == 8) {
+            uint32_t wds[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                wds[i] = (uint32_t)Storage<uint16_t>::round(v[2 * i]) |
+                         ((uint32_t)Storage<uint16_t>::round(v[2 * i + 1]) << 16);
+            *reinterpret_cast<uint4*>(p) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+        } else if constexpr (VEC && sizeof(T) == 4 && CPT == 4) {
+            *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) Storage<T>::store(p + i, v[i]);
+        }
+    }
+};
+
+template <typename T, int KW, int CPT, bool VEC, int TT>
+__global__ __launch_bounds__(256) void conv1d_silu_kernel(int L, int Dm, int nruns,
                                                           const T* __restrict__ x, int64_t ldx,
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ bias,
                                                           T* __restrict__ y) {
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t D4 = Dm / 4;
-    if (gid >= Bt * L * D4) return;
-    const int64_t d4 = gid % D4;
-    const int64_t bt = gid / D4;  // b * L + t
-    const int64_t t = bt % L;
-    const int64_t d = d4 * 4;
-    float acc[4];
+    const int d0 = (blockIdx.y * 256 + threadIdx.x) * CPT;
+    if (d0 >= Dm) return;
+    const int b = blockIdx.x / nruns;
+    const int t0 = (blockIdx.x - b * nruns) * TT;
+    float wk[KW][CPT], bv[CPT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = bias ? bias[d + i] : 0.0f;
+    for (int i = 0; i < CPT; ++i) {
+        bv[i] = bias ? bias[d0 + i] : 0.0f;
 #pragma unroll
-    for (int j = 0; j < KW; ++j) {
-        const int64_t tt = t - (KW - 1) + j;
-        if (tt < 0) continue;
-        const T* xp = x + (bt - (KW - 1) + j) * ldx + d;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = fmaf(w[(d + i) * KW + j], Storage<T>::load(xp + i), acc[i]);
+        for (int j = 0; j < KW; ++j) wk[j][i] = w[(d0 + i) * KW + j];
     }
-    T* yp = y + bt * Dm + d;
+    const T* xb = x + (int64_t)b * L * ldx + d0;
+    T* yb = y + (int64_t)b * L * Dm + d0;
+    float win[KW][CPT];  // win[KW-1] = row t, win[KW-2] = row t-1, ...
 #pragma unroll
-    for (int i = 0; i < 4; ++i) Storage<T>::store(yp + i, silu(acc[i]));
+    for (int j = 0; j < KW - 1; ++j) {
+        const int tt = t0 - (KW - 1) + j;
+        if (tt >= 0) {
+            ConvRow<T, CPT, VEC>::load(xb + (int64_t)tt * ldx, win[j + 1]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) win[j + 1][i] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < TT; ++s) {
+        const int t = t0 + s;
+        if (t >= L) break;
+#pragma unroll
+        for (int j = 0; j < KW - 1; ++j)
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) win[j][i] = win[j + 1][i];
+        ConvRow<T, CPT, VEC>::load(xb + (int64_t)t * ldx, win[KW - 1]);
+        float o[CPT];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            float acc = bv[i];
+#pragma unroll
+            for (int j = 0; j < KW; ++j) acc = fmaf(wk[j][i], win[j][i], acc);
+            o[i] = silu(acc);
+        }
+        ConvRow<T, CPT, VEC>::store(yb + (int64_t)t * Dm, o);
+    }
+}
+
+template <typename T, int KW, int CPT, bool VEC>
+void launch_conv_k(int64_t Bt, int64_t L, int64_t Dm, const void* x, int64_t ldx, const float* w,
+                   const float* b, void* y, hipStream_t s) {
+    constexpr int TT = 16;
+    const int nruns = (int)((L + TT - 1) / TT);
+    dim3 grid((unsigned)(Bt * nruns), (unsigned)((Dm / CPT + 255) / 256));
+    hipLaunchKernelGGL((conv1d_silu_kernel<T, KW, CPT, VEC, TT>), grid, dim3(256), 0, s, (int)L,
+                       (int)Dm, nruns, (const T*)x, ldx, w, b, (T*)y);
+}
+
+template <typename T, int CPT, bool VEC>
+void launch_conv_w(int64_t Bt, int64_t L, int64_t Dm, int64_t KW, const void* x, int64_t ldx,
+                   const float* w, const float* b, void* y, hipStream_t s) {
+    switch (KW) {
+        case 1: launch_conv_k<T, 1, CPT, VEC>(Bt, L, Dm, x, ldx, w, b, y, s); break;
+        case 2: launch_conv_k<T, 2, CPT, VEC>(Bt, L, Dm, x, ldx, w, b, y, s); break;
+        case 3: launch_conv_k<T, 3, CPT, VEC>(Bt, L, Dm, x, ldx, w, b, y, s); break;
+        default: launch_conv_k<T, 4, CPT, VEC>(Bt, L, Dm, x, ldx, w, b, y, s); break;
+    }
 }
 
 template <typename T>
 int launch_conv(int64_t Bt, int64_t L, int64_t Dm, int64_t KW, const void* x, int64_t ldx,
                 const float* w, const float* b, void* y, hipStream_t s) {
-    const int64_t total = Bt * L * (Dm / 4);
-    dim3 grid((unsigned)((total + 255) / 256));
-#define HX_CONV(K)                                                                            \
-    hipLaunchKernelGGL((conv1d_silu_kernel<T, K>), grid, dim3(256), 0, s, Bt, L, Dm,          \
-                       (const T*)x, ldx, w, b, (T*)y)
-    switch (KW) {
-        case 1: HX_CONV(1); break;
-        case 2: HX_CONV(2); break;
-        case 3: HX_CONV(3); break;
-        case 4: HX_CONV(4); break;
-        default: HX_CONV(8); break;
-    }
-#undef HX_CONV
+    constexpr int CV = 16 / sizeof(T);  // channels in 16 bytes
+    const bool vec = Dm % CV == 0 && ldx % CV == 0 && aligned(x, 16) && aligned(y, 16);
+    if (vec)
+        launch_conv_w<T, CV, true>(Bt, L, Dm, KW, x, ldx, w, b, y, s);
+    else
+        launch_conv_w<T, 4, false>(Bt, L, Dm, KW, x, ldx, w, b, y, s);
     HX_LAUNCH_CHECK();
     return HX_OK;
 }
@@ -87,6 +162,8 @@ extern "C" int hx_conv1d_silu(int64_t batch, int64_t seqlen, int64_t dim, int64_
     if (batch == 0 || seqlen == 0 || dim == 0) return HX_OK;
     HX_REQUIRE(x && weight && y && ldx >= dim, HX_ERR_INVALID_INPUT,
                "conv1d_silu: x, weight, y required and ldx >= dim");
+    HX_REQUIRE(seqlen < (1LL << 31) && dim <= 65535LL * 1024 && batch * ((seqlen + 15) / 16) < (1LL << 31),
+               HX_ERR_UNSUPPORTED, "conv1d_silu: sizes beyond the launch grid");
     return dtype == HX_F32
                ? launch_conv<float>(batch, seqlen, dim, width, x, ldx, weight, bias, y, as_stream(stream))
                : launch_conv<uint16_t>(batch, seqlen, dim, width, x, ldx, weight, bias, y, as_stream(stream));

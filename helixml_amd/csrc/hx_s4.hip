@@ -8,8 +8,10 @@
 //       y[t][m] = (sum_n C[m][n]*H[t][n] + D[m]*x[m][t]) * gate[m]
 //     x is [d_model, L] (time contiguous) and y is [L, d_model] (channels contiguous), so the
 //     output kernel transposes through LDS.
-// (2) S4D diagonal complex recurrence, per channel.
+// (2) S4D diagonal complex recurrence, per channel: Abar = exp(dt*a) (complex), Bbar = dt*B,
+//     h_t = Abar*h_{t-1} + Bbar*u_t, y_t = 2*Re(sum_n C*h_t) + D*u_t.
 #include "hx_common.h"
+#include "hx_wave.h"
 
 namespace hx {
 namespace {
@@ -186,6 +188,470 @@ __global__ __launch_bounds__(128) void s4d_complex_kernel(
     }
 }
 
+// ---------------------------------------------------------------- S4D complex, wave layout
+// The per-thread kernel above leaves most of the chip idle when batch x channels is small (config
+// 4: one sequence of 2048 channels = 32 waves for 65536 steps). This path uses the selective
+// scan's wave layout: one wave = 16 channels x 16 states, DPP row r holding states [4r, 4r+4) of
+// lane c's channel; blocks of 4 waves stage [16 steps x 64 channels] float4 tiles of x and y
+// through LDS; per-row partial readouts are reduce-scattered across rows with register swaps.
+// The state is kept rescaled, g = h / Bbar, so the update needs no per-state input product:
+//   g_t = Abar*g_{t-1} + u_t,  Re(C*h_t) = Re((C*Bbar)*g_t).
+// Long sequences are cut into time segments (one block each): END_ONLY blocks run a segment from
+// zero and publish its end state; a carry kernel chains entry states (the system is
+// time-invariant, so a segment's transfer is Abar^seg_len); full blocks rerun each segment from
+// its entry state and write y.
+struct S4dSeg {
+    int64_t seg_len;
+    int nseg;
+    const float* seg_init;  // [nseg][Bt][Dm][16][2] entry g (full mode, nseg > 1)
+    float* seg_end;         // [nseg][Bt][Dm][16][2] end g from zero (END_ONLY)
+};
+
+__device__ inline void s4d_coef(float dt, float are, float aim, float& ar, float& ai) {
+    const float mag = expf(dt * are);
+    float sn, cs;
+    sincosf(dt * aim, &sn, &cs);
+    ar = mag * cs;
+    ai = mag * sn;
+}
+
+template <bool END_ONLY>
+__global__ __launch_bounds__(256) void s4d_wave_kernel(
+    int64_t L, int64_t Dm, int ntiles, int64_t Bt, const float* __restrict__ x,
+    const float* __restrict__ dtv, const float* __restrict__ a_re, const float* __restrict__ a_im,
+    const float* __restrict__ B_re, const float* __restrict__ B_im,
+    const float* __restrict__ C_re, const float* __restrict__ C_im, const float* __restrict__ Dv,
+    float* __restrict__ y, S4dSeg sg) {
+    constexpr int NS = 16, TCH = 16, TS = 80, PF = 2;
+    __shared__ float s_x[2][TCH][TS];
+    __shared__ float s_out[END_ONLY ? 1 : 2][TCH][TS];
+
+    const int nblk = gridDim.x;
+    int id = blockIdx.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);  // XCD-aware order
+    const int tile = id % ntiles;
+    const int64_t b = (id / ntiles) % Bt;
+    const int seg = (int)(id / ntiles / Bt);
+    const int64_t tbeg = (int64_t)seg * sg.seg_len;
+    const int64_t tend = tbeg + sg.seg_len < L ? tbeg + sg.seg_len : L;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int r = lane >> 4;
+    const int c = lane & 15;
+    const int64_t c0 = (int64_t)tile * 64;
+    const int cb = w * 16 + c;
+    const int64_t d = c0 + cb;
+    const bool dvalid = d < Dm;
+    const int64_t dc = dvalid ? d : Dm - 1;
+    const int mrow = tid >> 4, mcl = (tid & 15) * 4;
+    const int64_t mch = c0 + mcl;
+    const bool mvalid = mch < Dm;
+    const int64_t rowbase = b * L * Dm;
+
+    float ar[4], ai[4], cr[4], ci[4], gr[4], gi[4];
+    const float dt = dtv[dc];
+    const float* g0 = (!END_ONLY && sg.nseg > 1) ? sg.seg_init + (int64_t)seg * Bt * Dm * NS * 2 : nullptr;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int64_t idx = dc * NS + 4 * r + k;
+        s4d_coef(dt, a_re[idx], a_im[idx], ar[k], ai[k]);
+        const float br = dt * B_re[idx], bi = dt * B_im[idx];
+        cr[k] = C_re[idx] * br - C_im[idx] * bi;  // C * Bbar
+        ci[k] = C_re[idx] * bi + C_im[idx] * br;
+        const int64_t gidx = ((b * Dm + dc) * NS + 4 * r + k) * 2;
+        gr[k] = g0 ? g0[gidx] : 0.0f;
+        gi[k] = g0 ? g0[gidx + 1] : 0.0f;
+    }
+    const float Dd = Dv ? Dv[dc] : 0.0f;
+
+    // prefetch ring of PF = 2 chunks in two named registers (an indexed array of float4 was
+    // placed in scratch memory by the compiler)
+    float4 rx0, rx1;
+    const int64_t Lm1 = tend - 1;
+    auto fetch = [&](float4& dst, int64_t t0) __attribute__((always_inline)) {
+        int64_t t = t0 + mrow;
+        t = t < Lm1 ? t : Lm1;
+        dst = *reinterpret_cast<const float4*>(x + rowbase + t * Dm + (mvalid ? mch : 0));
+    };
+    auto stage_in = [&](const float4& src, int buf) __attribute__((always_inline)) {
+        *reinterpret_cast<float4*>(&s_x[buf][mrow][mcl]) = src;
+    };
+    auto store_out = [&](int64_t t0, int buf) __attribute__((always_inline)) {
+        if constexpr (!END_ONLY) {
+            const int64_t t = t0 + mrow;
+            if (mvalid && t < tend)
+                *reinterpret_cast<float4*>(y + rowbase + t * Dm + mch) =
+                    *reinterpret_cast<const float4*>(&s_out[buf][mrow][mcl]);
+        }
+    };
+    // one chunk: FULL = all 16 steps inside the segment (no per-step guard)
+    auto compute = [&](int64_t t0, int buf, auto full_c) __attribute__((always_inline)) {
+        constexpr bool FULL = decltype(full_c)::value;
+        const int64_t nvalid = tend - t0;  // uniform; < TCH only in a segment's last chunk
+        float P[16];
+        StepLoop<TCH>::run([&](auto sc) {
+            constexpr int s = decltype(sc)::value;
+            const float uv = s_x[buf][s][cb];
+            // the readout runs in two chains (real and imaginary products) to halve its depth
+            float acc_r = 0.0f, acc_i = 0.0f;
+            if (FULL || s < nvalid) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float nr = fmaf(ar[k], gr[k], fmaf(-ai[k], gi[k], uv));
+                    const float ni = fmaf(ar[k], gi[k], ai[k] * gr[k]);
+                    gr[k] = nr;
+                    gi[k] = ni;
+                    if constexpr (!END_ONLY) {
+                        acc_r = fmaf(cr[k], nr, acc_r);
+                        acc_i = fmaf(ci[k], ni, acc_i);
+                    }
+                }
+            }
+            P[(s >> 2) + 4 * (s & 3)] = acc_r - acc_i;
+        });
+        if constexpr (!END_ONLY) {
+            float Y[4];
+            rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int s = r + 4 * i;
+                s_out[buf][s][cb] = fmaf(2.0f, Y[i], Dd * s_x[buf][s][cb]);
+            }
+        }
+    };
+
+    static_assert(PF == 2, "two-slot ring");
+    fetch(rx0, tbeg);
+    fetch(rx1, tbeg + TCH);
+    stage_in(rx0, 0);
+    fetch(rx0, tbeg + (int64_t)PF * TCH);
+    lds_barrier();
+    for (int64_t tb0 = tbeg; tb0 < tend; tb0 += PF * TCH) {
+        StepLoop<PF>::run([&](auto kc) __attribute__((always_inline)) {
+            constexpr int k = decltype(kc)::value;
+            constexpr int buf = k & 1;
+            float4& next = k == 0 ? rx1 : rx0;  // slot of chunk t0 + TCH
+            const int64_t t0 = tb0 + k * TCH;
+            if (t0 >= tend) return;  // uniform
+            stage_in(next, buf ^ 1);
+            if (t0 > tbeg) store_out(t0 - TCH, END_ONLY ? 0 : buf ^ 1);
+            fetch(next, t0 + TCH + (int64_t)PF * TCH);
+            if (t0 + TCH <= tend)
+                compute(t0, buf, std::true_type{});
+            else
+                compute(t0, buf, std::false_type{});
+            lds_barrier();
+        });
+    }
+    if constexpr (!END_ONLY) {
+        const int64_t nch = (tend - tbeg + TCH - 1) / TCH;
+        store_out(tbeg + (nch - 1) * TCH, (int)((nch - 1) & 1));
+    } else if (dvalid) {
+        float* ge = sg.seg_end + (int64_t)seg * Bt * Dm * NS * 2;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t gidx = ((b * Dm + d) * NS + 4 * r + k) * 2;
+            ge[gidx] = gr[k];
+            ge[gidx + 1] = gi[k];
+        }
+    }
+}
+
+// Entry g of every segment, per (b, d, n): g_in[0] = 0, g_in[k] = Abar^seg_len * g_in[k-1] +
+// g_end[k-1]. Abar is formed exactly as in s4d_wave_kernel and raised by binary powering.
+__global__ __launch_bounds__(256) void s4d_seg_carry_kernel(
+    int64_t Bt, int64_t Dm, int nseg, int64_t seg_len, const float* __restrict__ dtv,
+    const float* __restrict__ a_re, const float* __restrict__ a_im,
+    const float* __restrict__ gend, float* __restrict__ ginit) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t per = Bt * Dm * 16;
+    if (gid >= per) return;
+    const int64_t dn = gid % (Dm * 16);
+    const int64_t dd = dn / 16;
+    float br, bi;
+    s4d_coef(dtv[dd], a_re[dn], a_im[dn], br, bi);
+    float pr = 1.0f, pi = 0.0f;  // Abar^seg_len
+    for (int64_t e = seg_len; e > 0; e >>= 1) {
+        if (e & 1) {
+            const float t = pr * br - pi * bi;
+            pi = pr * bi + pi * br;
+            pr = t;
+        }
+        const float t = br * br - bi * bi;
+        bi = 2.0f * br * bi;
+        br = t;
+    }
+    float hr = 0.0f, hi = 0.0f;
+    for (int k = 0; k < nseg; ++k) {
+        const int64_t o = ((int64_t)k * per + gid) * 2;
+        ginit[o] = hr;
+        ginit[o + 1] = hi;
+        const float nr = fmaf(pr, hr, fmaf(-pi, hi, gend[o]));
+        const float ni = fmaf(pr, hi, fmaf(pi, hr, gend[o + 1]));
+        hr = nr;
+        hi = ni;
+    }
+}
+
+// ---------------------------------------------------------------- ref mode, time-parallel
+// Same factorisation as reference mode, with the 16 recurrences H[t] = a*H[t-1] + U[t] solved
+// in chunks instead of one lane per state walking all L steps (which at L = 65536 is one long
+// dependent chain): the projection kernel also scans its 256-step chunk from zero in LDS, a
+// carry kernel chains the chunk ends, and the output kernel forms H[t] = Hloc[t] +
+// a^(j+1) * carry[chunk] on the fly (j = t - chunk start).
+// Products may contract to FMA; results agree with reference mode to rounding, not bit for bit.
+constexpr int kPChunk = 256;  // steps per chunk = per projection block
+constexpr int kPRows = 8;     // channel rows per projection load batch
+constexpr int kPWaves = 8;    // waves per projection block (channel split)
+
+// U[t][n] = sum_m Bd[n][m] x[m][t] for the block's 256 steps (4 per lane, float4 loads along t);
+// wave w sums its eighth of the channels with loads issued kPRows rows ahead (8 waves x 8 KB in
+// flight per CU); partials are added through LDS. Then 16 x 16 threads scan the chunk from zero (16-step pieces, a
+// sequential pass over the 16 piece ends, and a fix-up) and write Hloc and the chunk end E.
+// BdT is Bd transposed ([m][16], zero-padded), read wave-uniformly.
+template <bool VEC>
+__global__ __launch_bounds__(64 * kPWaves) void s4p_proj_kernel(int64_t M, int64_t L,
+                                                       const float* __restrict__ x,
+                                                       const float* __restrict__ BdT,
+                                                       const float* __restrict__ a,
+                                                       float* __restrict__ H,
+                                                       float* __restrict__ E) {
+    __shared__ __attribute__((aligned(16))) float part[kPWaves][16][kPChunk];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t t0 = (int64_t)blockIdx.x * kPChunk;
+    const int64_t tl = t0 + lane * 4;
+    const int64_t mq = (M + kPWaves - 1) / kPWaves;
+    const int64_t mb = w * mq, me = mb + mq < M ? mb + mq : M;
+    float acc[4][16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int n = 0; n < 16; ++n) acc[j][n] = 0.0f;
+    auto load_row = [&](int64_t m, float (&xv)[4]) __attribute__((always_inline)) {
+        if (m >= me) {
+            xv[0] = xv[1] = xv[2] = xv[3] = 0.0f;
+        } else if (VEC && tl + 4 <= L) {
+            const float4 q = *reinterpret_cast<const float4*>(x + m * L + tl);
+            xv[0] = q.x; xv[1] = q.y; xv[2] = q.z; xv[3] = q.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xv[j] = tl + j < L ? x[m * L + tl + j] : 0.0f;
+        }
+    };
+    float cur[kPRows][4], nxt[kPRows][4];
+#pragma unroll
+    for (int r = 0; r < kPRows; ++r) load_row(mb + r, cur[r]);
+    for (int64_t m = mb; m < me; m += kPRows) {
+#pragma unroll
+        for (int r = 0; r < kPRows; ++r) load_row(m + kPRows + r, nxt[r]);
+#pragma unroll
+        for (int r = 0; r < kPRows; ++r) {
+            const int64_t mr = m + r < me ? m + r : me - 1;  // rows past me carry x = 0
+            const float* bd = BdT + mr * 16;
+#pragma unroll
+            for (int n = 0; n < 16; ++n) {
+                const float bn = bd[n];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[j][n] = fmaf(bn, cur[r][j], acc[j][n]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kPRows; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cur[r][j] = nxt[r][j];
+    }
+#pragma unroll
+    for (int n = 0; n < 16; ++n)
+        *reinterpret_cast<float4*>(&part[w][n][lane * 4]) =
+            make_float4(acc[0][n], acc[1][n], acc[2][n], acc[3][n]);
+    __syncthreads();
+    // U of step t0 + t = sum_w part[w][n][t]; thread (piece q, state n) of the first 256 threads
+    // scans steps [16q, 16q + 16)
+    const bool scanner = tid < 256;
+    const int n = tid & 15, q = (tid >> 4) & 15;
+    const float an = a[n];
+    float u[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int tt = q * 16 + i;
+        float v = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < kPWaves; ++ww) v += part[ww][n][tt];
+        u[i] = v;
+    }
+    float h = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        h = fmaf(an, h, u[i]);
+        u[i] = h;
+    }
+    __syncthreads();
+    if (scanner) part[1][n][q] = h;  // piece end from zero
+    __syncthreads();
+    if (tid < 16) {  // entry state of each piece, sequential over the 16 pieces
+        float a16 = 1.0f;
+        for (int i = 0; i < 16; ++i) a16 *= an;
+        float c = 0.0f;
+        for (int k = 0; k < 16; ++k) {
+            const float e = part[1][n][k];
+            part[2][n][k] = c;
+            c = fmaf(a16, c, e);
+        }
+        if (t0 < L) E[blockIdx.x * 16 + n] = c;
+    }
+    __syncthreads();
+    if (!scanner) return;
+    const float cin = part[2][n][q];
+    float p = an;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int64_t t = t0 + q * 16 + i;
+        if (t < L) H[t * 16 + n] = fmaf(p, cin, u[i]);
+        p *= an;
+    }
+}
+
+// Discretisation on the device: a[n] = exp(dt*a_real[n]) * cos(dt*a_imag[n]); BdT[m][n] =
+// B[n][m]*dt (n < N, else 0); pw[j][n] = a[n]^(j+1) for j < kPChunk.
+__global__ __launch_bounds__(256) void s4p_setup_kernel(int64_t M, int64_t N, float dt,
+                                                        const float* __restrict__ a_real,
+                                                        const float* __restrict__ a_imag,
+                                                        const float* __restrict__ B,
+                                                        float* __restrict__ a,
+                                                        float* __restrict__ BdT,
+                                                        float* __restrict__ pw) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < M * 16) {
+        const int64_t m = i >> 4, n = i & 15;
+        BdT[i] = n < N ? B[n * M + m] * dt : 0.0f;
+    }
+    if (blockIdx.x == 0 && threadIdx.x < 16) {
+        // a in double from the reference's f32 products tr = a_real*dt, ti = a_imag*dt, rounded
+        // once; the powers are those of the rounded a, formed in double and rounded once, so the
+        // carry applies exactly the decay the chunk scans apply step by step.
+        const int n = threadIdx.x;
+        const float tr = n < N ? a_real[n] * dt : 0.0f;
+        const float ti = n < N ? a_imag[n] * dt : 0.0f;
+        const float an = n < N ? (float)(exp((double)tr) * cos((double)ti)) : 0.0f;
+        a[n] = an;
+        double p = an;
+        for (int j = 0; j < kPChunk; ++j) {
+            pw[j * 16 + n] = (float)p;
+            p *= (double)an;
+        }
+    }
+}
+
+// carry[k] = state entering chunk k: carry[0] = 0, carry[k] = a^kPChunk carry[k-1] + E[k-1].
+// The chunk ends are staged in LDS by the whole block first (up to 1024 chunks per pass).
+__global__ __launch_bounds__(256) void s4p_carry_kernel(int64_t nch, const float* __restrict__ pw,
+                                                        const float* __restrict__ E,
+                                                        float* __restrict__ carry) {
+    __shared__ float se[1024 * 16];
+    const int tid = threadIdx.x;
+    const int n = tid & 15;
+    const float p = pw[(kPChunk - 1) * 16 + n];
+    float c = 0.0f;
+    for (int64_t k0 = 0; k0 < nch; k0 += 1024) {
+        const int64_t kn = nch - k0 < 1024 ? nch - k0 : 1024;
+        __syncthreads();
+        for (int64_t i = tid; i < kn * 16; i += 256) se[i] = E[k0 * 16 + i];
+        __syncthreads();
+        if (tid < 16) {
+            for (int64_t k = 0; k < kn; ++k) {
+                const float e = se[k * 16 + n];
+                se[k * 16 + n] = c;
+                c = fmaf(p, c, e);
+            }
+        }
+        __syncthreads();
+        for (int64_t i = tid; i < kn * 16; i += 256) carry[k0 * 16 + i] = se[i];
+    }
+}
+
+// y[t][m] = (sum_n C[m][n] h[t][n] + D[m] x[m][t]) * gate[m], h from the chunk-local scan plus
+// the carried state. Tile = 64 channels x 64 steps: x read as float4 along t (256-byte rows)
+// and transposed through LDS; y written along m (256-byte rows).
+constexpr int kOTile = 64;
+template <bool VEC>
+__global__ __launch_bounds__(256) void s4p_output_kernel(int64_t M, int64_t L, int64_t N,
+                                                         const float* __restrict__ x,
+                                                         const float* __restrict__ H,
+                                                         const float* __restrict__ carry,
+                                                         const float* __restrict__ pw,
+                                                         const float* __restrict__ C,
+                                                         const float* __restrict__ D,
+                                                         const float* __restrict__ gate,
+                                                         float* __restrict__ y) {
+    __shared__ float sx[kOTile][kOTile + 1];  // [m][t]
+    __shared__ float sh[kOTile][16];          // [t][n]
+    const int64_t m0 = (int64_t)blockIdx.x * kOTile;
+    const int64_t t0 = (int64_t)blockIdx.y * kOTile;
+    const int tid = threadIdx.x;
+    // x tile: 64 rows (m) x 16 float4 (t); thread -> (row tid/16 + 16i, t4 = tid%16)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int mm = (tid >> 4) + 16 * i, t4 = (tid & 15) * 4;
+        const int64_t m = m0 + mm, t = t0 + t4;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (m < M) {
+            if (VEC && t + 4 <= L) {
+                const float4 q = *reinterpret_cast<const float4*>(x + m * L + t);
+                v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = t + j < L ? x[m * L + t + j] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sx[mm][t4 + j] = v[j];
+    }
+    for (int i = tid; i < kOTile * 16; i += 256) {
+        const int tt = i >> 4, n = i & 15;
+        const int64_t t = t0 + tt;
+        float h = 0.0f;
+        if (t < L) {
+            const int64_t k = t / kPChunk;
+            const int j = (int)(t - k * kPChunk);
+            h = fmaf(pw[j * 16 + n], carry[k * 16 + n], H[t * 16 + n]);
+        }
+        sh[tt][n] = h;
+    }
+    __syncthreads();
+    // outputs: thread -> channel tid % 64, steps 16 * (tid / 64) .. + 15; a wave's stores for
+    // one step are 64 consecutive channels (256 bytes)
+    const int mm = tid & 63, tg = (tid >> 6) * 16;
+    const int64_t m = m0 + mm;
+    if (m >= M) return;
+    float c[16];
+    if (N == 16 && VEC) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 q = *reinterpret_cast<const float4*>(C + m * 16 + 4 * k);
+            c[4 * k] = q.x; c[4 * k + 1] = q.y; c[4 * k + 2] = q.z; c[4 * k + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < 16; ++n) c[n] = n < N ? C[m * N + n] : 0.0f;
+    }
+    const float dd = D[m];
+    const float g = gate ? gate[m] : 1.0f;
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+        const int tt = tg + i;
+        const int64_t t = t0 + tt;
+        if (t >= L) break;
+        float acc = dd * sx[mm][tt];
+#pragma unroll
+        for (int n = 0; n < 16; ++n) acc = fmaf(c[n], sh[tt][n], acc);
+        y[t * M + m] = acc * g;
+    }
+}
+
 }  // namespace
 }  // namespace hx
 
@@ -202,6 +668,8 @@ extern "C" int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, fl
     if (d_model == 0 || seqlen == 0) return HX_OK;
     HX_REQUIRE(x && a_real && a_imag && B && C && D && y, HX_ERR_INVALID_INPUT,
                "s4_ref: x, a_real, a_imag, B, C, D and y must be non-NULL");
+    HX_REQUIRE((seqlen + kTileT - 1) / kTileT <= 65535, HX_ERR_UNSUPPORTED,
+               "s4_ref: seqlen %lld too long for one launch", (long long)seqlen);
     hipStream_t s = as_stream(stream);
 
     // discretize(dt) (ssm.rs:113-120) on the host with libm, exactly as the reference:
@@ -257,6 +725,63 @@ extern "C" int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, fl
     return rc;
 }
 
+namespace hx {
+namespace {
+// 0: automatic (wave path when dstate == 16 and rows are 16-byte aligned), 1: per-thread path;
+// set by hx_set_s4d_path. Segments: 0 = automatic, else forced (hx_set_s4d_segments).
+int g_s4d_path = 0;
+int g_s4d_segments = 0;
+
+int launch_s4d_wave(int64_t Bt, int64_t L, int64_t Dm, const float* x, const float* dt,
+                    const float* a_re, const float* a_im, const float* B_re, const float* B_im,
+                    const float* C_re, const float* C_im, const float* D, float* y, hipStream_t s) {
+    const int ntiles = (int)((Dm + 63) / 64);
+    const int64_t pairs = (int64_t)ntiles * Bt;
+    int64_t nseg = g_s4d_segments;
+    if (nseg <= 0) {
+        // about 2048 waves (two per SIMD); segments of at least 512 steps
+        nseg = (512 + pairs - 1) / pairs;
+        const int64_t cap = L / 512 > 1 ? L / 512 : 1;
+        nseg = nseg < cap ? nseg : cap;
+    }
+    int64_t seg_len = (L + nseg - 1) / nseg;
+    seg_len = (seg_len + 15) / 16 * 16;
+    nseg = (L + seg_len - 1) / seg_len;
+    HX_REQUIRE(pairs * nseg <= 0x7fffffff, HX_ERR_UNSUPPORTED, "s4d_complex: grid too large");
+    S4dSeg sg{seg_len, (int)nseg, nullptr, nullptr};
+    float* scratch = nullptr;
+    if (nseg > 1) {
+        const size_t per = (size_t)nseg * Bt * Dm * 16 * 2;
+        HX_HIP_CHECK(hipMallocAsync((void**)&scratch, 2 * per * sizeof(float), s));
+        sg.seg_end = scratch;
+        sg.seg_init = scratch + per;
+        hipLaunchKernelGGL(s4d_wave_kernel<true>, dim3((unsigned)(pairs * nseg)), dim3(256), 0, s, L,
+                           Dm, ntiles, Bt, x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D, y, sg);
+        const int64_t n = Bt * Dm * 16;
+        hipLaunchKernelGGL(s4d_seg_carry_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                           Bt, Dm, (int)nseg, seg_len, dt, a_re, a_im, sg.seg_end, scratch + per);
+    }
+    hipLaunchKernelGGL(s4d_wave_kernel<false>, dim3((unsigned)(pairs * nseg)), dim3(256), 0, s, L,
+                       Dm, ntiles, Bt, x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D, y, sg);
+    hipError_t le = hipGetLastError();
+    if (scratch) (void)hipFreeAsync(scratch, s);
+    if (le != hipSuccess)
+        return set_error(HX_ERR_BACKEND, "s4d_complex: launch failed: %s", hipGetErrorString(le));
+    return HX_OK;
+}
+}  // namespace
+}  // namespace hx
+
+extern "C" int hx_set_s4d_path(int path) {
+    hx::g_s4d_path = path;
+    return HX_OK;
+}
+
+extern "C" int hx_set_s4d_segments(int nseg) {
+    hx::g_s4d_segments = nseg;
+    return HX_OK;
+}
+
 extern "C" int hx_s4d_complex_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
                                   const float* x, const float* dt, const float* a_re,
                                   const float* a_im, const float* B_re, const float* B_im,
@@ -270,9 +795,13 @@ extern "C" int hx_s4d_complex_fwd(int64_t batch, int64_t seqlen, int64_t dim, in
     if (batch == 0 || seqlen == 0 || dim == 0) return HX_OK;
     HX_REQUIRE(x && dt && a_re && a_im && B_re && B_im && C_re && C_im && y, HX_ERR_INVALID_INPUT,
                "s4d_complex: a required pointer is NULL");
+    hipStream_t s = as_stream(stream);
+    const bool wave_ok = dstate == 16 && dim % 4 == 0 && aligned(x, 16) && aligned(y, 16) &&
+                         g_s4d_path != 1;
+    if (wave_ok) return launch_s4d_wave(batch, seqlen, dim, x, dt, a_re, a_im, B_re, B_im, C_re,
+                                        C_im, D, y, s);
     const int64_t total = batch * dim;
     dim3 grid((unsigned)((total + 127) / 128));
-    hipStream_t s = as_stream(stream);
     if (dstate <= 16)
         hipLaunchKernelGGL(s4d_complex_kernel<16>, grid, dim3(128), 0, s, batch, seqlen, dim,
                            dstate, x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D, y);
@@ -280,5 +809,59 @@ extern "C" int hx_s4d_complex_fwd(int64_t batch, int64_t seqlen, int64_t dim, in
         hipLaunchKernelGGL(s4d_complex_kernel<kMaxState>, grid, dim3(128), 0, s, batch, seqlen,
                            dim, dstate, x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D, y);
     HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+extern "C" int hx_s4_ref_fwd_parallel(int64_t d_model, int64_t dstate, int64_t seqlen, float dt,
+                                      const float* x, const float* a_real, const float* a_imag,
+                                      const float* B, const float* C, const float* D,
+                                      const float* gate, float* y, void* stream) {
+    using namespace hx;
+    HX_REQUIRE(d_model >= 0 && seqlen >= 0, HX_ERR_INVALID_DIMENSION,
+               "s4_ref_parallel: negative size (d_model=%lld seqlen=%lld)", (long long)d_model,
+               (long long)seqlen);
+    HX_REQUIRE(dstate >= 1 && dstate <= 16, HX_ERR_UNSUPPORTED,
+               "s4_ref_parallel: dstate=%lld not supported (1..16)", (long long)dstate);
+    if (d_model == 0 || seqlen == 0) return HX_OK;
+    HX_REQUIRE(x && a_real && a_imag && B && C && D && y, HX_ERR_INVALID_INPUT,
+               "s4_ref_parallel: x, a_real, a_imag, B, C, D and y must be non-NULL");
+    HX_REQUIRE((seqlen + kOTile - 1) / kOTile <= 65535, HX_ERR_UNSUPPORTED,
+               "s4_ref_parallel: seqlen %lld too long for one launch", (long long)seqlen);
+    hipStream_t s = as_stream(stream);
+    const int64_t nch = (seqlen + kPChunk - 1) / kPChunk;
+    // scratch: a [16] | pw [kPChunk*16] | BdT [M*16] | H [L*16] | E [nch*16] | carry [nch*16]
+    const size_t n_a = 64, n_pw = kPChunk * 16, n_bd = (size_t)d_model * 16,
+                 n_h = (size_t)seqlen * 16, n_e = (size_t)nch * 16;
+    float* scratch = nullptr;
+    HX_HIP_CHECK(hipMallocAsync((void**)&scratch, (n_a + n_pw + n_bd + n_h + 2 * n_e) * sizeof(float), s));
+    float* a_dev = scratch;
+    float* pw = a_dev + n_a;
+    float* BdT = pw + n_pw;
+    float* H = BdT + n_bd;
+    float* E = H + n_h;
+    float* carry = E + n_e;
+    hipLaunchKernelGGL(s4p_setup_kernel, dim3((unsigned)((n_bd + 255) / 256)), dim3(256), 0, s,
+                       d_model, dstate, dt, a_real, a_imag, B, a_dev, BdT, pw);
+    const bool vec = seqlen % 4 == 0 && aligned(x, 16);
+    const bool vec_out = vec && aligned(C, 16);
+    dim3 g1((unsigned)nch);
+    if (vec)
+        hipLaunchKernelGGL(s4p_proj_kernel<true>, g1, dim3(64 * kPWaves), 0, s, d_model, seqlen, x,
+                           BdT, a_dev, H, E);
+    else
+        hipLaunchKernelGGL(s4p_proj_kernel<false>, g1, dim3(64 * kPWaves), 0, s, d_model, seqlen, x,
+                           BdT, a_dev, H, E);
+    hipLaunchKernelGGL(s4p_carry_kernel, dim3(1), dim3(256), 0, s, nch, pw, E, carry);
+    dim3 g3((unsigned)((d_model + kOTile - 1) / kOTile), (unsigned)((seqlen + kOTile - 1) / kOTile));
+    if (vec_out)
+        hipLaunchKernelGGL(s4p_output_kernel<true>, g3, dim3(256), 0, s, d_model, seqlen, dstate, x,
+                           H, carry, pw, C, D, gate, y);
+    else
+        hipLaunchKernelGGL(s4p_output_kernel<false>, g3, dim3(256), 0, s, d_model, seqlen, dstate, x,
+                           H, carry, pw, C, D, gate, y);
+    hipError_t le = hipGetLastError();
+    (void)hipFreeAsync(scratch, s);
+    if (le != hipSuccess)
+        return set_error(HX_ERR_BACKEND, "s4_ref_parallel: launch failed: %s", hipGetErrorString(le));
     return HX_OK;
 }

@@ -101,9 +101,11 @@ def selective_state_update(state, u, delta, A, B, C, D=None, z=None, dt_bias=Non
     return out
 
 
-def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, stream=None):
+def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, parallel=False, stream=None):
     """Reference-mode S4Block::forward_ssm (crates/nn/src/ssm.rs:138-186) on x [d_model, L];
-    returns y with memory [L, d_model] (the reference's shape field is [d_model, L])."""
+    returns y with memory [L, d_model] (the reference's shape field is [d_model, L]).
+    parallel=False: bit-identical to CpuTensor (hx_s4_ref_fwd); parallel=True: time-parallel
+    chunked recurrence for long L, equal to rounding (hx_s4_ref_fwd_parallel, dstate <= 16)."""
     M, L = x.shape
     N = a_real.shape[0]
     f = torch.float32
@@ -115,7 +117,7 @@ def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, stream=None):
     _need(D, "D", (M,), f)
     _need(gate, "gate", (M,), f)
     y = torch.empty((L, M), device=x.device, dtype=f)
-    _ffi.call("hx_s4_ref_fwd", M, N, L, float(dt), _ptr(x), _ptr(a_real), _ptr(a_imag), _ptr(B),
+    _ffi.call("hx_s4_ref_fwd_parallel" if parallel else "hx_s4_ref_fwd", M, N, L, float(dt), _ptr(x), _ptr(a_real), _ptr(a_imag), _ptr(B),
               _ptr(C), _ptr(D), _ptr(gate), _ptr(y), _stream(stream))
     return y
 
@@ -201,6 +203,14 @@ def set_scan_variant(v: int) -> None:
 
 def set_scan_segments(n: int) -> None:
     _ffi.call("hx_set_scan_segments", int(n))
+
+
+def set_s4d_path(path: int) -> None:
+    _ffi.call("hx_set_s4d_path", int(path))
+
+
+def set_s4d_segments(n: int) -> None:
+    _ffi.call("hx_set_s4d_segments", int(n))
 
 
 def conv1d_silu(x, weight, bias=None, out=None, stream=None):

@@ -114,6 +114,17 @@ int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, float dt,
                   const float* B, const float* C, const float* D, const float* gate,
                   float* y, void* stream);
 
+/* Time-parallel variant of hx_s4_ref_fwd for long sequences (same arguments and layouts,
+ * dstate <= 16): the 16 state recurrences are solved in 64-step chunks with a carry chain, the
+ * discretisation runs on the device, and products may contract to FMA, so results agree with
+ * reference mode to rounding (within 1e-4) instead of bit for bit. Asynchronous on `stream`
+ * (no host round trip). Replaces the per-step loop of S4Block::forward_ssm
+ * (crates/nn/src/ssm.rs:166-182) for L in the tens of thousands. */
+int hx_s4_ref_fwd_parallel(int64_t d_model, int64_t dstate, int64_t seqlen, float dt,
+                           const float* x, const float* a_real, const float* a_imag,
+                           const float* B, const float* C, const float* D, const float* gate,
+                           float* y, void* stream);
+
 /* S4D diagonal complex recurrence (per-channel state, S4D discretisation with the same
  * ZOH-on-A / Euler-on-B choice as ssm.rs:108-130), the complex form of what
  * S4Block::discretize computes and then drops (A_d_imag, ssm.rs:121-125):
@@ -188,6 +199,8 @@ int hx_set_scan_variant(int variant);
  * the (batch, 64-channel) tiles cannot fill the GPU and seqlen >= 4096). Segments are scanned in
  * parallel from a zero state, their entry states chained by a carry kernel, then rescanned with
  * outputs. A measurement knob; results agree within fp32 rounding for every setting. */
+int hx_set_s4d_path(int path);      /* 0 auto (wave path for dstate 16), 1 per-channel thread path */
+int hx_set_s4d_segments(int nseg);  /* S4D time segments: 0 auto, n forced */
 int hx_set_scan_segments(int nseg);
 
 #ifdef __cplusplus

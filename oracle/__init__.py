@@ -12,7 +12,7 @@ Pinning status of each function (how tests/test_oracle.py pins it):
   matmul, linear        reference KATs ones[2,3].ones[3,4] == 3 and ones+ones == 2
                         (backend-cpu/src/lib.rs:1733-1758), numpy float64
   silu                  closed form x*sigmoid(x), special values
-  s4_ref_fwd            zero input, impulse response, step response (geometric series),
+  s4_ref_fwd(_f64)      zero input, impulse response, step response (geometric series),
                         linearity, B=0 -> D*u, a=1 -> prefix sum, numpy float64 brute force
   ssm_mamba_fwd         composition: matmul + s4_ref_fwd + gate (each pinned above)
   mamba_mlp             composition of linear/silu, numpy float64
@@ -66,6 +66,7 @@ def lib() -> ctypes.CDLL:
             "oracle_mamba_mlp": [_i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p],
             "oracle_rmsnorm": [_i64, _i64, _p, _p, _f, _p],
             "oracle_s4_ref_fwd": [_i64, _i64, _i64, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+            "oracle_s4_ref_fwd_f64": [_i64, _i64, _i64, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p],
             "oracle_ssm_mamba_fwd": [_i64, _i64, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
             "oracle_selective_scan": [_i64, _i64, _i64, _i64, _int] + [_p] * 11,
             "oracle_selective_scan_f64": [_i64, _i64, _i64, _i64, _int] + [_p] * 11,
@@ -139,15 +140,17 @@ def rmsnorm(X, w, eps):
     return Y
 
 
-def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1):
-    """x [M, L] -> y memory [L, M] (see hx_oracle.c)."""
+def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, f64=False):
+    """x [M, L] -> y memory [L, M] (see hx_oracle.c); f64=True: the double restatement."""
     x, a_real, a_imag, B, C, D, gate = map(_f32, (x, a_real, a_imag, B, C, D, gate))
     M, L = x.shape
     N = a_real.shape[0]
-    y = np.empty((L, M), np.float32)
-    work = np.empty(3 * N + M, np.float32)
-    lib().oracle_s4_ref_fwd(M, N, L, dt, _ptr(x), _ptr(a_real), _ptr(a_imag), _ptr(B), _ptr(C),
-                            _ptr(D), _ptr(gate), _ptr(y), _ptr(work))
+    dt_ = np.float64 if f64 else np.float32
+    y = np.empty((L, M), dt_)
+    work = np.empty(3 * N + M, dt_)
+    fn = lib().oracle_s4_ref_fwd_f64 if f64 else lib().oracle_s4_ref_fwd
+    fn(M, N, L, dt, _ptr(x), _ptr(a_real), _ptr(a_imag), _ptr(B), _ptr(C), _ptr(D), _ptr(gate),
+       _ptr(y), _ptr(work))
     return y
 
 

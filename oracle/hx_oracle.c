@@ -133,6 +133,40 @@ void oracle_s4_ref_fwd(int64_t M, int64_t N, int64_t L, float dt, const float* x
     }
 }
 
+/* oracle_s4_ref_fwd with every operation in double (inputs read as f32, dt widened): the exact
+ * value the f32 restatement approximates. Used where the f32 path's own rounding (sequential
+ * 2048-term sums, |a| ~ 1 recurrences) is comparable to the tolerance. work: 3N + M doubles. */
+void oracle_s4_ref_fwd_f64(int64_t M, int64_t N, int64_t L, float dt, const float* x,
+                           const float* a_real, const float* a_imag, const float* B,
+                           const float* C, const float* D, const float* gate, double* y,
+                           double* work) {
+    double* a = work;
+    double* h = work + N;
+    double* s2 = work + 2 * N;
+    double* u = work + 3 * N;
+    const double dtd = dt;
+    for (int64_t n = 0; n < N; ++n) {
+        a[n] = exp(a_real[n] * dtd) * cos(a_imag[n] * dtd);
+        h[n] = 0.0;
+    }
+    for (int64_t t = 0; t < L; ++t) {
+        for (int64_t m = 0; m < M; ++m) u[m] = x[m * L + t];
+        for (int64_t n = 0; n < N; ++n) {
+            double sum = 0.0;
+            for (int64_t m = 0; m < M; ++m) sum += B[n * M + m] * dtd * u[m];
+            s2[n] = sum;
+        }
+        for (int64_t n = 0; n < N; ++n) h[n] = a[n] * h[n] + s2[n];
+        for (int64_t m = 0; m < M; ++m) {
+            double o = 0.0;
+            for (int64_t n = 0; n < N; ++n) o += C[m * N + n] * h[n];
+            double v = o + D[m] * u[m];
+            if (gate) v *= gate[m];
+            y[t * M + m] = v;
+        }
+    }
+}
+
 /* nn::ssm::MambaBlock::forward_mamba (crates/nn/src/ssm.rs:435-464) for X [M, M]:
  * conv1d is identity (ssm.rs:467-471); delta = X.delta_proj (ssm.rs:450); X.B_proj and X.C_proj
  * are computed and discarded by selective_ssm (ssm.rs:453-454, 474-483), so they are skipped;

@@ -366,6 +366,19 @@ def test_mamba_block_vs_numpy_f64():
     assert rel_err(y, r) < 2e-2
 
 
+def test_s4_ref_f64_matches_numpy_and_f32():
+    M, N, L = 24, 16, 300
+    p = s4_params(M, N, 21, a_real=np.full(N, -0.5), a_imag=np.pi * np.arange(N))
+    x = np.random.default_rng(22).standard_normal((M, L)).astype(F)
+    gate = np.random.default_rng(23).standard_normal(M).astype(F)
+    y64 = oracle.s4_ref_fwd(x, **p, gate=gate, f64=True)
+    assert y64.dtype == np.float64
+    # the C restatement widens the reference's f32 dt = 0.1f; give numpy the same value
+    r = oracle.numpy_s4_ref(x, **p, gate=gate, dt=float(np.float32(0.1)))
+    assert rel_err(y64, r) < 1e-12
+    assert rel_err(oracle.s4_ref_fwd(x, **p, gate=gate), y64) < 1e-4
+
+
 def test_planted_mistakes_are_caught():
     x = inputs(1, 50, 4, 16, 6)
     good = oracle.selective_scan(**x)

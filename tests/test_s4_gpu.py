@@ -5,7 +5,7 @@ import torch
 
 import oracle
 from helixml_amd import ssm
-from tests.util import TOL_F32, rel_err
+from tests.util import TOL_F32, norm_err, rel_err
 
 pytestmark = pytest.mark.gpu
 F = np.float32
@@ -79,3 +79,121 @@ def test_s4_ref_bit_exact(dev, M, N, L):
     g = ssm.s4_ref_fwd(**{k: dv(v, dev) for k, v in p.items()}, gate=dv(gate, dev)).cpu().numpy()
     r = oracle.s4_ref_fwd(**p, gate=gate)
     assert np.array_equal(g, r), f"max abs diff {np.abs(g - r).max()}"
+
+
+# ------------------------------------------------------------------ time-parallel reference mode
+
+@pytest.mark.parametrize("M,N,L", [(64, 16, 100), (8, 4, 16), (5, 3, 1), (130, 16, 513),
+                                   (256, 16, 1000), (40, 16, 4099), (64, 5, 2048)])
+@pytest.mark.parametrize("gated", [False, True])
+@pytest.mark.parametrize("init", ["decay", "default"])
+def test_s4_ref_parallel_matches_oracle(dev, M, N, L, gated, init):
+    """init "decay": config 4's A (|a| <= e^-0.05), compared with the f32 oracle at 1e-4.
+    init "default": the reference's own init (A_real = 0, so |a| = |cos(0.1 A_imag)| ~ 1 - 1e-5):
+    the recurrence is ill-conditioned and the reference's f32 result itself is off the exact
+    value by up to ~5e-3 at these lengths (elementwise, near-zero outputs). The parallel path
+    rounds differently, so it is held to the fp32 bar normwise against the f32 oracle, and
+    elementwise to the same order as the reference's own distance from the float64 restatement
+    (twice it: both share the f32 rounding of a and Bd)."""
+    if init == "decay":
+        p = s4_inputs(M, N, L, seed=M * 31 + L, a_real=np.full(N, -0.5), a_imag=np.pi * np.arange(N))
+    else:
+        p = s4_inputs(M, N, L, seed=M * 31 + L)
+    gate = np.random.default_rng(L).standard_normal(M).astype(F) if gated else None
+    g = ssm.s4_ref_fwd(**{k: dv(v, dev) for k, v in p.items()}, gate=dv(gate, dev), parallel=True)
+    torch.cuda.synchronize()
+    g = g.cpu().numpy()
+    r32 = oracle.s4_ref_fwd(**p, gate=gate)
+    if init == "decay":
+        err = rel_err(g, r32)
+        assert err <= TOL_F32, err
+    else:
+        r64 = oracle.numpy_s4_ref(**p, gate=gate)
+        err, ref_err = rel_err(g, r64), rel_err(r32, r64)
+        nerr = norm_err(g, r32)
+        assert nerr <= TOL_F32, nerr
+        assert err <= 2 * max(TOL_F32, ref_err), (err, ref_err)
+
+
+def test_s4_ref_parallel_rejects_large_dstate(dev):
+    from helixml_amd._ffi import UnsupportedOperation
+    p = s4_inputs(8, 32, 10, seed=1)
+    with pytest.raises(UnsupportedOperation):
+        ssm.s4_ref_fwd(**{k: dv(v, dev) for k, v in p.items()}, parallel=True)
+
+
+def test_s4_ref_parallel_config4_full_size(dev):
+    """BASELINE config 4, S4 reference mode: d_model 2048, N 16, L 65536, A_real = -0.5,
+    A_imag = pi*n, dt = 0.1, over the whole sequence. At this size the f32 reference's own
+    elementwise distance from the exact (float64) result is 1.15e-4 (its 2048-term sequential
+    sums), so the parallel path is held to 1e-4 against the float64 restatement, and normwise
+    to 1e-6 against the f32 restatement."""
+    M, N, L = 2048, 16, 65536
+    p = s4_inputs(M, N, L, seed=404, a_real=np.full(N, -0.5), a_imag=np.pi * np.arange(N))
+    g = ssm.s4_ref_fwd(**{k: dv(v, dev) for k, v in p.items()}, parallel=True)
+    torch.cuda.synchronize()
+    g = g.cpu().numpy()
+    err64 = rel_err(g, oracle.s4_ref_fwd(**p, f64=True))
+    assert err64 <= TOL_F32, err64
+    nerr = norm_err(g, oracle.s4_ref_fwd(**p))
+    assert nerr <= 1e-6, nerr
+
+
+# ------------------------------------------------------------------ S4D complex, wave path
+
+def s4d_inputs(bt, L, dim, N, seed):
+    rng = np.random.default_rng(seed)
+    p = dict(
+        dt=np.full(dim, 0.1, F),
+        a_re=np.full((dim, N), -0.5, F),
+        a_im=np.tile((np.pi * np.arange(N)).astype(F), (dim, 1)),
+        B_re=(rng.standard_normal((dim, N)) * 0.1).astype(F), B_im=(rng.standard_normal((dim, N)) * 0.1).astype(F),
+        C_re=(rng.standard_normal((dim, N)) * 0.1).astype(F), C_im=(rng.standard_normal((dim, N)) * 0.1).astype(F),
+        D=rng.standard_normal(dim).astype(F))
+    return rng.standard_normal((bt, L, dim), dtype=F), p
+
+
+@pytest.mark.parametrize("bt,L,dim,nseg", [(1, 100, 64, 0), (2, 333, 72, 0), (1, 1000, 128, 3),
+                                           (3, 517, 16, 7), (1, 4096, 256, 0), (1, 17, 64, 2)])
+def test_s4d_wave_path(dev, bt, L, dim, nseg):
+    x, p = s4d_inputs(bt, L, dim, 16, seed=L + dim)
+    ssm.set_s4d_segments(nseg)
+    try:
+        g = ssm.s4d_complex_fwd(dv(x, dev), **{k: dv(v, dev) for k, v in p.items()})
+        torch.cuda.synchronize()
+    finally:
+        ssm.set_s4d_segments(0)
+    err = rel_err(g.cpu().numpy(), oracle.s4d_complex(x, **p))
+    assert err <= TOL_F32, err
+
+
+def test_s4d_wave_path_equals_thread_path(dev):
+    x, p = s4d_inputs(2, 300, 64, 16, seed=9)
+    args = (dv(x, dev),)
+    kw = {k: dv(v, dev) for k, v in p.items()}
+    g1 = ssm.s4d_complex_fwd(*args, **kw)
+    ssm.set_s4d_path(1)
+    try:
+        g2 = ssm.s4d_complex_fwd(*args, **kw)
+    finally:
+        ssm.set_s4d_path(0)
+    err = rel_err(g1.cpu().numpy(), g2.cpu().numpy())
+    assert err <= TOL_F32, err
+
+
+def test_s4d_config4_full_size(dev):
+    """BASELINE config 4, S4D complex: batch 1, L 65536, d 2048, N 16 (A = -0.5 + i*pi*n).
+    Channels are independent, so the oracle checks the first and last 16 channels over the
+    whole sequence (every segment boundary and carry), and the whole output is finite."""
+    bt, L, dim = 1, 65536, 2048
+    x, p = s4d_inputs(bt, L, dim, 16, seed=4)
+    g = ssm.s4d_complex_fwd(dv(x, dev), **{k: dv(v, dev) for k, v in p.items()})
+    torch.cuda.synchronize()
+    assert torch.isfinite(g).all()
+    gh = g.cpu().numpy()
+    for lo in (0, dim - 16):
+        sl = slice(lo, lo + 16)
+        ps = {k: (v[sl] if v.ndim >= 1 else v) for k, v in p.items()}
+        r = oracle.s4d_complex(np.ascontiguousarray(x[:, :, sl]), **ps)
+        err = rel_err(gh[:, :, sl], r)
+        assert err <= TOL_F32, (lo, err)
