@@ -7,13 +7,15 @@ d_state 16, fp32, inputs resident in HBM, 3 rotating input sets (1.2 GB) so the 
 cannot serve a step from the previous one. A "step" is one hx_selective_scan_fwd call over one
 batch. Prints ONE JSON line.
 
-  python bench.py [--steps K] [--warmup W] [--workload c2|c2bf16|c3|c4|c4s4|c4s4exact|c4s4d|copy]
-                  [--no-cpu]
+  python bench.py [--steps K] [--warmup W]
+                  [--workload c2|c2bf16|c3|c4|c4s4|c4s4exact|c4s4d|c5|c5dec|copy] [--no-cpu]
 
 c3 = BASELINE config 3, the full Mamba block (in_proj, conv1d+SiLU, x_proj, dt_proj, fused scan,
 out_proj) at batch 4 x L 4096 x d_model 2048, bf16 storage; reported separately from the metric.
 c4s4 / c4s4exact / c4s4d = BASELINE config 4's S4 recurrence (d 2048, N 16, L 65536): reference
 mode time-parallel, reference mode bit-exact, and the S4D diagonal complex form.
+c5 / c5dec = BASELINE config 5's byte LM (12 x (RMSNorm + Mamba), d_model 512): prefill of
+16 x 8192 tokens, and one recurrent decode step at batch 256 (after a 64-token prefill).
 """
 from __future__ import annotations
 
@@ -226,13 +228,66 @@ def bench_s4(args, dev):
         "cpu_baseline": None}))
 
 
+def bench_lm(args, dev):
+    """byte-level LM, 12 x (RMSNorm + Mamba), d_model 512, d_state 16,
+    expand 2, dt_rank 32, conv 4, vocab 256; tokens uniform bytes (seeded)."""
+    from helixml_amd.lm import ByteLM
+    m = ByteLM(device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x48454C49 + 5)
+    if args.workload == "c5":
+        bt, L = 16, 8192
+        toks = [torch.randint(0, 256, (bt, L), generator=gen, device=dev, dtype=torch.int32)
+                for _ in range(2)]
+        states = [m.new_state(bt) for _ in range(2)]
+
+        def step(i):
+            m.prefill(toks[i], states[i])
+
+        steps = max(2, min(args.steps, 10))
+        ms = time_steps(step, 2, steps, min(args.warmup, 2))
+        tokens = bt * L
+        d, N, r, di = m.d_model, m.d_state, m.dt_rank, m.d_inner
+        flops = m.n_layers * 2 * tokens * (2 * di * d + (r + 2 * N) * di + di * r + d * di) \
+            + 2 * tokens * m.vocab * d
+        workload = "byte LM prefill, 12 x (RMSNorm + Mamba) d_model 512, batch 16 x L 8192"
+        extra = {"tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_flops": flops}
+    else:
+        bt = 256
+        pre = torch.randint(0, 256, (bt, 64), generator=gen, device=dev, dtype=torch.int32)
+        _, state = m.prefill(pre)
+        toks = [torch.randint(0, 256, (bt,), generator=gen, device=dev, dtype=torch.int32)
+                for _ in range(4)]
+
+        def step(i):
+            m.decode_step(toks[i], state)
+
+        steps = args.steps
+        ms = time_steps(step, 4, steps, args.warmup)
+        tokens = bt
+        workload = "byte LM recurrent decode step, 12 layers d_model 512, batch 256"
+        extra = {}
+    rec = {
+        "metric": ("byte LM prefill tokens/s (config 5), 1 GPU" if args.workload == "c5"
+                   else "byte LM decode tokens/s (config 5, one step at batch 256), 1 GPU"),
+        "value": tokens * 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16-storage/fp32-compute",
+        "data": "synthetic (uniform byte tokens, random-init weights, seeded)",
+        "config": {"workload": workload, "layers": m.n_layers, "d_model": m.d_model,
+                   "d_inner": m.d_inner, "d_state": m.d_state, "vocab": m.vocab},
+        "cpu_baseline": None, **extra}
+    print(json.dumps(rec))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c2bf16", "c4", "c3", "c4s4", "c4s4exact", "c4s4d", "copy"],
+                    choices=["c2", "c2bf16", "c4", "c3", "c4s4", "c4s4exact", "c4s4d", "c5", "c5dec",
+                             "copy"],
                     help="copy = plain device copy of 512 MiB (HBM ceiling and counter calibration)")
     ap.add_argument("--variant", type=int, default=0, help="scan kernel variant (hx_set_scan_variant)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -266,6 +321,9 @@ def main():
         return
     if args.workload in ("c4s4", "c4s4exact", "c4s4d"):
         bench_s4(args, dev)
+        return
+    if args.workload in ("c5", "c5dec"):
+        bench_lm(args, dev)
         return
     if args.workload in ("c2", "c2bf16"):
         bt, L, dim, N = 8, 2048, 1536, 16

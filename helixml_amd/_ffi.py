@@ -88,6 +88,12 @@ SIGNATURES = {
     "hx_conv1d_silu": [_i64, _i64, _i64, _i64, _int, _p, _i64, _p, _p, _p, _p],
     "hx_mamba_block_workspace_size": [_i64, _i64, _i64, _i64, _i64],
     "hx_mamba_block_fwd": [_i64] * 7 + [_p] * 12 + [_sz, _p],
+    "hx_embedding_fwd": [_i64, _i64, _i64, _p, _p, _p, _p],
+    "hx_rmsnorm_fwd": [_i64, _i64, _p, _p, _f, _int, _p, _p],
+    "hx_conv1d_step": [_i64, _i64, _i64, _int, _p, _i64, _p, _p, _p, _p, _p],
+    "hx_mamba_layer_workspace_size": [_i64] * 6,
+    "hx_mamba_layer_fwd": [_i64] * 7 + [_p, _p, _f] + [_p] * 11 + [_p, _sz, _p],
+    "hx_mamba_layer_decode": [_i64] * 6 + [_p, _p, _f] + [_p] * 11 + [_p, _sz, _p],
     "hx_set_scan_variant": [_int],
     "hx_set_scan_segments": [_int],
     "hx_set_s4d_path": [_int],
@@ -109,7 +115,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = (ctypes.c_char_p if name == "hx_last_error" else
-                          _sz if name == "hx_mamba_block_workspace_size" else _int)
+                          _sz if name.endswith("_workspace_size") else _int)
         _lib = L
     return _lib
 

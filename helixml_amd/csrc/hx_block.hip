@@ -170,7 +170,8 @@ extern "C" int hx_conv1d_silu(int64_t batch, int64_t seqlen, int64_t dim, int64_
 }
 
 // Workspace layout (bf16 elements, M = batch*seqlen): xpart | z | xconv | dt | y  [M, d_inner]
-// each, dt_lo [M, dt_rank], B [M, N], C [M, N]; every region 256-byte aligned.
+// each, dt_lo [M, dt_rank], B [M, N], C [M, N]; every region 256-byte aligned. The layer entry
+// points add a normalised-input region [M, d_model] in front.
 namespace {
 inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 }  // namespace
@@ -181,6 +182,104 @@ extern "C" size_t hx_mamba_block_workspace_size(int64_t batch, int64_t seqlen, i
     return 5 * align256(M * d_inner * 2) + align256(M * dt_rank * 2) + 2 * align256(M * dstate * 2);
 }
 
+extern "C" size_t hx_mamba_layer_workspace_size(int64_t batch, int64_t seqlen, int64_t d_model,
+                                                int64_t d_inner, int64_t dt_rank, int64_t dstate) {
+    return align256((size_t)batch * seqlen * d_model * 2) +
+           hx_mamba_block_workspace_size(batch, seqlen, d_inner, dt_rank, dstate);
+}
+
+namespace hx {
+int conv_state_capture(int64_t Bt, int64_t L, int64_t Dm, int K, const uint16_t* x, int64_t ldx,
+                       float* state, hipStream_t s);
+}  // namespace hx
+
+extern "C" int hx_conv1d_step(int64_t batch, int64_t dim, int64_t width, int dtype, const void* x,
+                              int64_t ldx, const float* weight, const float* bias, float* state,
+                              void* y, void* stream);
+extern "C" int hx_rmsnorm_fwd(int64_t rows, int64_t dim, const float* x, const float* weight,
+                              float eps, int out_dtype, void* y, void* stream);
+
+namespace {
+
+struct BlockWeights {
+    const void *w_in, *w_x, *w_dt, *w_out;
+    const float *conv_w, *conv_b, *dt_bias, *A, *D;
+};
+
+struct BlockBufs {
+    void *xpart, *z, *xconv, *dt, *y, *dtlo, *B, *C;
+};
+
+BlockBufs carve(char* p, int64_t M, int64_t d_inner, int64_t dt_rank, int64_t dstate) {
+    auto take = [&](size_t bytes) { void* r = p; p += align256(bytes); return r; };
+    BlockBufs b;
+    b.xpart = take(M * d_inner * 2);
+    b.z = take(M * d_inner * 2);
+    b.xconv = take(M * d_inner * 2);
+    b.dt = take(M * d_inner * 2);
+    b.y = take(M * d_inner * 2);
+    b.dtlo = take(M * dt_rank * 2);
+    b.B = take(M * dstate * 2);
+    b.C = take(M * dstate * 2);
+    return b;
+}
+
+int check_block_args(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner,
+                     int64_t dstate, int64_t dt_rank, int64_t d_conv, const BlockWeights& w) {
+    using namespace hx;
+    HX_REQUIRE(batch >= 0 && seqlen >= 0 && d_model > 0 && d_inner > 0 && dt_rank > 0,
+               HX_ERR_INVALID_DIMENSION, "mamba_block: bad sizes");
+    HX_REQUIRE(dstate == 16, HX_ERR_UNSUPPORTED, "mamba_block: dstate %lld (16 supported)",
+               (long long)dstate);
+    HX_REQUIRE(d_inner % 4 == 0, HX_ERR_UNSUPPORTED, "mamba_block: d_inner %lld not a multiple of 4",
+               (long long)d_inner);
+    HX_REQUIRE(d_conv >= 1 && d_conv <= 4, HX_ERR_UNSUPPORTED, "mamba_block: d_conv %lld (1..4)",
+               (long long)d_conv);
+    HX_REQUIRE(w.w_in && w.conv_w && w.w_x && w.w_dt && w.A && w.w_out, HX_ERR_INVALID_INPUT,
+               "mamba_block: a required weight pointer is NULL");
+    return HX_OK;
+}
+
+// The block on bf16 input x [M, d_model]: writes out (bf16, or fp32 accumulated into when
+// accumulate) and optionally the scan's last state and the conv window for decode.
+int block_core(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner, int64_t dstate,
+               int64_t dt_rank, int64_t d_conv, const void* x, const BlockWeights& w, void* out,
+               int out_dtype, bool accumulate, float* last_state, float* conv_state,
+               const BlockBufs& b, void* stream) {
+    const int64_t M = batch * seqlen;
+    int rc;
+    // in_proj: [M, d_model] x [2*d_inner, d_model]^T -> xpart | z
+    if ((rc = hx_gemm_bf16(M, 2 * d_inner, d_model, x, d_model, w.w_in, d_model, nullptr, 0,
+                           HX_BF16, b.xpart, d_inner, d_inner, b.z, d_inner, 2 * d_inner, nullptr,
+                           0, stream)))
+        return rc;
+    if (conv_state &&
+        (rc = hx::conv_state_capture(batch, seqlen, d_inner, (int)d_conv, (const uint16_t*)b.xpart,
+                                     d_inner, conv_state, hx::as_stream(stream))))
+        return rc;
+    if ((rc = hx_conv1d_silu(batch, seqlen, d_inner, d_conv, HX_BF16, b.xpart, d_inner, w.conv_w,
+                             w.conv_b, b.xconv, stream)))
+        return rc;
+    // x_proj: [M, d_inner] x [dt_rank + 2N, d_inner]^T -> dt_lo | B | C
+    if ((rc = hx_gemm_bf16(M, dt_rank + 2 * dstate, d_inner, b.xconv, d_inner, w.w_x, d_inner,
+                           nullptr, 0, HX_BF16, b.dtlo, dt_rank, dt_rank, b.B, dstate,
+                           dt_rank + dstate, b.C, dstate, stream)))
+        return rc;
+    // dt_proj: [M, dt_rank] x [d_inner, dt_rank]^T -> dt (dt_bias is added inside the scan)
+    if ((rc = hx_gemm_bf16(M, d_inner, dt_rank, b.dtlo, dt_rank, w.w_dt, dt_rank, nullptr, 0,
+                           HX_BF16, b.dt, d_inner, d_inner, nullptr, 0, d_inner, nullptr, 0, stream)))
+        return rc;
+    if ((rc = hx_selective_scan_fwd(batch, seqlen, d_inner, dstate, HX_BF16, 1, b.xconv, b.dt, w.A,
+                                    b.B, b.C, w.D, b.z, w.dt_bias, b.y, nullptr, last_state, stream)))
+        return rc;
+    // out_proj: [M, d_inner] x [d_model, d_inner]^T -> out (+= out when accumulating)
+    return hx_gemm_bf16(M, d_model, d_inner, b.y, d_inner, w.w_out, d_inner, nullptr,
+                        accumulate ? 2 : 0, out_dtype, out, d_model, d_model, nullptr, 0, d_model,
+                        nullptr, 0, stream);
+}
+
+}  // namespace
+
 extern "C" int hx_mamba_block_fwd(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner,
                                   int64_t dstate, int64_t dt_rank, int64_t d_conv,
                                   const void* x, const void* w_in, const float* conv_w,
@@ -189,50 +288,86 @@ extern "C" int hx_mamba_block_fwd(int64_t batch, int64_t seqlen, int64_t d_model
                                   const void* w_out, void* out, void* workspace,
                                   size_t workspace_bytes, void* stream) {
     using namespace hx;
-    HX_REQUIRE(batch >= 0 && seqlen >= 0 && d_model > 0 && d_inner > 0 && dt_rank > 0,
-               HX_ERR_INVALID_DIMENSION, "mamba_block: bad sizes");
-    HX_REQUIRE(dstate == 16, HX_ERR_UNSUPPORTED, "mamba_block: dstate %lld (16 supported)",
-               (long long)dstate);
-    HX_REQUIRE(d_inner % 4 == 0, HX_ERR_UNSUPPORTED, "mamba_block: d_inner %lld not a multiple of 4",
-               (long long)d_inner);
+    const BlockWeights w{w_in, w_x, w_dt, w_out, conv_w, conv_b, dt_bias, A, D};
+    int rc;
+    if ((rc = check_block_args(batch, seqlen, d_model, d_inner, dstate, dt_rank, d_conv, w))) return rc;
     if (batch == 0 || seqlen == 0) return HX_OK;
-    HX_REQUIRE(x && w_in && conv_w && w_x && w_dt && A && w_out && out && workspace,
-               HX_ERR_INVALID_INPUT, "mamba_block: a required pointer is NULL");
+    HX_REQUIRE(x && out && workspace, HX_ERR_INVALID_INPUT, "mamba_block: x, out, workspace required");
     const size_t need = hx_mamba_block_workspace_size(batch, seqlen, d_inner, dt_rank, dstate);
     HX_REQUIRE(workspace_bytes >= need, HX_ERR_INVALID_INPUT,
                "mamba_block: workspace %zu bytes < %zu required", workspace_bytes, need);
-    const int64_t M = batch * seqlen;
-    char* p = (char*)workspace;
-    auto take = [&](size_t bytes) { void* r = p; p += align256(bytes); return r; };
-    void* xpart = take(M * d_inner * 2);
-    void* zbuf = take(M * d_inner * 2);
-    void* xconv = take(M * d_inner * 2);
-    void* dtb = take(M * d_inner * 2);
-    void* ybuf = take(M * d_inner * 2);
-    void* dtlo = take(M * dt_rank * 2);
-    void* Bb = take(M * dstate * 2);
-    void* Cb = take(M * dstate * 2);
+    const BlockBufs b = carve((char*)workspace, batch * seqlen, d_inner, dt_rank, dstate);
+    return block_core(batch, seqlen, d_model, d_inner, dstate, dt_rank, d_conv, x, w, out, HX_BF16,
+                      false, nullptr, nullptr, b, stream);
+}
+
+extern "C" int hx_mamba_layer_fwd(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner,
+                                  int64_t dstate, int64_t dt_rank, int64_t d_conv, float* resid,
+                                  const float* norm_w, float eps, const void* w_in,
+                                  const float* conv_w, const float* conv_b, const void* w_x,
+                                  const void* w_dt, const float* dt_bias, const float* A,
+                                  const float* D, const void* w_out, float* ssm_state,
+                                  float* conv_state, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    using namespace hx;
+    const BlockWeights w{w_in, w_x, w_dt, w_out, conv_w, conv_b, dt_bias, A, D};
     int rc;
-    // in_proj: [M, d_model] x [2*d_inner, d_model]^T -> xpart | z
-    if ((rc = hx_gemm_bf16(M, 2 * d_inner, d_model, x, d_model, w_in, d_model, nullptr, 0, HX_BF16,
-                           xpart, d_inner, d_inner, zbuf, d_inner, 2 * d_inner, nullptr, 0, stream)))
+    if ((rc = check_block_args(batch, seqlen, d_model, d_inner, dstate, dt_rank, d_conv, w))) return rc;
+    if (batch == 0 || seqlen == 0) return HX_OK;
+    HX_REQUIRE(resid && norm_w && workspace, HX_ERR_INVALID_INPUT,
+               "mamba_layer: resid, norm_w, workspace required");
+    const int64_t M = batch * seqlen;
+    const size_t need = hx_mamba_layer_workspace_size(batch, seqlen, d_model, d_inner, dt_rank, dstate);
+    HX_REQUIRE(workspace_bytes >= need, HX_ERR_INVALID_INPUT,
+               "mamba_layer: workspace %zu bytes < %zu required", workspace_bytes, need);
+    char* p = (char*)workspace;
+    void* xn = p;
+    const BlockBufs b = carve(p + align256((size_t)M * d_model * 2), M, d_inner, dt_rank, dstate);
+    if ((rc = hx_rmsnorm_fwd(M, d_model, resid, norm_w, eps, HX_BF16, xn, stream))) return rc;
+    return block_core(batch, seqlen, d_model, d_inner, dstate, dt_rank, d_conv, xn, w, resid, HX_F32,
+                      true, ssm_state, conv_state, b, stream);
+}
+
+extern "C" int hx_mamba_layer_decode(int64_t batch, int64_t d_model, int64_t d_inner,
+                                     int64_t dstate, int64_t dt_rank, int64_t d_conv, float* resid,
+                                     const float* norm_w, float eps, const void* w_in,
+                                     const float* conv_w, const float* conv_b, const void* w_x,
+                                     const void* w_dt, const float* dt_bias, const float* A,
+                                     const float* D, const void* w_out, float* ssm_state,
+                                     float* conv_state, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    using namespace hx;
+    const BlockWeights w{w_in, w_x, w_dt, w_out, conv_w, conv_b, dt_bias, A, D};
+    int rc;
+    if ((rc = check_block_args(batch, 1, d_model, d_inner, dstate, dt_rank, d_conv, w))) return rc;
+    if (batch == 0) return HX_OK;
+    HX_REQUIRE(resid && norm_w && ssm_state && workspace && (d_conv == 1 || conv_state),
+               HX_ERR_INVALID_INPUT, "mamba_layer_decode: resid, norm_w, ssm_state, conv_state, "
+                                     "workspace required");
+    const size_t need = hx_mamba_layer_workspace_size(batch, 1, d_model, d_inner, dt_rank, dstate);
+    HX_REQUIRE(workspace_bytes >= need, HX_ERR_INVALID_INPUT,
+               "mamba_layer_decode: workspace %zu bytes < %zu required", workspace_bytes, need);
+    char* p = (char*)workspace;
+    void* xn = p;
+    const BlockBufs b = carve(p + align256((size_t)batch * d_model * 2), batch, d_inner, dt_rank, dstate);
+    if ((rc = hx_rmsnorm_fwd(batch, d_model, resid, norm_w, eps, HX_BF16, xn, stream))) return rc;
+    if ((rc = hx_gemm_bf16(batch, 2 * d_inner, d_model, xn, d_model, w.w_in, d_model, nullptr, 0,
+                           HX_BF16, b.xpart, d_inner, d_inner, b.z, d_inner, 2 * d_inner, nullptr,
+                           0, stream)))
         return rc;
-    if ((rc = hx_conv1d_silu(batch, seqlen, d_inner, d_conv, HX_BF16, xpart, d_inner, conv_w,
-                             conv_b, xconv, stream)))
+    if ((rc = hx_conv1d_step(batch, d_inner, d_conv, HX_BF16, b.xpart, d_inner, w.conv_w, w.conv_b,
+                             conv_state, b.xconv, stream)))
         return rc;
-    // x_proj: [M, d_inner] x [dt_rank + 2N, d_inner]^T -> dt_lo | B | C
-    if ((rc = hx_gemm_bf16(M, dt_rank + 2 * dstate, d_inner, xconv, d_inner, w_x, d_inner, nullptr,
-                           0, HX_BF16, dtlo, dt_rank, dt_rank, Bb, dstate, dt_rank + dstate, Cb,
-                           dstate, stream)))
+    if ((rc = hx_gemm_bf16(batch, dt_rank + 2 * dstate, d_inner, b.xconv, d_inner, w.w_x, d_inner,
+                           nullptr, 0, HX_BF16, b.dtlo, dt_rank, dt_rank, b.B, dstate,
+                           dt_rank + dstate, b.C, dstate, stream)))
         return rc;
-    // dt_proj: [M, dt_rank] x [d_inner, dt_rank]^T -> dt (dt_bias is added inside the scan)
-    if ((rc = hx_gemm_bf16(M, d_inner, dt_rank, dtlo, dt_rank, w_dt, dt_rank, nullptr, 0, HX_BF16,
-                           dtb, d_inner, d_inner, nullptr, 0, d_inner, nullptr, 0, stream)))
+    if ((rc = hx_gemm_bf16(batch, d_inner, dt_rank, b.dtlo, dt_rank, w.w_dt, dt_rank, nullptr, 0,
+                           HX_BF16, b.dt, d_inner, d_inner, nullptr, 0, d_inner, nullptr, 0, stream)))
         return rc;
-    if ((rc = hx_selective_scan_fwd(batch, seqlen, d_inner, dstate, HX_BF16, 1, xconv, dtb, A, Bb,
-                                    Cb, D, zbuf, dt_bias, ybuf, nullptr, nullptr, stream)))
+    if ((rc = hx_selective_state_update(batch, d_inner, dstate, HX_BF16, 1, ssm_state, b.xconv, b.dt,
+                                        w.A, b.B, b.C, w.D, b.z, w.dt_bias, b.y, stream)))
         return rc;
-    // out_proj: [M, d_inner] x [d_model, d_inner]^T -> out
-    return hx_gemm_bf16(M, d_model, d_inner, ybuf, d_inner, w_out, d_inner, nullptr, 0, HX_BF16, out,
-                        d_model, d_model, nullptr, 0, d_model, nullptr, 0, stream);
+    return hx_gemm_bf16(batch, d_model, d_inner, b.y, d_inner, w.w_out, d_inner, nullptr, 2, HX_F32,
+                        resid, d_model, d_model, nullptr, 0, d_model, nullptr, 0, stream);
 }

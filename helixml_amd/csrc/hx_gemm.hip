@@ -25,7 +25,7 @@ struct GemmOut {
     int64_t ld[3];
     int64_t split1, split2;  // column boundaries of outputs 0 | 1 | 2
     int out_bf16;
-    int act;                 // 0 none, 1 SiLU
+    int act;                 // bit 0: SiLU; bit 1: accumulate (Y += result, read-modify-write)
 };
 
 // 8 consecutive bf16 of row `row` from column `col`, zero outside [nrows, ncols). VEC: the row
@@ -136,11 +136,17 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_kernel(int64_t M, int64_t N,
                 const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (row >= M) continue;
                 float v = acc[i][j][r] + bv;
-                if (o.act == 1) v = silu(v);
-                if (o.out_bf16)
-                    Storage<uint16_t>::store((uint16_t*)o.y[seg] + row * o.ld[seg] + cc, v);
-                else
-                    ((float*)o.y[seg])[row * o.ld[seg] + cc] = v;
+                if (o.act & 1) v = silu(v);
+                const int64_t off = row * o.ld[seg] + cc;
+                if (o.out_bf16) {
+                    uint16_t* yp = (uint16_t*)o.y[seg] + off;
+                    if (o.act & 2) v += Storage<uint16_t>::load(yp);
+                    Storage<uint16_t>::store(yp, v);
+                } else {
+                    float* yp = (float*)o.y[seg] + off;
+                    if (o.act & 2) v += *yp;
+                    *yp = v;
+                }
             }
         }
 }
@@ -154,7 +160,8 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
                             int64_t split2, void* Y2, int64_t ld2, void* stream) {
     using namespace hx;
     HX_REQUIRE(M >= 0 && N >= 0 && K >= 0, HX_ERR_INVALID_DIMENSION, "gemm_bf16: negative size");
-    HX_REQUIRE(act == 0 || act == 1, HX_ERR_INVALID_INPUT, "gemm_bf16: act=%d (0 none, 1 silu)", act);
+    HX_REQUIRE(act >= 0 && act <= 3, HX_ERR_INVALID_INPUT,
+               "gemm_bf16: act=%d (bit 0 SiLU, bit 1 accumulate into Y)", act);
     HX_REQUIRE(out_dtype == HX_F32 || out_dtype == HX_BF16, HX_ERR_DTYPE_MISMATCH,
                "gemm_bf16: out_dtype %d", out_dtype);
     if (M == 0 || N == 0) return HX_OK;

@@ -152,7 +152,8 @@ int hx_linear_f32(int64_t rows, int64_t in_features, int64_t out_features,
  * W [N, K] (row stride ldw), bf16 (16-byte aligned rows take the fast 16-byte-load path, any
  * other stride an element-load path); fp32 accumulate; out_dtype HX_F32 or
  * HX_BF16. Columns [0, split1) go to Y0 (row stride ld0), [split1, split2) to Y1, [split2, N) to
- * Y2 (split1 = split2 = N for a single output). act: 0 none, 1 SiLU. */
+ * Y2 (split1 = split2 = N for a single output). act: bit 0 applies SiLU, bit 1 accumulates
+ * (Y = Y + result, after the SiLU if both are set): the residual add of a pre-norm layer. */
 int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
                  const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
                  void* Y0, int64_t ld0, int64_t split1, void* Y1, int64_t ld1,
@@ -184,6 +185,53 @@ int hx_mamba_block_fwd(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d
                        const void* w_x, const void* w_dt, const float* dt_bias, const float* A,
                        const float* D, const void* w_out, void* out, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/* ---- byte-level SSM LM: 12 x (RMSNorm + Mamba) with embedding and head ---- */
+
+/* Token embedding gather: out[t][:] = table[tokens[t]][:]; tokens outside [0, vocab) give a zero
+ * row. table [vocab, dim] fp32, out [n_tokens, dim] fp32. (The reference has no Embedding layer;
+ * its byte LM feeds random inputs, examples/ssm_byte_lm/src/main.rs:121-129.) */
+int hx_embedding_fwd(int64_t n_tokens, int64_t vocab, int64_t dim, const int32_t* tokens,
+                     const float* table, float* out, void* stream);
+
+/* nn::RMSNorm::forward (crates/nn/src/lib.rs:258-285) over rows of x [rows, dim] fp32:
+ * y = x / sqrt(mean(x^2) + eps) * weight, y fp32 or bf16 (out_dtype). The reference draws the
+ * epsilon per row from U[eps, eps + 1e-8) (lib.rs:262); this uses eps itself. */
+int hx_rmsnorm_fwd(int64_t rows, int64_t dim, const float* x, const float* weight, float eps,
+                   int out_dtype, void* y, void* stream);
+
+/* One recurrent step of the causal conv: y[b][d] = silu(bias[d] + sum_{j<w-1} weight[d][j] *
+ * state[b][j][d] + weight[d][w-1] * x[b][d]), then state shifts in x. state [batch][w-1][dim]
+ * fp32 (in/out); x rows of stride ldx; y [batch][dim]; dtype of x and y HX_F32 / HX_BF16. */
+int hx_conv1d_step(int64_t batch, int64_t dim, int64_t width, int dtype, const void* x,
+                   int64_t ldx, const float* weight, const float* bias, float* state, void* y,
+                   void* stream);
+
+/* One pre-norm LM layer over a prefill: resid [batch, seqlen, d_model] fp32 (in/out) +=
+ * MambaBlock(RMSNorm(resid)), with the block of hx_mamba_block_fwd. Optional outputs for the
+ * decode hand-off: ssm_state [batch, d_inner, dstate] (the scan's state after the last step) and
+ * conv_state [batch, d_conv-1, d_inner] (the last d_conv-1 conv inputs). workspace: at least
+ * hx_mamba_layer_workspace_size(batch, seqlen, ...) bytes of device memory. */
+size_t hx_mamba_layer_workspace_size(int64_t batch, int64_t seqlen, int64_t d_model,
+                                     int64_t d_inner, int64_t dt_rank, int64_t dstate);
+int hx_mamba_layer_fwd(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner,
+                       int64_t dstate, int64_t dt_rank, int64_t d_conv, float* resid,
+                       const float* norm_w, float eps, const void* w_in, const float* conv_w,
+                       const float* conv_b, const void* w_x, const void* w_dt,
+                       const float* dt_bias, const float* A, const float* D, const void* w_out,
+                       float* ssm_state, float* conv_state, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* One recurrent decode step of the same layer for one token per sequence: resid [batch,
+ * d_model] fp32 (in/out); ssm_state and conv_state (layouts as above) are read and advanced.
+ * workspace: hx_mamba_layer_workspace_size(batch, 1, ...) bytes. */
+int hx_mamba_layer_decode(int64_t batch, int64_t d_model, int64_t d_inner, int64_t dstate,
+                          int64_t dt_rank, int64_t d_conv, float* resid, const float* norm_w,
+                          float eps, const void* w_in, const float* conv_w, const float* conv_b,
+                          const void* w_x, const void* w_dt, const float* dt_bias,
+                          const float* A, const float* D, const void* w_out, float* ssm_state,
+                          float* conv_state, void* workspace, size_t workspace_bytes,
+                          void* stream);
 
 /* CpuTensor::matmul 2-D x 2-D (crates/backend-cpu/src/lib.rs:644-678): Y = A[M,K] . B[K,N]. */
 int hx_matmul_f32(int64_t M, int64_t K, int64_t N, const float* A, const float* B, float* Y,

@@ -22,6 +22,9 @@ Pinning status of each function (how tests/test_oracle.py pins it):
                         decode steps == prefill; f32 vs f64; numpy float64
   conv1d_silu           width 1 == silu(w*x+b); unit impulse -> time-reversed taps; causality
                         (future inputs change nothing); numpy float64 np.convolve per channel
+  lm_prefill/decode     compositions of the pinned pieces above (embedding = array indexing);
+                        cross-checked by decode-after-prefill == prefill of the longer sequence
+  conv1d_step           one step == the last output of conv1d_silu over the window
   mamba_block           composition of linear + conv1d_silu + selective_scan (each pinned),
                         bf16 rounding at the storage points; cross-checked against
                         numpy_mamba_block (float64, same storage rounding)
@@ -242,15 +245,20 @@ def bf16_round(a):
     return np.where(np.isnan(a), a, out)
 
 
-def mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, dt_rank, bf16=True):
+def mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, dt_rank, bf16=True,
+                round_out=True, return_state=False):
     """Mamba block forward: x [Bt, L, d_model] -> [Bt, L, d_model].
     in_proj -> (x | z); SiLU(conv1d(x)); x_proj -> (dt_lo | B | C); dt = dt_lo . w_dt^T;
     selective_scan(softplus(dt + dt_bias)); out_proj. Every intermediate the GPU stores in bf16 is
-    rounded to bf16 here too (``bf16=True``); arithmetic is f32."""
+    rounded to bf16 here too (``bf16=True``); arithmetic is f32. ``round_out=False`` leaves the
+    out_proj result in f32 (the layer form, which adds it to an f32 residual stream).
+    ``return_state``: also return the decode hand-off (scan last state [Bt, d_inner, N], conv
+    window [Bt, d_conv-1, d_inner] = the last d_conv-1 conv inputs)."""
     rnd = bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
     Bt, L, dm = x.shape
     di = w_dt.shape[0]
     N = A.shape[1]
+    K = conv_w.shape[1]
     X = rnd(x).reshape(Bt * L, dm)
     xz = linear(X, rnd(w_in))
     xp = rnd(xz[:, :di]).reshape(Bt, L, di)
@@ -261,8 +269,84 @@ def mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, dt_ran
     Bm = rnd(dbc[:, dt_rank:dt_rank + N]).reshape(Bt, L, N)
     Cm = rnd(dbc[:, dt_rank + N:]).reshape(Bt, L, N)
     dt = rnd(linear(dtlo, rnd(w_dt))).reshape(Bt, L, di)
-    y = rnd(selective_scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True))
-    return rnd(linear(y.reshape(Bt * L, di), rnd(w_out))).reshape(Bt, L, dm)
+    y, last = selective_scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True, return_last_state=True)
+    out = linear(rnd(y).reshape(Bt * L, di), rnd(w_out))
+    out = (rnd(out) if round_out else out).reshape(Bt, L, dm)
+    if not return_state:
+        return out
+    conv = np.zeros((Bt, max(K - 1, 1), di), np.float32)
+    for j in range(K - 1):
+        t = L - (K - 1) + j
+        if t >= 0:
+            conv[:, j, :] = xp[:, t, :]
+    return out, last, conv
+
+
+def conv1d_step(x, w, bias, state):
+    """One recurrent conv step: x [Bt, Dd]; state [Bt, W-1, Dd] (copied, returned advanced)."""
+    x = np.asarray(x, np.float32)
+    w = np.asarray(w, np.float32)
+    W = w.shape[1]
+    win = np.concatenate([np.asarray(state, np.float32)[:, :W - 1, :], x[:, None, :]], axis=1)
+    xc = np.empty(x.shape, np.float32)
+    # same op order as oracle_conv1d_silu: bias, then taps j ascending
+    acc = np.broadcast_to(np.asarray(bias, np.float32), x.shape).astype(np.float32) if bias is not None \
+        else np.zeros(x.shape, np.float32)
+    for j in range(W):
+        acc = (acc + w[:, j][None, :] * win[:, j, :]).astype(np.float32)
+    xc[:] = silu(acc)
+    new_state = win[:, 1:, :].copy() if W > 1 else np.asarray(state, np.float32).copy()
+    return xc, new_state
+
+
+def mamba_layer_decode(resid, p, state, dt_rank, eps):
+    """One decode step of a pre-norm layer; resid [Bt, d_model] f32. Returns (resid, state)."""
+    rnd = bf16_round
+    ssm_st, conv_st = state
+    di = p["w_dt"].shape[0]
+    N = p["A"].shape[1]
+    xn = rnd(rmsnorm(resid, p["norm_w"], eps))
+    xz = linear(xn, rnd(p["w_in"]))
+    xp, z = rnd(xz[:, :di]), rnd(xz[:, di:])
+    xc, conv_st = conv1d_step(xp, p["conv_w"], p["conv_b"], conv_st)
+    xc = rnd(xc)
+    dbc = linear(xc, rnd(p["w_x"]))
+    dtlo = rnd(dbc[:, :dt_rank])
+    Bv, Cv = rnd(dbc[:, dt_rank:dt_rank + N]), rnd(dbc[:, dt_rank + N:])
+    dt = rnd(linear(dtlo, rnd(p["w_dt"])))
+    y, ssm_st = selective_state_update(ssm_st, xc, dt, p["A"], Bv, Cv, p["D"], z, p["dt_bias"], True)
+    resid = (resid + linear(rnd(y), rnd(p["w_out"]))).astype(np.float32)
+    return resid, (ssm_st, conv_st)
+
+
+def lm_head(x, params, eps):
+    shp = x.shape
+    xn = bf16_round(rmsnorm(x.reshape(-1, shp[-1]), params["norm_f"], eps))
+    return linear(xn, bf16_round(params["w_head"])).reshape(*shp[:-1], -1)
+
+
+def lm_prefill(tokens, params, dt_rank, eps=1e-5):
+    """Byte LM prefill: tokens [Bt, L] int -> (logits [Bt, L, vocab] f32, per-layer state)."""
+    x = np.asarray(params["embed"], np.float32)[np.asarray(tokens)]
+    Bt, L, dm = x.shape
+    states = []
+    for p in params["layers"]:
+        xn = bf16_round(rmsnorm(x.reshape(-1, dm), p["norm_w"], eps)).reshape(Bt, L, dm)
+        blk = {k: p[k] for k in ("w_in", "conv_w", "conv_b", "w_x", "w_dt", "dt_bias", "A", "D", "w_out")}
+        out, last, conv = mamba_block(xn, **blk, dt_rank=dt_rank, round_out=False, return_state=True)
+        x = (x + out).astype(np.float32)
+        states.append((last, conv))
+    return lm_head(x, params, eps), states
+
+
+def lm_decode_step(tokens, params, states, dt_rank, eps=1e-5):
+    """One decode step: tokens [Bt] -> (logits [Bt, vocab], new per-layer states)."""
+    x = np.asarray(params["embed"], np.float32)[np.asarray(tokens)]
+    new = []
+    for p, st in zip(params["layers"], states):
+        x, st = mamba_layer_decode(x, p, st, dt_rank, eps)
+        new.append(st)
+    return lm_head(x, params, eps), new
 
 
 # ------------------------------------------------------------------ independent float64 restatements

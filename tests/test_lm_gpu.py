@@ -1,0 +1,180 @@
+"""Byte-level SSM LM on the GPU: embedding, RMSNorm, conv step, pre-norm
+layers (prefill and decode) and the whole model, against the CPU oracle (oracle.lm_prefill /
+oracle.lm_decode_step: f32 arithmetic with bf16 rounding at the device path's storage points).
+Bars: embedding exact; RMSNorm fp32 1e-5 (rel_err); everything through a bf16 GEMM is held
+normwise (max|g - r| / max|r|, see tests/test_block_gpu.py) at 1e-2 against the same-rounding
+oracle. The decode path must continue a prefill: decoding token L after prefilling L tokens
+matches the prefill of L + 1 tokens."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helixml_amd import lm
+from helixml_amd.lm import LAYER_KEYS, ByteLM
+from tests.util import TOL_F32, bf16_round, block_inputs, lm_params, norm_err, rel_err
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+BF_NAMES = {"w_in", "w_x", "w_dt", "w_out", "w_head"}
+
+
+def to_dev(p, dev):
+    return {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev, BF if k in BF_NAMES else torch.float32)
+            for k, v in p.items()}
+
+
+def model_from(P, dev, dt_rank, K=4, eps=1e-5):
+    """A ByteLM whose weights are the given host parameters."""
+    nl = len(P["layers"])
+    dm = P["embed"].shape[1]
+    di = P["layers"][0]["w_dt"].shape[0] if nl else 2 * dm
+    m = ByteLM(n_layers=nl, d_model=dm, d_state=16, d_conv=K, expand=di // dm, dt_rank=dt_rank,
+               vocab=P["embed"].shape[0], eps=eps, device=dev)
+    m.embed = torch.from_numpy(P["embed"]).to(dev)
+    m.norm_f = torch.from_numpy(P["norm_f"]).to(dev)
+    m.w_head = torch.from_numpy(P["w_head"]).to(dev, BF)
+    m.layers = [to_dev(p, dev) for p in P["layers"]]
+    return m
+
+
+def test_embedding_gather_and_invalid_tokens(dev):
+    rng = np.random.default_rng(1)
+    table = rng.standard_normal((256, 96)).astype(np.float32)
+    tok = rng.integers(0, 256, (5, 33)).astype(np.int32)
+    tok[0, 0], tok[1, 1] = -1, 256
+    g = lm.embedding(torch.from_numpy(tok).to(dev), torch.from_numpy(table).to(dev)).cpu().numpy()
+    ref = table[np.clip(tok, 0, 255)]
+    ref[0, 0] = 0
+    ref[1, 1] = 0
+    assert np.array_equal(g, ref)
+
+
+@pytest.mark.parametrize("rows,dim", [(7, 512), (130, 64), (3, 2048), (5, 100), (2, 3000)])
+def test_rmsnorm(dev, rows, dim):
+    rng = np.random.default_rng(rows + dim)
+    x = (rng.standard_normal((rows, dim)) * 3).astype(np.float32)
+    w = rng.standard_normal(dim).astype(np.float32)
+    xd, wd = torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev)
+    ref = oracle.rmsnorm(x, w, 1e-5)
+    g = lm.rmsnorm(xd, wd, 1e-5).cpu().numpy()
+    err = rel_err(g, ref)
+    assert err < 1e-5, err
+    gb = lm.rmsnorm(xd, wd, 1e-5, out_dtype=BF).float().cpu().numpy()
+    err = rel_err(gb, bf16_round(ref))
+    assert err <= 2.0 ** -7, err  # at most one bf16 ulp apart (rounding of nearly equal values)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, BF])
+@pytest.mark.parametrize("K", [4, 3, 2])
+def test_conv1d_step_matches_full_conv(dev, dtype, K):
+    rng = np.random.default_rng(K)
+    bt, L, dim = 3, 12, 40
+    x = bf16_round(rng.standard_normal((bt, L, 2 * dim)).astype(np.float32))
+    w = rng.standard_normal((dim, K)).astype(np.float32)
+    b = rng.standard_normal(dim).astype(np.float32)
+    xd = torch.from_numpy(x).to(dev, dtype)
+    wd, bd = torch.from_numpy(w).to(dev), torch.from_numpy(b).to(dev)
+    state = torch.zeros((bt, K - 1, dim), device=dev)
+    full = oracle.conv1d_silu(x[:, :, :dim], w, b)
+    for t in range(L):
+        y = lm.conv1d_step(xd[:, t, :dim], wd, bd, state).float().cpu().numpy()
+        if dtype == torch.float32:
+            err = rel_err(y, full[:, t])
+            assert err < TOL_F32, (t, err)
+        else:
+            err = norm_err(y, full[:, t])
+            assert err <= 2.0 ** -8, (t, err)
+    # the state holds the last K-1 inputs
+    want = x[:, L - (K - 1):, :dim].transpose(0, 1, 2)
+    assert np.array_equal(state.cpu().numpy(), want.astype(np.float32))
+
+
+def run_layer(dev, p, x, dt_rank, eps=1e-5):
+    bt, L, dm = x.shape
+    di = p["w_dt"].shape[0]
+    K = p["conv_w"].shape[1]
+    d = to_dev(p, dev)
+    resid = torch.from_numpy(x).to(dev).contiguous()
+    ssm_st = torch.zeros((bt, di, 16), device=dev)
+    conv_st = torch.zeros((bt, K - 1, di), device=dev)
+    need = int(lm._ffi.lib().hx_mamba_layer_workspace_size(bt, L, dm, di, dt_rank, 16))
+    ws = torch.empty(need, device=dev, dtype=torch.uint8)
+    lm._ffi.call("hx_mamba_layer_fwd", bt, L, dm, di, 16, dt_rank, K, resid.data_ptr(),
+                 d["norm_w"].data_ptr(), eps, *[d[k].data_ptr() for k in LAYER_KEYS],
+                 ssm_st.data_ptr(), conv_st.data_ptr(), ws.data_ptr(), need,
+                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return resid.cpu().numpy(), ssm_st.cpu().numpy(), conv_st.cpu().numpy()
+
+
+@pytest.mark.parametrize("bt,L,dm,di,r", [(2, 40, 64, 128, 8), (1, 130, 32, 64, 8), (3, 17, 48, 96, 16)])
+def test_layer_prefill_and_state_handoff(dev, bt, L, dm, di, r):
+    p = block_inputs(1, 1, dm, di, 16, r, 4, seed=bt + L)
+    p.pop("x")
+    p["norm_w"] = np.random.default_rng(L).uniform(0.5, 1.5, dm).astype(np.float32)
+    x = np.random.default_rng(bt).standard_normal((bt, L, dm)).astype(np.float32)
+    g, g_ssm, g_conv = run_layer(dev, p, x, r)
+    xn = bf16_round(oracle.rmsnorm(x.reshape(-1, dm), p["norm_w"], 1e-5)).reshape(bt, L, dm)
+    blk = {k: p[k] for k in LAYER_KEYS}
+    out, last, conv = oracle.mamba_block(xn, **blk, dt_rank=r, round_out=False, return_state=True)
+    ref = x + out
+    err = norm_err(g - x, ref - x)
+    assert err <= 1e-2, err
+    err = norm_err(g_ssm, last)
+    assert err <= 1e-2, err
+    assert np.array_equal(g_conv, conv)  # the conv window is copied bf16 inputs
+
+
+def test_lm_prefill_and_decode_vs_oracle(dev):
+    P = lm_params(2, 64, 128, 16, 8, 4, 256, seed=5)
+    m = model_from(P, dev, dt_rank=8)
+    tok = np.random.default_rng(6).integers(0, 256, (3, 20)).astype(np.int32)
+    td = torch.from_numpy(tok).to(dev)
+    logits, state = m.prefill(td[:, :18])
+    torch.cuda.synchronize()
+    ref, rstate = oracle.lm_prefill(tok[:, :18], P, 8)
+    err = norm_err(logits.cpu().numpy(), ref)
+    assert err <= 1e-2, err
+    for t in (18, 19):
+        lg = m.decode_step(td[:, t], state)
+        torch.cuda.synchronize()
+        rl, rstate = oracle.lm_decode_step(tok[:, t], P, rstate, 8)
+        err = norm_err(lg.cpu().numpy(), rl)
+        assert err <= 1e-2, (t, err)
+    # decode continues the prefill: same logits as prefilling all 20 tokens
+    full, _ = m.prefill(td)
+    err = norm_err(lg.cpu().numpy(), full[:, 19].cpu().numpy())
+    assert err <= 1e-2, err
+
+
+def test_lm_config5_full_size(dev):
+    """12 layers, d_model 512, d_inner 1024, N 16, dt_rank 32, conv 4, vocab
+    256, batch 16 x L 8192 prefill, then one decode step for all 16 sequences. The oracle checks
+    the first 24 positions of the first and last sequences (the model is causal and the batch
+    rows independent) and the decode step of those two sequences after a 24-token prefill."""
+    m = ByteLM(device=dev)
+    P = m.host_params()
+    bt, L = 16, 8192
+    rng = np.random.default_rng(0x48454C49)
+    tok = rng.integers(0, 256, (bt, L)).astype(np.int32)
+    td = torch.from_numpy(tok).to(dev)
+    logits, state = m.prefill(td)
+    torch.cuda.synchronize()
+    assert torch.isfinite(logits).all()
+    T = 24
+    for b in (0, bt - 1):
+        ref, _ = oracle.lm_prefill(tok[b:b + 1, :T], P, m.dt_rank)
+        err = norm_err(logits[b:b + 1, :T].cpu().numpy(), ref)
+        assert err <= 1e-2, (b, err)
+    lg = m.decode_step(td[:, -1], state)
+    torch.cuda.synchronize()
+    assert torch.isfinite(lg).all()
+    sub = tok[[0, bt - 1], :T]
+    _, rst = oracle.lm_prefill(sub[:, :T - 1], P, m.dt_rank)
+    rl, _ = oracle.lm_decode_step(sub[:, T - 1], P, rst, m.dt_rank)
+    small, st2 = m.prefill(torch.from_numpy(np.ascontiguousarray(sub[:, :T - 1])).to(dev))
+    g2 = m.decode_step(torch.from_numpy(np.ascontiguousarray(sub[:, T - 1])).to(dev), st2)
+    torch.cuda.synchronize()
+    err = norm_err(g2.cpu().numpy(), rl)
+    assert err <= 1e-2, err

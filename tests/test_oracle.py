@@ -379,6 +379,53 @@ def test_s4_ref_f64_matches_numpy_and_f32():
     assert rel_err(oracle.s4_ref_fwd(x, **p, gate=gate), y64) < 1e-4
 
 
+def test_conv1d_step_equals_last_conv_output():
+    rng = np.random.default_rng(40)
+    x = rng.standard_normal((2, 9, 12)).astype(F)
+    w = rng.standard_normal((12, 4)).astype(F)
+    b = rng.standard_normal(12).astype(F)
+    full = oracle.conv1d_silu(x, w, b)
+    state = np.zeros((2, 3, 12), F)
+    for t in range(9):
+        y, state = oracle.conv1d_step(x[:, t], w, b, state)
+        assert np.array_equal(y, full[:, t]), t
+
+
+def test_lm_decode_after_prefill_equals_longer_prefill():
+    from tests.util import lm_params
+    P = lm_params(2, 32, 64, 16, 8, 4, 256, seed=41)
+    tok = np.random.default_rng(42).integers(0, 256, (3, 11))
+    full, _ = oracle.lm_prefill(tok, P, 8)
+    pre, st = oracle.lm_prefill(tok[:, :9], P, 8)
+    assert np.array_equal(pre, full[:, :9])
+    d1, st = oracle.lm_decode_step(tok[:, 9], P, st, 8)
+    d2, st = oracle.lm_decode_step(tok[:, 10], P, st, 8)
+    assert rel_err(d1, full[:, 9]) < 1e-5 and rel_err(d2, full[:, 10]) < 1e-5
+
+
+def test_lm_zero_layers_is_head_of_embedding():
+    from tests.util import lm_params
+    P = lm_params(0, 32, 64, 16, 8, 4, 256, seed=43)
+    tok = np.array([[0, 255, 7]])
+    lg, _ = oracle.lm_prefill(tok, P, 8)
+    xn = oracle.bf16_round(P["embed"][tok[0]] / np.sqrt((P["embed"][tok[0]] ** 2).mean(-1, keepdims=True) + 1e-5)
+                           * P["norm_f"])
+    ref = xn.astype(np.float64) @ P["w_head"].astype(np.float64).T
+    assert rel_err(lg[0], ref) < 1e-2  # one bf16 flip of the normalised input at most
+
+
+def test_rmsnorm_random_eps_is_below_resolution():
+    # the reference draws eps' ~ U[eps, eps + 1e-8) per row (nn/src/lib.rs:262); on rows with
+    # mean square >= 1e-2 the jitter is below f32 resolution of ms + eps, so a fixed eps agrees
+    rng = np.random.default_rng(44)
+    x = rng.standard_normal((64, 512)).astype(F)
+    w = rng.standard_normal(512).astype(F)
+    y0 = oracle.rmsnorm(x, w, 1e-5)
+    for _ in range(3):
+        ej = np.float32(1e-5 + rng.uniform(0, 1e-8))
+        assert rel_err(oracle.rmsnorm(x, w, ej), y0) < 1e-6
+
+
 def test_planted_mistakes_are_caught():
     x = inputs(1, 50, 4, 16, 6)
     good = oracle.selective_scan(**x)

@@ -75,3 +75,21 @@ def block_inputs(bt, L, dm, di, N, dt_rank, k, seed):
         D=rng.standard_normal(di).astype(f),
         w_out=bf16_round(nrm((dm, di), di)),
     )
+
+
+def lm_params(n_layers, dm, di, N, r, K, vocab, seed):
+    """Byte-LM parameters (float32 arrays; projection weights bf16-representable), the
+    distributions of helixml_amd.lm.ByteLM with random RMSNorm weights so a dropped weight shows."""
+    rng = np.random.default_rng(seed)
+    f = np.float32
+    layers = []
+    for i in range(n_layers):
+        p = block_inputs(1, 1, dm, di, N, r, K, seed=seed * 100 + i)
+        p.pop("x")
+        p["D"] = np.ones(di, f)
+        p["norm_w"] = (1.0 + 0.1 * rng.standard_normal(dm)).astype(f)
+        layers.append(p)
+    return dict(embed=rng.standard_normal((vocab, dm), dtype=f),
+                norm_f=(1.0 + 0.1 * rng.standard_normal(dm)).astype(f),
+                w_head=bf16_round(rng.standard_normal((vocab, dm), dtype=f) * f(np.sqrt(2.0 / dm))),
+                layers=layers)
