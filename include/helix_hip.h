@@ -4,9 +4,11 @@
  *
  * This is the drop-in boundary a Rust `crates/backend-hip` binds with an `extern "C"` block
  * (the binding is shown in INTEGRATION.md). Every entry point takes plain pointers, sizes and
- * enums: no HIP, torch or C++ types cross it. Device buffers are allocated by the caller
- * (hx_malloc, or any HIP allocation on the same device); the library never allocates on the
- * caller's behalf except in hx_malloc. A `stream` argument is a hipStream_t passed as void*
+ * enums: no HIP, torch or C++ types cross it. Inputs and outputs are allocated by the caller
+ * (hx_malloc, or any HIP allocation on the same device). Block and layer entry points take a
+ * caller-owned workspace (sizes from the *_workspace_size functions); the long-sequence scan
+ * and the S4 paths take stream-ordered scratch (hipMallocAsync / hipFreeAsync on `stream`).
+ * A `stream` argument is a hipStream_t passed as void*
  * (NULL = the legacy default stream). All compute entry points are stream-ordered and
  * asynchronous; they validate shapes on the host before any launch and return a status code.
  * No C++ exception or panic crosses this boundary.
