@@ -49,12 +49,21 @@ class BackendError(TensorError):
     status = 7
 
 
+class SerializationError(TensorError):
+    status = 8
+
+
 class InvalidInput(TensorError):
     status = 9
 
 
+class InvalidCheckpoint(TensorError):
+    status = 10
+
+
 _BY_STATUS = {c.status: c for c in (ShapeMismatch, InvalidDimension, DeviceMismatch, DTypeMismatch,
-                                    UnsupportedOperation, AllocationFailed, BackendError, InvalidInput)}
+                                    UnsupportedOperation, AllocationFailed, BackendError,
+                                    SerializationError, InvalidInput, InvalidCheckpoint)}
 
 HX_F32 = 0
 HX_BF16 = 1
@@ -75,6 +84,7 @@ SIGNATURES = {
     "hx_memcpy_d2h": [_p, _p, _sz],
     "hx_memcpy_d2d": [_p, _p, _sz, _p],
     "hx_sync": [],
+    "hx_device_info": [_int, ctypes.POINTER(_int), ctypes.POINTER(_sz)],
     "hx_last_error": [],
     "hx_selective_scan_fwd": [_i64, _i64, _i64, _i64, _int, _int] + [_p] * 11 + [_p],
     "hx_selective_state_update": [_i64, _i64, _i64, _int, _int] + [_p] * 10 + [_p],

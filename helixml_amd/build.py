@@ -1,8 +1,8 @@
 """Builds libhelix_hip.so (gfx950) in-tree with hipcc.
 
-Each ``csrc/*.hip`` file is compiled to an object in parallel, then linked into
-``helixml_amd/libhelix_hip.so``. The library has no torch dependency: the C ABI in
-``include/helix_hip.h`` is the whole interface.
+Each ``csrc/*.hip`` file (kernels and the C ABI) is compiled with hipcc and each ``host/*.cpp``
+file (the native C++ host layer of ``include/helix/helix.hpp``) with g++, in parallel; all are
+linked into ``helixml_amd/libhelix_hip.so``. The library has no torch dependency.
 """
 from __future__ import annotations
 
@@ -48,16 +48,24 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
+HOST = PKG / "host"
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}"]
+
+
 def sources() -> list[Path]:
-    return sorted(CSRC.glob("*.hip"))
+    return sorted(CSRC.glob("*.hip")) + sorted(HOST.glob("*.cpp"))
 
 
 def _compile(src: Path) -> Path:
-    obj = OBJDIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        obj = OBJDIR / (src.stem + ".host.o")
+        cmd = [os.environ.get("CXX", "g++"), *CXX_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        obj = OBJDIR / (src.stem + ".o")
+        cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+        raise RuntimeError(f"compile failed for {src.name}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     return obj
 
 

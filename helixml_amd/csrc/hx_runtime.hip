@@ -83,4 +83,12 @@ int hx_sync(void) {
     return HX_OK;
 }
 
+int hx_device_info(int device, int* compute_units, size_t* memory_bytes) {
+    hipDeviceProp_t prop;
+    HX_HIP_CHECK(hipGetDeviceProperties(&prop, device));
+    if (compute_units) *compute_units = prop.multiProcessorCount;
+    if (memory_bytes) *memory_bytes = prop.totalGlobalMem;
+    return HX_OK;
+}
+
 }  // extern "C"

@@ -42,7 +42,9 @@ typedef enum {
     HX_ERR_UNSUPPORTED = 5,        /* TensorError::UnsupportedOperation (error.rs:21) */
     HX_ERR_ALLOCATION = 6,         /* TensorError::AllocationFailed   (error.rs:24) */
     HX_ERR_BACKEND = 7,            /* TensorError::BackendError       (error.rs:27) */
-    HX_ERR_INVALID_INPUT = 9       /* TensorError::InvalidInput       (error.rs:36) */
+    HX_ERR_SERIALIZATION = 8,      /* TensorError::SerializationError (error.rs:30) */
+    HX_ERR_INVALID_INPUT = 9,      /* TensorError::InvalidInput       (error.rs:36) */
+    HX_ERR_INVALID_CHECKPOINT = 10 /* TensorError::InvalidCheckpoint  (error.rs:33) */
 } hx_status;
 
 /* Storage dtypes. Arithmetic and recurrent state are always fp32.
@@ -65,6 +67,9 @@ int hx_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int hx_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 /* Waits for all work on the device. */
 int hx_sync(void);
+/* Compute units and global memory bytes of `device` (for hal::ComputeBackend::compute_units and
+ * capabilities, hal/src/backend.rs:31-35). */
+int hx_device_info(int device, int* compute_units, size_t* memory_bytes);
 /* Text of the last error raised on the calling thread ("" if none). Becomes the message of
  * TensorError::BackendError / the variant matching the status. */
 const char* hx_last_error(void);

@@ -1,0 +1,391 @@
+// test_host.cpp — tests of the native C++ host layer (include/helix/helix.hpp), written the way
+// the reference's own Rust tests read (crates/backend-cpu/src/lib.rs:1733-1758,
+// crates/training/src/checkpoint.rs:290+, crates/nn tests): construct modules, run forward,
+// compare. GPU results are checked against the C oracle (oracle/hx_oracle.c, linked here as test
+// infrastructure), bit for bit where the device path reproduces the reference's f32 order.
+//
+//   helix_host_tests --cpu [checkpoint_path]   host-only tests (no GPU touched); writes a
+//                                               checkpoint of known tensors for the Python
+//                                               cross-check of the byte format
+//   helix_host_tests --gpu                     device tests
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "helix/helix.hpp"
+
+extern "C" {
+void oracle_matmul(int64_t M, int64_t K, int64_t N, const float* A, const float* B, float* Y);
+void oracle_linear(int64_t R, int64_t IN, int64_t OUT, const float* X, const float* W,
+                   const float* bias, int act, float* Y);
+void oracle_mamba_mlp(int64_t R, int64_t d_model, int64_t d_inner, const float* X, const float* Wg,
+                      const float* bg, const float* Wo, const float* bo, float* tmp, float* Y);
+void oracle_rmsnorm(int64_t R, int64_t Dm, const float* X, const float* w, float eps, float* Y);
+void oracle_s4_ref_fwd(int64_t M, int64_t N, int64_t L, float dt, const float* x,
+                       const float* a_real, const float* a_imag, const float* B, const float* C,
+                       const float* D, const float* gate, float* y, float* work);
+void oracle_ssm_mamba_fwd(int64_t M, int64_t N, float dt, const float* X, const float* delta_proj,
+                          const float* a_real, const float* a_imag, const float* B, const float* C,
+                          const float* D, const float* gate, float* y, float* work);
+void oracle_selective_scan(int64_t Bt, int64_t L, int64_t Dd, int64_t N, int delta_softplus,
+                           const float* u, const float* delta, const float* A, const float* Bm,
+                           const float* Cm, const float* D, const float* z, const float* dt_bias,
+                           float* out, const float* init_state, float* last_state);
+}
+
+using namespace helix;
+
+namespace {
+int g_fail = 0, g_run = 0;
+std::string g_cur;
+
+#define CHECK(cond)                                                                        \
+    do {                                                                                   \
+        if (!(cond)) {                                                                     \
+            std::printf("  FAIL %s: %s (line %d)\n", g_cur.c_str(), #cond, __LINE__);      \
+            ++g_fail;                                                                      \
+            return;                                                                        \
+        }                                                                                  \
+    } while (0)
+
+template <typename F>
+bool throws_kind(F&& f, ErrorKind k, std::string* msg = nullptr) {
+    try {
+        f();
+    } catch (const TensorError& e) {
+        if (msg) *msg = e.what();
+        return e.kind() == k;
+    }
+    return false;
+}
+
+bool bits_equal(const std::vector<float>& a, const std::vector<float>& b) {
+    return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * 4) == 0;
+}
+
+double rel_err(const std::vector<float>& g, const std::vector<float>& r) {
+    double amax = 0.0, e = 0.0;
+    for (float v : r) amax = std::fmax(amax, std::fabs(v));
+    const double floor = 1e-3 * (amax > 0 ? amax : 1e-30);
+    for (size_t i = 0; i < g.size(); ++i)
+        e = std::fmax(e, std::fabs((double)g[i] - r[i]) / std::fmax(std::fabs((double)r[i]), floor));
+    return e;
+}
+
+struct Case {
+    const char* name;
+    bool gpu;
+    std::function<void()> fn;
+};
+std::vector<Case>& cases() {
+    static std::vector<Case> c;
+    return c;
+}
+struct Reg {
+    Reg(const char* n, bool gpu, std::function<void()> f) { cases().push_back({n, gpu, std::move(f)}); }
+};
+#define TEST_CPU(name) static void name(); static Reg reg_##name(#name, false, name); static void name()
+#define TEST_GPU(name) static void name(); static Reg reg_##name(#name, true, name); static void name()
+
+std::vector<float> randn(size_t n, uint64_t seed, float std = 1.0f) {
+    Rng r(seed);
+    std::vector<float> v(n);
+    for (auto& x : v) x = r.normal(0.0f, std);
+    return v;
+}
+
+std::string g_ckpt_path;
+}  // namespace
+
+// ============================================================================ host-only tests
+TEST_CPU(shape_dim_out_of_range_is_invalid_dimension) {
+    Shape s({2, 3});
+    CHECK(s.numel() == 6 && s.dim(1) == 3);
+    CHECK(throws_kind([&] { (void)s.dim(2); }, ErrorKind::InvalidDimension));
+}
+
+TEST_CPU(rng_normal_and_uniform_moments) {
+    Rng r(0x48454C49);
+    double s = 0, s2 = 0, umin = 1e9, umax = -1e9;
+    const int n = 200000;
+    for (int i = 0; i < n; ++i) {
+        const double x = r.normal(0.0f, 0.1f);
+        s += x;
+        s2 += x * x;
+        const double u = r.uniform(0.001f, 0.1f);
+        umin = std::fmin(umin, u);
+        umax = std::fmax(umax, u);
+    }
+    const double mean = s / n, sd = std::sqrt(s2 / n - mean * mean);
+    CHECK(std::fabs(mean) < 1e-3 && std::fabs(sd - 0.1) < 1e-3);
+    CHECK(umin >= 0.001 && umax < 0.1 && umin < 0.0011 && umax > 0.0999);
+}
+
+TEST_CPU(status_codes_map_to_tensor_error_variants) {
+    CHECK(TensorError::from_status(1, "").kind() == ErrorKind::ShapeMismatch);
+    CHECK(TensorError::from_status(5, "").kind() == ErrorKind::UnsupportedOperation);
+    CHECK(TensorError::from_status(8, "").kind() == ErrorKind::SerializationError);
+    CHECK(TensorError::from_status(9, "").kind() == ErrorKind::InvalidInput);
+    CHECK(TensorError::from_status(10, "").kind() == ErrorKind::InvalidCheckpoint);
+    CHECK(TensorError::from_status(7, "").kind() == ErrorKind::BackendError);
+}
+
+TEST_CPU(checkpoint_bytes_round_trip) {
+    std::vector<HostTensor> p = {{{3}, {1.0f, -2.5f, 3.25f}},
+                                 {{2, 2}, {0.0f, -0.0f, 1e-30f, 7.0f}},
+                                 {{}, {42.0f}},
+                                 {{0, 4}, {}}};
+    const auto bytes = encode_params(p);
+    // Vec length 4 (u64 LE) first
+    CHECK(bytes.size() > 8 && bytes[0] == 4 && bytes[1] == 0 && bytes[7] == 0);
+    const auto q = decode_params(bytes);
+    CHECK(q.size() == p.size());
+    for (size_t i = 0; i < p.size(); ++i) {
+        CHECK(q[i].shape == p[i].shape);
+        CHECK(bits_equal(q[i].values, p[i].values));
+    }
+    // truncation and trailing bytes are serialization errors
+    auto cut = bytes;
+    cut.pop_back();
+    CHECK(throws_kind([&] { (void)decode_params(cut); }, ErrorKind::SerializationError));
+    auto extra = bytes;
+    extra.push_back(0);
+    CHECK(throws_kind([&] { (void)decode_params(extra); }, ErrorKind::SerializationError));
+    // a count that cannot fit the buffer is refused before allocating
+    auto huge = bytes;
+    huge[6] = 0x7f;
+    CHECK(throws_kind([&] { (void)decode_params(huge); }, ErrorKind::SerializationError));
+}
+
+TEST_CPU(checkpoint_file_layout) {
+    const std::string meta = "{\"epoch\":3,\"step\":120}";
+    std::vector<HostTensor> p = {{{2, 3}, {1, 2, 3, 4, 5, 6}}, {{4}, {0.5f, -0.5f, 0.25f, 8.0f}}};
+    const std::string path = g_ckpt_path.empty() ? "/tmp/helix_ckpt_test.bin" : g_ckpt_path;
+    save_checkpoint(path, meta, p);
+    auto [m2, q] = load_checkpoint_host(path);
+    CHECK(m2 == meta);
+    CHECK(q.size() == 2 && q[0].shape == p[0].shape && bits_equal(q[1].values, p[1].values));
+    FILE* f = std::fopen(path.c_str(), "rb");
+    CHECK(f);
+    unsigned char hdr[4];
+    CHECK(std::fread(hdr, 1, 4, f) == 4);
+    std::fclose(f);
+    CHECK(hdr[0] == 0 && hdr[1] == 0 && hdr[2] == 0 && hdr[3] == meta.size());  // u32 big-endian
+}
+
+// ============================================================================ device tests
+TEST_GPU(reference_kat_matmul_ones) {
+    // backend-cpu/src/lib.rs:1747-1758: ones[2,3] . ones[3,4] == 3
+    auto a = HipTensor::ones(Shape({2, 3}));
+    auto b = HipTensor::ones(Shape({3, 4}));
+    auto y = a.matmul(b);
+    CHECK((y.shape() == Shape({2, 4})));
+    for (float v : y.to_host()) CHECK(std::fabs(v - 3.0f) < 1e-6f);
+    std::string msg;
+    CHECK(throws_kind([&] { (void)a.matmul(HipTensor::ones(Shape({4, 2}))); }, ErrorKind::ShapeMismatch, &msg));
+    CHECK(msg.find("expected [3], got [4]") != std::string::npos);
+}
+
+TEST_GPU(matmul_bit_exact_vs_cpu_tensor_order) {
+    const size_t M = 37, K = 129, N = 70;
+    auto av = randn(M * K, 1), bv = randn(K * N, 2);
+    auto y = HipTensor::from_host(av, Shape({M, K})).matmul(HipTensor::from_host(bv, Shape({K, N})));
+    std::vector<float> r(M * N);
+    oracle_matmul(M, K, N, av.data(), bv.data(), r.data());
+    CHECK(bits_equal(y.to_host(), r));
+}
+
+TEST_GPU(linear_and_exported_mamba_block_vs_oracle) {
+    Rng rng(7);
+    MambaBlock blk(64, 16, 4, 2, rng);  // README example shape (config 1)
+    auto xv = randn(100 * 64, 3);
+    for (auto& v : xv) v = std::fmod(v, 1.0f);
+    auto x = HipTensor::from_host(xv, Shape({100, 64}));
+    auto y = blk.forward(x).to_host();
+    std::vector<float> tmp(100 * 128), r(100 * 64);
+    auto wg = blk.gate().weight().to_host(), bg = blk.gate().bias().to_host();
+    auto wo = blk.out_proj().weight().to_host(), bo = blk.out_proj().bias().to_host();
+    oracle_mamba_mlp(100, 64, 128, xv.data(), wg.data(), bg.data(), wo.data(), bo.data(), tmp.data(), r.data());
+    CHECK(rel_err(y, r) < 1e-4);  // the fp32 bar (device SiLU vs libm expf differ by ulps)
+    std::vector<float> r2(100 * 128);
+    oracle_linear(100, 64, 128, xv.data(), wg.data(), bg.data(), 0, r2.data());
+    CHECK(bits_equal(blk.gate().forward(x).to_host(), r2));
+}
+
+TEST_GPU(rmsnorm_vs_oracle) {
+    RMSNorm norm(512, 1e-5f);
+    auto xv = randn(33 * 512, 4, 2.0f);
+    auto y = norm.forward(HipTensor::from_host(xv, Shape({33, 512}))).to_host();
+    std::vector<float> w(512, 1.0f), r(33 * 512);
+    oracle_rmsnorm(33, 512, xv.data(), w.data(), 1e-5f, r.data());
+    CHECK(rel_err(y, r) < 1e-5);
+}
+
+TEST_GPU(s4block_forward_ssm_bit_exact_and_shape_rules) {
+    Rng rng(11);
+    S4Block s4(64, 16, rng);  // ssm::S4Block::new(64, 16) distributions
+    const size_t L = 100;
+    auto xv = randn(64 * L, 5);
+    auto y = s4.forward_ssm(HipTensor::from_host(xv, Shape({64, L})));
+    CHECK((y.shape() == Shape({64, L})));  // the reference's shape field; memory is [L, 64]
+    std::vector<float> r(L * 64), work(3 * 16 + 64);
+    auto ar = s4.A_real.to_host(), ai = s4.A_imag.to_host(), B = s4.B.to_host(), C = s4.C.to_host(),
+         D = s4.D.to_host();
+    oracle_s4_ref_fwd(64, 16, L, 0.1f, xv.data(), ar.data(), ai.data(), B.data(), C.data(), D.data(),
+                      nullptr, r.data(), work.data());
+    CHECK(bits_equal(y.to_host(), r));
+    // ssm.rs:142-147: dim 0 must be d_model
+    std::string msg;
+    CHECK(throws_kind([&] { (void)s4.forward_ssm(HipTensor::zeros(Shape({100, 64}))); },
+                      ErrorKind::ShapeMismatch, &msg));
+    CHECK(msg.find("expected [64], got [100]") != std::string::npos);
+    // the time-parallel form agrees to rounding on a decaying system
+    S4Block s4b(64, 16, rng);
+    std::vector<float> are(16, -0.5f), aim(16);
+    for (int n = 0; n < 16; ++n) aim[n] = (float)(M_PI * n);
+    s4b.A_real = HipTensor::from_host(are, Shape({16}));
+    s4b.A_imag = HipTensor::from_host(aim, Shape({16}));
+    auto xp = HipTensor::from_host(xv, Shape({64, L}));
+    // D = 0 in this init, so outputs cross zero: compared normwise
+    auto yp = s4b.forward_ssm(xp, nullptr, true).to_host(), ye = s4b.forward_ssm(xp).to_host();
+    double num = 0, den = 0;
+    for (size_t i = 0; i < yp.size(); ++i) {
+        num = std::fmax(num, std::fabs((double)yp[i] - ye[i]));
+        den = std::fmax(den, std::fabs((double)ye[i]));
+    }
+    CHECK(num <= 1e-5 * den);
+}
+
+TEST_GPU(s4block_checkpoint_restore_through_file) {
+    Rng rng(13);
+    S4Block a(32, 8, rng), b(32, 8, rng);
+    auto x = HipTensor::from_host(randn(32 * 50, 6), Shape({32, 50}));
+    const std::string path = "/tmp/helix_s4_ckpt.bin";
+    save_checkpoint(path, "{\"epoch\":0}", a.checkpoint());
+    auto [meta, params] = load_checkpoint(path);
+    CHECK(meta == "{\"epoch\":0}" && params.size() == 7);
+    b.restore(params);
+    CHECK(bits_equal(a.forward_ssm(x).to_host(), b.forward_ssm(x).to_host()));
+    params.pop_back();  // ssm.rs:345-350
+    std::string msg;
+    CHECK(throws_kind([&] { b.restore(params); }, ErrorKind::InvalidCheckpoint, &msg));
+    CHECK(msg.find("expected 7 parameters, got 6") != std::string::npos);
+}
+
+TEST_GPU(ssm_mamba_block_forward_bit_exact) {
+    Rng rng(17);
+    SsmMambaBlock m(32, 16, rng);
+    auto xv = randn(32 * 32, 8);
+    auto y = m.forward_mamba(HipTensor::from_host(xv, Shape({32, 32}))).to_host();
+    std::vector<float> r(32 * 32), work(32 * 32 + 3 * 16 + 32);
+    auto dp = m.delta_proj.to_host(), ar = m.s4.A_real.to_host(), ai = m.s4.A_imag.to_host(),
+         B = m.s4.B.to_host(), C = m.s4.C.to_host(), D = m.s4.D.to_host(), g = m.gate.to_host();
+    oracle_ssm_mamba_fwd(32, 16, 0.1f, xv.data(), dp.data(), ar.data(), ai.data(), B.data(), C.data(),
+                         D.data(), g.data(), r.data(), work.data());
+    CHECK(bits_equal(y, r));
+}
+
+TEST_GPU(selective_scan_and_backend_ssm_forward) {
+    const size_t bt = 2, L = 300, dim = 128, N = 16;
+    auto u = randn(bt * L * dim, 20), dl = randn(bt * L * dim, 21), Bv = randn(bt * L * N, 22),
+         Cv = randn(bt * L * N, 23), Dv = randn(dim, 24), zv = randn(bt * L * dim, 25);
+    for (auto& v : dl) v = v * 0.5f - 4.0f;
+    std::vector<float> Av(dim * N);
+    for (size_t d = 0; d < dim; ++d)
+        for (size_t n = 0; n < N; ++n) Av[d * N + n] = -(float)(n + 1);
+    auto tu = HipTensor::from_host(u, Shape({bt, L, dim})), td = HipTensor::from_host(dl, Shape({bt, L, dim}));
+    auto tA = HipTensor::from_host(Av, Shape({dim, N})), tB = HipTensor::from_host(Bv, Shape({bt, L, N}));
+    auto tC = HipTensor::from_host(Cv, Shape({bt, L, N})), tD = HipTensor::from_host(Dv, Shape({dim}));
+    auto tz = HipTensor::from_host(zv, Shape({bt, L, dim}));
+    auto y = selective_scan(tu, td, tA, tB, tC, &tD, &tz, nullptr, true);
+    std::vector<float> r(bt * L * dim);
+    oracle_selective_scan(bt, L, dim, N, 1, u.data(), dl.data(), Av.data(), Bv.data(), Cv.data(), Dv.data(),
+                          zv.data(), nullptr, r.data(), nullptr, nullptr);
+    auto yh = y.to_host();
+    CHECK(rel_err(yh, r) < 1e-4);
+
+    // hal::ComputeBackend for ROCm: SSMForward through execute_op is the same kernel
+    RocmBackend be(0);
+    CHECK(be.device_type() == DeviceType::ROCm && be.is_available());
+    CHECK(be.supports_operation(OperationType::SSMForward) && be.supports_operation(OperationType::MatMul));
+    CHECK(!be.supports_operation(OperationType::SSMBackward));
+    CHECK(be.compute_units() > 0 && be.memory_bandwidth() > 0 && be.optimal_batch_size() >= 1);
+    auto handle = [&](const HipTensor& t, std::vector<size_t> shape) {
+        MemoryHandle h;
+        h.address = (uintptr_t)t.data();
+        h.size = t.nbytes();
+        h.shape = std::move(shape);
+        return h;
+    };
+    Operation op(OperationType::SSMForward);
+    op.inputs = {handle(tu, {bt, L, dim}), handle(td, {bt, L, dim}), handle(tA, {dim, N}),
+                 handle(tB, {bt, L, N}), handle(tC, {bt, L, N}), handle(tD, {dim}), handle(tz, {bt, L, dim})};
+    op.params = {{"batch", (double)bt}, {"seqlen", (double)L}, {"dim", (double)dim}, {"dstate", (double)N},
+                 {"softplus", 1.0}};
+    MemoryHandle out = be.execute_op(op);
+    std::vector<float> yb(bt * L * dim);
+    be.copy_to_host(yb.data(), out, yb.size() * 4);
+    CHECK(bits_equal(yb, yh));
+    be.deallocate(out);
+    CHECK(throws_kind([&] { be.deallocate(out); }, ErrorKind::InvalidInput));
+    Operation bad(OperationType::SSMForward);
+    bad.inputs = op.inputs;
+    CHECK(throws_kind([&] { (void)be.execute_op(bad); }, ErrorKind::InvalidInput));  // no params
+    CHECK(throws_kind([&] { (void)be.execute_op(Operation(OperationType::SSMBackward)); },
+                      ErrorKind::UnsupportedOperation));
+    // MatMul through the backend equals HipTensor::matmul
+    auto a = HipTensor::from_host(randn(12 * 20, 30), Shape({12, 20}));
+    auto b = HipTensor::from_host(randn(20 * 9, 31), Shape({20, 9}));
+    Operation mm(OperationType::MatMul);
+    mm.inputs = {handle(a, {12, 20}), handle(b, {20, 9})};
+    MemoryHandle mo = be.execute_op(mm);
+    std::vector<float> mh(12 * 9);
+    be.copy_to_host(mh.data(), mo, mh.size() * 4);
+    CHECK(bits_equal(mh, a.matmul(b).to_host()));
+}
+
+TEST_GPU(fused_mamba_block_runs_and_regrows_workspace) {
+    Rng rng(19);
+    MambaBlockFused blk(64, 16, 4, 2, rng);
+    auto x1 = HipTensor::from_host(randn(2 * 40 * 64, 40), Shape({2, 40, 64}), Storage::BF16);
+    auto x2 = HipTensor::from_host(randn(1 * 300 * 64, 41), Shape({1, 300, 64}), Storage::BF16);
+    auto y1 = blk.forward(x1).to_host();
+    auto y2 = blk.forward(x2).to_host();
+    auto y1b = blk.forward(x1).to_host();
+    CHECK(y1.size() == 2 * 40 * 64 && y2.size() == 300 * 64);
+    CHECK(bits_equal(y1, y1b));  // deterministic, workspace reuse is safe
+    for (float v : y2) CHECK(std::isfinite(v));
+    CHECK(throws_kind([&] { (void)blk.forward(x1.to_storage(Storage::F32)); }, ErrorKind::DTypeMismatch));
+}
+
+int main(int argc, char** argv) {
+    bool want_gpu = false, want_cpu = false;
+    for (int i = 1; i < argc; ++i) {
+        const std::string a = argv[i];
+        if (a == "--gpu") want_gpu = true;
+        else if (a == "--cpu") want_cpu = true;
+        else g_ckpt_path = a;
+    }
+    if (!want_cpu && !want_gpu) want_cpu = want_gpu = true;
+    for (auto& c : cases()) {
+        if ((c.gpu && !want_gpu) || (!c.gpu && !want_cpu)) continue;
+        g_cur = c.name;
+        ++g_run;
+        const int before = g_fail;
+        std::printf("RUN  %s\n", c.name);
+        std::fflush(stdout);
+        try {
+            c.fn();
+        } catch (const std::exception& e) {
+            std::printf("  FAIL %s: exception %s\n", c.name, e.what());
+            ++g_fail;
+        }
+        std::printf("%s %s\n", g_fail == before ? "OK  " : "FAIL", c.name);
+        std::fflush(stdout);
+    }
+    std::printf("%d run, %d failed\n", g_run, g_fail);
+    return g_fail ? 1 : 0;
+}

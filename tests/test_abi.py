@@ -84,4 +84,5 @@ def test_error_mapping_covers_tensor_error_variants():
     # status codes mirror tensor_core::TensorError (crates/tensor-core/src/error.rs:7-37)
     assert {c.__name__ for c in _ffi._BY_STATUS.values()} == {
         "ShapeMismatch", "InvalidDimension", "DeviceMismatch", "DTypeMismatch",
-        "UnsupportedOperation", "AllocationFailed", "BackendError", "InvalidInput"}
+        "UnsupportedOperation", "AllocationFailed", "BackendError", "SerializationError",
+        "InvalidInput", "InvalidCheckpoint"}
