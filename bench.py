@@ -364,7 +364,7 @@ def main():
     tfile = os.path.join(ROOT, "profiles", "traffic.json")
     if args.workload == "c2" and args.variant == 0 and os.path.exists(tfile):
         # measured HBM bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)
-        rec_t = json.load(open(tfile)).get("scan_wave_kernel<float, 2, true, true, false>@config2")
+        rec_t = json.load(open(tfile)).get("scan_wave2_kernel<float, 2, true, true, false>@config2")
         traffic = rec_t["traffic_bytes"] if rec_t else None
 
     rec = {

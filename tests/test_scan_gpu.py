@@ -16,7 +16,7 @@ from tests.util import TOL_BF16, TOL_F32, bf16_round, rel_err, scan_inputs
 
 pytestmark = pytest.mark.gpu
 
-VARIANTS = [-1, 1, 2, 4, 8, 16, 32, 33, 34, 35, 36, 40]
+VARIANTS = [-1, 1, 2, 4, 8, 16, 32, 33, 34, 35, 36, 40, 41]
 
 
 def to_dev(x, dev, dtype=torch.float32):
@@ -64,7 +64,7 @@ def test_scan_matches_oracle(dev, shape, variant):
 @pytest.mark.parametrize("with_z", [True, False])
 @pytest.mark.parametrize("with_D", [True, False])
 @pytest.mark.parametrize("softplus", [True, False])
-@pytest.mark.parametrize("variant", [40, 32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", [41, 40, 32, 33, 16, 4, -1])
 def test_scan_optional_operands(dev, with_z, with_D, softplus, variant):
     ssm.set_scan_variant(variant)
     x = scan_inputs(2, 70, 96, 16, seed=7, with_z=with_z, with_D=with_D)
@@ -108,7 +108,7 @@ def test_scan_zero_length_returns_initial_state(dev):
     assert np.array_equal(s, init)
 
 
-@pytest.mark.parametrize("variant", [40, 32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", [41, 40, 32, 33, 16, 4, -1])
 @pytest.mark.parametrize("shape", [(2, 37, 70, 16), (1, 300, 256, 16)], ids=str)
 def test_scan_bf16_storage(dev, variant, shape):
     ssm.set_scan_variant(variant)
@@ -159,11 +159,16 @@ def test_shape_errors_raise_reference_variants(dev):
                                to_dev(x["B"], dev), to_dev(x["C"], dev))
 
 
-def test_baseline_config2_full_size(dev):
+@pytest.mark.parametrize("variant", [0, 40, 41])
+def test_baseline_config2_full_size(dev, variant):
     """BASELINE config 2 (batch 8, L 2048, d_inner 1536, d_state 16, fp32) end to end against the
     (multi-threaded, arithmetic-identical) CPU oracle."""
+    ssm.set_scan_variant(variant)
     x = scan_inputs(8, 2048, 1536, 16, seed=0xC2)
-    g = run_gpu(x, dev)
+    try:
+        g = run_gpu(x, dev)
+    finally:
+        ssm.set_scan_variant(0)
     r = oracle.selective_scan_omp(**x)
     err = rel_err(g, r)
     print(f"config2 rel err {err:.3e}")
@@ -174,14 +179,17 @@ def test_baseline_config2_full_size(dev):
 def _reset_segments(dev):
     yield
     ssm.set_scan_segments(0)
+    ssm.set_scan_variant(0)
 
 
+@pytest.mark.parametrize("variant", [40, 41])
 @pytest.mark.parametrize("nseg", [2, 3, 7])
 @pytest.mark.parametrize("shape", [(2, 300, 128, 16), (1, 1000, 64, 16), (1, 77, 192, 16)], ids=str)
-def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape):
+def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape, variant):
     """Time-segmented path (segment end states from zero, carry chain, rescan from entry
     states) against the sequential oracle, with an initial state and the final state checked."""
     ssm.set_scan_segments(nseg)
+    ssm.set_scan_variant(variant)
     x = scan_inputs(*shape, seed=nseg * 11 + shape[1], with_bias=True)
     init = (np.random.default_rng(nseg).standard_normal((shape[0], shape[2], 16)) * 0.5).astype(np.float32)
     r, rlast = oracle.selective_scan(**x, init_state=init, return_last_state=True)
@@ -190,11 +198,16 @@ def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape):
     assert rel_err(glast, rlast) <= TOL_F32
 
 
-def test_baseline_config4_scan_full_size(dev):
+@pytest.mark.parametrize("variant", [0, 40, 41])
+def test_baseline_config4_scan_full_size(dev, variant):
     """BASELINE config 4 scan (batch 1, L 65536, d_inner 2048, d_state 16, fp32): the automatic
     segmented path against the (multi-threaded, arithmetic-identical) CPU oracle."""
+    ssm.set_scan_variant(variant)
     x = scan_inputs(1, 65536, 2048, 16, seed=0xC4)
-    g = run_gpu(x, dev)
+    try:
+        g = run_gpu(x, dev)
+    finally:
+        ssm.set_scan_variant(0)
     r = oracle.selective_scan_omp(**x)
     err = rel_err(g, r)
     print(f"config4 rel err {err:.3e}")
