@@ -258,14 +258,15 @@ def bench_lm(args, dev):
         _, state = m.prefill(pre)
         toks = [torch.randint(0, 256, (bt,), generator=gen, device=dev, dtype=torch.int32)
                 for _ in range(4)]
+        graph_step = m.decode_graph(state)  # the step captured as a HIP graph
 
         def step(i):
-            m.decode_step(toks[i], state)
+            graph_step(toks[i])
 
         steps = args.steps
         ms = time_steps(step, 4, steps, args.warmup)
         tokens = bt
-        workload = "byte LM recurrent decode step, 12 layers d_model 512, batch 256"
+        workload = "byte LM recurrent decode step (HIP graph), 12 layers d_model 512, batch 256"
         extra = {}
     rec = {
         "metric": ("byte LM prefill tokens/s (config 5), 1 GPU" if args.workload == "c5"

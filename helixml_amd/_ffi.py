@@ -106,6 +106,7 @@ SIGNATURES = {
     "hx_mamba_layer_decode": [_i64] * 6 + [_p, _p, _f] + [_p] * 11 + [_p, _sz, _p],
     "hx_set_scan_variant": [_int],
     "hx_set_scan_segments": [_int],
+    "hx_set_gemm_kernel": [_int],
     "hx_set_s4d_path": [_int],
     "hx_set_s4d_segments": [_int],
 }

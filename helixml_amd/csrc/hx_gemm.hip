@@ -14,6 +14,10 @@
 namespace hx {
 namespace {
 
+// 0 = automatic, 1 = always the 128 x 128 kernel, 2 = the 256 x 128 kernel where rows are aligned,
+// 3 = the split-K 32 x 64 kernel where rows are aligned
+int g_gemm_kernel = 0;
+
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
@@ -151,8 +155,321 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_kernel(int64_t M, int64_t N,
         }
 }
 
+// ----------------------------------------------------------------------------- small tiles
+// For small M (recurrent decode: one token per sequence, M = batch): a block of 4 waves owns one
+// 32 x 64 output tile (2 MFMA tiles) and splits K four ways; each wave loads its fragments
+// straight from global memory into registers (16 bytes per lane) with SPK K-steps in flight, and
+// the four partial tiles are summed through LDS. No barrier inside the K loop, and a K = 1024
+// reduction is 16 steps per wave instead of 64, so the latency of the dependent loads, not
+// occupancy, sets the time. Rows must be 16-byte aligned (ld % 8 == 0).
+constexpr int SPK = 4;  // K-steps of 16 in flight per wave
+
+__global__ __launch_bounds__(256) void gemm_bf16_nt_small_kernel(int64_t M, int64_t N, int64_t K,
+                                                                 const uint16_t* __restrict__ X,
+                                                                 int64_t ldx,
+                                                                 const uint16_t* __restrict__ W,
+                                                                 int64_t ldw,
+                                                                 const float* __restrict__ bias,
+                                                                 GemmOut o) {
+    __shared__ float red[3][2][16][64];  // partial tiles of waves 1..3: [wave][j][r][lane]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t m0 = (int64_t)blockIdx.y * 32, n0 = (int64_t)blockIdx.x * 64;
+    const int fr = lane & 31, fk = (lane >> 5) * 8;
+    const int64_t ra = m0 + fr, rb0 = n0 + fr, rb1 = n0 + 32 + fr;
+    // wave w takes K-steps w, w + 4, w + 8, ... (interleaved so all four waves stream the same
+    // rows of X and W at once)
+    const int64_t nsteps = (K + 15) / 16;
+    auto ld = [&](const uint16_t* base, int64_t row, int64_t nrows, int64_t k, int64_t ldm) {
+        const uint4 v = load16_guard<true>(base, row, nrows, k, K, ldm);
+        return __builtin_bit_cast(bf16x8, v);
+    };
+    f32x16 acc0, acc1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.0f;
+    bf16x8 a[SPK], b0[SPK], b1[SPK];
+#pragma unroll
+    for (int q = 0; q < SPK; ++q) {
+        const int64_t k = (wave + 4 * (int64_t)q) * 16 + fk;  // beyond K: zero fragments
+        a[q] = ld(X, ra, M, k, ldx);
+        b0[q] = ld(W, rb0, N, k, ldw);
+        b1[q] = ld(W, rb1, N, k, ldw);
+    }
+    for (int64_t s0 = wave; s0 < nsteps; s0 += 4 * SPK) {
+#pragma unroll
+        for (int q = 0; q < SPK; ++q) {
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[q], b0[q], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[q], b1[q], acc1, 0, 0, 0);
+            const int64_t k = (s0 + 4 * (int64_t)(q + SPK)) * 16 + fk;
+            a[q] = ld(X, ra, M, k, ldx);
+            b0[q] = ld(W, rb0, N, k, ldw);
+            b1[q] = ld(W, rb1, N, k, ldw);
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            red[wave - 1][0][r][lane] = acc0[r];
+            red[wave - 1][1][r][lane] = acc1[r];
+        }
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        acc0[r] += red[0][0][r][lane] + red[1][0][r][lane] + red[2][0][r][lane];
+        acc1[r] += red[0][1][r][lane] + red[1][1][r][lane] + red[2][1][r][lane];
+    }
+    // epilogue (element stores; these tiles are small)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int64_t col = n0 + j * 32 + (lane & 31);
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.0f;
+        int seg = 0;
+        int64_t cc = col;
+        if (col >= o.split2) { seg = 2; cc = col - o.split2; }
+        else if (col >= o.split1) { seg = 1; cc = col - o.split1; }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (row >= M) continue;
+            float v = (j ? acc1[r] : acc0[r]) + bv;
+            if (o.act & 1) v = silu(v);
+            const int64_t off = row * o.ld[seg] + cc;
+            if (o.out_bf16) {
+                uint16_t* yp = (uint16_t*)o.y[seg] + off;
+                if (o.act & 2) v += Storage<uint16_t>::load(yp);
+                Storage<uint16_t>::store(yp, v);
+            } else {
+                float* yp = (float*)o.y[seg] + off;
+                if (o.act & 2) v += *yp;
+                *yp = v;
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------- large tiles
+// Block tile 256 x 128 x 64, 4 waves in 2 x 2, each wave 128 x 64 = 4 x 2 tiles of
+// v_mfma_f32_32x32x16_bf16 (8 MFMAs per 6 LDS fragment reads, vs 4 per 4 in the 128 x 128 kernel).
+// Global -> registers -> LDS, double-buffered, rows padded by 16 bytes. The epilogue stages each
+// wave's 32 x 64 sub-tiles through LDS and writes rows as 16-byte vectors (8 bf16 or 4 fp32 per
+// lane), applying bias, SiLU and accumulate; a vector that would straddle a column split or the
+// N edge falls back to element stores.
+constexpr int LBM = 256, LBN = 128, LBK = 64;
+constexpr int LLDK = LBK + 8;  // padded row: 144 bytes
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void gemm_bf16_nt_large_kernel(int64_t M, int64_t N, int64_t K,
+                                                                 const uint16_t* __restrict__ X,
+                                                                 int64_t ldx,
+                                                                 const uint16_t* __restrict__ W,
+                                                                 int64_t ldw,
+                                                                 const float* __restrict__ bias,
+                                                                 GemmOut o) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    uint16_t* sA = smem;                        // [2][LBM][LLDK]
+    uint16_t* sB = smem + 2 * LBM * LLDK;       // [2][LBN][LLDK]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    // XCD-aware tile order: consecutive block ids go to different XCDs; give each XCD a
+    // contiguous run of tiles so neighbouring tiles share its L2
+    const int nbx = gridDim.x, nby = gridDim.y;
+    const int nb = nbx * nby;
+    int bid = blockIdx.y * nbx + blockIdx.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    const int64_t m0 = (int64_t)(bid / nbx) * LBM, n0 = (int64_t)(bid % nbx) * LBN;
+
+    // per K-step: A 256 x 64 (2048 16-byte pieces, 8 per thread), B 128 x 64 (1024, 4 per thread)
+    uint4 ra[8], rb[4];
+    auto gload = [&](int64_t k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int e = tid + j * 256;
+            const int row = e >> 3, kc = (e & 7) * 8;
+            ra[j] = load16_guard<VEC>(X, m0 + row, M, k0 + kc, K, ldx);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = tid + j * 256;
+            const int row = e >> 3, kc = (e & 7) * 8;
+            rb[j] = load16_guard<VEC>(W, n0 + row, N, k0 + kc, K, ldw);
+        }
+    };
+    auto sstore = [&](int buf) __attribute__((always_inline)) {
+        uint16_t* a = sA + buf * LBM * LLDK;
+        uint16_t* bb = sB + buf * LBN * LLDK;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int e = tid + j * 256;
+            *reinterpret_cast<uint4*>(a + (e >> 3) * LLDK + (e & 7) * 8) = ra[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = tid + j * 256;
+            *reinterpret_cast<uint4*>(bb + (e >> 3) * LLDK + (e & 7) * 8) = rb[j];
+        }
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int fr = lane & 31;
+    const int fk = (lane >> 5) * 8;
+    const int64_t nk = (K + LBK - 1) / LBK;
+    gload(0);
+    sstore(0);
+    if (nk > 1) gload(LBK);
+    __syncthreads();
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int buf = (int)(kt & 1);
+        const uint16_t* a = sA + buf * LBM * LLDK + (wm * 128 + fr) * LLDK + fk;
+        const uint16_t* bb = sB + buf * LBN * LLDK + (wn * 64 + fr) * LLDK + fk;
+#pragma unroll
+        for (int kk = 0; kk < LBK; kk += 16) {
+            bf16x8 af[4], bf[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(a + i * 32 * LLDK + kk);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(bb + j * 32 * LLDK + kk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) {
+            sstore(buf ^ 1);
+            if (kt + 2 < nk) gload((kt + 2) * LBK);
+        }
+        __syncthreads();
+    }
+
+    // epilogue: per wave, 4 row groups of 32 x 64 staged in a private 32 x 64 fp32 LDS tile
+    float* st = reinterpret_cast<float*>(smem) + wave * (32 * 68);  // row stride 68 floats
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                st[row * 68 + j * 32 + (lane & 31)] = acc[i][j][r];
+            }
+        __builtin_amdgcn_wave_barrier();
+        // rows of 64 columns: o.out_bf16 -> 8 lanes x 8 columns per row (8 rows per pass),
+        // fp32 -> 16 lanes x 4 columns per row (4 rows per pass)
+        const int vw = o.out_bf16 ? 8 : 4;
+        const int lpr = 64 / vw;             // lanes per row
+        const int rpp = 64 / lpr;            // rows per pass
+        const int rl = lane / lpr, cl = (lane % lpr) * vw;
+        for (int rr = rl; rr < 32; rr += rpp) {
+            const int64_t row = m0 + wm * 128 + i * 32 + rr;
+            const int64_t col = n0 + wn * 64 + cl;
+            if (row >= M || col >= N) continue;
+            float v[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                if (q < vw) {
+                    float x = st[rr * 68 + cl + q];
+                    if (bias && col + q < N) x += bias[col + q];
+                    if (o.act & 1) x = silu(x);
+                    v[q] = x;
+                }
+            }
+            int seg = 0;
+            int64_t cc = col;
+            if (col >= o.split2) { seg = 2; cc = col - o.split2; }
+            else if (col >= o.split1) { seg = 1; cc = col - o.split1; }
+            const int64_t seg_end = seg == 0 ? o.split1 : seg == 1 ? o.split2 : N;
+            const int64_t off = row * o.ld[seg] + cc;
+            const bool whole = col + vw <= seg_end &&
+                               ((uintptr_t)((char*)o.y[seg] + off * (o.out_bf16 ? 2 : 4)) & 15) == 0;
+            if (whole) {
+                if (o.out_bf16) {
+                    uint16_t* yp = (uint16_t*)o.y[seg] + off;
+                    if (o.act & 2) {
+                        const uint4 old = *reinterpret_cast<const uint4*>(yp);
+                        const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            v[2 * q] += __uint_as_float(ow[q] << 16);
+                            v[2 * q + 1] += __uint_as_float(ow[q] & 0xffff0000u);
+                        }
+                    }
+                    uint32_t wv[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        wv[q] = (uint32_t)Storage<uint16_t>::round(v[2 * q]) |
+                                ((uint32_t)Storage<uint16_t>::round(v[2 * q + 1]) << 16);
+                    *reinterpret_cast<uint4*>(yp) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+                } else {
+                    float* yp = (float*)o.y[seg] + off;
+                    if (o.act & 2) {
+                        const float4 old = *reinterpret_cast<const float4*>(yp);
+                        v[0] += old.x; v[1] += old.y; v[2] += old.z; v[3] += old.w;
+                    }
+                    *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+                }
+            } else {
+                for (int q = 0; q < vw; ++q) {
+                    const int64_t cq = col + q;
+                    if (cq >= N) break;
+                    int sq = 0;
+                    int64_t ccq = cq;
+                    if (cq >= o.split2) { sq = 2; ccq = cq - o.split2; }
+                    else if (cq >= o.split1) { sq = 1; ccq = cq - o.split1; }
+                    const int64_t oq = row * o.ld[sq] + ccq;
+                    float x = v[q];
+                    if (o.out_bf16) {
+                        uint16_t* yp = (uint16_t*)o.y[sq] + oq;
+                        if (o.act & 2) x += Storage<uint16_t>::load(yp);
+                        Storage<uint16_t>::store(yp, x);
+                    } else {
+                        float* yp = (float*)o.y[sq] + oq;
+                        if (o.act & 2) x += *yp;
+                        *yp = x;
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 }  // namespace
 }  // namespace hx
+
+namespace {
+// The 256 x 128 kernel needs 108 KB of LDS per block: use it only where the device grants that
+// (the MI355X's CUs have 160 KB); the result is cached per device.
+bool large_lds_ok(size_t bytes) {
+    static int cached[64] = {0};  // 0 unknown, 1 yes, 2 no
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    if (cached[dev] == 0) {
+        int v = 0;
+        const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
+                            hipSuccess &&
+                        (size_t)v >= bytes &&
+                        hipFuncSetAttribute((const void*)hx::gemm_bf16_nt_large_kernel<true>,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)bytes) == hipSuccess;
+        cached[dev] = ok ? 1 : 2;
+    }
+    return cached[dev] == 1;
+}
+}  // namespace
 
 extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
                             const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
@@ -176,6 +493,25 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     HX_REQUIRE((N + BN - 1) / BN <= 0x7fffffff && (M + BM - 1) / BM <= 65535, HX_ERR_UNSUPPORTED,
                "gemm_bf16: M=%lld too large for the grid", (long long)M);
     GemmOut o{{Y0, Y1, Y2}, {ld0, ld1, ld2}, split1, split2, out_dtype == HX_BF16, act};
+    const int64_t large_tiles = ((M + LBM - 1) / LBM) * ((N + LBN - 1) / LBN);
+    const size_t lds = (size_t)2 * (LBM + LBN) * LLDK * sizeof(uint16_t);
+    if (vec && g_gemm_kernel != 1 && (g_gemm_kernel == 2 || (large_tiles >= 256 && K >= 256)) &&
+        large_lds_ok(lds)) {
+        dim3 lg((unsigned)((N + LBN - 1) / LBN), (unsigned)((M + LBM - 1) / LBM));
+        hipLaunchKernelGGL(gemm_bf16_nt_large_kernel<true>, lg, dim3(256), lds, as_stream(stream),
+                           M, N, K, (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
+        HX_LAUNCH_CHECK();
+        return HX_OK;
+    }
+    const int64_t tiles128 = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    if (vec && g_gemm_kernel != 1 && g_gemm_kernel != 2 &&
+        (g_gemm_kernel == 3 || (tiles128 < 128 && (M + 31) / 32 <= 65535))) {
+        dim3 sg((unsigned)((N + 63) / 64), (unsigned)((M + 31) / 32));
+        hipLaunchKernelGGL(gemm_bf16_nt_small_kernel, sg, dim3(256), 0, as_stream(stream), M, N, K,
+                           (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
+        HX_LAUNCH_CHECK();
+        return HX_OK;
+    }
     dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
     if (vec)
         hipLaunchKernelGGL(gemm_bf16_nt_kernel<true>, grid, dim3(256), 0, as_stream(stream), M, N, K,
@@ -184,5 +520,12 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
         hipLaunchKernelGGL(gemm_bf16_nt_kernel<false>, grid, dim3(256), 0, as_stream(stream), M, N, K,
                            (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
     HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+extern "C" int hx_set_gemm_kernel(int k) {
+    using namespace hx;
+    HX_REQUIRE(k >= 0 && k <= 3, HX_ERR_INVALID_INPUT, "hx_set_gemm_kernel: %d (0 auto, 1, 2, 3)", k);
+    g_gemm_kernel = k;
     return HX_OK;
 }

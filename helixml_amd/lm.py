@@ -160,6 +160,34 @@ class ByteLM:
                       ws.numel(), s)
         return self._head(x, stream)
 
+    def decode_graph(self, state, stream=None):
+        """Captures one decode step for ``state``'s batch into a HIP graph (torch.cuda.CUDAGraph
+        over the C ABI's launches: no host round trips, no allocations, no memsets in the step).
+        Returns ``step(tokens) -> logits``: it copies the tokens into the graph's input buffer
+        and replays; ``state`` is advanced in place exactly as by decode_step. The logits tensor
+        is the graph's output buffer, overwritten by the next replay."""
+        bt = state[0][0].shape[0]
+        tok = torch.zeros((bt,), dtype=torch.int32, device=self.device)
+        self._workspace(bt, 1)
+        # warm up on a copy of the state so capture sees allocated buffers
+        scratch = [(s.clone(), c.clone()) for s, c in state]
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.decode_step(tok, scratch)
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            logits = self.decode_step(tok, state)
+
+        def step(tokens):
+            tok.copy_(tokens)
+            g.replay()
+            return logits
+
+        step.graph = g
+        return step
+
     def host_params(self):
         """Every parameter as float32 numpy arrays (for the CPU oracle in tests)."""
         f = lambda t: t.float().cpu().numpy()  # noqa: E731

@@ -205,6 +205,10 @@ def set_scan_segments(n: int) -> None:
     _ffi.call("hx_set_scan_segments", int(n))
 
 
+def set_gemm_kernel(k: int) -> None:
+    _ffi.call("hx_set_gemm_kernel", int(k))
+
+
 def set_s4d_path(path: int) -> None:
     _ffi.call("hx_set_s4d_path", int(path))
 

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from helixml_amd import ssm
-from tests.util import norm_err, rel_err
+from tests.util import bf16_round, norm_err, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -58,3 +58,61 @@ def test_gemm_unaligned_rows(dev, M, N, K):
     y = ssm.gemm_bf16(X, W, out_dtype=torch.float32)
     err = norm_err(y.cpu().numpy(), ref(X, W))
     assert err <= 1e-5, err
+
+
+@pytest.fixture
+def gemm_kernel(dev, request):
+    ssm.set_gemm_kernel(request.param)
+    yield request.param
+    ssm.set_gemm_kernel(0)
+
+
+@pytest.mark.parametrize("gemm_kernel", [1, 2, 3], indirect=True)
+@pytest.mark.parametrize("M,N,K", [(512, 256, 512), (300, 200, 136), (257, 129, 64), (1024, 2048, 1024),
+                                   (100, 72, 1000), (256, 64, 1024), (33, 40, 24)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_gemm_tile_kernels_fp32_out(dev, gemm_kernel, M, N, K, act):
+    """Both tile kernels (128 x 128 x 32 and 256 x 128 x 64) on aligned and ragged shapes."""
+    g = torch.Generator().manual_seed(M + N + K)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
+    b = torch.randn(N, generator=g).to(dev)
+    y = ssm.gemm_bf16(X, W, b, act=act, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    err = norm_err(y.cpu().numpy(), ref(X, W, b, act))
+    assert err <= 1e-5, err
+
+
+@pytest.mark.parametrize("gemm_kernel", [1, 2, 3], indirect=True)
+@pytest.mark.parametrize("splits", [(128, 144), (100, 133), (8, 16)])
+def test_gemm_tile_kernels_splits_bf16(dev, gemm_kernel, splits):
+    """Column splits on vector boundaries and straddling them (100, 133 are not multiples of 8)."""
+    g = torch.Generator().manual_seed(sum(splits))
+    M, K, N = 520, 256, 200
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / 16).to(torch.bfloat16).to(dev)
+    parts = ssm.gemm_bf16(X, W, splits=splits)
+    torch.cuda.synchronize()
+    got = np.concatenate([p.float().cpu().numpy() for p in parts], 1)
+    err = rel_err(got, bf16_round(ref(X, W)))
+    assert err <= 2 ** -7, err  # within one bf16 ulp of the rounded reference
+
+
+@pytest.mark.parametrize("gemm_kernel", [1, 2, 3], indirect=True)
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_accumulate_into_output(dev, gemm_kernel, out_dtype):
+    """act bit 1: Y += X . W^T (the residual add of a pre-norm layer)."""
+    g = torch.Generator().manual_seed(77)
+    M, K, N = 600, 512, 384
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
+    Y0 = torch.randn(M, N, generator=g).to(dev).to(out_dtype)
+    Y = Y0.clone()
+    from helixml_amd import _ffi
+    od = _ffi.HX_F32 if out_dtype == torch.float32 else _ffi.HX_BF16
+    _ffi.call("hx_gemm_bf16", M, N, K, X.data_ptr(), K, W.data_ptr(), K, None, 2, od,
+              Y.data_ptr(), N, N, None, 0, N, None, 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    r = Y0.float().cpu().numpy() + ref(X, W)
+    err = norm_err(Y.float().cpu().numpy(), r)
+    assert err <= (1e-5 if out_dtype == torch.float32 else 2 ** -8), err

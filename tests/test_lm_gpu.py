@@ -178,3 +178,26 @@ def test_lm_config5_full_size(dev):
     torch.cuda.synchronize()
     err = norm_err(g2.cpu().numpy(), rl)
     assert err <= 1e-2, err
+
+
+def test_decode_graph_replays_match_eager(dev):
+    """The captured decode step (HIP graph) against eager decode steps from the same state, with
+    eager work and synchronisation between replays; every replay is checked, bit for bit (the
+    same kernels run in the same order)."""
+    P = lm_params(2, 64, 128, 16, 8, 4, 256, seed=9)
+    m = model_from(P, dev, dt_rank=8)
+    rng = np.random.default_rng(10)
+    tok = torch.from_numpy(rng.integers(0, 256, (4, 12)).astype(np.int32)).to(dev)
+    _, st_eager = m.prefill(tok)
+    st_graph = [(s.clone(), c.clone()) for s, c in st_eager]
+    step = m.decode_graph(st_graph)
+    for t in range(5):
+        nxt = torch.from_numpy(rng.integers(0, 256, (4,)).astype(np.int32)).to(dev)
+        want = m.decode_step(nxt, st_eager).clone()
+        _ = torch.randn(1000, device=dev).sum()  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        got = step(nxt).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), t
+        for (a, b), (c, d) in zip(st_graph, st_eager):
+            assert torch.equal(a, c) and torch.equal(b, d), t
