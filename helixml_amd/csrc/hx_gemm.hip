@@ -15,7 +15,8 @@ namespace hx {
 namespace {
 
 // 0 = automatic, 1 = always the 128 x 128 kernel, 2 = the 256 x 128 kernel where rows are aligned,
-// 3 = the split-K 32 x 64 kernel where rows are aligned
+// 3 = the split-K 32 x 64 kernel where rows are aligned, 4 = the direct-to-LDS 256 x 128 kernel
+// where K % 64 == 0 and rows are aligned
 int g_gemm_kernel = 0;
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
@@ -30,6 +31,19 @@ struct GemmOut {
     int64_t split1, split2;  // column boundaries of outputs 0 | 1 | 2
     int out_bf16;
     int act;                 // bit 0: SiLU; bit 1: accumulate (Y += result, read-modify-write)
+    // output and leading dimension of segment s, selected without indexing the arrays with a
+    // runtime value (which would place the struct in scratch memory)
+    // (a select chain is folded back into an indexed load, so the choice is made with masks)
+    __device__ uint64_t pick(uint64_t a, uint64_t b, uint64_t c, int s) const {
+        const uint64_t m1 = 0 - (uint64_t)(s == 1), m2 = 0 - (uint64_t)(s == 2), m0 = ~(m1 | m2);
+        return (a & m0) | (b & m1) | (c & m2);
+    }
+    __device__ void* yp(int s) const {
+        return (void*)pick((uint64_t)y[0], (uint64_t)y[1], (uint64_t)y[2], s);
+    }
+    __device__ int64_t ldp(int s) const {
+        return (int64_t)pick((uint64_t)ld[0], (uint64_t)ld[1], (uint64_t)ld[2], s);
+    }
 };
 
 // 8 consecutive bf16 of row `row` from column `col`, zero outside [nrows, ncols). VEC: the row
@@ -141,13 +155,13 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_kernel(int64_t M, int64_t N,
                 if (row >= M) continue;
                 float v = acc[i][j][r] + bv;
                 if (o.act & 1) v = silu(v);
-                const int64_t off = row * o.ld[seg] + cc;
+                const int64_t off = row * o.ldp(seg) + cc;
                 if (o.out_bf16) {
-                    uint16_t* yp = (uint16_t*)o.y[seg] + off;
+                    uint16_t* yp = (uint16_t*)o.yp(seg) + off;
                     if (o.act & 2) v += Storage<uint16_t>::load(yp);
                     Storage<uint16_t>::store(yp, v);
                 } else {
-                    float* yp = (float*)o.y[seg] + off;
+                    float* yp = (float*)o.yp(seg) + off;
                     if (o.act & 2) v += *yp;
                     *yp = v;
                 }
@@ -237,18 +251,102 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_small_kernel(int64_t M, int6
             if (row >= M) continue;
             float v = (j ? acc1[r] : acc0[r]) + bv;
             if (o.act & 1) v = silu(v);
-            const int64_t off = row * o.ld[seg] + cc;
+            const int64_t off = row * o.ldp(seg) + cc;
             if (o.out_bf16) {
-                uint16_t* yp = (uint16_t*)o.y[seg] + off;
+                uint16_t* yp = (uint16_t*)o.yp(seg) + off;
                 if (o.act & 2) v += Storage<uint16_t>::load(yp);
                 Storage<uint16_t>::store(yp, v);
             } else {
-                float* yp = (float*)o.y[seg] + off;
+                float* yp = (float*)o.yp(seg) + off;
                 if (o.act & 2) v += *yp;
                 *yp = v;
             }
         }
     }
+}
+
+// Writes a wave's staged 32 x 64 fp32 tile (st, row stride 68) to the outputs: rows of 64
+// columns as 16-byte vectors (8 bf16 or 4 fp32 per lane) with bias, SiLU and accumulate; a
+// vector that would straddle a column split or the N edge falls back to element stores.
+__device__ inline void store_tile_rows(const GemmOut& o, const float* __restrict__ bias,
+                                       const float* st, int64_t M, int64_t N, int64_t row0,
+                                       int64_t col0, int lane) {
+        // rows of 64 columns: o.out_bf16 -> 8 lanes x 8 columns per row (8 rows per pass),
+        // fp32 -> 16 lanes x 4 columns per row (4 rows per pass)
+        const int vw = o.out_bf16 ? 8 : 4;
+        const int lpr = 64 / vw;             // lanes per row
+        const int rpp = 64 / lpr;            // rows per pass
+        const int rl = lane / lpr, cl = (lane % lpr) * vw;
+        for (int rr = rl; rr < 32; rr += rpp) {
+            const int64_t row = row0 + rr;
+            const int64_t col = col0 + cl;
+            if (row >= M || col >= N) continue;
+            float v[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                if (q < vw) {
+                    float x = st[rr * 68 + cl + q];
+                    if (bias && col + q < N) x += bias[col + q];
+                    if (o.act & 1) x = silu(x);
+                    v[q] = x;
+                }
+            }
+            int seg = 0;
+            int64_t cc = col;
+            if (col >= o.split2) { seg = 2; cc = col - o.split2; }
+            else if (col >= o.split1) { seg = 1; cc = col - o.split1; }
+            const int64_t seg_end = seg == 0 ? o.split1 : seg == 1 ? o.split2 : N;
+            const int64_t off = row * o.ldp(seg) + cc;
+            const bool whole = col + vw <= seg_end &&
+                               ((uintptr_t)((char*)o.yp(seg) + off * (o.out_bf16 ? 2 : 4)) & 15) == 0;
+            if (whole) {
+                if (o.out_bf16) {
+                    uint16_t* yp = (uint16_t*)o.yp(seg) + off;
+                    if (o.act & 2) {
+                        const uint4 old = *reinterpret_cast<const uint4*>(yp);
+                        const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            v[2 * q] += __uint_as_float(ow[q] << 16);
+                            v[2 * q + 1] += __uint_as_float(ow[q] & 0xffff0000u);
+                        }
+                    }
+                    uint32_t wv[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        wv[q] = (uint32_t)Storage<uint16_t>::round(v[2 * q]) |
+                                ((uint32_t)Storage<uint16_t>::round(v[2 * q + 1]) << 16);
+                    *reinterpret_cast<uint4*>(yp) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+                } else {
+                    float* yp = (float*)o.yp(seg) + off;
+                    if (o.act & 2) {
+                        const float4 old = *reinterpret_cast<const float4*>(yp);
+                        v[0] += old.x; v[1] += old.y; v[2] += old.z; v[3] += old.w;
+                    }
+                    *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+                }
+            } else {
+                for (int q = 0; q < vw; ++q) {
+                    const int64_t cq = col + q;
+                    if (cq >= N) break;
+                    int sq = 0;
+                    int64_t ccq = cq;
+                    if (cq >= o.split2) { sq = 2; ccq = cq - o.split2; }
+                    else if (cq >= o.split1) { sq = 1; ccq = cq - o.split1; }
+                    const int64_t oq = row * o.ldp(sq) + ccq;
+                    float x = v[q];
+                    if (o.out_bf16) {
+                        uint16_t* yp = (uint16_t*)o.yp(sq) + oq;
+                        if (o.act & 2) x += Storage<uint16_t>::load(yp);
+                        Storage<uint16_t>::store(yp, x);
+                    } else {
+                        float* yp = (float*)o.yp(sq) + oq;
+                        if (o.act & 2) x += *yp;
+                        *yp = x;
+                    }
+                }
+            }
+        }
 }
 
 // ----------------------------------------------------------------------------- large tiles
@@ -367,82 +465,137 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_large_kernel(int64_t M, int6
                 st[row * 68 + j * 32 + (lane & 31)] = acc[i][j][r];
             }
         __builtin_amdgcn_wave_barrier();
-        // rows of 64 columns: o.out_bf16 -> 8 lanes x 8 columns per row (8 rows per pass),
-        // fp32 -> 16 lanes x 4 columns per row (4 rows per pass)
-        const int vw = o.out_bf16 ? 8 : 4;
-        const int lpr = 64 / vw;             // lanes per row
-        const int rpp = 64 / lpr;            // rows per pass
-        const int rl = lane / lpr, cl = (lane % lpr) * vw;
-        for (int rr = rl; rr < 32; rr += rpp) {
-            const int64_t row = m0 + wm * 128 + i * 32 + rr;
-            const int64_t col = n0 + wn * 64 + cl;
-            if (row >= M || col >= N) continue;
-            float v[8];
+        store_tile_rows(o, bias, st, M, N, m0 + wm * 128 + i * 32, n0 + wn * 64, lane);
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// ----------------------------------------------------------------------------- direct-to-LDS
+// Same 256 x 128 x 64 tiling and epilogue as gemm_bf16_nt_large_kernel, but tiles move from
+// global memory straight into LDS with gfx950's global_load_lds_dwordx4 (64 lanes x 16 bytes into
+// one contiguous KiB of LDS per instruction): no register staging, a 3-stage LDS ring, and the
+// loads of tile kt+2 issued while tile kt is multiplied. Each KiB holds 8 tile rows of 128 bytes;
+// within a row the 16-byte K-chunks are XOR-swizzled (chunk c of row r sits in slot c ^ (r & 7))
+// by choosing which global chunk each lane loads, so the MFMA fragment reads (one chunk of 32
+// consecutive rows) spread over the banks. Requires K % 64 == 0 and 16-byte aligned rows; rows
+// past M or N are clamped (their outputs are discarded).
+typedef __attribute__((address_space(1))) void gvoid_t;
+typedef __attribute__((address_space(3))) void lvoid_t;
+constexpr int DSTAGES = 3;
+constexpr int DSTAGE_BYTES = (LBM + LBN) * LBK * 2;  // 48 KiB
+
+__global__ __launch_bounds__(256) void gemm_bf16_nt_dlds_kernel(int64_t M, int64_t N, int64_t K,
+                                                                const uint16_t* __restrict__ X,
+                                                                int64_t ldx,
+                                                                const uint16_t* __restrict__ W,
+                                                                int64_t ldw,
+                                                                const float* __restrict__ bias,
+                                                                GemmOut o) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    char* sbase = reinterpret_cast<char*>(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nbx = gridDim.x, nby = gridDim.y;
+    const int nb = nbx * nby;
+    int bid = blockIdx.y * nbx + blockIdx.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    const int64_t m0 = (int64_t)(bid / nbx) * LBM, n0 = (int64_t)(bid % nbx) * LBN;
+
+    // this lane's 12 global sources per tile: wave w issues KiB regions q = 12w .. 12w + 11 of
+    // the 48 KiB stage (0..31 = A rows 8q.., 32..47 = B rows 8(q-32)..); lane L fills row
+    // 8q' + L/8, slot L%8 with K-chunk (L%8) ^ (row & 7)
+    const uint16_t* src[12];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                if (q < vw) {
-                    float x = st[rr * 68 + cl + q];
-                    if (bias && col + q < N) x += bias[col + q];
-                    if (o.act & 1) x = silu(x);
-                    v[q] = x;
-                }
-            }
-            int seg = 0;
-            int64_t cc = col;
-            if (col >= o.split2) { seg = 2; cc = col - o.split2; }
-            else if (col >= o.split1) { seg = 1; cc = col - o.split1; }
-            const int64_t seg_end = seg == 0 ? o.split1 : seg == 1 ? o.split2 : N;
-            const int64_t off = row * o.ld[seg] + cc;
-            const bool whole = col + vw <= seg_end &&
-                               ((uintptr_t)((char*)o.y[seg] + off * (o.out_bf16 ? 2 : 4)) & 15) == 0;
-            if (whole) {
-                if (o.out_bf16) {
-                    uint16_t* yp = (uint16_t*)o.y[seg] + off;
-                    if (o.act & 2) {
-                        const uint4 old = *reinterpret_cast<const uint4*>(yp);
-                        const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            v[2 * q] += __uint_as_float(ow[q] << 16);
-                            v[2 * q + 1] += __uint_as_float(ow[q] & 0xffff0000u);
-                        }
-                    }
-                    uint32_t wv[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        wv[q] = (uint32_t)Storage<uint16_t>::round(v[2 * q]) |
-                                ((uint32_t)Storage<uint16_t>::round(v[2 * q + 1]) << 16);
-                    *reinterpret_cast<uint4*>(yp) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-                } else {
-                    float* yp = (float*)o.y[seg] + off;
-                    if (o.act & 2) {
-                        const float4 old = *reinterpret_cast<const float4*>(yp);
-                        v[0] += old.x; v[1] += old.y; v[2] += old.z; v[3] += old.w;
-                    }
-                    *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
-                }
-            } else {
-                for (int q = 0; q < vw; ++q) {
-                    const int64_t cq = col + q;
-                    if (cq >= N) break;
-                    int sq = 0;
-                    int64_t ccq = cq;
-                    if (cq >= o.split2) { sq = 2; ccq = cq - o.split2; }
-                    else if (cq >= o.split1) { sq = 1; ccq = cq - o.split1; }
-                    const int64_t oq = row * o.ld[sq] + ccq;
-                    float x = v[q];
-                    if (o.out_bf16) {
-                        uint16_t* yp = (uint16_t*)o.y[sq] + oq;
-                        if (o.act & 2) x += Storage<uint16_t>::load(yp);
-                        Storage<uint16_t>::store(yp, x);
-                    } else {
-                        float* yp = (float*)o.y[sq] + oq;
-                        if (o.act & 2) x += *yp;
-                        *yp = x;
-                    }
-                }
-            }
+    for (int j = 0; j < 12; ++j) {
+        const int q = wave * 12 + j;
+        const bool isA = q < 32;
+        const int row = (isA ? q : q - 32) * 8 + (lane >> 3);
+        const int chunk = (lane & 7) ^ (row & 7);
+        if (isA) {
+            const int64_t gr = m0 + row < M ? m0 + row : M - 1;
+            src[j] = X + gr * ldx + chunk * 8;
+        } else {
+            const int64_t gr = n0 + row < N ? n0 + row : N - 1;
+            src[j] = W + gr * ldw + chunk * 8;
         }
+    }
+    auto issue = [&](int64_t kt) __attribute__((always_inline)) {
+        char* stage = sbase + (int)(kt % DSTAGES) * DSTAGE_BYTES;
+#pragma unroll
+        for (int j = 0; j < 12; ++j) {
+            const int q = wave * 12 + j;
+            __builtin_amdgcn_global_load_lds((gvoid_t*)(src[j] + kt * LBK), (lvoid_t*)(stage + q * 1024),
+                                             16, 0, 0);
+        }
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int fr = lane & 31;
+    const int fc = lane >> 5;  // chunk half within a 16-wide K sub-step
+    const int64_t nk = K / LBK;
+    issue(0);
+    if (nk > 1) issue(1);
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        // tile kt's 12 loads of this wave are done when at most the 12 of tile kt+1 remain
+        // (wait and barrier in one asm statement: a fenced barrier would make the compiler wait
+        // for tile kt+1's loads too, as they also write LDS; the "memory" clobber keeps the LDS
+        // reads of this iteration below it)
+        if (kt + 1 < nk) asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kt + 2 < nk) issue(kt + 2);  // stage (kt+2)%3 was last read in iteration kt-1
+        const char* stage = sbase + (int)(kt % DSTAGES) * DSTAGE_BYTES;
+        const char* aw = stage + (wm * 128 + fr) * 128;                 // A rows of this lane
+        const char* bw = stage + 32 * 1024 + (wn * 64 + fr) * 128;      // B rows of this lane
+        // fragments of K-chunk pair s (chunks 2s + fc): rows r = base + fr, with r & 7 == fr & 7
+        // since every base is a multiple of 8
+        auto load = [&](int s, bf16x8* af, bf16x8* bf) __attribute__((always_inline)) {
+            const int off = ((2 * s + fc) ^ (fr & 7)) << 4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(aw + i * 32 * 128 + off);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(bw + j * 32 * 128 + off);
+        };
+        // register double buffer: the fragments of pair s+1 are read while pair s is multiplied
+        bf16x8 fa[2][4], fb[2][2];
+        load(0, fa[0], fb[0]);
+#pragma unroll
+        for (int s = 0; s < LBK / 16; ++s) {
+            if (s + 1 < LBK / 16) load(s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s & 1][i], fb[s & 1][j],
+                                                                        acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();  // the epilogue reuses stage memory
+
+    float* st = reinterpret_cast<float*>(smem) + wave * (32 * 68);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                st[row * 68 + j * 32 + (lane & 31)] = acc[i][j][r];
+            }
+        __builtin_amdgcn_wave_barrier();
+        store_tile_rows(o, bias, st, M, N, m0 + wm * 128 + i * 32, n0 + wn * 64, lane);
         __builtin_amdgcn_wave_barrier();
     }
 }
@@ -463,6 +616,23 @@ bool large_lds_ok(size_t bytes) {
                             hipSuccess &&
                         (size_t)v >= bytes &&
                         hipFuncSetAttribute((const void*)hx::gemm_bf16_nt_large_kernel<true>,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)bytes) == hipSuccess;
+        cached[dev] = ok ? 1 : 2;
+    }
+    return cached[dev] == 1;
+}
+
+bool dlds_ok(size_t bytes) {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    if (cached[dev] == 0) {
+        int v = 0;
+        const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
+                            hipSuccess &&
+                        (size_t)v >= bytes &&
+                        hipFuncSetAttribute((const void*)hx::gemm_bf16_nt_dlds_kernel,
                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                             (int)bytes) == hipSuccess;
         cached[dev] = ok ? 1 : 2;
@@ -493,10 +663,20 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     HX_REQUIRE((N + BN - 1) / BN <= 0x7fffffff && (M + BM - 1) / BM <= 65535, HX_ERR_UNSUPPORTED,
                "gemm_bf16: M=%lld too large for the grid", (long long)M);
     GemmOut o{{Y0, Y1, Y2}, {ld0, ld1, ld2}, split1, split2, out_dtype == HX_BF16, act};
-    const int64_t large_tiles = ((M + LBM - 1) / LBM) * ((N + LBN - 1) / LBN);
+    const size_t dlds = (size_t)DSTAGES * DSTAGE_BYTES;
+    // auto: the direct-to-LDS kernel for long K (measured ahead of the 128 x 128 kernel from
+    // K = 2048 on, behind it at K <= 512 where its one block per CU cannot hide the epilogue)
+    if (vec && K % LBK == 0 && (g_gemm_kernel == 4 || (g_gemm_kernel == 0 && K >= 2048)) &&
+        dlds_ok(dlds)) {
+        dim3 lg((unsigned)((N + LBN - 1) / LBN), (unsigned)((M + LBM - 1) / LBM));
+        hipLaunchKernelGGL(gemm_bf16_nt_dlds_kernel, lg, dim3(256), dlds, as_stream(stream), M, N, K,
+                           (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
+        HX_LAUNCH_CHECK();
+        return HX_OK;
+    }
     const size_t lds = (size_t)2 * (LBM + LBN) * LLDK * sizeof(uint16_t);
-    if (vec && g_gemm_kernel != 1 && (g_gemm_kernel == 2 || (large_tiles >= 256 && K >= 256)) &&
-        large_lds_ok(lds)) {
+    if (vec && g_gemm_kernel != 1 && g_gemm_kernel != 3 &&
+        g_gemm_kernel == 2 && large_lds_ok(lds)) {
         dim3 lg((unsigned)((N + LBN - 1) / LBN), (unsigned)((M + LBM - 1) / LBM));
         hipLaunchKernelGGL(gemm_bf16_nt_large_kernel<true>, lg, dim3(256), lds, as_stream(stream),
                            M, N, K, (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
@@ -504,7 +684,7 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
         return HX_OK;
     }
     const int64_t tiles128 = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    if (vec && g_gemm_kernel != 1 && g_gemm_kernel != 2 &&
+    if (vec && g_gemm_kernel != 1 && g_gemm_kernel != 2 && g_gemm_kernel != 4 &&
         (g_gemm_kernel == 3 || (tiles128 < 128 && (M + 31) / 32 <= 65535))) {
         dim3 sg((unsigned)((N + 63) / 64), (unsigned)((M + 31) / 32));
         hipLaunchKernelGGL(gemm_bf16_nt_small_kernel, sg, dim3(256), 0, as_stream(stream), M, N, K,
@@ -525,7 +705,7 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
 
 extern "C" int hx_set_gemm_kernel(int k) {
     using namespace hx;
-    HX_REQUIRE(k >= 0 && k <= 3, HX_ERR_INVALID_INPUT, "hx_set_gemm_kernel: %d (0 auto, 1, 2, 3)", k);
+    HX_REQUIRE(k >= 0 && k <= 4, HX_ERR_INVALID_INPUT, "hx_set_gemm_kernel: %d (0 auto, 1..4)", k);
     g_gemm_kernel = k;
     return HX_OK;
 }

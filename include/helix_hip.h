@@ -254,7 +254,8 @@ int hx_set_scan_variant(int variant);
  * the (batch, 64-channel) tiles cannot fill the GPU and seqlen >= 4096). Segments are scanned in
  * parallel from a zero state, their entry states chained by a carry kernel, then rescanned with
  * outputs. A measurement knob; results agree within fp32 rounding for every setting. */
-int hx_set_gemm_kernel(int k);     /* 0 auto, 1 128x128 tiles, 2 256x128 tiles, 3 split-K 32x64 tiles */
+int hx_set_gemm_kernel(int k);     /* 0 auto, 1 128x128 tiles, 2 256x128 tiles, 3 split-K 32x64 tiles,
+                                      4 direct-to-LDS 256x128 tiles (K % 64 == 0) */
 int hx_set_s4d_path(int path);      /* 0 auto (wave path for dstate 16), 1 per-channel thread path */
 int hx_set_s4d_segments(int nseg);  /* S4D time segments: 0 auto, n forced */
 int hx_set_scan_segments(int nseg);

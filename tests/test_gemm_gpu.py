@@ -67,12 +67,15 @@ def gemm_kernel(dev, request):
     ssm.set_gemm_kernel(0)
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 2, 3], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 2, 3, 4], indirect=True)
 @pytest.mark.parametrize("M,N,K", [(512, 256, 512), (300, 200, 136), (257, 129, 64), (1024, 2048, 1024),
-                                   (100, 72, 1000), (256, 64, 1024), (33, 40, 24)])
+                                   (100, 72, 1000), (256, 64, 1024), (33, 40, 24), (300, 260, 192),
+                                   (600, 136, 128)])
 @pytest.mark.parametrize("act", [0, 1])
 def test_gemm_tile_kernels_fp32_out(dev, gemm_kernel, M, N, K, act):
-    """Both tile kernels (128 x 128 x 32 and 256 x 128 x 64) on aligned and ragged shapes."""
+    """Each tile kernel (128 x 128 x 32, 256 x 128 x 64 register-staged, split-K 32 x 64, 256 x
+    128 x 64 direct-to-LDS) on aligned and ragged shapes; the direct-to-LDS kernel takes the
+    shapes with K % 64 == 0 (1, 2, 3 and more K tiles) and falls back on the others."""
     g = torch.Generator().manual_seed(M + N + K)
     X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
     W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
@@ -83,7 +86,7 @@ def test_gemm_tile_kernels_fp32_out(dev, gemm_kernel, M, N, K, act):
     assert err <= 1e-5, err
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 2, 3], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 2, 3, 4], indirect=True)
 @pytest.mark.parametrize("splits", [(128, 144), (100, 133), (8, 16)])
 def test_gemm_tile_kernels_splits_bf16(dev, gemm_kernel, splits):
     """Column splits on vector boundaries and straddling them (100, 133 are not multiples of 8)."""
@@ -98,7 +101,7 @@ def test_gemm_tile_kernels_splits_bf16(dev, gemm_kernel, splits):
     assert err <= 2 ** -7, err  # within one bf16 ulp of the rounded reference
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 2, 3], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 2, 3, 4], indirect=True)
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 def test_gemm_accumulate_into_output(dev, gemm_kernel, out_dtype):
     """act bit 1: Y += X . W^T (the residual add of a pre-norm layer)."""
