@@ -34,6 +34,8 @@ sys.path.insert(0, ROOT)
 from helixml_amd import _ffi, ssm  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
+# the kernel the automatic dispatch runs for config 2 (the name rocprofv3 reports)
+SCAN_KERNEL = "scan_wave3_kernel<float, 2, true, true, false, 4>"
 
 
 def scan_bytes(bt, L, dim, N, es, with_z=True, with_D=True):
@@ -365,7 +367,7 @@ def main():
     tfile = os.path.join(ROOT, "profiles", "traffic.json")
     if args.workload == "c2" and args.variant == 0 and os.path.exists(tfile):
         # measured HBM bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)
-        rec_t = json.load(open(tfile)).get("scan_wave2_kernel<float, 2, true, true, false>@config2")
+        rec_t = json.load(open(tfile)).get(SCAN_KERNEL + "@config2")
         traffic = rec_t["traffic_bytes"] if rec_t else None
 
     rec = {

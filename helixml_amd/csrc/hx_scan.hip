@@ -1034,6 +1034,227 @@ __global__ __launch_bounds__(256) void scan_wave2_kernel(
     }
 }
 
+// scan_wave2_kernel with every wave on its own: each wave stages its own 16 channels x 16 steps
+// tiles (one float4 per lane per operand, 64-byte row pieces) in its own LDS region, so the
+// waves of a block never wait for each other (no block barrier per chunk; LDS operations of one
+// wave execute in order, so program order alone orders each wave's staging writes and reads).
+// WPB waves per block (64 * WPB threads). Same arithmetic, results identical to wave2's.
+// Requires L * Dm < 2^31 (32-bit offsets within a batch row).
+template <typename T, int PF, bool HAS_Z, bool SOFTPLUS, bool END_ONLY, int WPB>
+__global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
+    int64_t L, int64_t Dm, int ntiles, int64_t Bt,
+    const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
+    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
+    const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
+    const float* __restrict__ init_state, float* __restrict__ last_state, WaveSeg sg) {
+    constexpr int NS = 16, TCH = 16;
+    constexpr int GS = 20;  // gather row stride (floats): 16 values + pad
+    constexpr bool USE_Z = HAS_Z && !END_ONLY;
+    __shared__ __attribute__((aligned(16))) float s_in[WPB][2][3][TCH][16];  // [w][buf][u|dt|z][step][ch]
+    __shared__ __attribute__((aligned(16))) float s_out[WPB][END_ONLY ? 1 : 2][TCH][16];
+    __shared__ __attribute__((aligned(16))) float s_g[WPB][2][16][GS];  // [w][dt|dt*u][ch][4i + r]
+
+    const int nblk = gridDim.x;
+    int id = blockIdx.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);  // XCD-aware order
+    const int tile = id % ntiles;
+    const int64_t b = (id / ntiles) % Bt;
+    const int seg = (int)(id / ntiles / Bt);
+    const int64_t tbeg = (int64_t)seg * sg.seg_len;
+    const int64_t tend = tbeg + sg.seg_len < L ? tbeg + sg.seg_len : L;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int r = lane >> 4;
+    const int c = lane & 15;
+    const int64_t c0 = ((int64_t)tile * WPB + w) * 16;  // this wave's 16 channels
+    const int cb = c;
+    const int64_t d = c0 + cb;
+    const bool dvalid = d < Dm;
+    const int64_t dc = dvalid ? d : Dm - 1;
+    const int mrow = lane >> 2, mcl = (lane & 3) * 4;  // staging: step row, 4 channels
+    const int64_t mch = c0 + mcl;
+    const bool mvalid = mch < Dm;
+
+    // per-row bases; 32-bit offsets inside the row
+    const T* ub = u + b * L * Dm;
+    const T* db = delta + b * L * Dm;
+    const T* zb = USE_Z ? z + b * L * Dm : nullptr;
+    T* ob = END_ONLY ? nullptr : out + b * L * Dm;
+    const T* Bb = Bm + b * L * NS;
+    const T* Cb = Cm + b * L * NS;
+    const uint32_t D32 = (uint32_t)Dm;
+    const uint32_t mcol = (uint32_t)(mvalid ? mch : 0);
+    const uint32_t x_last = (uint32_t)(tend - 1) * D32 + mcol;          // clamp of tile offsets
+    const uint32_t bc_last = (uint32_t)(tend - 1) * NS + 4 * r;         // clamp of B/C offsets
+    uint32_t x_next = (uint32_t)(tbeg + mrow) * D32 + mcol;             // next tile fetch
+    uint32_t bc_next = (uint32_t)(tbeg + c) * NS + 4 * r;               // next B/C fetch
+    const uint32_t x_step = TCH * D32, bc_step = TCH * NS;
+
+    float A2[4], h[4];
+    const float* h0 = END_ONLY ? nullptr
+                    : (sg.nseg > 1 ? sg.seg_init + (int64_t)seg * Bt * Dm * NS : init_state);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        A2[k] = A[dc * NS + 4 * r + k] * kLog2e;
+        h[k] = h0 ? h0[(b * Dm + dc) * NS + 4 * r + k] : 0.0f;
+    }
+    const float Dd = Dv ? Dv[dc] : 0.0f;
+    const float bias = dt_bias ? dt_bias[dc] : 0.0f;
+    float sumdt = 0.0f;
+
+    float4 ru[PF], rd[PF], rz[PF], rb[PF], rc[PF];
+    auto fetch = [&](int k) __attribute__((always_inline)) {
+        const uint32_t xo = x_next < x_last ? x_next : x_last;
+        ru[k] = Vec4<T>::load(ub + xo);
+        rd[k] = Vec4<T>::load(db + xo);
+        rz[k] = USE_Z ? Vec4<T>::load(zb + xo) : make_float4(0, 0, 0, 0);
+        const uint32_t bo = bc_next < bc_last ? bc_next : bc_last;
+        rb[k] = Vec4<T>::load(Bb + bo);
+        rc[k] = END_ONLY ? make_float4(0, 0, 0, 0) : Vec4<T>::load(Cb + bo);
+        x_next += x_step;
+        bc_next += bc_step;
+    };
+    auto stage_in = [&](int k, int buf) __attribute__((always_inline)) {
+        *reinterpret_cast<float4*>(&s_in[w][buf][0][mrow][mcl]) = ru[k];
+        *reinterpret_cast<float4*>(&s_in[w][buf][1][mrow][mcl]) = rd[k];
+        if (USE_Z) *reinterpret_cast<float4*>(&s_in[w][buf][2][mrow][mcl]) = rz[k];
+    };
+    auto store_out = [&](int64_t t0, int buf) __attribute__((always_inline)) {
+        if constexpr (!END_ONLY) {
+            const int64_t t = t0 + mrow;
+            if (mvalid && t < tend)
+                Vec4<T>::store(ob + ((uint32_t)t * D32 + mcol),
+                               *reinterpret_cast<const float4*>(&s_out[w][buf][mrow][mcl]));
+        }
+    };
+
+    // math for one chunk: inputs from s_in[buf], outputs into s_out[buf]; FULL = all 16 steps
+    // inside the segment
+    auto compute = [&](int64_t t0, int buf, const float4& B4, const float4& C4, auto full_c)
+        __attribute__((always_inline)) {
+        constexpr bool FULL = decltype(full_c)::value;
+        const int nvalid = FULL ? TCH : (int)(tend - t0);
+        float uu[4], zz[4], dl[4], du[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int s = r + 4 * i;
+            uu[i] = s_in[w][buf][0][s][cb];
+            float x = s_in[w][buf][1][s][cb] + bias;
+            zz[i] = USE_Z ? s_in[w][buf][2][s][cb] : 0.0f;
+            if (SOFTPLUS) x = softplus(x);
+            if (!FULL) x = s < nvalid ? x : 0.0f;  // steps past the end leave the state unchanged
+            dl[i] = x;
+            du[i] = x * uu[i];
+            if (END_ONLY) sumdt += x;
+        }
+        // row all-gather through LDS: lane (r, c) holds steps r + 4i, stored step-major
+        // (s_g[.][cb][s], s = 4i + r) so the float4 at [4g] is exactly the steps of group g and
+        // each group's read can be in flight while the previous group computes
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s_g[w][0][cb][4 * i + r] = dl[i];
+            s_g[w][1][cb][4 * i + r] = du[i];
+        }
+        __builtin_amdgcn_wave_barrier();
+        float gdl[4][4], gdu[4][4];  // [row rr][i]: step rr + 4i
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 a = *reinterpret_cast<const float4*>(&s_g[w][0][cb][4 * i]);
+            const float4 q = *reinterpret_cast<const float4*>(&s_g[w][1][cb][4 * i]);
+            gdl[0][i] = a.x; gdl[1][i] = a.y; gdl[2][i] = a.z; gdl[3][i] = a.w;
+            gdu[0][i] = q.x; gdu[1][i] = q.y; gdu[2][i] = q.z; gdu[3][i] = q.w;
+        }
+        const float bk[4] = {B4.x, B4.y, B4.z, B4.w};
+        const float ck[4] = {C4.x, C4.y, C4.z, C4.w};
+        float P[16];
+        StepLoop<4>::run([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            float ab[4][4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int s = 4 * g + e;
+                    ab[e][k] = fast_exp2(gdl[s & 3][s >> 2] * A2[k]);
+                }
+            StepLoop<4>::run([&](auto ec) {
+                constexpr int s = 4 * g + decltype(ec)::value;
+                const float dus = gdu[s & 3][s >> 2];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) h[k] = fmaf(ab[s - 4 * g][k], h[k], dpp<kDppBcast<s>>(bk[k]) * dus);
+                if constexpr (!END_ONLY) {
+                    float acc = dpp<kDppBcast<s>>(ck[0]) * h[0];
+                    acc = fmac_bcast<s>(acc, ck[1], h[1]);
+                    acc = fmac_bcast<s>(acc, ck[2], h[2]);
+                    acc = fmac_bcast<s>(acc, ck[3], h[3]);
+                    P[(s >> 2) + 4 * (s & 3)] = acc;  // j = i + 4*rr for s = rr + 4*i
+                }
+            });
+        });
+        if constexpr (!END_ONLY) {
+            float Y[4];
+            rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int s = r + 4 * i;
+                float y = fmaf(Dd, uu[i], Y[i]);
+                if (HAS_Z) y *= silu(zz[i]);
+                s_out[w][buf][s][cb] = y;
+            }
+        }
+    };
+
+#pragma unroll
+    for (int k = 0; k < PF; ++k) fetch(k);
+    stage_in(0, 0);
+    float4 B4 = rb[0], C4 = rc[0];
+    fetch(0);
+    for (int64_t tb0 = tbeg; tb0 < tend; tb0 += PF * TCH) {
+        StepLoop<PF>::run([&](auto kc) __attribute__((always_inline)) {
+            constexpr int k = decltype(kc)::value;
+            constexpr int kn = (k + 1) % PF;
+            constexpr int buf = k & 1;  // PF is even
+            const int64_t t0 = tb0 + k * TCH;
+            if (t0 >= tend) return;  // uniform
+            stage_in(kn, buf ^ 1);
+            if (t0 > tbeg) store_out(t0 - TCH, END_ONLY ? 0 : buf ^ 1);
+            const float4 Bn = rb[kn], Cn = rc[kn];
+            fetch(kn);
+            if (t0 + TCH <= tend)
+                compute(t0, buf, B4, C4, std::true_type{});
+            else
+                compute(t0, buf, B4, C4, std::false_type{});
+            B4 = Bn;
+            C4 = Cn;
+            __builtin_amdgcn_wave_barrier();
+        });
+    }
+    if constexpr (!END_ONLY) {
+        const int64_t nch = (tend - tbeg + TCH - 1) / TCH;
+        store_out(tbeg + (nch - 1) * TCH, (int)((nch - 1) & 1));
+        if (last_state && dvalid && seg == sg.nseg - 1) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) last_state[(b * Dm + d) * NS + 4 * r + k] = h[k];
+        }
+    } else {
+        float t1 = sumdt, t2 = sumdt;
+        swap16(t1, t2);
+        float sa = t1 + t2;
+        float t3 = sa, t4 = sa;
+        swap32(t3, t4);
+        sumdt = t3 + t4;
+        if (dvalid) {
+            float* he = sg.seg_hend + (int64_t)seg * Bt * Dm * NS;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) he[(b * Dm + d) * NS + 4 * r + k] = h[k];
+            if (r == 0) sg.seg_sumdt[((int64_t)seg * Bt + b) * Dm + d] = sumdt;
+        }
+    }
+}
+
+
 // Entry state of every segment: h_in[0] = init (or 0); h_in[k] = exp(A * sumdt[k-1]) * h_in[k-1]
 // + hend[k-1], per (b, d, n). Writes seg_init[k] for k = 0..nseg-1 (reads hend/sumdt of the
 // first nseg-1 segments only).
@@ -1233,27 +1454,37 @@ int dispatch_tile(const ScanArgs& a) {
     return launch_tile<T, W, TCH, PF, false, false, SBC>(a);
 }
 
-template <typename T, int PF, bool HAS_Z, bool SP, bool END_ONLY, bool V2>
+// VER: 1 scan_wave_kernel, 2 scan_wave2_kernel, 3 scan_wave3_kernel with 4 waves per block,
+// 4 scan_wave3_kernel with 1 wave per block
+template <typename T, int PF, bool HAS_Z, bool SP, bool END_ONLY, int VER>
 int launch_wave_one(const ScanArgs& a, const WaveSeg& sg) {
-    const int ntiles = (int)((a.Dm + 63) / 64);
+    constexpr int WPB = VER == 4 ? 1 : 4;
+    const int64_t ntiles = (a.Dm + 16 * WPB - 1) / (16 * WPB);
     // the end-state pass skips the last segment: nothing consumes its end state
     const int64_t nseg_run = END_ONLY ? sg.nseg - 1 : sg.nseg;
-    dim3 grid((unsigned)((int64_t)ntiles * a.Bt * nseg_run));
-    if constexpr (V2)
+    HX_REQUIRE(ntiles * a.Bt * nseg_run <= 0x7fffffff, HX_ERR_UNSUPPORTED,
+               "selective scan: %lld blocks exceed the grid", (long long)(ntiles * a.Bt * nseg_run));
+    dim3 grid((unsigned)(ntiles * a.Bt * nseg_run));
+    if constexpr (VER >= 3)
+        hipLaunchKernelGGL((scan_wave3_kernel<T, PF, HAS_Z, SP, END_ONLY, WPB>), grid, dim3(64 * WPB), 0,
+                           a.stream, a.L, a.Dm, (int)ntiles, a.Bt, (const T*)a.u, (const T*)a.delta, a.A,
+                           (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
+                           a.init_state, a.last_state, sg);
+    else if constexpr (VER == 2)
         hipLaunchKernelGGL((scan_wave2_kernel<T, PF, HAS_Z, SP, END_ONLY>), grid, dim3(256), 0,
-                           a.stream, a.L, a.Dm, ntiles, a.Bt, (const T*)a.u, (const T*)a.delta, a.A,
+                           a.stream, a.L, a.Dm, (int)ntiles, a.Bt, (const T*)a.u, (const T*)a.delta, a.A,
                            (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
                            a.init_state, a.last_state, sg);
     else
         hipLaunchKernelGGL((scan_wave_kernel<T, PF, HAS_Z, SP, END_ONLY>), grid, dim3(256), 0,
-                           a.stream, a.L, a.Dm, ntiles, a.Bt, (const T*)a.u, (const T*)a.delta, a.A,
+                           a.stream, a.L, a.Dm, (int)ntiles, a.Bt, (const T*)a.u, (const T*)a.delta, a.A,
                            (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
                            a.init_state, a.last_state, sg);
     HX_LAUNCH_CHECK();
     return HX_OK;
 }
 
-template <typename T, int PF, bool HAS_Z, bool SP, bool V2>
+template <typename T, int PF, bool HAS_Z, bool SP, int VER>
 int launch_wave(const ScanArgs& a) {
     // Segment the sequence when the (batch, 64-channel tile) pairs alone cannot fill the GPU.
     const int64_t ntiles = (a.Dm + 63) / 64;
@@ -1270,7 +1501,7 @@ int launch_wave(const ScanArgs& a) {
     int64_t seg_len = (a.L + nseg - 1) / nseg;
     seg_len = (seg_len + 15) / 16 * 16;
     nseg = (int)((a.L + seg_len - 1) / seg_len);
-    if (nseg <= 1) return launch_wave_one<T, PF, HAS_Z, SP, false, V2>(a, WaveSeg{a.L, 1, nullptr, nullptr, nullptr});
+    if (nseg <= 1) return launch_wave_one<T, PF, HAS_Z, SP, false, VER>(a, WaveSeg{a.L, 1, nullptr, nullptr, nullptr});
 
     const size_t per = (size_t)a.Bt * a.Dm * 16;
     const size_t nfloat = (size_t)nseg * (2 * per + (size_t)a.Bt * a.Dm);
@@ -1279,7 +1510,7 @@ int launch_wave(const ScanArgs& a) {
     float* hend = scratch;
     float* seg_init = hend + (size_t)nseg * per;
     float* sumdt = seg_init + (size_t)nseg * per;
-    int rc = launch_wave_one<T, PF, false, SP, true, V2>(a, WaveSeg{seg_len, nseg, nullptr, hend, sumdt});
+    int rc = launch_wave_one<T, PF, false, SP, true, VER>(a, WaveSeg{seg_len, nseg, nullptr, hend, sumdt});
     if (rc == HX_OK) {
         hipLaunchKernelGGL(scan_seg_carry_kernel, dim3((unsigned)((per + 255) / 256)), dim3(256), 0,
                            a.stream, a.Bt, a.Dm, nseg, a.A, a.init_state, hend, sumdt, seg_init);
@@ -1288,18 +1519,18 @@ int launch_wave(const ScanArgs& a) {
             rc = set_error(HX_ERR_BACKEND, "scan carry launch failed: %s", hipGetErrorString(e));
     }
     if (rc == HX_OK)
-        rc = launch_wave_one<T, PF, HAS_Z, SP, false, V2>(a, WaveSeg{seg_len, nseg, seg_init, nullptr, nullptr});
+        rc = launch_wave_one<T, PF, HAS_Z, SP, false, VER>(a, WaveSeg{seg_len, nseg, seg_init, nullptr, nullptr});
     (void)hipFreeAsync(scratch, a.stream);
     return rc;
 }
 
-template <typename T, int PF, bool V2 = false>
+template <typename T, int PF, int VER = 1>
 int dispatch_wave(const ScanArgs& a) {
     const bool hz = a.z != nullptr;
-    if (hz && a.softplus) return launch_wave<T, PF, true, true, V2>(a);
-    if (hz) return launch_wave<T, PF, true, false, V2>(a);
-    if (a.softplus) return launch_wave<T, PF, false, true, V2>(a);
-    return launch_wave<T, PF, false, false, V2>(a);
+    if (hz && a.softplus) return launch_wave<T, PF, true, true, VER>(a);
+    if (hz) return launch_wave<T, PF, true, false, VER>(a);
+    if (a.softplus) return launch_wave<T, PF, false, true, VER>(a);
+    return launch_wave<T, PF, false, false, VER>(a);
 }
 
 template <typename T, bool HAS_Z, bool SP>
@@ -1364,7 +1595,7 @@ int run_scan(const ScanArgs& a) {
                          a.Bt * ((a.Dm + 63) / 64) <= 0x7fffffff;
     if (v == 0) {  // auto: the wave-complete kernel where its float4 access is legal
         if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16))
-            return a.L * a.Dm < (1LL << 31) ? dispatch_wave<T, 2, true>(a) : dispatch_wave<T, 2>(a);
+            return a.L * a.Dm < (1LL << 31) ? dispatch_wave<T, 2, 3>(a) : dispatch_wave<T, 2>(a);
         if (tile_ok) return dispatch_tile<T, 8, 32, 2, false>(a);
         return dispatch_fast<T, 8, 16>(a);
     }
@@ -1376,7 +1607,15 @@ int run_scan(const ScanArgs& a) {
         case 40: if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16)) return dispatch_wave<T, 2>(a); break;
         case 41:
             if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && a.L * a.Dm < (1LL << 31))
-                return dispatch_wave<T, 2, true>(a);
+                return dispatch_wave<T, 2, 2>(a);
+            break;
+        case 42:
+            if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && a.L * a.Dm < (1LL << 31))
+                return dispatch_wave<T, 2, 3>(a);
+            break;
+        case 43:
+            if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && a.L * a.Dm < (1LL << 31))
+                return dispatch_wave<T, 2, 4>(a);
             break;
         case 36: if (tile_ok) return dispatch_tile<T, 4, 16, 2, true>(a); break;
         case 16: return dispatch_state_lane<T>(a);
@@ -1437,9 +1676,9 @@ extern "C" int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim,
 extern "C" int hx_set_scan_variant(int variant) {
     HX_REQUIRE(variant == 0 || variant == -1 || variant == 1 || variant == 2 || variant == 4 ||
                    variant == 8 || variant == 16 || (variant >= 32 && variant <= 36) || variant == 40 ||
-                   variant == 41,
+                   variant == 41 || variant == 42 || variant == 43,
                HX_ERR_INVALID_INPUT,
-               "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8, 16, 32..36, 40, 41", variant);
+               "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8, 16, 32..36, 40..43", variant);
     hx::g_scan_variant = variant;
     return HX_OK;
 }

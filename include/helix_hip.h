@@ -247,8 +247,11 @@ int hx_matmul_f32(int64_t M, int64_t K, int64_t N, const float* A, const float* 
 /* ------------------------------------------------------------------ tuning */
 /* Selects the selective-scan kernel variant for later calls in this process: 0 = auto (default),
  * 1/2/4/8 = the fast kernel with that many waves per block (16/W states per wave), -1 = the
- * generic one-thread-per-channel kernel. A measurement knob with no reference counterpart;
- * results are identical within fp32 rounding for every variant. */
+ * generic one-thread-per-channel kernel, 16 = one lane per state, 32..36 = block-tiled kernels,
+ * 40 = wave-complete kernel (a wave owns 16 channels x 16 states), 41 = its leaner form, 42/43 =
+ * the leaner form with per-wave staging and no block barrier, 4 / 1 waves per block. A
+ * measurement knob with no reference counterpart; results are identical within fp32 rounding
+ * for every variant. */
 int hx_set_scan_variant(int variant);
 /* Number of time segments the long-sequence path splits a scan into (0 = automatic: only when
  * the (batch, 64-channel) tiles cannot fill the GPU and seqlen >= 4096). Segments are scanned in

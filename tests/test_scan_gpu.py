@@ -16,7 +16,7 @@ from tests.util import TOL_BF16, TOL_F32, bf16_round, rel_err, scan_inputs
 
 pytestmark = pytest.mark.gpu
 
-VARIANTS = [-1, 1, 2, 4, 8, 16, 32, 33, 34, 35, 36, 40, 41]
+VARIANTS = [-1, 1, 2, 4, 8, 16, 32, 33, 34, 35, 36, 40, 41, 42, 43]
 
 
 def to_dev(x, dev, dtype=torch.float32):
@@ -64,7 +64,7 @@ def test_scan_matches_oracle(dev, shape, variant):
 @pytest.mark.parametrize("with_z", [True, False])
 @pytest.mark.parametrize("with_D", [True, False])
 @pytest.mark.parametrize("softplus", [True, False])
-@pytest.mark.parametrize("variant", [41, 40, 32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", [43, 42, 41, 40, 32, 33, 16, 4, -1])
 def test_scan_optional_operands(dev, with_z, with_D, softplus, variant):
     ssm.set_scan_variant(variant)
     x = scan_inputs(2, 70, 96, 16, seed=7, with_z=with_z, with_D=with_D)
@@ -108,7 +108,7 @@ def test_scan_zero_length_returns_initial_state(dev):
     assert np.array_equal(s, init)
 
 
-@pytest.mark.parametrize("variant", [41, 40, 32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", [43, 42, 41, 40, 32, 33, 16, 4, -1])
 @pytest.mark.parametrize("shape", [(2, 37, 70, 16), (1, 300, 256, 16)], ids=str)
 def test_scan_bf16_storage(dev, variant, shape):
     ssm.set_scan_variant(variant)
@@ -159,7 +159,7 @@ def test_shape_errors_raise_reference_variants(dev):
                                to_dev(x["B"], dev), to_dev(x["C"], dev))
 
 
-@pytest.mark.parametrize("variant", [0, 40, 41])
+@pytest.mark.parametrize("variant", [0, 40, 41, 42, 43])
 def test_baseline_config2_full_size(dev, variant):
     """BASELINE config 2 (batch 8, L 2048, d_inner 1536, d_state 16, fp32) end to end against the
     (multi-threaded, arithmetic-identical) CPU oracle."""
@@ -182,7 +182,7 @@ def _reset_segments(dev):
     ssm.set_scan_variant(0)
 
 
-@pytest.mark.parametrize("variant", [40, 41])
+@pytest.mark.parametrize("variant", [40, 41, 42, 43])
 @pytest.mark.parametrize("nseg", [2, 3, 7])
 @pytest.mark.parametrize("shape", [(2, 300, 128, 16), (1, 1000, 64, 16), (1, 77, 192, 16)], ids=str)
 def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape, variant):
@@ -198,7 +198,7 @@ def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape, va
     assert rel_err(glast, rlast) <= TOL_F32
 
 
-@pytest.mark.parametrize("variant", [0, 40, 41])
+@pytest.mark.parametrize("variant", [0, 40, 41, 42, 43])
 def test_baseline_config4_scan_full_size(dev, variant):
     """BASELINE config 4 scan (batch 1, L 65536, d_inner 2048, d_state 16, fp32): the automatic
     segmented path against the (multi-threaded, arithmetic-identical) CPU oracle."""
