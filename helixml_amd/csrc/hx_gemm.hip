@@ -479,8 +479,6 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_large_kernel(int64_t M, int6
 // by choosing which global chunk each lane loads, so the MFMA fragment reads (one chunk of 32
 // consecutive rows) spread over the banks. Requires K % 64 == 0 and 16-byte aligned rows; rows
 // past M or N are clamped (their outputs are discarded).
-typedef __attribute__((address_space(1))) void gvoid_t;
-typedef __attribute__((address_space(3))) void lvoid_t;
 constexpr int DSTAGES = 3;
 constexpr int DSTAGE_BYTES = (LBM + LBN) * LBK * 2;  // 48 KiB
 

@@ -1276,6 +1276,382 @@ __global__ __launch_bounds__(256) void scan_seg_carry_kernel(
     }
 }
 
+// global_load_lds of VB bytes per lane: lane i's VB bytes at g land at l + i * VB.
+template <int VB> __device__ inline void load_lds(const void* g, void* l);
+template <> __device__ inline void load_lds<16>(const void* g, void* l) {
+    __builtin_amdgcn_global_load_lds((gvoid_t*)g, (lvoid_t*)l, 16, 0, 0);
+}
+template <> __device__ inline void load_lds<4>(const void* g, void* l) {
+    __builtin_amdgcn_global_load_lds((gvoid_t*)g, (lvoid_t*)l, 4, 0, 0);
+}
+
+// LDS reads written as inline asm that complete inside the statement (s_waitcnt lgkmcnt(0)).
+// The element wave of scan_ws_kernel reads LDS while its global_load_lds loads are still in
+// flight; for compiler-visible LDS reads the compiler inserts a wait for all of those loads
+// (vmcnt(0)), which would drain the load ring every chunk. These reads are ordered by the
+// wave's own explicit vmcnt waits instead. Addresses are LDS byte offsets.
+typedef float hx_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t hx_u32x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)p; }
+__device__ inline float4 to_f4(hx_f32x4 v) { return make_float4(v[0], v[1], v[2], v[3]); }
+__device__ inline float4 bf16x4_to_f4(hx_u32x2 v) {
+    return make_float4(__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u),
+                       __uint_as_float(v[1] << 16), __uint_as_float(v[1] & 0xffff0000u));
+}
+// r[j][o] = 4 storage elements at a[j] + o * OPB, o < NOP (2 or 3), j < 3; fp32 (16-byte reads)
+// or bf16 (8-byte reads) storage
+template <typename T, int NOP, int OPB> struct RingRead;
+template <int OPB> struct RingRead<float, 3, OPB> {
+    __device__ static inline void run(const uint32_t (&a)[3], float4 (&r)[3][3]) {
+        hx_f32x4 v[3][3];
+        asm volatile(
+            "ds_read_b128 %0, %9\n\tds_read_b128 %1, %9 offset:%12\n\tds_read_b128 %2, %9 offset:%13\n\t"
+            "ds_read_b128 %3, %10\n\tds_read_b128 %4, %10 offset:%12\n\tds_read_b128 %5, %10 offset:%13\n\t"
+            "ds_read_b128 %6, %11\n\tds_read_b128 %7, %11 offset:%12\n\tds_read_b128 %8, %11 offset:%13\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(v[0][2]), "=&v"(v[1][0]), "=&v"(v[1][1]), "=&v"(v[1][2]),
+              "=&v"(v[2][0]), "=&v"(v[2][1]), "=&v"(v[2][2])
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "n"(OPB), "n"(2 * OPB)
+            : "memory");
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int o = 0; o < 3; ++o) r[j][o] = to_f4(v[j][o]);
+    }
+};
+template <int OPB> struct RingRead<float, 2, OPB> {
+    __device__ static inline void run(const uint32_t (&a)[3], float4 (&r)[3][3]) {
+        hx_f32x4 v[3][2];
+        asm volatile(
+            "ds_read_b128 %0, %6\n\tds_read_b128 %1, %6 offset:%9\n\t"
+            "ds_read_b128 %2, %7\n\tds_read_b128 %3, %7 offset:%9\n\t"
+            "ds_read_b128 %4, %8\n\tds_read_b128 %5, %8 offset:%9\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(v[1][0]), "=&v"(v[1][1]), "=&v"(v[2][0]), "=&v"(v[2][1])
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "n"(OPB)
+            : "memory");
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int o = 0; o < 2; ++o) r[j][o] = to_f4(v[j][o]);
+    }
+};
+template <int OPB> struct RingRead<uint16_t, 3, OPB> {
+    __device__ static inline void run(const uint32_t (&a)[3], float4 (&r)[3][3]) {
+        hx_u32x2 v[3][3];
+        asm volatile(
+            "ds_read_b64 %0, %9\n\tds_read_b64 %1, %9 offset:%12\n\tds_read_b64 %2, %9 offset:%13\n\t"
+            "ds_read_b64 %3, %10\n\tds_read_b64 %4, %10 offset:%12\n\tds_read_b64 %5, %10 offset:%13\n\t"
+            "ds_read_b64 %6, %11\n\tds_read_b64 %7, %11 offset:%12\n\tds_read_b64 %8, %11 offset:%13\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(v[0][2]), "=&v"(v[1][0]), "=&v"(v[1][1]), "=&v"(v[1][2]),
+              "=&v"(v[2][0]), "=&v"(v[2][1]), "=&v"(v[2][2])
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "n"(OPB), "n"(2 * OPB)
+            : "memory");
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int o = 0; o < 3; ++o) r[j][o] = bf16x4_to_f4(v[j][o]);
+    }
+};
+template <int OPB> struct RingRead<uint16_t, 2, OPB> {
+    __device__ static inline void run(const uint32_t (&a)[3], float4 (&r)[3][3]) {
+        hx_u32x2 v[3][2];
+        asm volatile(
+            "ds_read_b64 %0, %6\n\tds_read_b64 %1, %6 offset:%9\n\t"
+            "ds_read_b64 %2, %7\n\tds_read_b64 %3, %7 offset:%9\n\t"
+            "ds_read_b64 %4, %8\n\tds_read_b64 %5, %8 offset:%9\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(v[1][0]), "=&v"(v[1][1]), "=&v"(v[2][0]), "=&v"(v[2][1])
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "n"(OPB)
+            : "memory");
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int o = 0; o < 2; ++o) r[j][o] = bf16x4_to_f4(v[j][o]);
+    }
+};
+
+// One element stored through a raw buffer resource: offsets at or past the resource's size are
+// dropped by the hardware, so a store needs no branch (and the compiler's wait counts stay exact).
+__device__ inline void buf_store(float v, __amdgpu_buffer_rsrc_t rs, uint32_t off, float*) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, off, 0, 0);
+}
+__device__ inline void buf_store(float v, __amdgpu_buffer_rsrc_t rs, uint32_t off, uint16_t*) {
+    __builtin_amdgcn_raw_buffer_store_b16(Storage<uint16_t>::round(v), rs, off, 0, 0);
+}
+constexpr int kBufRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+// ----------------------------------------------------------------------------- warp-specialised
+// A block of 4 waves owns 48 channels of one batch row, and its waves have different jobs:
+//   * waves 0..2 ("state waves") each own 16 of the channels x all 16 states in the layout of
+//     scan_wave3_kernel (lane (r, c): channel c, states 4r..4r+3; B/C of step t0+j in lane j of
+//     row r, reaching the multiplies by DPP row_newbcast). Per state update they issue one
+//     v_exp, dt*A, B*(dt*u), the FMA and the DPP readout FMA; per chunk they reduce-scatter the
+//     per-row readouts across rows (lane (r, c) ends with steps r + 4i of channel c), add D*u,
+//     apply the gate and store, in scan_wave3_kernel's operation order (the two kernels give
+//     bit-identical results);
+//   * wave 3 (the "element wave") does the rest of the per-(t, channel) work for the 48
+//     channels: u/delta/z move from HBM straight into an NR-deep LDS ring (gfx950
+//     global_load_lds: 64 lanes x VB bytes into one contiguous piece of LDS per instruction,
+//     so a chunk lands as [operand][step][48 channels] rows) under the wave's own vmcnt waits;
+//     from there it computes softplus(delta + bias), dt*u and SiLU(z).
+// The roles hand over through LDS with one barrier per 16-step chunk and a 3-deep buffer: in
+// phase p the state waves scan chunk p (dt, dt*u read during phase p-1; u, SiLU(z) from
+// buffer p%3) and read chunk p+1's dt and dt*u, while the element wave prepares chunk p+2 into
+// buffer (p+2)%3. Steps past the end get dt = 0 and dt*u = 0, which leave the state unchanged,
+// and their stores fall outside the buffer resource. The dynamic LDS request keeps one block per
+// CU, so every SIMD runs one wave. Requires Dm % 4 == 0, 16-byte rows,
+// (L + 16) * Dm * es < 2^32 (byte offsets of a batch row, padded steps included, in 32 bits).
+template <typename T, int NR, bool HAS_Z, bool SOFTPLUS>
+__global__ __launch_bounds__(256) void scan_ws_kernel(
+    int64_t L, int64_t Dm, int ngrp,
+    const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
+    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
+    const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
+    const float* __restrict__ init_state, float* __restrict__ last_state) {
+    constexpr int NS = 16, TCH = 16, GCH = 48, DS = 20;
+    // Hand-over buffers [buf][dt | dt*u | u | SiLU(z)][ch][.], rows padded to 20 words:
+    // dt and dt*u by step (a state lane reads its channel's 16 steps as 4 float4s); u and
+    // SiLU(z) with step r + 4i at index 4r + i (the order in which the state waves' lanes hold
+    // the steps after the reduce-scatter: one float4 per lane)
+    __shared__ __attribute__((aligned(16))) float s_x[3][4][GCH][DS];
+
+    const int nblk = gridDim.x;
+    int id = blockIdx.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);  // XCD-aware order
+    const int grp = id % ngrp;
+    const int64_t b = id / ngrp;
+    const int64_t cblk = (int64_t)grp * GCH;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nch = (int)((L + TCH - 1) / TCH);
+    const uint32_t D32 = (uint32_t)Dm;
+
+    if (w < 3) {
+        // ------------------------------------------------------------ state wave
+        const int r = lane >> 4, c = lane & 15;
+        const int lch = 16 * w + c;  // channel within the block
+        const int64_t d = cblk + lch;
+        const bool dvalid = d < Dm;
+        const int64_t dc = dvalid ? d : Dm - 1;
+        float A2[4], h[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            A2[k] = A[dc * NS + 4 * r + k] * kLog2e;
+            h[k] = init_state ? init_state[(b * Dm + dc) * NS + 4 * r + k] : 0.0f;
+        }
+        const float Dd = Dv ? Dv[dc] : 0.0f;
+        const T* Bb = Bm + b * L * NS;
+        const T* Cb = Cm + b * L * NS;
+        const uint32_t bc_last = (uint32_t)(L - 1) * NS + 4 * r;
+        uint32_t bc_next = (uint32_t)c * NS + 4 * r;
+        float4 rb[2], rc[2];
+        auto fetch = [&](int k) __attribute__((always_inline)) {
+            const uint32_t bo = bc_next < bc_last ? bc_next : bc_last;
+            rb[k] = Vec4<T>::load(Bb + bo);
+            rc[k] = Vec4<T>::load(Cb + bo);
+            bc_next += TCH * NS;
+        };
+        const uint32_t nrec = (uint32_t)(L * Dm * (int64_t)sizeof(T));
+        const uint32_t row_bytes = D32 * (uint32_t)sizeof(T);
+        // byte offset of (step r, this channel); invalid channels start past the end
+        const uint32_t lane_off = dvalid ? ((uint32_t)r * D32 + (uint32_t)d) * (uint32_t)sizeof(T) : nrec;
+        const __amdgpu_buffer_rsrc_t ors =
+            __builtin_amdgcn_make_buffer_rsrc(out + b * L * Dm, (short)0, (int)nrec, kBufRsrcWord3);
+        float dl[2][16], du[2][16];
+        auto read_dt = [&](auto kc, int b3) __attribute__((always_inline)) {
+            constexpr int k = decltype(kc)::value;
+            const float* p0 = &s_x[b3][0][lch][0];
+            const float* p1 = &s_x[b3][1][lch][0];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 a = *reinterpret_cast<const float4*>(p0 + 4 * i);
+                const float4 q = *reinterpret_cast<const float4*>(p1 + 4 * i);
+                dl[k][4 * i] = a.x; dl[k][4 * i + 1] = a.y; dl[k][4 * i + 2] = a.z; dl[k][4 * i + 3] = a.w;
+                du[k][4 * i] = q.x; du[k][4 * i + 1] = q.y; du[k][4 * i + 2] = q.z; du[k][4 * i + 3] = q.w;
+            }
+        };
+        fetch(0);
+        fetch(1);
+        lds_barrier();  // chunks 0 and 1 prepared
+        read_dt(std::integral_constant<int, 0>{}, 0);
+        int b3 = 0;  // p % 3
+        for (int p0 = 0; p0 < nch; p0 += 2) {
+            StepLoop<2>::run([&](auto kc) __attribute__((always_inline)) {
+                constexpr int k = decltype(kc)::value;  // = p & 1: dt register set and B/C slot
+                const int p = p0 + k;
+                if (p >= nch) return;  // uniform
+                const int b3n = b3 == 2 ? 0 : b3 + 1;
+                if (p + 1 < nch) read_dt(std::integral_constant<int, k ^ 1>{}, b3n);
+                const float4 fu = *reinterpret_cast<const float4*>(&s_x[b3][2][lch][4 * r]);  // u
+                const float4 fz = HAS_Z ? *reinterpret_cast<const float4*>(&s_x[b3][3][lch][4 * r])
+                                        : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+                const float fuv[4] = {fu.x, fu.y, fu.z, fu.w};
+                const float fzv[4] = {fz.x, fz.y, fz.z, fz.w};
+                const float bk[4] = {rb[k].x, rb[k].y, rb[k].z, rb[k].w};
+                const float ck[4] = {rc[k].x, rc[k].y, rc[k].z, rc[k].w};
+                float P[16];
+                StepLoop<4>::run([&](auto gc) __attribute__((always_inline)) {
+                    constexpr int g = decltype(gc)::value;
+                    float ab[4][4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) ab[e][kk] = fast_exp2(dl[k][4 * g + e] * A2[kk]);
+                    StepLoop<4>::run([&](auto ec) __attribute__((always_inline)) {
+                        constexpr int e = decltype(ec)::value;
+                        constexpr int s = 4 * g + e;
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk)
+                            h[kk] = fmaf(ab[e][kk], h[kk], dpp<kDppBcast<s>>(bk[kk]) * du[k][s]);
+                        float acc = dpp<kDppBcast<s>>(ck[0]) * h[0];
+                        acc = fmac_bcast<s>(acc, ck[1], h[1]);
+                        acc = fmac_bcast<s>(acc, ck[2], h[2]);
+                        acc = fmac_bcast<s>(acc, ck[3], h[3]);
+                        P[(s >> 2) + 4 * (s & 3)] = acc;  // j = i + 4*rr for s = rr + 4*i
+                    });
+                });
+                fetch(k);  // chunk p + 2, into the slot this chunk's B/C came from
+                float Y[4];
+                rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i
+                // step r + 4i of this chunk sits at lane_off + (16p + 4i) * row bytes; steps past
+                // the end land at or past nrec and are dropped
+                const uint32_t chunk_off = lane_off + (uint32_t)p * (uint32_t)TCH * row_bytes;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float y = fmaf(Dd, fuv[i], Y[i]);  // as scan_wave3_kernel: identical results
+                    if (HAS_Z) y *= fzv[i];
+                    buf_store(y, ors, chunk_off + 4 * i * row_bytes, (T*)nullptr);
+                }
+                b3 = b3n;
+                lds_barrier();
+            });
+        }
+        if (last_state && dvalid) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) last_state[(b * Dm + d) * NS + 4 * r + k] = h[k];
+        }
+    } else {
+        // ------------------------------------------------------------ element wave
+        constexpr int ES = (int)sizeof(T);
+        constexpr int VB = ES == 4 ? 16 : 4;           // bytes per lane per load
+        constexpr int ROWB = GCH * ES;                 // one step of 48 channels
+        constexpr int OPB = TCH * ROWB;                // one operand of one chunk
+        constexpr int NI = OPB / (64 * VB);            // loads per operand per chunk
+        constexpr int LPR = ROWB / VB;                 // lanes per step row
+        constexpr int NOP = HAS_Z ? 3 : 2;
+        constexpr int LPC = NOP * NI;                  // loads per chunk
+        constexpr int STB = NOP * OPB;                 // LDS bytes per ring stage
+        constexpr int WAITN = (NR - 1) * LPC;
+        static_assert(OPB % (64 * VB) == 0 && WAITN <= 63, "load split / vmcnt range");
+        extern __shared__ __attribute__((aligned(16))) char s_ring[];  // [NR][operand][step][ch]
+
+        // this lane's source offsets (elements within a batch row, chunk 0) per load instruction
+        uint32_t srow[NI], scol[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int q = 64 * i + lane;
+            srow[i] = (uint32_t)(q / LPR);
+            const int64_t ch = cblk + (q % LPR) * (VB / ES);
+            scol[i] = (uint32_t)(ch < Dm ? ch : 0);  // a lane's channels are all valid or all not
+        }
+        const T* ub = u + b * L * Dm;
+        const T* db = delta + b * L * Dm;
+        const T* zb = HAS_Z ? z + b * L * Dm : nullptr;
+        const uint32_t t_last = (uint32_t)(L - 1);
+        auto issue = [&](int stage, int q) __attribute__((always_inline)) {
+            char* dst = s_ring + stage * STB;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                uint32_t t = (uint32_t)q * TCH + srow[i];
+                t = t < t_last ? t : t_last;  // rows past the end: loaded, never used
+                const uint32_t off = t * D32 + scol[i];
+                load_lds<VB>(ub + off, dst + i * 64 * VB);
+                load_lds<VB>(db + off, dst + OPB + i * 64 * VB);
+                if (HAS_Z) load_lds<VB>(zb + off, dst + 2 * OPB + i * 64 * VB);
+            }
+        };
+
+        // element group j (0..2) of a chunk: step sj[j], channels cj[j] .. cj[j]+3 of the block
+        int sj[3], cj[3];
+        float bias_r[3][4];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int q = 64 * j + lane;
+            sj[j] = q / 12;
+            cj[j] = (q % 12) * 4;
+            const int64_t ch = cblk + cj[j];
+            const bool cv = ch < Dm;  // Dm % 4 == 0: a group is all valid or all invalid
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bias_r[j][e] = (dt_bias && cv) ? dt_bias[ch + e] : 0.0f;
+        }
+        // chunk q, from ring stage `stage`, into buffer b3
+        auto prepare = [&](int stage, int b3, int q) __attribute__((always_inline)) {
+            const char* src = s_ring + stage * STB;
+            uint32_t ra[3];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) ra[j] = lds_off(src + sj[j] * ROWB + cj[j] * ES);
+            float4 raw[3][3];  // [j][u | delta | z]
+            RingRead<T, NOP, OPB>::run(ra, raw);
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const bool tv = (int64_t)q * TCH + sj[j] < L;
+                const int sp = (sj[j] & 3) * 4 + (sj[j] >> 2);  // step r + 4i at 4r + i
+                float x[4], xu[4], uv[4], fz[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v = f4get(raw[j][1], e) + bias_r[j][e];
+                    if (SOFTPLUS) v = softplus(v);
+                    v = tv ? v : 0.0f;
+                    const float uu = f4get(raw[j][0], e);
+                    x[e] = v;
+                    xu[e] = v * uu;
+                    uv[e] = uu;
+                    fz[e] = HAS_Z ? silu(f4get(raw[j][NOP - 1], e)) : 1.0f;
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    s_x[b3][0][cj[j] + e][sj[j]] = x[e];
+                    s_x[b3][1][cj[j] + e][sj[j]] = xu[e];
+                    s_x[b3][2][cj[j] + e][sp] = uv[e];
+                    if (HAS_Z) s_x[b3][3][cj[j] + e][sp] = fz[e];
+                }
+            }
+        };
+        auto wait_loads = [&]() __attribute__((always_inline)) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
+        };
+        auto barrier = [&]() __attribute__((always_inline)) {
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        };
+        // ring stage of chunk q is q % NR; every chunk index issues exactly LPC loads (clamped
+        // rows past the end), so the wait count is the same before every prepare
+#pragma unroll
+        for (int k = 0; k < NR; ++k) issue(k, k);
+        int stage = 0;  // q % NR of the next chunk to prepare
+        int b3 = 0;     // q % 3 of the next chunk to prepare
+        int q = 0;      // next chunk to prepare
+        auto step = [&]() __attribute__((always_inline)) {
+            wait_loads();
+            prepare(stage, b3, q);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage read before it is refilled
+            issue(stage, q + NR);
+            stage = stage + 1 == NR ? 0 : stage + 1;
+            b3 = b3 == 2 ? 0 : b3 + 1;
+            ++q;
+        };
+        step();               // chunk 0
+        if (nch > 1) step();  // chunk 1
+        barrier();
+        for (int p = 0; p < nch; ++p) {
+            if (p + 2 < nch) step();  // chunk p + 2
+            barrier();
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load still writing LDS at exit
+    }
+}
+
 // ----------------------------------------------------------------------------- generic path
 // One thread per (b, d), states in registers, any dstate <= NMAX, no alignment assumptions.
 template <typename T, int NMAX>
@@ -1533,6 +1909,60 @@ int dispatch_wave(const ScanArgs& a) {
     return launch_wave<T, PF, false, false, VER>(a);
 }
 
+// Dynamic LDS of the warp-specialised kernel: its NR-stage ring of u/delta/z chunks, rounded
+// up so that with the static LDS (s_x) the block holds more than half a CU's 160 KB and no CU
+// runs two of its blocks: one wave per SIMD, the element wave on a SIMD of its own. Granted per
+// kernel and device through hipFuncSetAttribute (cached).
+constexpr size_t kWsStaticLds = 3 * 4 * 48 * 20 * 4;
+size_t ws_dyn_lds(int NR, bool has_z, size_t es) {
+    const size_t ring = (size_t)NR * (has_z ? 3 : 2) * 16 * 48 * es;
+    const size_t need = 84 * 1024 - kWsStaticLds;
+    return ring > need ? ring : need;
+}
+bool ws_lds_ok(const void* fn, size_t bytes) {
+    struct Entry { const void* fn; int dev; int ok; };
+    static Entry cache[64];
+    static int n = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    for (int i = 0; i < n; ++i)
+        if (cache[i].fn == fn && cache[i].dev == dev) return cache[i].ok != 0;
+    int v = 0;
+    const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+                    (size_t)v >= bytes + kWsStaticLds &&
+                    hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
+    (void)hipGetLastError();
+    if (n < 64) cache[n++] = Entry{fn, dev, ok ? 1 : 0};
+    return ok;
+}
+
+template <typename T, int NR, bool HAS_Z, bool SP>
+int launch_ws(const ScanArgs& a) {
+    const int64_t ngrp = (a.Dm + 47) / 48;
+    HX_REQUIRE(ngrp * a.Bt <= 0x7fffffff, HX_ERR_UNSUPPORTED,
+               "selective scan: %lld blocks exceed the grid", (long long)(ngrp * a.Bt));
+    const void* fn = (const void*)scan_ws_kernel<T, NR, HAS_Z, SP>;
+    const size_t dyn = ws_dyn_lds(NR, HAS_Z, sizeof(T));
+    HX_REQUIRE(ws_lds_ok(fn, dyn), HX_ERR_UNSUPPORTED,
+               "selective scan: the device does not grant %zu bytes of LDS per block",
+               dyn + kWsStaticLds);
+    hipLaunchKernelGGL((scan_ws_kernel<T, NR, HAS_Z, SP>), dim3((unsigned)(ngrp * a.Bt)), dim3(256), dyn,
+                       a.stream, a.L, a.Dm, (int)ngrp, (const T*)a.u, (const T*)a.delta, a.A,
+                       (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
+                       a.init_state, a.last_state);
+    HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+template <typename T, int NR>
+int dispatch_ws(const ScanArgs& a) {
+    const bool hz = a.z != nullptr;
+    if (hz && a.softplus) return launch_ws<T, NR, true, true>(a);
+    if (hz) return launch_ws<T, NR, true, false>(a);
+    if (a.softplus) return launch_ws<T, NR, false, true>(a);
+    return launch_ws<T, NR, false, false>(a);
+}
+
 template <typename T, bool HAS_Z, bool SP>
 int launch_state_lane(const ScanArgs& a) {
     constexpr int PF = 4;
@@ -1576,6 +2006,36 @@ int dispatch_generic(const ScanArgs& a) {
     return launch_generic<T, 64>(a);
 }
 
+// Compute units of the current device (cached per device; 256 on an MI355X).
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int v = 0;
+        cached[dev] = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+                          ? v : 256;
+    }
+    return cached[dev];
+}
+
+// Whether the automatic choice takes the warp-specialised kernel over scan_wave3_kernel. Both
+// are bound by the state waves' issue rate. wave3 runs one wave per SIMD per 16 channels; the
+// warp-specialised kernel one block per CU per 48 channels (3 state waves plus the element
+// wave), and its state waves are the faster of the two (measured on MI355X at config 2: 0.89 of
+// wave3's time per round) because the element wave takes the per-element work off them. A round
+// is one wave per SIMD (wave3) or one block per CU (warp-specialised); a partial round costs a
+// full one. The long-sequence shapes that wave3 cuts into time segments stay with wave3.
+bool ws_preferred(const ScanArgs& a, size_t es) {
+    if ((a.L + 16) * a.Dm * (int64_t)es >= (1LL << 32) || g_scan_segments > 0) return false;
+    const int64_t pairs = a.Bt * ((a.Dm + 63) / 64);
+    if (pairs < 256 && a.L >= 4096) return false;  // wave3 segments these
+    const int64_t cus = device_cus();
+    const int64_t ws_rounds = (a.Bt * ((a.Dm + 47) / 48) + cus - 1) / cus;
+    const int64_t w3_rounds = (a.Bt * ((a.Dm + 15) / 16) + 4 * cus - 1) / (4 * cus);
+    return (double)ws_rounds * 0.89 < (double)w3_rounds;
+}
+
 // Kernel variant: 0 = auto, 1/2/4/8 = fast kernel with that many waves, -1 = generic.
 // hx_set_scan_variant() sets it; HX_SCAN_VARIANT in the environment gives the initial value.
 int g_scan_variant = [] {
@@ -1593,9 +2053,11 @@ int run_scan(const ScanArgs& a) {
                          aligned(a.out, 16) && (!a.z || aligned(a.z, 16)) &&
                          (!a.D || aligned(a.D, 16)) && (!a.dt_bias || aligned(a.dt_bias, 16)) &&
                          a.Bt * ((a.Dm + 63) / 64) <= 0x7fffffff;
-    if (v == 0) {  // auto: the wave-complete kernel where its float4 access is legal
-        if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16))
+    if (v == 0) {  // auto: the wave-complete kernels where their float4 access is legal
+        if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16)) {
+            if (ws_preferred(a, sizeof(T))) return dispatch_ws<T, 2>(a);
             return a.L * a.Dm < (1LL << 31) ? dispatch_wave<T, 2, 3>(a) : dispatch_wave<T, 2>(a);
+        }
         if (tile_ok) return dispatch_tile<T, 8, 32, 2, false>(a);
         return dispatch_fast<T, 8, 16>(a);
     }
@@ -1616,6 +2078,14 @@ int run_scan(const ScanArgs& a) {
         case 43:
             if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && a.L * a.Dm < (1LL << 31))
                 return dispatch_wave<T, 2, 4>(a);
+            break;
+        case 44:
+            if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && (a.L + 16) * a.Dm * (int64_t)sizeof(T) < (1LL << 32))
+                return dispatch_ws<T, 2>(a);
+            break;
+        case 45:
+            if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && (a.L + 16) * a.Dm * (int64_t)sizeof(T) < (1LL << 32))
+                return dispatch_ws<T, sizeof(T) == 4 ? 8 : 4>(a);
             break;
         case 36: if (tile_ok) return dispatch_tile<T, 4, 16, 2, true>(a); break;
         case 16: return dispatch_state_lane<T>(a);
@@ -1676,9 +2146,9 @@ extern "C" int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim,
 extern "C" int hx_set_scan_variant(int variant) {
     HX_REQUIRE(variant == 0 || variant == -1 || variant == 1 || variant == 2 || variant == 4 ||
                    variant == 8 || variant == 16 || (variant >= 32 && variant <= 36) || variant == 40 ||
-                   variant == 41 || variant == 42 || variant == 43,
+                   (variant >= 41 && variant <= 45),
                HX_ERR_INVALID_INPUT,
-               "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8, 16, 32..36, 40..43", variant);
+               "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8, 16, 32..36, 40..45", variant);
     hx::g_scan_variant = variant;
     return HX_OK;
 }

@@ -16,7 +16,7 @@ from tests.util import TOL_BF16, TOL_F32, bf16_round, rel_err, scan_inputs
 
 pytestmark = pytest.mark.gpu
 
-VARIANTS = [-1, 1, 2, 4, 8, 16, 32, 33, 34, 35, 36, 40, 41, 42, 43]
+VARIANTS = [-1, 1, 2, 4, 8, 16, 32, 33, 34, 35, 36, 40, 41, 42, 43, 44, 45]
 
 
 def to_dev(x, dev, dtype=torch.float32):
@@ -64,7 +64,7 @@ def test_scan_matches_oracle(dev, shape, variant):
 @pytest.mark.parametrize("with_z", [True, False])
 @pytest.mark.parametrize("with_D", [True, False])
 @pytest.mark.parametrize("softplus", [True, False])
-@pytest.mark.parametrize("variant", [43, 42, 41, 40, 32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", [45, 44, 43, 42, 41, 40, 32, 33, 16, 4, -1])
 def test_scan_optional_operands(dev, with_z, with_D, softplus, variant):
     ssm.set_scan_variant(variant)
     x = scan_inputs(2, 70, 96, 16, seed=7, with_z=with_z, with_D=with_D)
@@ -73,6 +73,36 @@ def test_scan_optional_operands(dev, with_z, with_D, softplus, variant):
     g = run_gpu(x, dev, softplus=softplus)
     r = oracle.selective_scan(**x, delta_softplus=softplus)
     assert rel_err(g, r) <= TOL_F32
+
+
+@pytest.mark.parametrize("variant", [0, 42, 44, 45, -1])
+def test_scan_softplus_all_regimes(dev, variant):
+    """delta spread over softplus's regimes: e^x far below f32 resolution of 1 + e^x (x < -17,
+    where softplus(x) = e^x), the log1p range, and past the x > 20 cut-over."""
+    ssm.set_scan_variant(variant)
+    x = scan_inputs(2, 130, 96, 16, seed=21, with_bias=True)
+    rng = np.random.default_rng(22)
+    x["delta"] = (rng.standard_normal(x["delta"].shape) * 9.0).astype(np.float32)
+    x["delta"][:, ::7] = np.float32(-30.0)
+    x["delta"][:, 3::11] = np.float32(25.0)
+    x["A"] = (x["A"] * np.float32(0.05)).astype(np.float32)  # keep exp(dt*A) away from 0 at dt ~ 25
+    g = run_gpu(x, dev)
+    assert rel_err(g, oracle.selective_scan(**x)) <= TOL_F32
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_scan_warp_specialised_matches_wave_kernel_bitwise(dev, dtype):
+    """The warp-specialised kernel (44/45) keeps scan_wave3_kernel's (42) operation order, so the
+    automatic choice between them never changes a result bit; ragged L and dim included."""
+    x = scan_inputs(3, 203, 100, 16, seed=23, with_bias=True)
+    init = (np.random.default_rng(24).standard_normal((3, 100, 16)) * 0.5).astype(np.float32)
+    outs = {}
+    for v in (42, 44, 45):
+        ssm.set_scan_variant(v)
+        outs[v] = run_gpu(x, dev, dtype=dtype, init_state=init, last=True)
+    for v in (44, 45):
+        assert np.array_equal(outs[v][0], outs[42][0]), v
+        assert np.array_equal(outs[v][1], outs[42][1]), v
 
 
 def test_scan_general_A(dev):
@@ -108,7 +138,7 @@ def test_scan_zero_length_returns_initial_state(dev):
     assert np.array_equal(s, init)
 
 
-@pytest.mark.parametrize("variant", [43, 42, 41, 40, 32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", [45, 44, 43, 42, 41, 40, 32, 33, 16, 4, -1])
 @pytest.mark.parametrize("shape", [(2, 37, 70, 16), (1, 300, 256, 16)], ids=str)
 def test_scan_bf16_storage(dev, variant, shape):
     ssm.set_scan_variant(variant)
@@ -159,7 +189,7 @@ def test_shape_errors_raise_reference_variants(dev):
                                to_dev(x["B"], dev), to_dev(x["C"], dev))
 
 
-@pytest.mark.parametrize("variant", [0, 40, 41, 42, 43])
+@pytest.mark.parametrize("variant", [0, 40, 41, 42, 43, 44, 45])
 def test_baseline_config2_full_size(dev, variant):
     """BASELINE config 2 (batch 8, L 2048, d_inner 1536, d_state 16, fp32) end to end against the
     (multi-threaded, arithmetic-identical) CPU oracle."""
