@@ -598,6 +598,149 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_dlds_kernel(int64_t M, int64
     }
 }
 
+
+// ----------------------------------------------------------------------------- 256 x 256
+// Direct-to-LDS kernel with a 256 x 256 block tile: 4 waves in 2 x 2, each a 128 x 128 tile
+// (4 x 4 v_mfma_f32_32x32x16_bf16 per 16-wide K step, 256 fp32 accumulators per lane, kept in
+// AGPRs). Per K step a wave reads 8 fragments of 16 bytes per lane from LDS for 16 MFMAs, half
+// the LDS bytes per MFMA of the 256 x 128 kernel (4 x 2 tiles per wave), whose LDS reads plus the
+// loads landing in LDS kept it near the CU's LDS bandwidth. K tiles of KB (32 or 64) in an
+// NST-stage LDS ring (A rows 0..255 then B rows 0..255, rows of KB K-values, 16-byte chunks
+// XOR-swizzled by row so that the 8 lanes of each 128-byte LDS access hit distinct banks); the
+// loads of tile kt+NST-1 are issued while tile kt is multiplied, behind one barrier per tile.
+// Requires K % KB == 0 and 16-byte aligned rows; rows past M or N are clamped (their outputs are
+// discarded).
+constexpr int XBM = 256, XBN = 256;
+
+template <int KB>
+__device__ inline int xswz(int row) {  // XOR applied to the 16-byte chunk index of a row
+    return KB == 64 ? (row & 7) : ((row >> 1) & 3);
+}
+
+template <int KB, int NST>
+__global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64_t N, int64_t K,
+                                                                const uint16_t* __restrict__ X,
+                                                                int64_t ldx,
+                                                                const uint16_t* __restrict__ W,
+                                                                int64_t ldw,
+                                                                const float* __restrict__ bias,
+                                                                GemmOut o) {
+    constexpr int RB = KB * 2;              // bytes per tile row
+    constexpr int CPR = KB / 8;             // 16-byte chunks per row
+    constexpr int RPK = 1024 / RB;          // rows per KiB (one load instruction)
+    constexpr int STB = (XBM + XBN) * RB;   // stage bytes
+    constexpr int QPW = STB / 1024 / 4;     // load instructions per wave per tile
+    constexpr int QA = XBM * RB / 1024;     // KiB regions of A
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    char* sbase = reinterpret_cast<char*>(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nbx = gridDim.x, nby = gridDim.y;
+    const int nb = nbx * nby;
+    int bid = blockIdx.y * nbx + blockIdx.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    const int64_t m0 = (int64_t)(bid / nbx) * XBM, n0 = (int64_t)(bid % nbx) * XBN;
+
+    // this lane's QPW global sources per tile: wave w issues KiB regions q = QPW*w .. of the
+    // stage (q < QA: A rows RPK*q.., else B rows RPK*(q-QA)..); lane L fills row RPK*q' + L/CPR,
+    // slot L%CPR with the K-chunk (L%CPR) ^ xswz(row)
+    const uint16_t* src[QPW];
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+        const int q = wave * QPW + j;
+        const bool isA = q < QA;
+        const int row = (isA ? q : q - QA) * RPK + lane / CPR;
+        const int chunk = (lane % CPR) ^ xswz<KB>(row);
+        if (isA) {
+            const int64_t gr = m0 + row < M ? m0 + row : M - 1;
+            src[j] = X + gr * ldx + chunk * 8;
+        } else {
+            const int64_t gr = n0 + row < N ? n0 + row : N - 1;
+            src[j] = W + gr * ldw + chunk * 8;
+        }
+    }
+    auto issue = [&](int64_t kt) __attribute__((always_inline)) {
+        char* stage = sbase + (int)(kt % NST) * STB;
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const int q = wave * QPW + j;
+            __builtin_amdgcn_global_load_lds((gvoid_t*)(src[j] + kt * KB), (lvoid_t*)(stage + q * 1024),
+                                             16, 0, 0);
+        }
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int fr = lane & 31;
+    const int fc = lane >> 5;  // chunk half within a 16-wide K sub-step
+    const int64_t nk = K / KB;
+#pragma unroll
+    for (int t = 0; t < NST - 1; ++t)
+        if (t < nk) issue(t);
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        // tile kt's loads are done when at most those of the tiles after it remain (wait and
+        // barrier in one statement: a fenced barrier would wait for every load in flight); the
+        // barrier also means every wave is past tile kt-1, whose stage tile kt+NST-1 refills
+        const int64_t after = nk - 1 - kt < NST - 2 ? nk - 1 - kt : NST - 2;
+        if (after >= 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * QPW) : "memory");
+        else if (after == 1) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(QPW) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kt + NST - 1 < nk) issue(kt + NST - 1);
+        const char* stage = sbase + (int)(kt % NST) * STB;
+        const char* aw = stage + (wm * 128 + fr) * RB;              // A rows of this lane
+        const char* bw = stage + XBM * RB + (wn * 128 + fr) * RB;   // B rows of this lane
+        auto load = [&](int s, bf16x8* af, bf16x8* bf) __attribute__((always_inline)) {
+            const int off = ((2 * s + fc) ^ xswz<KB>(fr)) << 4;  // row bases are multiples of 32
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(aw + i * 32 * RB + off);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(bw + j * 32 * RB + off);
+        };
+        bf16x8 fa[2][4], fb[2][4];
+        load(0, fa[0], fb[0]);
+#pragma unroll
+        for (int s = 0; s < KB / 16; ++s) {
+            if (s + 1 < KB / 16) load(s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s & 1][i], fb[s & 1][j],
+                                                                        acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    lds_barrier();  // the epilogue reuses stage memory
+
+    float* st = reinterpret_cast<float*>(smem) + wave * (32 * 68);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    st[row * 68 + j * 32 + (lane & 31)] = acc[i][2 * jj + j][r];
+                }
+            __builtin_amdgcn_wave_barrier();
+            store_tile_rows(o, bias, st, M, N, m0 + wm * 128 + i * 32, n0 + wn * 128 + jj * 64, lane);
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
 }  // namespace
 }  // namespace hx
 
@@ -619,6 +762,37 @@ bool large_lds_ok(size_t bytes) {
         cached[dev] = ok ? 1 : 2;
     }
     return cached[dev] == 1;
+}
+
+template <int KB, int NST>
+bool d256_ok() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    if (cached[dev] == 0) {
+        const size_t bytes = (size_t)NST * (hx::XBM + hx::XBN) * KB * 2;
+        int v = 0;
+        const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
+                            hipSuccess &&
+                        (size_t)v >= bytes &&
+                        hipFuncSetAttribute((const void*)hx::gemm_bf16_nt_d256_kernel<KB, NST>,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)bytes) == hipSuccess;
+        cached[dev] = ok ? 1 : 2;
+    }
+    return cached[dev] == 1;
+}
+
+template <int KB, int NST>
+int launch_d256(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* W, int64_t ldw,
+                const float* bias, const hx::GemmOut& o, void* stream) {
+    using namespace hx;
+    const size_t bytes = (size_t)NST * (XBM + XBN) * KB * 2;
+    dim3 lg((unsigned)((N + XBN - 1) / XBN), (unsigned)((M + XBM - 1) / XBM));
+    hipLaunchKernelGGL((gemm_bf16_nt_d256_kernel<KB, NST>), lg, dim3(256), bytes, as_stream(stream), M, N, K,
+                       (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
+    HX_LAUNCH_CHECK();
+    return HX_OK;
 }
 
 bool dlds_ok(size_t bytes) {
@@ -661,6 +835,15 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     HX_REQUIRE((N + BN - 1) / BN <= 0x7fffffff && (M + BM - 1) / BM <= 65535, HX_ERR_UNSUPPORTED,
                "gemm_bf16: M=%lld too large for the grid", (long long)M);
     GemmOut o{{Y0, Y1, Y2}, {ld0, ld1, ld2}, split1, split2, out_dtype == HX_BF16, act};
+    // auto: the 256 x 256 kernel for the big projections (measured ahead of the 256 x 128 one at
+    // K = 1024..4096 with N >= 512 on MI355X: config 3 in_proj 712-725 vs 597-651 TFLOP/s,
+    // out_proj 918-947 vs 721-753; behind the 128 x 128 kernel at K = 512)
+    if (vec && K % 64 == 0 &&
+        (g_gemm_kernel == 5 || (g_gemm_kernel == 0 && K >= 1024 && N >= 512 && M >= 512)) &&
+        d256_ok<64, 2>())
+        return launch_d256<64, 2>(M, N, K, X, ldx, W, ldw, bias, o, stream);
+    if (vec && K % 32 == 0 && g_gemm_kernel == 6 && d256_ok<32, 4>())
+        return launch_d256<32, 4>(M, N, K, X, ldx, W, ldw, bias, o, stream);
     const size_t dlds = (size_t)DSTAGES * DSTAGE_BYTES;
     // auto: the direct-to-LDS kernel for long K (measured ahead of the 128 x 128 kernel from
     // K = 2048 on, behind it at K <= 512 where its one block per CU cannot hide the epilogue)
@@ -703,7 +886,7 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
 
 extern "C" int hx_set_gemm_kernel(int k) {
     using namespace hx;
-    HX_REQUIRE(k >= 0 && k <= 4, HX_ERR_INVALID_INPUT, "hx_set_gemm_kernel: %d (0 auto, 1..4)", k);
+    HX_REQUIRE(k >= 0 && k <= 6, HX_ERR_INVALID_INPUT, "hx_set_gemm_kernel: %d (0 auto, 1..6)", k);
     g_gemm_kernel = k;
     return HX_OK;
 }

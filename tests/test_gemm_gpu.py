@@ -67,7 +67,7 @@ def gemm_kernel(dev, request):
     ssm.set_gemm_kernel(0)
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 2, 3, 4], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 2, 3, 4, 5, 6], indirect=True)
 @pytest.mark.parametrize("M,N,K", [(512, 256, 512), (300, 200, 136), (257, 129, 64), (1024, 2048, 1024),
                                    (100, 72, 1000), (256, 64, 1024), (33, 40, 24), (300, 260, 192),
                                    (600, 136, 128)])
@@ -86,7 +86,7 @@ def test_gemm_tile_kernels_fp32_out(dev, gemm_kernel, M, N, K, act):
     assert err <= 1e-5, err
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 2, 3, 4], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 2, 3, 4, 5, 6], indirect=True)
 @pytest.mark.parametrize("splits", [(128, 144), (100, 133), (8, 16)])
 def test_gemm_tile_kernels_splits_bf16(dev, gemm_kernel, splits):
     """Column splits on vector boundaries and straddling them (100, 133 are not multiples of 8)."""
@@ -101,7 +101,7 @@ def test_gemm_tile_kernels_splits_bf16(dev, gemm_kernel, splits):
     assert err <= 2 ** -7, err  # within one bf16 ulp of the rounded reference
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 2, 3, 4], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 2, 3, 4, 5, 6], indirect=True)
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 def test_gemm_accumulate_into_output(dev, gemm_kernel, out_dtype):
     """act bit 1: Y += X . W^T (the residual add of a pre-norm layer)."""
