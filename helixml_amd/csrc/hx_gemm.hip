@@ -741,6 +741,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
     }
 }
 
+
 }  // namespace
 }  // namespace hx
 
