@@ -87,14 +87,16 @@ __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 __device__ inline float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// softplus(x) = log(1 + e^x), x > 20 -> x. log1p is evaluated as log(u) * e / (u - 1) with
-// u = 1 + e (Goldberg, "What every computer scientist should know about floating-point
-// arithmetic", 1991, Thm. 4), which keeps full relative accuracy for small e^x.
+// softplus(x) = log(1 + e^x), x > 20 -> x. With u = fl(1 + e), log1p(e) = log(u) + log(1 + d/u)
+// where d = (1 + e) - u is the rounding error of u. For e < 1, d = e - (u - 1) exactly (Fast2Sum,
+// Dekker 1971), and log(1 + d/u) = d to within |d| e/(1+e) <= 2^-24 log1p(e); for e >= 1 the
+// term is below 2^-24 log(u) and is dropped. Two transcendentals, no reciprocal, and full
+// relative accuracy for small e^x (u == 1 gives e).
 __device__ inline float softplus(float x) {
     float e = fast_exp2(x * kLog2e);
     float u = 1.0f + e;
-    float lg = fast_log2(u) * kLn2;
-    float r = (u == 1.0f) ? e : lg * (e * fast_rcp(u - 1.0f));
+    float d = e - (u - 1.0f);
+    float r = fast_log2(u) * kLn2 + (e < 1.0f ? d : 0.0f);
     return x > 20.0f ? x : r;
 }
 

@@ -265,6 +265,75 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_small_kernel(int64_t M, int6
     }
 }
 
+// Whole-slab store of a staged 32 x 64 fp32 tile (st, row stride 68) without bias or SiLU:
+// `yb` points at the slab's first output element, `ldb` is the output row pitch in bytes, both
+// 16-byte aligned. bf16: 8 lanes x 8 columns per row, 8 rows per pass; fp32: 16 lanes x 4
+// columns, 4 rows per pass.
+// ACC adds the existing output (Y += X W^T), in the same order as the general path.
+template <bool BF16, bool ACC>
+__device__ inline void store_slab_fast(char* __restrict__ yb, int64_t ldb, const float* st, int lane) {
+    // explicit address spaces: LDS reads, and global (not flat) output accesses, since a flat
+    // access also counts in lgkmcnt and would hold up the next slab's LDS waits until it completes
+    typedef uint32_t u32v4 __attribute__((ext_vector_type(4)));
+    typedef float f32v4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(1))) u32v4 g_u32v4;
+    typedef __attribute__((address_space(1))) f32v4 g_f32v4;
+    typedef __attribute__((address_space(3))) const f32v4 l_f32v4;
+    constexpr int LPR = BF16 ? 8 : 16;    // lanes per row
+    constexpr int RPP = 64 / LPR;         // rows per pass
+    constexpr int NP = 32 / RPP;          // passes
+    constexpr int VW = BF16 ? 8 : 4;      // columns per lane
+    const int rl = lane / LPR, cl = (lane % LPR) * VW;
+    l_f32v4* sp = (l_f32v4*)(st + rl * 68 + cl);
+    char* yp = yb + rl * ldb + cl * (BF16 ? 2 : 4);
+    // all of the slab's loads first (the outputs read for ACC, then the staged values), so their
+    // latencies overlap instead of each store waiting on the next load
+    f32v4 v[NP][VW / 4];
+    u32v4 old[ACC ? NP : 1];
+    if constexpr (ACC) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) old[p] = *(const g_u32v4*)(yp + p * RPP * ldb);
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int h = 0; h < VW / 4; ++h) v[p][h] = sp[p * RPP * 17 + h];  // 17 vectors per row
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        char* q = yp + p * RPP * ldb;
+        if constexpr (BF16) {
+            float f[8] = {v[p][0].x, v[p][0].y, v[p][0].z, v[p][0].w,
+                          v[p][1].x, v[p][1].y, v[p][1].z, v[p][1].w};
+            if constexpr (ACC) {
+                const uint32_t ow[4] = {old[p].x, old[p].y, old[p].z, old[p].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    f[2 * k] += __uint_as_float(ow[k] << 16);
+                    f[2 * k + 1] += __uint_as_float(ow[k] & 0xffff0000u);
+                }
+            }
+            // v_cvt_pk_bf16_f32: round to nearest even, as Storage<uint16_t>::round for every
+            // finite normal value
+            typedef float f32v2 __attribute__((ext_vector_type(2)));
+            typedef __bf16 bf16v2 __attribute__((ext_vector_type(2)));
+            uint32_t wv[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                wv[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32v2{f[2 * k], f[2 * k + 1]}, bf16v2));
+            *(g_u32v4*)q = u32v4{wv[0], wv[1], wv[2], wv[3]};
+        } else {
+            f32v4 f = v[p][0];
+            if constexpr (ACC) {
+                f.x += __uint_as_float(old[p].x);
+                f.y += __uint_as_float(old[p].y);
+                f.z += __uint_as_float(old[p].z);
+                f.w += __uint_as_float(old[p].w);
+            }
+            *(g_f32v4*)q = f;
+        }
+    }
+}
+
 // Writes a wave's staged 32 x 64 fp32 tile (st, row stride 68) to the outputs: rows of 64
 // columns as 16-byte vectors (8 bf16 or 4 fp32 per lane) with bias, SiLU and accumulate; a
 // vector that would straddle a column split or the N edge falls back to element stores.
@@ -617,6 +686,30 @@ __device__ inline int xswz(int row) {  // XOR applied to the 16-byte chunk index
     return KB == 64 ? (row & 7) : ((row >> 1) & 3);
 }
 
+// Epilogue of one wave's 128 x 128 sub-tile when it lies inside one output with aligned rows and
+// neither bias nor SiLU applies: 8 slabs of 32 x 64, each staged through the wave's LDS slab and
+// written with store_slab_fast. `yb` points at the sub-tile's first output element.
+template <bool BF16, bool ACC>
+__device__ __forceinline__ void d256_epilogue_fast(f32x16 (&acc)[4][4], float* st, char* yb, int64_t ldb,
+                                                   int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    st[row * 68 + j * 32 + (lane & 31)] = acc[i][2 * jj + j][r];
+                }
+            __builtin_amdgcn_wave_barrier();
+            store_slab_fast<BF16, ACC>(yb + i * 32 * ldb + jj * 64 * (BF16 ? 2 : 4), ldb, st, lane);
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
 template <int KB, int NST>
 __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64_t N, int64_t K,
                                                                 const uint16_t* __restrict__ X,
@@ -723,6 +816,28 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
     lds_barrier();  // the epilogue reuses stage memory
 
     float* st = reinterpret_cast<float*>(smem) + wave * (32 * 68);
+    {
+        // this wave's 128 x 128 sub-tile inside one output, rows aligned, no bias or SiLU: the
+        // unguarded slab stores
+        const int64_t r0 = m0 + wm * 128, c0 = n0 + wn * 128;
+        int seg = 0;
+        int64_t cc = c0;
+        if (c0 >= o.split2) { seg = 2; cc = c0 - o.split2; }
+        else if (c0 >= o.split1) { seg = 1; cc = c0 - o.split1; }
+        const int64_t seg_end = seg == 0 ? o.split1 : seg == 1 ? o.split2 : N;
+        const int64_t es = o.out_bf16 ? 2 : 4;
+        char* yb = (char*)o.yp(seg) + (r0 * o.ldp(seg) + cc) * es;
+        const int64_t ldb = o.ldp(seg) * es;
+        if (!bias && !(o.act & 1) && r0 + 128 <= M && c0 + 128 <= seg_end &&
+            (((uintptr_t)yb | (uint64_t)ldb) & 15) == 0) {
+            const int kind = (o.out_bf16 ? 0 : 2) + ((o.act & 2) ? 1 : 0);
+            if (kind == 0) d256_epilogue_fast<true, false>(acc, st, yb, ldb, lane);
+            else if (kind == 1) d256_epilogue_fast<true, true>(acc, st, yb, ldb, lane);
+            else if (kind == 2) d256_epilogue_fast<false, false>(acc, st, yb, ldb, lane);
+            else d256_epilogue_fast<false, true>(acc, st, yb, ldb, lane);
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -836,14 +951,15 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     HX_REQUIRE((N + BN - 1) / BN <= 0x7fffffff && (M + BM - 1) / BM <= 65535, HX_ERR_UNSUPPORTED,
                "gemm_bf16: M=%lld too large for the grid", (long long)M);
     GemmOut o{{Y0, Y1, Y2}, {ld0, ld1, ld2}, split1, split2, out_dtype == HX_BF16, act};
-    // auto: the 256 x 256 kernel for the big projections (measured ahead of the 256 x 128 one at
-    // K = 1024..4096 with N >= 512 on MI355X: config 3 in_proj 712-725 vs 597-651 TFLOP/s,
-    // out_proj 918-947 vs 721-753; behind the 128 x 128 kernel at K = 512)
-    if (vec && K % 64 == 0 &&
-        (g_gemm_kernel == 5 || (g_gemm_kernel == 0 && K >= 1024 && N >= 512 && M >= 512)) &&
-        d256_ok<64, 2>())
+    // auto: the 256 x 256 kernel wherever it fills the GPU with tiles at least 256 columns wide
+    // (measured on MI355X ahead of every other kernel here for the block's in_proj, out_proj,
+    // dt_proj and the LM head: 1.5-2.3x the 128 x 128 kernel; behind it for the narrow x_proj);
+    // the 32-wide K tile where K is not a multiple of 64 (config 5 dt_proj, K = 32)
+    const bool d256_auto = g_gemm_kernel == 0 && N >= 256 && M >= 256 &&
+                           ((M + XBM - 1) / XBM) * ((N + XBN - 1) / XBN) >= 256;
+    if (vec && K % 64 == 0 && (g_gemm_kernel == 5 || d256_auto) && d256_ok<64, 2>())
         return launch_d256<64, 2>(M, N, K, X, ldx, W, ldw, bias, o, stream);
-    if (vec && K % 32 == 0 && g_gemm_kernel == 6 && d256_ok<32, 4>())
+    if (vec && K % 32 == 0 && (g_gemm_kernel == 6 || (d256_auto && K % 64 != 0)) && d256_ok<32, 4>())
         return launch_d256<32, 4>(M, N, K, X, ldx, W, ldw, bias, o, stream);
     const size_t dlds = (size_t)DSTAGES * DSTAGE_BYTES;
     // auto: the direct-to-LDS kernel for long K (measured ahead of the 128 x 128 kernel from
