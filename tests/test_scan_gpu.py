@@ -217,15 +217,21 @@ def _reset_segments(dev):
 @pytest.mark.parametrize("shape", [(2, 300, 128, 16), (1, 1000, 64, 16), (1, 77, 192, 16)], ids=str)
 def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape, variant):
     """Time-segmented path (segment end states from zero, carry chain, rescan from entry
-    states) against the sequential oracle, with an initial state and the final state checked."""
+    states) against the sequential oracle, with an initial state and the final state checked.
+
+    The final state is compared with the float64 restatement: on (1, 77, 192) the f32 oracle's
+    own final state is 1.16e-4 away from it (a component at 1.2e-3 of the largest, 8e-8 off in
+    absolute terms), so the bar is the tolerance or 1.5x the f32 oracle's own error, whichever
+    is larger."""
     ssm.set_scan_segments(nseg)
     ssm.set_scan_variant(variant)
     x = scan_inputs(*shape, seed=nseg * 11 + shape[1], with_bias=True)
     init = (np.random.default_rng(nseg).standard_normal((shape[0], shape[2], 16)) * 0.5).astype(np.float32)
     r, rlast = oracle.selective_scan(**x, init_state=init, return_last_state=True)
+    _, rlast64 = oracle.numpy_selective_scan(**x, init_state=init)
     g, glast = run_gpu(x, dev, init_state=init, last=True)
     assert rel_err(g, r) <= TOL_F32
-    assert rel_err(glast, rlast) <= TOL_F32
+    assert rel_err(glast, rlast64) <= max(TOL_F32, 1.5 * rel_err(rlast, rlast64))
 
 
 @pytest.mark.parametrize("variant", [0, 40, 41, 42, 43])
