@@ -119,3 +119,21 @@ def test_gemm_accumulate_into_output(dev, gemm_kernel, out_dtype):
     r = Y0.float().cpu().numpy() + ref(X, W)
     err = norm_err(Y.float().cpu().numpy(), r)
     assert err <= (1e-5 if out_dtype == torch.float32 else 2 ** -8), err
+
+
+@pytest.mark.parametrize("gemm_kernel", [0, 5, 6], indirect=True)
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 256), (700, 520, 64), (1024, 768, 1088)])
+def test_gemm_whole_tile_stores(dev, gemm_kernel, out_dtype, M, N, K):
+    """No bias, no activation: the 256 x 256 kernel's whole-tile epilogue (interior 128 x 128
+    wave tiles) beside the guarded one (edge tiles), for 1, 2 and 17 K tiles."""
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
+    y = ssm.gemm_bf16(X, W, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    r = ref(X, W)
+    if out_dtype == torch.float32:
+        assert norm_err(y.cpu().numpy(), r) <= 1e-5
+    else:
+        assert rel_err(y.float().cpu().numpy(), bf16_round(r)) <= 2 ** -7
