@@ -16,7 +16,8 @@ namespace {
 
 // 0 = automatic, 1 = always the 128 x 128 kernel, 2 = the 256 x 128 kernel where rows are aligned,
 // 3 = the split-K 32 x 64 kernel where rows are aligned, 4 = the direct-to-LDS 256 x 128 kernel
-// where K % 64 == 0 and rows are aligned
+// where K % 64 == 0 and rows are aligned, 5 / 6 = the direct-to-LDS 256 x 256 kernel with 64- /
+// 32-wide K tiles where K is a multiple of them and rows are aligned
 int g_gemm_kernel = 0;
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
