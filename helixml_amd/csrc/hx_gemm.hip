@@ -176,9 +176,10 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_kernel(int64_t M, int64_t N,
 // straight from global memory into registers (16 bytes per lane) with SPK K-steps in flight, and
 // the four partial tiles are summed through LDS. No barrier inside the K loop, and a K = 1024
 // reduction is 16 steps per wave instead of 64, so the latency of the dependent loads, not
-// occupancy, sets the time. Rows must be 16-byte aligned (ld % 8 == 0).
-constexpr int SPK = 4;  // K-steps of 16 in flight per wave
-
+// occupancy, sets the time. SPK (K-steps of 16 in flight per wave) is chosen per launch so that a
+// wave usually issues all of its loads at once: one round of load latency per GEMM. Rows must be
+// 16-byte aligned (ld % 8 == 0).
+template <int SPK>
 __global__ __launch_bounds__(256) void gemm_bf16_nt_small_kernel(int64_t M, int64_t N, int64_t K,
                                                                  const uint16_t* __restrict__ X,
                                                                  int64_t ldx,
@@ -212,14 +213,17 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_small_kernel(int64_t M, int6
         b1[q] = ld(W, rb1, N, k, ldw);
     }
     for (int64_t s0 = wave; s0 < nsteps; s0 += 4 * SPK) {
+        const bool more = s0 + 4 * SPK < nsteps;  // uniform: another round of loads
 #pragma unroll
         for (int q = 0; q < SPK; ++q) {
             acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[q], b0[q], acc0, 0, 0, 0);
             acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[q], b1[q], acc1, 0, 0, 0);
-            const int64_t k = (s0 + 4 * (int64_t)(q + SPK)) * 16 + fk;
-            a[q] = ld(X, ra, M, k, ldx);
-            b0[q] = ld(W, rb0, N, k, ldw);
-            b1[q] = ld(W, rb1, N, k, ldw);
+            if (more) {
+                const int64_t k = (s0 + 4 * (int64_t)(q + SPK)) * 16 + fk;
+                a[q] = ld(X, ra, M, k, ldx);
+                b0[q] = ld(W, rb0, N, k, ldw);
+                b1[q] = ld(W, rb1, N, k, ldw);
+            }
         }
     }
     if (wave > 0) {
@@ -1040,8 +1044,15 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     if (vec && g_gemm_kernel != 1 && g_gemm_kernel != 2 && g_gemm_kernel != 4 &&
         (g_gemm_kernel == 3 || (tiles128 < 128 && (M + 31) / 32 <= 65535))) {
         dim3 sg((unsigned)((N + 63) / 64), (unsigned)((M + 31) / 32));
-        hipLaunchKernelGGL(gemm_bf16_nt_small_kernel, sg, dim3(256), 0, as_stream(stream), M, N, K,
-                           (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
+        const int64_t spw = ((K + 15) / 16 + 3) / 4;  // K-steps per wave
+        auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, sg, dim3(256), 0, as_stream(stream), M, N, K, (const uint16_t*)X,
+                               ldx, (const uint16_t*)W, ldw, bias, o);
+        };
+        if (spw <= 2) launch(gemm_bf16_nt_small_kernel<2>);
+        else if (spw <= 4) launch(gemm_bf16_nt_small_kernel<4>);
+        else if (spw <= 8) launch(gemm_bf16_nt_small_kernel<8>);
+        else launch(gemm_bf16_nt_small_kernel<16>);
         HX_LAUNCH_CHECK();
         return HX_OK;
     }
