@@ -781,96 +781,67 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
     const int fr = lane & 31;
     const int fc = lane >> 5;  // chunk half within a 16-wide K sub-step
     const int64_t nk = K / KB;
-    if constexpr (KB == 64 && NST == 2) {
-        // Sub-steps 0..3 (16 K each) of tile kt; the fragments of sub-step s+1 are read while
-        // the 16 MFMAs of sub-step s issue (one read after each of the first 8 MFMAs), so the
-        // MFMA pipe does not wait on LDS. The tile barrier sits before sub-step 3: by then each
-        // wave has read all of tile kt (the sub-step 3 fragments were waited for), so after it
-        // the freed stage takes tile kt+2 and sub-step 3 overlaps the reads of tile kt+1's first
-        // fragments from the other stage. Tile kt+1's loads (issued one tile earlier) are
-        // complete at that barrier.
-        auto frag = [&](int stg, int s, int q) __attribute__((always_inline)) {
-            const char* stage = sbase + stg * STB;
-            const int off = ((2 * s + fc) ^ xswz<KB>(fr)) << 4;  // row bases are multiples of 32
-            return q < 4 ? *reinterpret_cast<const bf16x8*>(stage + (wm * 128 + fr) * RB + q * 32 * RB + off)
-                         : *reinterpret_cast<const bf16x8*>(stage + XBM * RB + (wn * 128 + fr) * RB +
-                                                            (q - 4) * 32 * RB + off);
-        };
-        bf16x8 fg[2][8];  // [buffer][A rows 0..3, B rows 0..3] (32-row fragments)
-        if (nk > 0) issue(0);
-        if (nk > 1) issue(1);
-        if (nk > 1) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(QPW) : "memory");
-        else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    // Sub-steps 0..SUB-1 (16 K each) of tile kt; the fragments of sub-step s+1 are read while the
+    // 16 MFMAs of sub-step s issue (one read after each of the first 8 MFMAs), so the MFMA pipe
+    // does not wait on LDS. The tile barrier sits before the last sub-step: by then each wave has
+    // read all of tile kt (the last sub-step's fragments were waited for), so after it the freed
+    // stage takes tile kt+NST and the last sub-step overlaps the reads of tile kt+1's first
+    // fragments from the next stage. Tile kt+1's loads, issued NST-1 tiles earlier, are complete
+    // at that barrier (the wait leaves the loads of the tiles after it in flight).
+    constexpr int SUB = KB / 16;
+    auto frag = [&](int stg, int s, int q) __attribute__((always_inline)) {
+        const char* stage = sbase + stg * STB;
+        const int off = ((2 * s + fc) ^ xswz<KB>(fr)) << 4;  // row bases are multiples of 32
+        return q < 4 ? *reinterpret_cast<const bf16x8*>(stage + (wm * 128 + fr) * RB + q * 32 * RB + off)
+                     : *reinterpret_cast<const bf16x8*>(stage + XBM * RB + (wn * 128 + fr) * RB +
+                                                        (q - 4) * 32 * RB + off);
+    };
+    // wait until at most `after` tiles' loads are in flight (this wave's), then the barrier
+    auto wait_barrier = [&](int64_t after) __attribute__((always_inline)) {
+        if (after >= 3) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(3 * QPW) : "memory");
+        else if (after == 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * QPW) : "memory");
+        else if (after == 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(QPW) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    static_assert(NST >= 2 && NST <= 4 && (SUB == 2 || SUB == 4) && 3 * QPW <= 63, "ring depth / K tile");
+    bf16x8 fg[2][8];  // [buffer][A rows 0..3, B rows 0..3] (32-row fragments)
 #pragma unroll
-        for (int q = 0; q < 8; ++q) fg[0][q] = frag(0, 0, q);
-        for (int64_t kt = 0; kt < nk; ++kt) {
-            const int stg = (int)(kt & 1);
+    for (int t = 0; t < NST; ++t)
+        if (t < nk) issue(t);
+    wait_barrier((nk < NST ? nk : NST) - 1);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int cur = s & 1, nxt = cur ^ 1;
-                if (s == 3) {
-                    if (kt + 1 < nk) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                    if (kt + 2 < nk) issue(kt + 2);
-                }
+    for (int q = 0; q < 8; ++q) fg[0][q] = frag(0, 0, q);
+    int stg = 0;
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int nstg = stg + 1 == NST ? 0 : stg + 1;
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
-#pragma unroll
-                    for (int jj = 0; jj < 2; ++jj) {
-                        const int i = q >> 1, j = (q & 1) * 2 + jj;
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fg[cur][i], fg[cur][4 + j],
-                                                                            acc[i][j], 0, 0, 0);
-                    }
-                    // (the last tile's sub-step 3 reads unused fragments of the other stage, so
-                    // that no sub-step branches)
-                    fg[nxt][q] = s < 3 ? frag(stg, s + 1, q) : frag(stg ^ 1, 0, q);
-                }
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-                }
-                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-                __builtin_amdgcn_sched_barrier(0);
+        for (int s = 0; s < SUB; ++s) {
+            const int cur = s & 1, nxt = cur ^ 1;
+            if (s == SUB - 1) {
+                if (kt + 1 < nk) wait_barrier(nk - 2 - kt < NST - 2 ? nk - 2 - kt : NST - 2);
+                if (kt + NST < nk) issue(kt + NST);
             }
-        }
-    } else {
-    #pragma unroll
-        for (int t = 0; t < NST - 1; ++t)
-            if (t < nk) issue(t);
-        for (int64_t kt = 0; kt < nk; ++kt) {
-            // tile kt's loads are done when at most those of the tiles after it remain (wait and
-            // barrier in one statement: a fenced barrier would wait for every load in flight); the
-            // barrier also means every wave is past tile kt-1, whose stage tile kt+NST-1 refills
-            const int64_t after = nk - 1 - kt < NST - 2 ? nk - 1 - kt : NST - 2;
-            if (after >= 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * QPW) : "memory");
-            else if (after == 1) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(QPW) : "memory");
-            else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-            if (kt + NST - 1 < nk) issue(kt + NST - 1);
-            const char* stage = sbase + (int)(kt % NST) * STB;
-            const char* aw = stage + (wm * 128 + fr) * RB;              // A rows of this lane
-            const char* bw = stage + XBM * RB + (wn * 128 + fr) * RB;   // B rows of this lane
-            auto load = [&](int s, bf16x8* af, bf16x8* bf) __attribute__((always_inline)) {
-                const int off = ((2 * s + fc) ^ xswz<KB>(fr)) << 4;  // row bases are multiples of 32
-    #pragma unroll
-                for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(aw + i * 32 * RB + off);
-    #pragma unroll
-                for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(bw + j * 32 * RB + off);
-            };
-            bf16x8 fa[2][4], fb[2][4];
-            load(0, fa[0], fb[0]);
-    #pragma unroll
-            for (int s = 0; s < KB / 16; ++s) {
-                if (s + 1 < KB / 16) load(s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
-                __builtin_amdgcn_sched_barrier(0);
-    #pragma unroll
-                for (int i = 0; i < 4; ++i)
-    #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s & 1][i], fb[s & 1][j],
-                                                                            acc[i][j], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int i = q >> 1, j = (q & 1) * 2 + jj;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fg[cur][i], fg[cur][4 + j],
+                                                                        acc[i][j], 0, 0, 0);
+                }
+                // (the last tile's last sub-step reads unused fragments of the next stage, which
+                // no load targets any more, so that no sub-step branches)
+                fg[nxt][q] = s < SUB - 1 ? frag(stg, s + 1, q) : frag(nstg, 0, q);
             }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        stg = nstg;
     }
     lds_barrier();  // the epilogue reuses stage memory
 
