@@ -298,8 +298,8 @@ def main():
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs on one GPU only: the scan shards by channel with "
-                                   "no exchange (see DESIGN.md); multi-GPU runs are not part of it",
+        print(json.dumps({"error": "this build runs on one GPU only: the scan would shard by channel "
+                                   "with no exchange; multi-GPU runs are not part of it",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 

@@ -2,8 +2,8 @@
  * helix_hip.h — C ABI of libhelix_hip.so, the MI355X (gfx950) backend for HelixML's
  * state-space-model forward path.
  *
- * This is the drop-in boundary a Rust `crates/backend-hip` binds with an `extern "C"` block
- * (the binding is shown in INTEGRATION.md). Every entry point takes plain pointers, sizes and
+ * This is the drop-in boundary a Rust `crates/backend-hip` binds with an `extern "C"` block.
+ * Every entry point takes plain pointers, sizes and
  * enums: no HIP, torch or C++ types cross it. Inputs and outputs are allocated by the caller
  * (hx_malloc, or any HIP allocation on the same device). Block and layer entry points take a
  * caller-owned workspace (sizes from the *_workspace_size functions); the long-sequence scan
