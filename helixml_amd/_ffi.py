@@ -95,6 +95,8 @@ SIGNATURES = {
     "hx_matmul_f32": [_i64, _i64, _i64, _p, _p, _p, _p],
     "hx_gemm_bf16": [_i64, _i64, _i64, _p, _i64, _p, _i64, _p, _int, _int,
                      _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p],
+    "hx_gemm_bf16_splitk": [_i64, _i64, _i64, _p, _i64, _p, _i64, _p, _int, _int,
+                            _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _int, _p, _sz, _p],
     "hx_conv1d_silu": [_i64, _i64, _i64, _i64, _int, _p, _i64, _p, _p, _p, _p],
     "hx_mamba_block_workspace_size": [_i64, _i64, _i64, _i64, _i64],
     "hx_mamba_block_fwd": [_i64] * 7 + [_p] * 12 + [_sz, _p],

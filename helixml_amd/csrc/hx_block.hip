@@ -260,11 +260,19 @@ int block_core(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner, 
     if ((rc = hx_conv1d_silu(batch, seqlen, d_inner, d_conv, HX_BF16, b.xpart, d_inner, w.conv_w,
                              w.conv_b, b.xconv, stream)))
         return rc;
-    // x_proj: [M, d_inner] x [dt_rank + 2N, d_inner]^T -> dt_lo | B | C
-    if ((rc = hx_gemm_bf16(M, dt_rank + 2 * dstate, d_inner, b.xconv, d_inner, w.w_x, d_inner,
-                           nullptr, 0, HX_BF16, b.dtlo, dt_rank, dt_rank, b.B, dstate,
-                           dt_rank + dstate, b.C, dstate, stream)))
-        return rc;
+    // x_proj: [M, d_inner] x [dt_rank + 2N, d_inner]^T -> dt_lo | B | C. Narrow and long (config 3:
+    // N 160, K 4096, 64 tiles of 256 x 256): K is split four ways and the fp32 partials go to the
+    // in_proj x region, which the conv has consumed by now. The choice depends on the weight shape
+    // only, so every batch size and sequence length gets the same arithmetic per token.
+    const int64_t nx = dt_rank + 2 * dstate;
+    const int splits = (d_inner >= 2048 && d_inner % 256 == 0 && nx <= 256 && 4 * nx * 2 <= d_inner) ? 4 : 1;
+    rc = splits > 1 ? hx_gemm_bf16_splitk(M, nx, d_inner, b.xconv, d_inner, w.w_x, d_inner, nullptr, 0,
+                                          HX_BF16, b.dtlo, dt_rank, dt_rank, b.B, dstate, dt_rank + dstate,
+                                          b.C, dstate, splits, b.xpart, (size_t)M * d_inner * 2, stream)
+                    : hx_gemm_bf16(M, nx, d_inner, b.xconv, d_inner, w.w_x, d_inner, nullptr, 0, HX_BF16,
+                                   b.dtlo, dt_rank, dt_rank, b.B, dstate, dt_rank + dstate, b.C, dstate,
+                                   stream);
+    if (rc) return rc;
     // dt_proj: [M, dt_rank] x [d_inner, dt_rank]^T -> dt (dt_bias is added inside the scan)
     if ((rc = hx_gemm_bf16(M, d_inner, dt_rank, b.dtlo, dt_rank, w.w_dt, dt_rank, nullptr, 0,
                            HX_BF16, b.dt, d_inner, d_inner, nullptr, 0, d_inner, nullptr, 0, stream)))

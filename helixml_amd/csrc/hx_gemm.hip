@@ -722,7 +722,14 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
                                                                 const uint16_t* __restrict__ W,
                                                                 int64_t ldw,
                                                                 const float* __restrict__ bias,
-                                                                GemmOut o) {
+                                                                GemmOut o, int64_t zstride) {
+    // split K (gridDim.z > 1): slice z multiplies columns [z K, z K + K) of X and W into its own
+    // single-output partial, zstride elements after slice z-1's
+    if (gridDim.z > 1) {
+        X += blockIdx.z * K;
+        W += blockIdx.z * K;
+        o.y[0] = (char*)o.y[0] + blockIdx.z * zstride * (o.out_bf16 ? 2 : 4);
+    }
     constexpr int RB = KB * 2;              // bytes per tile row
     constexpr int CPR = KB / 8;             // 16-byte chunks per row
     constexpr int RPK = 1024 / RB;          // rows per KiB (one load instruction)
@@ -887,6 +894,36 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
 }
 
 
+
+// Sum of the S split-K partials P[z][M][N] (fp32, row stride N) in slice order, then bias, SiLU,
+// accumulate and the column split of o, one element per thread (consecutive threads take
+// consecutive columns).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(int64_t M, int64_t N, int S,
+                                                            const float* __restrict__ P,
+                                                            const float* __restrict__ bias, GemmOut o) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= M * N) return;
+    const int64_t row = i / N, col = i % N;
+    float v = P[i];
+    for (int z = 1; z < S; ++z) v += P[(int64_t)z * M * N + i];
+    if (bias) v += bias[col];
+    if (o.act & 1) v = silu(v);
+    int seg = 0;
+    int64_t cc = col;
+    if (col >= o.split2) { seg = 2; cc = col - o.split2; }
+    else if (col >= o.split1) { seg = 1; cc = col - o.split1; }
+    const int64_t off = row * o.ldp(seg) + cc;
+    if (o.out_bf16) {
+        uint16_t* yp = (uint16_t*)o.yp(seg) + off;
+        if (o.act & 2) v += Storage<uint16_t>::load(yp);
+        Storage<uint16_t>::store(yp, v);
+    } else {
+        float* yp = (float*)o.yp(seg) + off;
+        if (o.act & 2) v += *yp;
+        *yp = v;
+    }
+}
+
 }  // namespace
 }  // namespace hx
 
@@ -936,7 +973,7 @@ int launch_d256(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, con
     const size_t bytes = (size_t)NST * (XBM + XBN) * KB * 2;
     dim3 lg((unsigned)((N + XBN - 1) / XBN), (unsigned)((M + XBM - 1) / XBM));
     hipLaunchKernelGGL((gemm_bf16_nt_d256_kernel<KB, NST>), lg, dim3(256), bytes, as_stream(stream), M, N, K,
-                       (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
+                       (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o, (int64_t)0);
     HX_LAUNCH_CHECK();
     return HX_OK;
 }
@@ -1034,6 +1071,60 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     else  // rows not 16-byte aligned: element loads (odd K such as a small dt_rank)
         hipLaunchKernelGGL(gemm_bf16_nt_kernel<false>, grid, dim3(256), 0, as_stream(stream), M, N, K,
                            (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
+    HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+// Split-K form of hx_gemm_bf16 for GEMMs with too few 256 x 256 tiles to fill the GPU (a narrow N
+// with a long K: the block's x_proj). The K range is cut into `splits` slices of whole 64-wide K
+// tiles, each slice's product goes to its own fp32 partial in the workspace (splits * M * N
+// floats), and one pass sums the partials in slice order and applies hx_gemm_bf16's epilogue
+// (same output arguments).
+extern "C" int hx_gemm_bf16_splitk(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
+                                   const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
+                                   void* Y0, int64_t ld0, int64_t split1, void* Y1, int64_t ld1,
+                                   int64_t split2, void* Y2, int64_t ld2, int splits, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    using namespace hx;
+    HX_REQUIRE(M >= 0 && N >= 0 && K >= 0, HX_ERR_INVALID_DIMENSION, "gemm_bf16_splitk: negative size");
+    HX_REQUIRE(act >= 0 && act <= 3, HX_ERR_INVALID_INPUT,
+               "gemm_bf16_splitk: act=%d (bit 0 SiLU, bit 1 accumulate into Y)", act);
+    HX_REQUIRE(out_dtype == HX_F32 || out_dtype == HX_BF16, HX_ERR_DTYPE_MISMATCH,
+               "gemm_bf16_splitk: out_dtype %d", out_dtype);
+    HX_REQUIRE(splits >= 1 && splits <= 16, HX_ERR_INVALID_INPUT, "gemm_bf16_splitk: splits %d (1..16)",
+               splits);
+    if (M == 0 || N == 0) return HX_OK;
+    HX_REQUIRE(X && W && Y0, HX_ERR_INVALID_INPUT, "gemm_bf16_splitk: X, W and Y0 must be non-NULL");
+    HX_REQUIRE(ldx >= K && ldw >= K && ld0 >= 0, HX_ERR_INVALID_DIMENSION,
+               "gemm_bf16_splitk: leading dimensions smaller than K");
+    HX_REQUIRE(K % ((int64_t)splits * 64) == 0, HX_ERR_UNSUPPORTED,
+               "gemm_bf16_splitk: K %lld is not a multiple of 64 * splits", (long long)K);
+    HX_REQUIRE(ldx % 8 == 0 && ldw % 8 == 0 && aligned(X, 16) && aligned(W, 16), HX_ERR_UNSUPPORTED,
+               "gemm_bf16_splitk: rows of X and W must be 16-byte aligned");
+    HX_REQUIRE(workspace && aligned(workspace, 16) &&
+                   workspace_bytes >= (size_t)splits * (size_t)M * (size_t)N * sizeof(float),
+               HX_ERR_INVALID_INPUT, "gemm_bf16_splitk: workspace %zu bytes < %zu required",
+               workspace_bytes, (size_t)splits * (size_t)M * (size_t)N * sizeof(float));
+    HX_REQUIRE((M + XBM - 1) / XBM <= 65535, HX_ERR_UNSUPPORTED, "gemm_bf16_splitk: M=%lld too large",
+               (long long)M);
+    HX_REQUIRE((d256_ok<64, 2>()), HX_ERR_UNSUPPORTED, "gemm_bf16_splitk: the device does not grant "
+               "the 256 x 256 kernel's LDS");
+    if (split1 <= 0 || split1 > N) split1 = N;
+    if (split2 < split1 || split2 > N) split2 = N;
+    HX_REQUIRE(split1 == N || Y1, HX_ERR_INVALID_INPUT, "gemm_bf16_splitk: Y1 is NULL but split1 < N");
+    HX_REQUIRE(split2 == N || Y2, HX_ERR_INVALID_INPUT, "gemm_bf16_splitk: Y2 is NULL but split2 < N");
+    float* partial = (float*)workspace;
+    const GemmOut po{{partial, nullptr, nullptr}, {N, 0, 0}, N, N, 0, 0};
+    const size_t bytes = (size_t)2 * (XBM + XBN) * 64 * 2;
+    dim3 lg((unsigned)((N + XBN - 1) / XBN), (unsigned)((M + XBM - 1) / XBM), (unsigned)splits);
+    hipLaunchKernelGGL((gemm_bf16_nt_d256_kernel<64, 2>), lg, dim3(256), bytes, as_stream(stream), M, N,
+                       K / splits, (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, (const float*)nullptr,
+                       po, M * N);
+    HX_LAUNCH_CHECK();
+    const GemmOut o{{Y0, Y1, Y2}, {ld0, ld1, ld2}, split1, split2, out_dtype == HX_BF16, act};
+    const int64_t n = M * N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), M, N, splits, (const float*)partial, bias, o);
     HX_LAUNCH_CHECK();
     return HX_OK;
 }

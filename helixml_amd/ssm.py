@@ -170,10 +170,12 @@ def matmul(A, B, stream=None):
     return Y
 
 
-def gemm_bf16(X, W, bias=None, act=0, out_dtype=torch.bfloat16, splits=None, stream=None):
+def gemm_bf16(X, W, bias=None, act=0, out_dtype=torch.bfloat16, splits=None, stream=None,
+              k_splits=None):
     """Matrix-core GEMM Y = X . W^T (+ bias)(, SiLU) (hx_gemm_bf16). X [M, K], W [N, K] bf16
     (row-major; X may be a row-strided view). splits=(s1[, s2]) returns the column blocks
-    [0, s1), [s1, s2), [s2, N) as separate contiguous tensors."""
+    [0, s1), [s1, s2), [s2, N) as separate contiguous tensors. k_splits=S runs the split-K form
+    (hx_gemm_bf16_splitk) with an fp32 workspace of S * M * N floats."""
     M, K = X.shape
     N = W.shape[0]
     if W.shape[1] != K:
@@ -190,10 +192,14 @@ def gemm_bf16(X, W, bias=None, act=0, out_dtype=torch.bfloat16, splits=None, str
     s1 = cuts[1] if len(cuts) > 2 else N
     s2 = cuts[2] if len(cuts) > 3 else N
     od = _STORAGE[out_dtype]
-    _ffi.call("hx_gemm_bf16", M, N, K, _ptr(X), X.stride(0), _ptr(W), W.stride(0), _ptr(bias),
-              int(act), od, _ptr(ys[0]), ys[0].shape[1], s1,
-              _ptr(ys[1]), ys[1].shape[1] if ys[1] is not None else 0, s2,
-              _ptr(ys[2]), ys[2].shape[1] if ys[2] is not None else 0, _stream(stream))
+    args = (M, N, K, _ptr(X), X.stride(0), _ptr(W), W.stride(0), _ptr(bias), int(act), od,
+            _ptr(ys[0]), ys[0].shape[1], s1, _ptr(ys[1]), ys[1].shape[1] if ys[1] is not None else 0,
+            s2, _ptr(ys[2]), ys[2].shape[1] if ys[2] is not None else 0)
+    if k_splits:
+        ws = torch.empty(int(k_splits) * M * N, device=X.device, dtype=torch.float32)
+        _ffi.call("hx_gemm_bf16_splitk", *args, int(k_splits), _ptr(ws), ws.numel() * 4, _stream(stream))
+    else:
+        _ffi.call("hx_gemm_bf16", *args, _stream(stream))
     return outs[0] if len(outs) == 1 else tuple(outs)
 
 

@@ -165,6 +165,18 @@ int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
                  const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
                  void* Y0, int64_t ld0, int64_t split1, void* Y1, int64_t ld1,
                  int64_t split2, void* Y2, int64_t ld2, void* stream);
+/* hx_gemm_bf16 with K split into `splits` (1..16) slices of whole 64-wide K tiles, for products
+ * with a narrow N and a long K that leave the GPU mostly idle (the block's x_proj: N 160, K 4096):
+ * each slice's fp32 partial goes to `workspace` (at least splits * M * N * 4 bytes, 16-byte
+ * aligned, caller-owned), then one pass sums the partials in slice order and applies the same
+ * epilogue and outputs as hx_gemm_bf16. Requires K % (64 * splits) == 0 and 16-byte aligned rows
+ * (HX_ERR_UNSUPPORTED otherwise). Same Linear layout (crates/nn/src/lib.rs:120-134); the summation
+ * order differs from hx_gemm_bf16's only in where the slices' fp32 sums are added. */
+int hx_gemm_bf16_splitk(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
+                        const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
+                        void* Y0, int64_t ld0, int64_t split1, void* Y1, int64_t ld1,
+                        int64_t split2, void* Y2, int64_t ld2, int splits, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* Causal depthwise conv1d over time + bias + SiLU (the Mamba block's conv, kernel `width` <= 4):
  * y[b,t,d] = silu(bias[d] + sum_j weight[d,j] * x[b, t-width+1+j, d]) with zero padding.

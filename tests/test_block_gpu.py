@@ -67,8 +67,10 @@ def test_conv1d_rejects_bad_width_and_dim(dev):
 
 
 @pytest.mark.parametrize("bt,L,dm,di,r", [(2, 64, 64, 128, 16), (1, 100, 32, 64, 8),
-                                          (2, 300, 128, 256, 16), (3, 17, 48, 96, 8)])
+                                          (2, 300, 128, 256, 16), (3, 17, 48, 96, 8),
+                                          (2, 60, 64, 2048, 16)])
 def test_mamba_block_vs_oracle(dev, bt, L, dm, di, r):
+    """(2, 60, 64, 2048, 16) runs x_proj split four ways along K."""
     p = block_inputs(bt, L, dm, di, 16, r, 4, seed=bt * 1000 + L)
     y = ssm.mamba_block_fwd(**to_dev(p, dev))
     torch.cuda.synchronize()

@@ -5,6 +5,7 @@ import pytest
 import torch
 
 from helixml_amd import ssm
+from helixml_amd._ffi import InvalidInput, UnsupportedOperation
 from tests.util import bf16_round, norm_err, rel_err
 
 pytestmark = pytest.mark.gpu
@@ -137,3 +138,39 @@ def test_gemm_whole_tile_stores(dev, gemm_kernel, out_dtype, M, N, K):
         assert norm_err(y.cpu().numpy(), r) <= 1e-5
     else:
         assert rel_err(y.float().cpu().numpy(), bf16_round(r)) <= 2 ** -7
+
+
+@pytest.mark.parametrize("M,N,K,S", [(300, 160, 4096, 4), (1000, 48, 2048, 2), (257, 64, 1024, 16),
+                                     (64, 300, 512, 8)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_splitk(dev, M, N, K, S, out_dtype):
+    """hx_gemm_bf16_splitk: K in S slices, fp32 partials summed in slice order, then the usual
+    epilogue (bias, SiLU, column split)."""
+    g = torch.Generator().manual_seed(M + N + K + S)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
+    b = torch.randn(N, generator=g).to(dev)
+    if out_dtype == torch.float32:
+        y = ssm.gemm_bf16(X, W, b, act=1, out_dtype=out_dtype, k_splits=S)
+        torch.cuda.synchronize()
+        assert norm_err(y.cpu().numpy(), ref(X, W, b, 1)) <= 1e-5
+    else:
+        parts = ssm.gemm_bf16(X, W, splits=(N // 3, N // 2), k_splits=S)
+        torch.cuda.synchronize()
+        got = np.concatenate([p.float().cpu().numpy() for p in parts], 1)
+        assert rel_err(got, bf16_round(ref(X, W))) <= 2 ** -7
+
+
+def test_gemm_splitk_rejects(dev):
+    X = torch.zeros(64, 96, device=dev, dtype=torch.bfloat16)
+    W = torch.zeros(32, 96, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(UnsupportedOperation):
+        ssm.gemm_bf16(X, W, k_splits=2)  # K = 96 is not a multiple of 128
+    from helixml_amd import _ffi
+    X2 = torch.zeros(64, 128, device=dev, dtype=torch.bfloat16)
+    W2 = torch.zeros(32, 128, device=dev, dtype=torch.bfloat16)
+    Y = torch.empty(64, 32, device=dev)
+    ws = torch.empty(16, device=dev)
+    with pytest.raises(InvalidInput):  # workspace smaller than 2 * 64 * 32 floats
+        _ffi.call("hx_gemm_bf16_splitk", 64, 32, 128, X2.data_ptr(), 128, W2.data_ptr(), 128, None, 0,
+                  _ffi.HX_F32, Y.data_ptr(), 32, 32, None, 0, 32, None, 0, 2, ws.data_ptr(), 64, None)
