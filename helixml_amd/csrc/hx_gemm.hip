@@ -1030,8 +1030,14 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
         return launch_d256<32, 4>(M, N, K, X, ldx, W, ldw, bias, o, stream);
     const size_t dlds = (size_t)DSTAGES * DSTAGE_BYTES;
     // auto: the direct-to-LDS kernel for long K (measured ahead of the 128 x 128 kernel from
-    // K = 2048 on, behind it at K <= 512 where its one block per CU cannot hide the epilogue)
-    if (vec && K % LBK == 0 && (g_gemm_kernel == 4 || (g_gemm_kernel == 0 && K >= 2048)) &&
+    // K = 2048 on, and from K = 1024 for N <= 128 where its tiles fill half the GPU: config 5
+    // x_proj 78 vs 87 us; behind it at K <= 512 where its one block per CU cannot hide the
+    // epilogue). Its per-element arithmetic is the 256 x 256 kernel's (K ascending in 16-wide
+    // MFMA steps), so a short batch that lands here matches a long one that takes that kernel.
+    const int64_t tiles_dlds = ((M + LBM - 1) / LBM) * ((N + LBN - 1) / LBN);
+    if (vec && K % LBK == 0 &&
+        (g_gemm_kernel == 4 ||
+         (g_gemm_kernel == 0 && (K >= 2048 || (K >= 1024 && N <= 128 && tiles_dlds >= 128)))) &&
         dlds_ok(dlds)) {
         dim3 lg((unsigned)((N + LBN - 1) / LBN), (unsigned)((M + LBM - 1) / LBM));
         hipLaunchKernelGGL(gemm_bf16_nt_dlds_kernel, lg, dim3(256), dlds, as_stream(stream), M, N, K,
