@@ -240,32 +240,42 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_small_kernel(int64_t M, int6
         acc0[r] += red[0][0][r][lane] + red[1][0][r][lane] + red[2][0][r][lane];
         acc1[r] += red[0][1][r][lane] + red[1][1][r][lane] + red[2][1][r][lane];
     }
-    // epilogue (element stores; these tiles are small)
+    // epilogue (element stores; these tiles are small). With accumulate, every output to be read
+    // is loaded before the first store, so the loads' latencies overlap (a load after a store to
+    // a possibly aliasing address would wait for it).
+    int64_t offs[2][16];
+    int segs[2];
+    float old[2][16];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int64_t col = n0 + j * 32 + (lane & 31);
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
         int seg = 0;
         int64_t cc = col;
         if (col >= o.split2) { seg = 2; cc = col - o.split2; }
         else if (col >= o.split1) { seg = 1; cc = col - o.split1; }
+        segs[j] = seg;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t row = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (row >= M) continue;
+            offs[j][r] = (row < M && col < N) ? row * o.ldp(seg) + cc : -1;
+            old[j][r] = 0.0f;
+            if ((o.act & 2) && offs[j][r] >= 0)
+                old[j][r] = o.out_bf16 ? Storage<uint16_t>::load((uint16_t*)o.yp(seg) + offs[j][r])
+                                       : ((float*)o.yp(seg))[offs[j][r]];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int64_t col = n0 + j * 32 + (lane & 31);
+        const float bv = (bias && col < N) ? bias[col] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            if (offs[j][r] < 0) continue;
             float v = (j ? acc1[r] : acc0[r]) + bv;
             if (o.act & 1) v = silu(v);
-            const int64_t off = row * o.ldp(seg) + cc;
-            if (o.out_bf16) {
-                uint16_t* yp = (uint16_t*)o.yp(seg) + off;
-                if (o.act & 2) v += Storage<uint16_t>::load(yp);
-                Storage<uint16_t>::store(yp, v);
-            } else {
-                float* yp = (float*)o.yp(seg) + off;
-                if (o.act & 2) v += *yp;
-                *yp = v;
-            }
+            if (o.act & 2) v += old[j][r];
+            if (o.out_bf16) Storage<uint16_t>::store((uint16_t*)o.yp(segs[j]) + offs[j][r], v);
+            else ((float*)o.yp(segs[j]))[offs[j][r]] = v;
         }
     }
 }
