@@ -755,9 +755,27 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
     const int wm = wave >> 1, wn = wave & 1;
     const int nbx = gridDim.x, nby = gridDim.y;
     const int nb = nbx * nby;
+    // Tile order. Consecutive block ids go to different XCDs (8, each with its own L2), so each
+    // XCD takes a contiguous run of row panels; inside it, tiles go out in groups of up to 4 row
+    // panels, column-major within a group, so the tiles in flight on an XCD (one per CU) share 4
+    // A panels and a few W panels instead of one A panel and every W panel (config 3 in_proj:
+    // 12 MB instead of 33 MB through L2 per round, 705 -> 634 us).
     int bid = blockIdx.y * nbx + blockIdx.x;
-    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-    const int64_t m0 = (int64_t)(bid / nbx) * XBM, n0 = (int64_t)(bid % nbx) * XBN;
+    int tm, tn;
+    if ((nb & 7) == 0 && ((nb >> 3) % nbx) == 0) {
+        const int rows_x = (nb >> 3) / nbx;  // row panels per XCD
+        const int xcd = bid & 7, li = bid >> 3;
+        const int gm = rows_x < 4 ? rows_x : 4;
+        const int g = li / (gm * nbx), rem = li % (gm * nbx);
+        const int rig = rows_x - g * gm < gm ? rows_x - g * gm : gm;  // row panels in this group
+        tm = xcd * rows_x + g * gm + rem % rig;
+        tn = rem / rig;
+    } else {
+        if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+        tm = bid / nbx;
+        tn = bid % nbx;
+    }
+    const int64_t m0 = (int64_t)tm * XBM, n0 = (int64_t)tn * XBN;
 
     // this lane's QPW global sources per tile: wave w issues KiB regions q = QPW*w .. of the
     // stage (q < QA: A rows RPK*q.., else B rows RPK*(q-QA)..); lane L fills row RPK*q' + L/CPR,
