@@ -174,3 +174,17 @@ def test_gemm_splitk_rejects(dev):
     with pytest.raises(InvalidInput):  # workspace smaller than 2 * 64 * 32 floats
         _ffi.call("hx_gemm_bf16_splitk", 64, 32, 128, X2.data_ptr(), 128, W2.data_ptr(), 128, None, 0,
                   _ffi.HX_F32, Y.data_ptr(), 32, 32, None, 0, 32, None, 0, 2, ws.data_ptr(), 64, None)
+
+
+@pytest.mark.parametrize("gemm_kernel", [5], indirect=True)
+@pytest.mark.parametrize("M,N,K", [(2048, 512, 64), (8192, 1024, 256), (12288, 512, 128)])
+def test_gemm_grouped_tile_order(dev, gemm_kernel, M, N, K):
+    """Grids whose tiles split evenly into whole row panels per XCD take the grouped tile order
+    (groups of up to 4 row panels; 12288 x 512 gives each XCD 6 panels: a group of 4 and one of
+    2): every output tile is computed exactly once, against the fp32 reference."""
+    g = torch.Generator().manual_seed(M + N + K)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
+    y = ssm.gemm_bf16(X, W, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert norm_err(y.cpu().numpy(), ref(X, W)) <= 1e-5
