@@ -433,6 +433,28 @@ __device__ inline void store_tile_rows(const GemmOut& o, const float* __restrict
         }
 }
 
+// Tile order of the big-tile kernels (blocks = tiles, one or two per CU). Consecutive block ids
+// go to different XCDs (8, each with its own L2), so each XCD takes a contiguous run of the
+// row-major tile range; when that run is whole row panels, its tiles go out in groups of up to 4
+// row panels, column-major inside a group, so the tiles in flight on an XCD (one per CU) share
+// 4 A panels and a few W panels instead of one A panel and every W panel (config 3 in_proj with
+// 256 x 256 tiles: 12 MB instead of 33 MB through L2 per round, 585 -> 495 us).
+__device__ inline void tile_of(int nbx, int nb, int bid, int& tm, int& tn) {
+    if ((nb & 7) == 0 && ((nb >> 3) % nbx) == 0) {
+        const int rows_x = (nb >> 3) / nbx;  // row panels per XCD
+        const int xcd = bid & 7, li = bid >> 3;
+        const int gm = rows_x < 4 ? rows_x : 4;
+        const int g = li / (gm * nbx), rem = li % (gm * nbx);
+        const int rig = rows_x - g * gm < gm ? rows_x - g * gm : gm;  // row panels in this group
+        tm = xcd * rows_x + g * gm + rem % rig;
+        tn = rem / rig;
+    } else {
+        if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+        tm = bid / nbx;
+        tn = bid % nbx;
+    }
+}
+
 // ----------------------------------------------------------------------------- large tiles
 // Block tile 256 x 128 x 64, 4 waves in 2 x 2, each wave 128 x 64 = 4 x 2 tiles of
 // v_mfma_f32_32x32x16_bf16 (8 MFMAs per 6 LDS fragment reads, vs 4 per 4 in the 128 x 128 kernel).
@@ -459,13 +481,12 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_large_kernel(int64_t M, int6
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    // XCD-aware tile order: consecutive block ids go to different XCDs; give each XCD a
-    // contiguous run of tiles so neighbouring tiles share its L2
+    // XCD-aware, L2-grouped tile order (tile_of)
     const int nbx = gridDim.x, nby = gridDim.y;
     const int nb = nbx * nby;
-    int bid = blockIdx.y * nbx + blockIdx.x;
-    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-    const int64_t m0 = (int64_t)(bid / nbx) * LBM, n0 = (int64_t)(bid % nbx) * LBN;
+    int tm, tn;
+    tile_of(nbx, nb, blockIdx.y * nbx + blockIdx.x, tm, tn);
+    const int64_t m0 = (int64_t)tm * LBM, n0 = (int64_t)tn * LBN;
 
     // per K-step: A 256 x 64 (2048 16-byte pieces, 8 per thread), B 128 x 64 (1024, 4 per thread)
     uint4 ra[8], rb[4];
@@ -582,9 +603,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_dlds_kernel(int64_t M, int64
     const int wm = wave >> 1, wn = wave & 1;
     const int nbx = gridDim.x, nby = gridDim.y;
     const int nb = nbx * nby;
-    int bid = blockIdx.y * nbx + blockIdx.x;
-    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-    const int64_t m0 = (int64_t)(bid / nbx) * LBM, n0 = (int64_t)(bid % nbx) * LBN;
+    int tm, tn;
+    tile_of(nbx, nb, blockIdx.y * nbx + blockIdx.x, tm, tn);
+    const int64_t m0 = (int64_t)tm * LBM, n0 = (int64_t)tn * LBN;
 
     // this lane's 12 global sources per tile: wave w issues KiB regions q = 12w .. 12w + 11 of
     // the 48 KiB stage (0..31 = A rows 8q.., 32..47 = B rows 8(q-32)..); lane L fills row
@@ -755,26 +776,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
     const int wm = wave >> 1, wn = wave & 1;
     const int nbx = gridDim.x, nby = gridDim.y;
     const int nb = nbx * nby;
-    // Tile order. Consecutive block ids go to different XCDs (8, each with its own L2), so each
-    // XCD takes a contiguous run of row panels; inside it, tiles go out in groups of up to 4 row
-    // panels, column-major within a group, so the tiles in flight on an XCD (one per CU) share 4
-    // A panels and a few W panels instead of one A panel and every W panel (config 3 in_proj:
-    // 12 MB instead of 33 MB through L2 per round, 705 -> 634 us).
-    int bid = blockIdx.y * nbx + blockIdx.x;
     int tm, tn;
-    if ((nb & 7) == 0 && ((nb >> 3) % nbx) == 0) {
-        const int rows_x = (nb >> 3) / nbx;  // row panels per XCD
-        const int xcd = bid & 7, li = bid >> 3;
-        const int gm = rows_x < 4 ? rows_x : 4;
-        const int g = li / (gm * nbx), rem = li % (gm * nbx);
-        const int rig = rows_x - g * gm < gm ? rows_x - g * gm : gm;  // row panels in this group
-        tm = xcd * rows_x + g * gm + rem % rig;
-        tn = rem / rig;
-    } else {
-        if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-        tm = bid / nbx;
-        tn = bid % nbx;
-    }
+    tile_of(nbx, nb, blockIdx.y * nbx + blockIdx.x, tm, tn);
     const int64_t m0 = (int64_t)tm * XBM, n0 = (int64_t)tn * XBN;
 
     // this lane's QPW global sources per tile: wave w issues KiB regions q = QPW*w .. of the
