@@ -280,7 +280,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_small_kernel(int64_t M, int6
     }
 }
 
-// Whole-slab store of a staged 32 x 64 fp32 tile (st, row stride 68) without bias or SiLU:
+// Whole-slab store of a staged 32 x 64 fp32 tile (st, row stride 68) without bias or SiLU,
+// with nontemporal stores: an output streams out without displacing the A and W panels the
+// other tiles still read from L2 (config 5 in_proj, 537 MB out: 439 -> 391 us):
 // `yb` points at the slab's first output element, `ldb` is the output row pitch in bytes, both
 // 16-byte aligned. bf16: 8 lanes x 8 columns per row, 8 rows per pass; fp32: 16 lanes x 4
 // columns, 4 rows per pass.
@@ -335,7 +337,7 @@ __device__ inline void store_slab_fast(char* __restrict__ yb, int64_t ldb, const
 #pragma unroll
             for (int k = 0; k < 4; ++k)
                 wv[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32v2{f[2 * k], f[2 * k + 1]}, bf16v2));
-            *(g_u32v4*)q = u32v4{wv[0], wv[1], wv[2], wv[3]};
+            __builtin_nontemporal_store(u32v4{wv[0], wv[1], wv[2], wv[3]}, (g_u32v4*)q);
         } else {
             f32v4 f = v[p][0];
             if constexpr (ACC) {
@@ -344,7 +346,7 @@ __device__ inline void store_slab_fast(char* __restrict__ yb, int64_t ldb, const
                 f.z += __uint_as_float(old[p].z);
                 f.w += __uint_as_float(old[p].w);
             }
-            *(g_f32v4*)q = f;
+            __builtin_nontemporal_store(f, (g_f32v4*)q);
         }
     }
 }
