@@ -18,7 +18,7 @@ namespace {
 // 3 = the split-K 32 x 64 kernel where rows are aligned, 4 = the direct-to-LDS 256 x 128 kernel
 // where K % 64 == 0 and rows are aligned, 5 / 6 = the direct-to-LDS 256 x 256 kernel with 64- /
 // 32-wide K tiles where K is a multiple of them and rows are aligned
-int g_gemm_kernel = 0;
+thread_local int g_gemm_kernel = 0;  // per calling thread (hx_set_gemm_kernel)
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;

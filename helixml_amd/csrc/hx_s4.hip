@@ -729,8 +729,8 @@ namespace hx {
 namespace {
 // 0: automatic (wave path when dstate == 16 and rows are 16-byte aligned), 1: per-thread path;
 // set by hx_set_s4d_path. Segments: 0 = automatic, else forced (hx_set_s4d_segments).
-int g_s4d_path = 0;
-int g_s4d_segments = 0;
+thread_local int g_s4d_path = 0;  // per calling thread (hx_set_s4d_path)
+thread_local int g_s4d_segments = 0;  // per calling thread (hx_set_s4d_segments)
 
 int launch_s4d_wave(int64_t Bt, int64_t L, int64_t Dm, const float* x, const float* dt,
                     const float* a_re, const float* a_im, const float* B_re, const float* B_im,

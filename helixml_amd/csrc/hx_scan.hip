@@ -181,417 +181,6 @@ __global__ __launch_bounds__(64 * W) void scan_fwd_kernel(
     }
 }
 
-// ----------------------------------------------------------------------------- state-lane path
-// One lane per (channel, state): a 16-lane DPP row holds the 16 states of one channel, a wave
-// holds 4 channels, a block of 4 waves 16 consecutive channels. Per chunk of 16 steps:
-//   * pre:  lane n of a row does the per-element work of step t0+n for its channel
-//           (softplus, dt*u) — each (t, d) exactly once;
-//   * main: step s broadcasts lane s's dt and dt*u across the row with DPP row_newbcast, which
-//           the compiler folds into the consuming v_mul (no extra instruction); B[t][n], C[t][n]
-//           come from an LDS tile of the block's batch row; per lane-step: v_mul, v_exp, v_mul,
-//           v_fma, v_mul = the minimum for the recurrence;
-//   * readout: the 16 per-state partials of each step are reduce-scattered across the row
-//           (recursive halving over DPP row_ror:8 / row_half_mirror / quad_perm), leaving lane n
-//           with y for step t0+n; then D*u, SiLU(z) and the store, again once per element.
-// 49152 channel-states of config 2 give 3072 waves, three per SIMD.
-
-
-// Recursive-halving reduce-scatter over the 16 lanes of a DPP row: on return lane j holds
-// sum over the row's lanes of p[j].
-__device__ inline float row_reduce_scatter16(const float (&p)[16], int j) {
-    const bool hi8 = j & 8, hi4 = j & 4, hi2 = j & 2, hi1 = j & 1;
-    float q[8], r[4], v[2];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float send = hi8 ? p[i] : p[i + 8];
-        const float keep = hi8 ? p[i + 8] : p[i];
-        q[i] = keep + dpp<kDppRor8>(send);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float send = hi4 ? q[i] : q[i + 4];
-        const float keep = hi4 ? q[i + 4] : q[i];
-        r[i] = keep + dpp<kDppHalfMirror>(send);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const float send = hi2 ? r[i] : r[i + 2];
-        const float keep = hi2 ? r[i + 2] : r[i];
-        v[i] = keep + dpp<kDppXor2>(send);
-    }
-    const float send = hi1 ? v[0] : v[1];
-    const float keep = hi1 ? v[1] : v[0];
-    return keep + dpp<kDppXor1>(send);
-}
-
-
-template <typename T, int PF, bool HAS_Z, bool SOFTPLUS>
-__global__ __launch_bounds__(256) void scan_state_lane_kernel(
-    int64_t L, int64_t Dm, int ntiles,
-    const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
-    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
-    const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
-    const float* __restrict__ init_state, float* __restrict__ last_state) {
-    constexpr int NS = 16, TCH = 16, BSTR = TCH + 4;  // padded row: conflict-free b128 reads
-    __shared__ float s_bc[2][2][NS][BSTR];             // [buf][B|C][state][step]
-
-    // XCD-aware block order: hardware dispatches block ids round-robin over the 8 XCDs, so
-    // consecutive ids are renumbered to land on one XCD (neighbouring channel tiles share L2
-    // lines; the tiles of one batch row share its B/C).
-    const int nblk = gridDim.x * gridDim.y;
-    int id = blockIdx.x + gridDim.x * blockIdx.y;
-    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
-    const int tile = id % ntiles;
-    const int64_t b = id / ntiles;
-
-    const int tid = threadIdx.x;
-    const int n = tid & 15;                             // state == lane within the DPP row
-    const int64_t d = (int64_t)tile * 16 + (tid >> 4);  // channel of this row
-    const bool dvalid = d < Dm;
-    const int64_t dc = dvalid ? d : Dm - 1;
-
-    const int64_t col0 = b * L * Dm + dc;
-    const T* __restrict__ up = u + col0;
-    const T* __restrict__ dp = delta + col0;
-    const T* __restrict__ zp = HAS_Z ? z + col0 : nullptr;
-    T* __restrict__ op = out + col0;
-    const T* __restrict__ Bb = Bm + b * L * NS;
-    const T* __restrict__ Cb = Cm + b * L * NS;
-
-    const float A2 = A[dc * NS + n] * kLog2e;
-    float h = init_state ? init_state[(b * Dm + dc) * NS + n] : 0.0f;
-    const float Dd = Dv ? Dv[dc] : 0.0f;
-    const float bias = dt_bias ? dt_bias[dc] : 0.0f;
-
-    // Prefetch ring of PF chunks: slot k holds this lane's (t0+n, d) element of u/delta/z and one
-    // B and one C value of its chunk. Memory latency under load is several chunks of compute,
-    // so PF chunks stay in flight per wave.
-    float pu[PF], pd[PF], pz[PF], pb[PF], pc[PF];
-    const int64_t Lm1 = L - 1;
-    auto fetch = [&](int k, int64_t t0) {
-        const int64_t t = t0 + n < Lm1 ? t0 + n : Lm1;  // clamped: chunks past the end re-read row L-1
-        pu[k] = ld(up + t * Dm);
-        pd[k] = ld(dp + t * Dm);
-        pz[k] = HAS_Z ? ld(zp + t * Dm) : 0.0f;
-        const int64_t tb = t0 + (tid >> 4) < Lm1 ? t0 + (tid >> 4) : Lm1;
-        pb[k] = ld(Bb + tb * NS + n);
-        pc[k] = ld(Cb + tb * NS + n);
-    };
-    auto stage = [&](int k, int buf) {
-        s_bc[buf][0][n][tid >> 4] = pb[k];
-        s_bc[buf][1][n][tid >> 4] = pc[k];
-    };
-
-#pragma unroll
-    for (int k = 0; k < PF; ++k) fetch(k, (int64_t)k * TCH);
-    stage(0, 0);
-    lds_barrier();
-    for (int64_t tb0 = 0; tb0 < L; tb0 += PF * TCH) {
-#pragma unroll
-        for (int k = 0; k < PF; ++k) {
-            const int64_t t0 = tb0 + k * TCH;
-            const int buf = k & 1;  // PF is even: the LDS buffer alternates chunk by chunk
-            // ---- pre: step t0+n of this row's channel (slot k was filled PF chunks ago)
-            const bool tv = t0 + n < L;
-            const float uu = pu[k], zz = pz[k];
-            float dl = pd[k] + bias;
-            if (SOFTPLUS) dl = softplus(dl);
-            dl = tv ? dl : 0.0f;  // steps past the end leave the state unchanged
-            const float du = dl * uu;
-
-            float bv[TCH], cv[TCH];
-#pragma unroll
-            for (int q = 0; q < TCH; q += 4) {
-                const float4 b4 = *reinterpret_cast<const float4*>(&s_bc[buf][0][n][q]);
-                const float4 c4 = *reinterpret_cast<const float4*>(&s_bc[buf][1][n][q]);
-                bv[q] = b4.x; bv[q + 1] = b4.y; bv[q + 2] = b4.z; bv[q + 3] = b4.w;
-                cv[q] = c4.x; cv[q + 1] = c4.y; cv[q + 2] = c4.z; cv[q + 3] = c4.w;
-            }
-            // B/C of the next chunk (slot k+1, fetched PF-1 chunks ago) into the other buffer,
-            // which every wave finished reading before the previous barrier.
-            stage((k + 1) % PF, buf ^ 1);
-            // refill slot k with the chunk PF ahead
-            fetch(k, t0 + PF * TCH);
-
-            // ---- main: 16 steps, state n
-            float p[TCH];
-            StepLoop<TCH>::run([&](auto sc) {
-                constexpr int s = decltype(sc)::value;
-                const float ab = fast_exp2(dpp<kDppBcast<s>>(dl) * A2);
-                h = fmaf(ab, h, dpp<kDppBcast<s>>(du) * bv[s]);
-                p[s] = cv[s] * h;
-            });
-
-            // ---- readout for step t0+n, then D skip, gate, store
-            float y = row_reduce_scatter16(p, n);
-            y = fmaf(Dd, uu, y);
-            if (HAS_Z) y *= silu(zz);
-            if (dvalid && tv) Storage<T>::store(op + (t0 + n) * Dm, y);
-            lds_barrier();
-            if (t0 + TCH >= L) break;
-        }
-    }
-    if (last_state && dvalid) last_state[(b * Dm + d) * NS + n] = h;
-}
-
-// ----------------------------------------------------------------------------- tile path
-// Memory side and math side are decoupled through LDS:
-//   * a block owns 64 consecutive channels of one batch row and walks time in chunks of TCH
-//     steps. u, delta, z are read and out is written as float4 tiles [TCH x 64]: 256-byte row
-//     segments, the pattern that streams best on this HBM (vs 16-64 B segments). Each thread
-//     owns one float4 (4 channels at one step) per chunk and does all per-element work for it:
-//     softplus and dt*u before the chunk, the readout sum, D*u, SiLU(z) and the store after it;
-//   * wave w owns states [w*SPW, (w+1)*SPW) of all 64 channels (lane = channel). dt and dt*u come
-//     from LDS; B and C of the wave's states are held in lane-distributed registers (every DPP
-//     row a full copy) and reach the multiplies through DPP row_newbcast, which the compiler
-//     folds into v_mul_f32_dpp, so delivering them costs no extra instruction or LDS traffic;
-//   * per-wave partial readouts are summed by the owning thread through LDS.
-// Loads run PF chunks ahead through a register ring.
-
-template <typename T, int W, int TCH, int PF, bool HAS_Z, bool SOFTPLUS, bool SBC>
-__global__ __launch_bounds__(64 * W) void scan_tile_kernel(
-    int64_t L, int64_t Dm, int ntiles,
-    const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
-    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
-    const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
-    const float* __restrict__ init_state, float* __restrict__ last_state) {
-    constexpr int NS = 16;
-    constexpr int SPW = NS / W;            // states per wave
-    constexpr int NT = 64 * W;             // threads
-    constexpr int F4 = TCH * 16 / NT;      // float4 per thread per chunk per tensor
-    constexpr int NBC = TCH * SPW * 2;     // B/C values per wave per chunk
-    // lane-distributed registers holding them (SBC: B/C come through scalar loads instead)
-    constexpr int QBC = SBC ? 1 : NBC / 16;
-    static_assert(NS % W == 0 && F4 >= 1 && F4 * NT == TCH * 16, "bad tiling");
-    static_assert(NBC % 16 == 0, "B/C values must fill whole DPP rows");
-
-    __shared__ float2 s_du[2][TCH][64];    // (dt, dt*u), double-buffered
-    __shared__ float s_part[2][W][TCH][64];  // per-wave partial readouts, double-buffered
-
-    // XCD-aware block order (block ids are dispatched round-robin over 8 XCDs): the tiles of
-    // one batch row, which share its B/C, land on one XCD.
-    const int nblk = gridDim.x;
-    int id = blockIdx.x;
-    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
-    const int tile = id % ntiles;
-    const int64_t b = id / ntiles;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t c0 = (int64_t)tile * 64;
-    const int64_t dl_ = c0 + lane;                 // this lane's channel in the math phase
-    const bool lvalid = dl_ < Dm;
-    const int64_t dlc = lvalid ? dl_ : Dm - 1;
-
-    // ---- per-thread float4 ownership (memory phase): element e = tid + j*NT of the tile
-    const int64_t rowbase = b * L * Dm;
-    int frow[F4], fcl[F4];
-    int64_t fch[F4];
-    bool fvalid[F4];
-    float4 fbias[F4], fD[F4];
-#pragma unroll
-    for (int j = 0; j < F4; ++j) {
-        const int e = tid + j * NT;
-        frow[j] = e >> 4;
-        fcl[j] = (e & 15) * 4;
-        fch[j] = c0 + fcl[j];
-        fvalid[j] = fch[j] < Dm;  // Dm % 4 == 0: a float4 is wholly in or out
-        const int64_t cc = fvalid[j] ? fch[j] : 0;
-        fbias[j] = dt_bias ? *reinterpret_cast<const float4*>(dt_bias + cc) : make_float4(0, 0, 0, 0);
-        fD[j] = Dv ? *reinterpret_cast<const float4*>(Dv + cc) : make_float4(0, 0, 0, 0);
-    }
-
-    float A2[SPW], h[SPW];
-#pragma unroll
-    for (int k = 0; k < SPW; ++k) {
-        A2[k] = A[dlc * NS + w * SPW + k] * kLog2e;
-        h[k] = init_state ? init_state[(b * Dm + dlc) * NS + w * SPW + k] : 0.0f;
-    }
-
-    // ---- prefetch ring (PF chunks in flight)
-    float4 ru[PF][F4], rd[PF][F4], rz[PF][F4];
-    float rbc[PF][QBC];
-    const int64_t Lm1 = L - 1;
-    const int jr = lane & 15;  // position within the DPP row
-    auto fetch = [&](int k, int64_t t0) {
-#pragma unroll
-        for (int j = 0; j < F4; ++j) {
-            int64_t t = t0 + frow[j];
-            t = t < Lm1 ? t : Lm1;
-            const int64_t off = rowbase + t * Dm + (fvalid[j] ? fch[j] : 0);
-            ru[k][j] = Vec4<T>::load(u + off);
-            rd[k][j] = Vec4<T>::load(delta + off);
-            rz[k][j] = HAS_Z ? Vec4<T>::load(z + off) : make_float4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int q = 0; q < (SBC ? 0 : QBC); ++q) {
-            const int v = q * 16 + jr;         // value index: step s, B/C, state k
-            const int st = v / (2 * SPW);
-            const int bc = (v / SPW) & 1;
-            const int kk = v % SPW;
-            int64_t t = t0 + st;
-            t = t < Lm1 ? t : Lm1;
-            rbc[k][q] = ld((bc ? Cm : Bm) + (b * L + t) * NS + w * SPW + kk);
-        }
-    };
-
-    // pre: dt and dt*u of this thread's float4s of chunk t0 (ring slot k) into s_du[buf];
-    // keeps u and z for the chunk's post phase.
-    auto pre = [&](int k, int64_t t0, int buf, float4 (&uu)[F4], float4 (&zz)[F4]) {
-#pragma unroll
-        for (int j = 0; j < F4; ++j) {
-            uu[j] = ru[k][j];
-            zz[j] = rz[k][j];
-            const bool tv = t0 + frow[j] < L;
-            float dlv[4], duv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float x = f4get(rd[k][j], i) + f4get(fbias[j], i);
-                if (SOFTPLUS) x = softplus(x);
-                x = tv ? x : 0.0f;  // steps past the end leave the state unchanged
-                dlv[i] = x;
-                duv[i] = x * f4get(uu[j], i);
-            }
-            float4* p4 = reinterpret_cast<float4*>(&s_du[buf][frow[j]][fcl[j]]);
-            p4[0] = make_float4(dlv[0], duv[0], dlv[1], duv[1]);
-            p4[1] = make_float4(dlv[2], duv[2], dlv[3], duv[3]);
-        }
-    };
-    // post: readout sum over the waves' partials, D skip, gate, store for chunk t0.
-    auto post = [&](int64_t t0, int buf, const float4 (&uu)[F4], const float4 (&zz)[F4]) {
-#pragma unroll
-        for (int j = 0; j < F4; ++j) {
-            float4 y = make_float4(0, 0, 0, 0);
-#pragma unroll
-            for (int ww = 0; ww < W; ++ww) {
-                const float4 pv = *reinterpret_cast<const float4*>(&s_part[buf][ww][frow[j]][fcl[j]]);
-                y.x += pv.x; y.y += pv.y; y.z += pv.z; y.w += pv.w;
-            }
-            y.x = fmaf(fD[j].x, uu[j].x, y.x);
-            y.y = fmaf(fD[j].y, uu[j].y, y.y);
-            y.z = fmaf(fD[j].z, uu[j].z, y.z);
-            y.w = fmaf(fD[j].w, uu[j].w, y.w);
-            if (HAS_Z) {
-                y.x *= silu(zz[j].x); y.y *= silu(zz[j].y);
-                y.z *= silu(zz[j].z); y.w *= silu(zz[j].w);
-            }
-            const int64_t t = t0 + frow[j];
-            if (fvalid[j] && t < L) Vec4<T>::store(out + rowbase + t * Dm + fch[j], y);
-        }
-    };
-    // main: all TCH steps of chunk (s_du[buf], B/C values bc) for this wave's states, partial
-    // readouts into s_part[buf]. dt, dt*u are read in one batch; the decays of a group of EG
-    // steps are issued together ahead of the recurrence that consumes them.
-    auto main_phase = [&](int buf, const float (&bc)[QBC], int64_t t0) {
-        float2 q2[TCH];
-#pragma unroll
-        for (int s = 0; s < TCH; ++s) q2[s] = s_du[buf][s][lane];
-        // SBC: this wave's B/C values are wave-uniform -> scalar loads into SGPRs, one group of
-        // EG steps loaded a group ahead, used directly as VALU operands.
-        const T* __restrict__ Bw = Bm + b * L * NS + w * SPW;
-        const T* __restrict__ Cw = Cm + b * L * NS + w * SPW;
-        const int smax = __builtin_amdgcn_readfirstlane(
-            (int)((Lm1 - t0) < (int64_t)(TCH - 1) ? (Lm1 - t0) : (int64_t)(TCH - 1)));
-        // group of EG steps: 8 decays in flight; with SBC, 2 x EG x SPW x 2 = 32 SGPRs of B/C
-        constexpr int EG = 8 / SPW >= 1 ? 8 / SPW : 1;
-        float sbv[2][EG][SPW], scv[2][EG][SPW];
-        auto load_group = [&](int slot, int g0) {
-#pragma unroll
-            for (int e = 0; e < EG; ++e) {
-                const int ss = g0 + e < smax ? g0 + e : smax;
-                const int64_t off = (t0 + ss) * NS;
-#pragma unroll
-                for (int kk = 0; kk < SPW; ++kk) {
-                    sbv[slot][e][kk] = ld(Bw + off + kk);
-                    scv[slot][e][kk] = ld(Cw + off + kk);
-                }
-            }
-        };
-        if constexpr (SBC) load_group(0, 0);
-        // The decays exp2(dt*A) of a group of EG steps are issued together, ahead of the
-        // recurrence that consumes them, so the transcendental unit's latency overlaps.
-        float part[TCH];
-        StepLoop<TCH / EG>::run([&](auto gc) {
-            constexpr int gi = decltype(gc)::value;
-            constexpr int g0 = gi * EG;
-            if constexpr (SBC && g0 + EG < TCH) load_group((gi + 1) & 1, g0 + EG);
-            float ab[EG][SPW];
-#pragma unroll
-            for (int e = 0; e < EG; ++e)
-#pragma unroll
-                for (int kk = 0; kk < SPW; ++kk) ab[e][kk] = fast_exp2(q2[g0 + e].x * A2[kk]);
-            StepLoop<EG>::run([&](auto ec) {
-                constexpr int e = decltype(ec)::value;
-                constexpr int s = g0 + e;
-                float acc = 0.0f;
-                StepLoop<SPW>::run([&](auto kc) {
-                    constexpr int kk = decltype(kc)::value;
-                    constexpr int vb = s * 2 * SPW + kk;        // B value index
-                    constexpr int vc = s * 2 * SPW + SPW + kk;  // C value index
-                    if constexpr (SBC) {
-                        h[kk] = fmaf(ab[e][kk], h[kk], sbv[gi & 1][e][kk] * q2[s].y);
-                        acc = fmaf(scv[gi & 1][e][kk], h[kk], acc);
-                    } else {
-                        h[kk] = fmaf(ab[e][kk], h[kk],
-                                     dpp<kDppBcast<vb % 16>>(bc[vb / 16]) * q2[s].y);
-                        acc += dpp<kDppBcast<vc % 16>>(bc[vc / 16]) * h[kk];
-                    }
-                });
-                part[s] = acc;
-            });
-        });
-#pragma unroll
-        for (int s = 0; s < TCH; ++s) s_part[buf][w][s][lane] = part[s];
-    };
-
-    // Software pipeline, one barrier per chunk: iteration k runs post(k-1), main(k) and
-    // pre(k+1) in one barrier-free region (they touch different LDS buffers), so the scheduler
-    // overlaps their latencies.
-#pragma unroll
-    for (int k = 0; k < PF; ++k) fetch(k, (int64_t)k * TCH);
-    float4 u_cur[F4], z_cur[F4], u_prev[F4], z_prev[F4];
-    float bc_cur[QBC];
-    pre(0, 0, 0, u_cur, z_cur);
-#pragma unroll
-    for (int q = 0; q < QBC; ++q) bc_cur[q] = SBC ? 0.0f : rbc[0][q];
-    fetch(0, (int64_t)PF * TCH);
-    lds_barrier();
-    bool have_prev = false;
-    for (int64_t tb0 = 0; tb0 < L; tb0 += PF * TCH) {
-        // ring slots are compile-time indices: the PF chunks of one round are expanded by
-        // template recursion (a plain unrolled loop was left rolled by the compiler)
-        StepLoop<PF>::run([&](auto kc) {
-            constexpr int k = decltype(kc)::value;
-            constexpr int kn = (k + 1) % PF;
-            const int64_t t0 = tb0 + k * TCH;
-            if (t0 >= L) return;  // uniform
-            constexpr int buf = k & 1;  // PF is even
-            if (have_prev) post(t0 - TCH, buf ^ 1, u_prev, z_prev);
-            main_phase(buf, bc_cur, t0);
-#pragma unroll
-            for (int j = 0; j < F4; ++j) { u_prev[j] = u_cur[j]; z_prev[j] = z_cur[j]; }
-            have_prev = true;
-            // next chunk: its slot kn was fetched PF-1 chunks ago; refill it afterwards
-            pre(kn, t0 + TCH, buf ^ 1, u_cur, z_cur);
-#pragma unroll
-            for (int q = 0; q < QBC; ++q) bc_cur[q] = SBC ? 0.0f : rbc[kn][q];
-            fetch(kn, t0 + TCH + (int64_t)PF * TCH);
-            lds_barrier();
-        });
-    }
-    // the last chunk's post (its partials are in the buffer main wrote last)
-    {
-        const int64_t nchunks = (L + TCH - 1) / TCH;
-        const int64_t tl = (nchunks - 1) * TCH;
-        post(tl, (int)((nchunks - 1) & 1), u_prev, z_prev);
-    }
-    if (last_state && lvalid) {
-#pragma unroll
-        for (int k = 0; k < SPW; ++k) last_state[(b * Dm + dl_) * NS + w * SPW + k] = h[k];
-    }
-}
-
 // ----------------------------------------------------------------------------- wave-complete path
 // One wave owns 16 channels x all 16 states: DPP row r (16 lanes) holds states [4r, 4r+4) of the
 // wave's 16 channels, lane c of the row one channel. Nothing of the math crosses waves, so the
@@ -612,7 +201,7 @@ __global__ __launch_bounds__(64 * W) void scan_tile_kernel(
 // exp(A * sum dt)); a carry kernel chains the segments' entry states; full blocks then run each
 // segment from its entry state (seg_init) and write the outputs.
 // Number of time segments for the wave kernel: 0 = automatic; set by hx_set_scan_segments.
-int g_scan_segments = 0;
+thread_local int g_scan_segments = 0;
 
 struct WaveSeg {
     int64_t seg_len;
@@ -809,237 +398,20 @@ __global__ __launch_bounds__(256) void scan_wave_kernel(
     }
 }
 
-// Leaner form of scan_wave_kernel (same decomposition and results, fewer VALU instructions
-// per state update, which is what bounds the wave kernel):
+// Leaner wave-complete kernel with every wave on its own. Same decomposition as
+// scan_wave_kernel, fewer VALU instructions per state update (which is what bounds it):
 //   * addresses are 32-bit offsets from per-row base pointers, advanced by a constant per chunk
-//     and clamped with one min (the 64-bit recomputation cost ~2 instructions per state update);
+//     and clamped with one min;
 //   * steps past the segment end are guarded only in a segment's last chunk;
 //   * dt and dt*u reach the other rows through LDS (each lane writes its 4 steps as one float4,
-//     reads its channel's 16 as four) instead of register swaps and the copies they need;
-//   * the readout's first term is a DPP multiply, so no accumulator is zeroed.
-// Requires L * Dm < 2^31 (32-bit offsets within a batch row).
-template <typename T, int PF, bool HAS_Z, bool SOFTPLUS, bool END_ONLY>
-__global__ __launch_bounds__(256) void scan_wave2_kernel(
-    int64_t L, int64_t Dm, int ntiles, int64_t Bt,
-    const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
-    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
-    const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
-    const float* __restrict__ init_state, float* __restrict__ last_state, WaveSeg sg) {
-    constexpr int NS = 16, TCH = 16;
-    constexpr int TS = 80;  // tile row stride (floats)
-    constexpr int GS = 20;  // gather row stride (floats): 16 values + pad
-    constexpr bool USE_Z = HAS_Z && !END_ONLY;
-    __shared__ float s_in[2][3][TCH][TS];  // [buf][u|delta|z][step][channel]
-    __shared__ float s_out[END_ONLY ? 1 : 2][TCH][TS];
-    __shared__ __attribute__((aligned(16))) float s_g[2][64][GS];  // [dt|dt*u][channel][4i + r]
-
-    const int nblk = gridDim.x;
-    int id = blockIdx.x;
-    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);  // XCD-aware order
-    const int tile = id % ntiles;
-    const int64_t b = (id / ntiles) % Bt;
-    const int seg = (int)(id / ntiles / Bt);
-    const int64_t tbeg = (int64_t)seg * sg.seg_len;
-    const int64_t tend = tbeg + sg.seg_len < L ? tbeg + sg.seg_len : L;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int w = tid >> 6;
-    const int r = lane >> 4;
-    const int c = lane & 15;
-    const int64_t c0 = (int64_t)tile * 64;
-    const int cb = w * 16 + c;
-    const int64_t d = c0 + cb;
-    const bool dvalid = d < Dm;
-    const int64_t dc = dvalid ? d : Dm - 1;
-    const int mrow = tid >> 4, mcl = (tid & 15) * 4;
-    const int64_t mch = c0 + mcl;
-    const bool mvalid = mch < Dm;
-
-    // per-row bases; 32-bit offsets inside the row
-    const T* ub = u + b * L * Dm;
-    const T* db = delta + b * L * Dm;
-    const T* zb = USE_Z ? z + b * L * Dm : nullptr;
-    T* ob = END_ONLY ? nullptr : out + b * L * Dm;
-    const T* Bb = Bm + b * L * NS;
-    const T* Cb = Cm + b * L * NS;
-    const uint32_t D32 = (uint32_t)Dm;
-    const uint32_t mcol = (uint32_t)(mvalid ? mch : 0);
-    const uint32_t x_last = (uint32_t)(tend - 1) * D32 + mcol;          // clamp of tile offsets
-    const uint32_t bc_last = (uint32_t)(tend - 1) * NS + 4 * r;         // clamp of B/C offsets
-    uint32_t x_next = (uint32_t)(tbeg + mrow) * D32 + mcol;             // next tile fetch
-    uint32_t bc_next = (uint32_t)(tbeg + c) * NS + 4 * r;               // next B/C fetch
-    const uint32_t x_step = TCH * D32, bc_step = TCH * NS;
-
-    float A2[4], h[4];
-    const float* h0 = END_ONLY ? nullptr
-                    : (sg.nseg > 1 ? sg.seg_init + (int64_t)seg * Bt * Dm * NS : init_state);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        A2[k] = A[dc * NS + 4 * r + k] * kLog2e;
-        h[k] = h0 ? h0[(b * Dm + dc) * NS + 4 * r + k] : 0.0f;
-    }
-    const float Dd = Dv ? Dv[dc] : 0.0f;
-    const float bias = dt_bias ? dt_bias[dc] : 0.0f;
-    float sumdt = 0.0f;
-
-    float4 ru[PF], rd[PF], rz[PF], rb[PF], rc[PF];
-    auto fetch = [&](int k) __attribute__((always_inline)) {
-        const uint32_t xo = x_next < x_last ? x_next : x_last;
-        ru[k] = Vec4<T>::load(ub + xo);
-        rd[k] = Vec4<T>::load(db + xo);
-        rz[k] = USE_Z ? Vec4<T>::load(zb + xo) : make_float4(0, 0, 0, 0);
-        const uint32_t bo = bc_next < bc_last ? bc_next : bc_last;
-        rb[k] = Vec4<T>::load(Bb + bo);
-        rc[k] = END_ONLY ? make_float4(0, 0, 0, 0) : Vec4<T>::load(Cb + bo);
-        x_next += x_step;
-        bc_next += bc_step;
-    };
-    auto stage_in = [&](int k, int buf) __attribute__((always_inline)) {
-        *reinterpret_cast<float4*>(&s_in[buf][0][mrow][mcl]) = ru[k];
-        *reinterpret_cast<float4*>(&s_in[buf][1][mrow][mcl]) = rd[k];
-        if (USE_Z) *reinterpret_cast<float4*>(&s_in[buf][2][mrow][mcl]) = rz[k];
-    };
-    auto store_out = [&](int64_t t0, int buf) __attribute__((always_inline)) {
-        if constexpr (!END_ONLY) {
-            const int64_t t = t0 + mrow;
-            if (mvalid && t < tend)
-                Vec4<T>::store(ob + ((uint32_t)t * D32 + mcol),
-                               *reinterpret_cast<const float4*>(&s_out[buf][mrow][mcl]));
-        }
-    };
-
-    // math for one chunk: inputs from s_in[buf], outputs into s_out[buf]; FULL = all 16 steps
-    // inside the segment
-    auto compute = [&](int64_t t0, int buf, const float4& B4, const float4& C4, auto full_c)
-        __attribute__((always_inline)) {
-        constexpr bool FULL = decltype(full_c)::value;
-        const int nvalid = FULL ? TCH : (int)(tend - t0);
-        float uu[4], zz[4], dl[4], du[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int s = r + 4 * i;
-            uu[i] = s_in[buf][0][s][cb];
-            float x = s_in[buf][1][s][cb] + bias;
-            zz[i] = USE_Z ? s_in[buf][2][s][cb] : 0.0f;
-            if (SOFTPLUS) x = softplus(x);
-            if (!FULL) x = s < nvalid ? x : 0.0f;  // steps past the end leave the state unchanged
-            dl[i] = x;
-            du[i] = x * uu[i];
-            if (END_ONLY) sumdt += x;
-        }
-        // row all-gather through LDS: lane (r, c) holds steps r + 4i, stored step-major
-        // (s_g[.][cb][s], s = 4i + r) so the float4 at [4g] is exactly the steps of group g and
-        // each group's read can be in flight while the previous group computes
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s_g[0][cb][4 * i + r] = dl[i];
-            s_g[1][cb][4 * i + r] = du[i];
-        }
-        __builtin_amdgcn_wave_barrier();
-        float gdl[4][4], gdu[4][4];  // [row rr][i]: step rr + 4i
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 a = *reinterpret_cast<const float4*>(&s_g[0][cb][4 * i]);
-            const float4 q = *reinterpret_cast<const float4*>(&s_g[1][cb][4 * i]);
-            gdl[0][i] = a.x; gdl[1][i] = a.y; gdl[2][i] = a.z; gdl[3][i] = a.w;
-            gdu[0][i] = q.x; gdu[1][i] = q.y; gdu[2][i] = q.z; gdu[3][i] = q.w;
-        }
-        const float bk[4] = {B4.x, B4.y, B4.z, B4.w};
-        const float ck[4] = {C4.x, C4.y, C4.z, C4.w};
-        float P[16];
-        StepLoop<4>::run([&](auto gc) {
-            constexpr int g = decltype(gc)::value;
-            float ab[4][4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int s = 4 * g + e;
-                    ab[e][k] = fast_exp2(gdl[s & 3][s >> 2] * A2[k]);
-                }
-            StepLoop<4>::run([&](auto ec) {
-                constexpr int s = 4 * g + decltype(ec)::value;
-                const float dus = gdu[s & 3][s >> 2];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) h[k] = fmaf(ab[s - 4 * g][k], h[k], dpp<kDppBcast<s>>(bk[k]) * dus);
-                if constexpr (!END_ONLY) {
-                    float acc = dpp<kDppBcast<s>>(ck[0]) * h[0];
-                    acc = fmac_bcast<s>(acc, ck[1], h[1]);
-                    acc = fmac_bcast<s>(acc, ck[2], h[2]);
-                    acc = fmac_bcast<s>(acc, ck[3], h[3]);
-                    P[(s >> 2) + 4 * (s & 3)] = acc;  // j = i + 4*rr for s = rr + 4*i
-                }
-            });
-        });
-        if constexpr (!END_ONLY) {
-            float Y[4];
-            rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int s = r + 4 * i;
-                float y = fmaf(Dd, uu[i], Y[i]);
-                if (HAS_Z) y *= silu(zz[i]);
-                s_out[buf][s][cb] = y;
-            }
-        }
-    };
-
-#pragma unroll
-    for (int k = 0; k < PF; ++k) fetch(k);
-    stage_in(0, 0);
-    float4 B4 = rb[0], C4 = rc[0];
-    fetch(0);
-    lds_barrier();
-    for (int64_t tb0 = tbeg; tb0 < tend; tb0 += PF * TCH) {
-        StepLoop<PF>::run([&](auto kc) __attribute__((always_inline)) {
-            constexpr int k = decltype(kc)::value;
-            constexpr int kn = (k + 1) % PF;
-            constexpr int buf = k & 1;  // PF is even
-            const int64_t t0 = tb0 + k * TCH;
-            if (t0 >= tend) return;  // uniform
-            stage_in(kn, buf ^ 1);
-            if (t0 > tbeg) store_out(t0 - TCH, END_ONLY ? 0 : buf ^ 1);
-            const float4 Bn = rb[kn], Cn = rc[kn];
-            fetch(kn);
-            if (t0 + TCH <= tend)
-                compute(t0, buf, B4, C4, std::true_type{});
-            else
-                compute(t0, buf, B4, C4, std::false_type{});
-            B4 = Bn;
-            C4 = Cn;
-            lds_barrier();
-        });
-    }
-    if constexpr (!END_ONLY) {
-        const int64_t nch = (tend - tbeg + TCH - 1) / TCH;
-        store_out(tbeg + (nch - 1) * TCH, (int)((nch - 1) & 1));
-        if (last_state && dvalid && seg == sg.nseg - 1) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) last_state[(b * Dm + d) * NS + 4 * r + k] = h[k];
-        }
-    } else {
-        float t1 = sumdt, t2 = sumdt;
-        swap16(t1, t2);
-        float sa = t1 + t2;
-        float t3 = sa, t4 = sa;
-        swap32(t3, t4);
-        sumdt = t3 + t4;
-        if (dvalid) {
-            float* he = sg.seg_hend + (int64_t)seg * Bt * Dm * NS;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) he[(b * Dm + d) * NS + 4 * r + k] = h[k];
-            if (r == 0) sg.seg_sumdt[((int64_t)seg * Bt + b) * Dm + d] = sumdt;
-        }
-    }
-}
-
-// scan_wave2_kernel with every wave on its own: each wave stages its own 16 channels x 16 steps
-// tiles (one float4 per lane per operand, 64-byte row pieces) in its own LDS region, so the
-// waves of a block never wait for each other (no block barrier per chunk; LDS operations of one
-// wave execute in order, so program order alone orders each wave's staging writes and reads).
-// WPB waves per block (64 * WPB threads). Same arithmetic, results identical to wave2's.
-// Requires L * Dm < 2^31 (32-bit offsets within a batch row).
+//     reads its channel's 16 as four) instead of register swaps;
+//   * the readout's first term is a DPP multiply, so no accumulator is zeroed;
+//   * each wave stages its own 16 channels x 16 steps tiles (one float4 per lane per operand,
+//     64-byte row pieces) in its own LDS region, so the waves of a block never wait for each
+//     other (LDS operations of one wave execute in order, so program order alone orders each
+//     wave's staging writes and reads).
+// WPB waves per block (64 * WPB threads). Requires L * Dm < 2^31 (32-bit offsets within a
+// batch row).
 template <typename T, int PF, bool HAS_Z, bool SOFTPLUS, bool END_ONLY, int WPB>
 __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
     int64_t L, int64_t Dm, int ntiles, int64_t Bt,
@@ -1516,8 +888,10 @@ __global__ __launch_bounds__(256) void scan_ws_kernel(
                 float Y[4];
                 rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i
                 // step r + 4i of this chunk sits at lane_off + (16p + 4i) * row bytes; steps past
-                // the end land at or past nrec and are dropped
-                const uint32_t chunk_off = lane_off + (uint32_t)p * (uint32_t)TCH * row_bytes;
+                // the end land at or past nrec and are dropped. Lanes of channels past Dm stay at
+                // nrec: adding the chunk term could wrap their 32-bit offset back below nrec.
+                const uint32_t chunk_off =
+                    dvalid ? lane_off + (uint32_t)p * (uint32_t)TCH * row_bytes : nrec;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float y = fmaf(Dd, fuv[i], Y[i]);  // as scan_wave3_kernel: identical results
@@ -1809,32 +1183,10 @@ int dispatch_fast(const ScanArgs& a) {
     return launch_fast<T, W, TCH, false, false>(a);
 }
 
-template <typename T, int W, int TCH, int PF, bool HAS_Z, bool SP, bool SBC>
-int launch_tile(const ScanArgs& a) {
-    const int ntiles = (int)((a.Dm + 63) / 64);
-    dim3 grid((unsigned)(ntiles * a.Bt));
-    hipLaunchKernelGGL((scan_tile_kernel<T, W, TCH, PF, HAS_Z, SP, SBC>), grid, dim3(64 * W), 0,
-                       a.stream, a.L, a.Dm, ntiles, (const T*)a.u, (const T*)a.delta, a.A,
-                       (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
-                       a.init_state, a.last_state);
-    HX_LAUNCH_CHECK();
-    return HX_OK;
-}
-
-template <typename T, int W, int TCH, int PF, bool SBC>
-int dispatch_tile(const ScanArgs& a) {
-    const bool hz = a.z != nullptr;
-    if (hz && a.softplus) return launch_tile<T, W, TCH, PF, true, true, SBC>(a);
-    if (hz) return launch_tile<T, W, TCH, PF, true, false, SBC>(a);
-    if (a.softplus) return launch_tile<T, W, TCH, PF, false, true, SBC>(a);
-    return launch_tile<T, W, TCH, PF, false, false, SBC>(a);
-}
-
-// VER: 1 scan_wave_kernel, 2 scan_wave2_kernel, 3 scan_wave3_kernel with 4 waves per block,
-// 4 scan_wave3_kernel with 1 wave per block
+// VER: 1 scan_wave_kernel (64-bit row offsets), 3 scan_wave3_kernel with 4 waves per block
 template <typename T, int PF, bool HAS_Z, bool SP, bool END_ONLY, int VER>
 int launch_wave_one(const ScanArgs& a, const WaveSeg& sg) {
-    constexpr int WPB = VER == 4 ? 1 : 4;
+    constexpr int WPB = 4;
     const int64_t ntiles = (a.Dm + 16 * WPB - 1) / (16 * WPB);
     // the end-state pass skips the last segment: nothing consumes its end state
     const int64_t nseg_run = END_ONLY ? sg.nseg - 1 : sg.nseg;
@@ -1843,11 +1195,6 @@ int launch_wave_one(const ScanArgs& a, const WaveSeg& sg) {
     dim3 grid((unsigned)(ntiles * a.Bt * nseg_run));
     if constexpr (VER >= 3)
         hipLaunchKernelGGL((scan_wave3_kernel<T, PF, HAS_Z, SP, END_ONLY, WPB>), grid, dim3(64 * WPB), 0,
-                           a.stream, a.L, a.Dm, (int)ntiles, a.Bt, (const T*)a.u, (const T*)a.delta, a.A,
-                           (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
-                           a.init_state, a.last_state, sg);
-    else if constexpr (VER == 2)
-        hipLaunchKernelGGL((scan_wave2_kernel<T, PF, HAS_Z, SP, END_ONLY>), grid, dim3(256), 0,
                            a.stream, a.L, a.Dm, (int)ntiles, a.Bt, (const T*)a.u, (const T*)a.delta, a.A,
                            (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
                            a.init_state, a.last_state, sg);
@@ -1963,28 +1310,6 @@ int dispatch_ws(const ScanArgs& a) {
     return launch_ws<T, NR, false, false>(a);
 }
 
-template <typename T, bool HAS_Z, bool SP>
-int launch_state_lane(const ScanArgs& a) {
-    constexpr int PF = 4;
-    const int ntiles = (int)((a.Dm + 15) / 16);
-    dim3 grid((unsigned)ntiles, (unsigned)a.Bt);
-    hipLaunchKernelGGL((scan_state_lane_kernel<T, PF, HAS_Z, SP>), grid, dim3(256), 0, a.stream, a.L,
-                       a.Dm, ntiles, (const T*)a.u, (const T*)a.delta, a.A, (const T*)a.B,
-                       (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out, a.init_state,
-                       a.last_state);
-    HX_LAUNCH_CHECK();
-    return HX_OK;
-}
-
-template <typename T>
-int dispatch_state_lane(const ScanArgs& a) {
-    const bool hz = a.z != nullptr;
-    if (hz && a.softplus) return launch_state_lane<T, true, true>(a);
-    if (hz) return launch_state_lane<T, true, false>(a);
-    if (a.softplus) return launch_state_lane<T, false, true>(a);
-    return launch_state_lane<T, false, false>(a);
-}
-
 template <typename T, int NMAX>
 int launch_generic(const ScanArgs& a) {
     const int64_t total = a.Bt * a.Dm;
@@ -2036,12 +1361,11 @@ bool ws_preferred(const ScanArgs& a, size_t es) {
     return (double)ws_rounds * 0.89 < (double)w3_rounds;
 }
 
-// Kernel variant: 0 = auto, 1/2/4/8 = fast kernel with that many waves, -1 = generic.
-// hx_set_scan_variant() sets it; HX_SCAN_VARIANT in the environment gives the initial value.
-int g_scan_variant = [] {
-    const char* s = getenv("HX_SCAN_VARIANT");
-    return s ? atoi(s) : 0;
-}();
+// Kernel variant of the calling thread: 0 = auto, -1 = generic, 8 = the fast kernel, 40 =
+// scan_wave_kernel, 42 = scan_wave3_kernel, 44 = the warp-specialised kernel (set by
+// hx_set_scan_variant; a measurement knob, per thread so concurrent callers do not see each
+// other's setting).
+thread_local int g_scan_variant = 0;
 
 template <typename T>
 int run_scan(const ScanArgs& a) {
@@ -2054,45 +1378,19 @@ int run_scan(const ScanArgs& a) {
                          (!a.D || aligned(a.D, 16)) && (!a.dt_bias || aligned(a.dt_bias, 16)) &&
                          a.Bt * ((a.Dm + 63) / 64) <= 0x7fffffff;
     if (v == 0) {  // auto: the wave-complete kernels where their float4 access is legal
-        if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16)) {
+        if (tile_ok) {
             if (ws_preferred(a, sizeof(T))) return dispatch_ws<T, 2>(a);
             return a.L * a.Dm < (1LL << 31) ? dispatch_wave<T, 2, 3>(a) : dispatch_wave<T, 2>(a);
         }
-        if (tile_ok) return dispatch_tile<T, 8, 32, 2, false>(a);
         return dispatch_fast<T, 8, 16>(a);
     }
     switch (v) {
-        case 32: if (tile_ok) return dispatch_tile<T, 8, 32, 2, false>(a); break;
-        case 33: if (tile_ok) return dispatch_tile<T, 4, 16, 2, false>(a); break;
-        case 34: if (tile_ok) return dispatch_tile<T, 4, 32, 2, false>(a); break;
-        case 35: if (tile_ok) return dispatch_tile<T, 8, 32, 2, true>(a); break;
-        case 40: if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16)) return dispatch_wave<T, 2>(a); break;
-        case 41:
-            if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && a.L * a.Dm < (1LL << 31))
-                return dispatch_wave<T, 2, 2>(a);
-            break;
-        case 42:
-            if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && a.L * a.Dm < (1LL << 31))
-                return dispatch_wave<T, 2, 3>(a);
-            break;
-        case 43:
-            if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && a.L * a.Dm < (1LL << 31))
-                return dispatch_wave<T, 2, 4>(a);
-            break;
+        case 40: if (tile_ok) return dispatch_wave<T, 2>(a); break;
+        case 42: if (tile_ok && a.L * a.Dm < (1LL << 31)) return dispatch_wave<T, 2, 3>(a); break;
         case 44:
-            if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && (a.L + 16) * a.Dm * (int64_t)sizeof(T) < (1LL << 32))
-                return dispatch_ws<T, 2>(a);
+            if (tile_ok && (a.L + 16) * a.Dm * (int64_t)sizeof(T) < (1LL << 32)) return dispatch_ws<T, 2>(a);
             break;
-        case 45:
-            if (tile_ok && aligned(a.B, 16) && aligned(a.C, 16) && (a.L + 16) * a.Dm * (int64_t)sizeof(T) < (1LL << 32))
-                return dispatch_ws<T, sizeof(T) == 4 ? 8 : 4>(a);
-            break;
-        case 36: if (tile_ok) return dispatch_tile<T, 4, 16, 2, true>(a); break;
-        case 16: return dispatch_state_lane<T>(a);
-        case 1: return dispatch_fast<T, 1, 16>(a);
-        case 2: return dispatch_fast<T, 2, 16>(a);
-        case 8: return dispatch_fast<T, 8, 16>(a);
-        default: return dispatch_fast<T, 4, 16>(a);
+        default: break;
     }
     return dispatch_fast<T, 8, 16>(a);
 }
@@ -2144,11 +1442,10 @@ extern "C" int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim,
 }
 
 extern "C" int hx_set_scan_variant(int variant) {
-    HX_REQUIRE(variant == 0 || variant == -1 || variant == 1 || variant == 2 || variant == 4 ||
-                   variant == 8 || variant == 16 || (variant >= 32 && variant <= 36) || variant == 40 ||
-                   (variant >= 41 && variant <= 45),
-               HX_ERR_INVALID_INPUT,
-               "hx_set_scan_variant: %d is not one of 0, -1, 1, 2, 4, 8, 16, 32..36, 40..45", variant);
+    HX_REQUIRE(variant == 0 || variant == -1 || variant == 8 || variant == 40 || variant == 42 ||
+                   variant == 44,
+               HX_ERR_INVALID_INPUT, "hx_set_scan_variant: %d is not one of 0, -1, 8, 40, 42, 44",
+               variant);
     hx::g_scan_variant = variant;
     return HX_OK;
 }

@@ -147,11 +147,13 @@ class ByteLM:
                       ws.numel(), s)
         return self._head(x, stream), state
 
-    def decode_step(self, tokens, state, stream=None):
-        """tokens int32 [batch] -> logits fp32 [batch, vocab]; advances ``state`` in place."""
+    def decode_step(self, tokens, state, stream=None, workspace=None):
+        """tokens int32 [batch] -> logits fp32 [batch, vocab]; advances ``state`` in place.
+        ``workspace`` (uint8 device tensor of at least hx_mamba_layer_workspace_size(batch, 1,
+        ...) bytes) replaces the model's shared workspace."""
         bt = tokens.shape[0]
         x = embedding(tokens, self.embed, stream=stream)
-        ws = self._workspace(bt, 1)
+        ws = self._workspace(bt, 1) if workspace is None else workspace
         s = _stream(stream)
         for p, (ssm_st, conv_st) in zip(self.layers, state):
             _ffi.call("hx_mamba_layer_decode", bt, self.d_model, self.d_inner, self.d_state,
@@ -168,17 +170,22 @@ class ByteLM:
         is the graph's output buffer, overwritten by the next replay."""
         bt = state[0][0].shape[0]
         tok = torch.zeros((bt,), dtype=torch.int32, device=self.device)
-        self._workspace(bt, 1)
+        # the graph's own workspace: the captured launches hold its raw address, so it must live
+        # as long as the graph and never be replaced (the model's shared workspace is, whenever
+        # a longer prefill needs more)
+        need = int(_ffi.lib().hx_mamba_layer_workspace_size(bt, 1, self.d_model, self.d_inner,
+                                                            self.dt_rank, self.d_state))
+        ws = torch.empty(need, device=self.device, dtype=torch.uint8)
         # warm up on a copy of the state so capture sees allocated buffers
         scratch = [(s.clone(), c.clone()) for s, c in state]
         side = torch.cuda.Stream(device=self.device)
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            self.decode_step(tok, scratch)
+            self.decode_step(tok, scratch, workspace=ws)
         torch.cuda.current_stream().wait_stream(side)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            logits = self.decode_step(tok, state)
+            logits = self.decode_step(tok, state, workspace=ws)
 
         def step(tokens):
             tok.copy_(tokens)
@@ -186,6 +193,9 @@ class ByteLM:
             return logits
 
         step.graph = g
+        step.workspace = ws
+        step.tokens = tok
+        step.state = state
         return step
 
     def host_params(self):

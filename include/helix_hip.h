@@ -257,27 +257,29 @@ int hx_matmul_f32(int64_t M, int64_t K, int64_t N, const float* A, const float* 
                   void* stream);
 
 /* ------------------------------------------------------------------ tuning */
-/* Selects the selective-scan kernel variant for later calls in this process: 0 = auto (default),
- * 1/2/4/8 = the fast kernel with that many waves per block (16/W states per wave), -1 = the
- * generic one-thread-per-channel kernel, 16 = one lane per state, 32..36 = block-tiled kernels,
- * 40 = wave-complete kernel (a wave owns 16 channels x 16 states), 41 = its leaner form, 42/43 =
- * the leaner form with per-wave staging and no block barrier, 4 / 1 waves per block, 44 = the
- * warp-specialised kernel (3 state waves + 1 element wave per CU, 48 channels per block), 45 =
- * the same with 32-step chunks. A measurement knob with no reference counterpart; results are
- * identical within fp32 rounding for every variant. */
+/* Selects the selective-scan kernel variant for later calls on the calling thread: 0 = auto
+ * (default), -1 = the generic one-thread-per-channel kernel (any dstate <= 64, no alignment
+ * needs), 8 = the fast kernel (8 waves split the states of 64 channels), 40 = the wave-complete
+ * kernel (a wave owns 16 channels x 16 states; 64-bit row offsets), 42 = its leaner form with
+ * per-wave staging, 44 = the warp-specialised kernel (3 state waves + 1 element wave per CU, 48
+ * channels per block). A measurement knob with no reference counterpart; results agree within
+ * fp32 rounding for every variant. */
 int hx_set_scan_variant(int variant);
-/* Selects the bf16 GEMM kernel: 0 auto, 1 128x128 tiles, 2 256x128 tiles, 3 split-K 32x64 tiles,
+/* Selects the bf16 GEMM kernel for later calls on the calling thread: 0 auto, 1 128x128 tiles, 2 256x128 tiles, 3 split-K 32x64 tiles,
  * 4 direct-to-LDS 256x128 tiles (K % 64 == 0), 5 direct-to-LDS 256x256 tiles with 64-wide K tiles
  * (K % 64 == 0), 6 the same with 32-wide K tiles in a 4-stage ring (K % 32 == 0). A shape a
  * forced kernel cannot take goes to the 128x128 kernel (the split-K one for small shapes). A
  * measurement knob. */
 int hx_set_gemm_kernel(int k);
-int hx_set_s4d_path(int path);      /* 0 auto (wave path for dstate 16), 1 per-channel thread path */
-int hx_set_s4d_segments(int nseg);  /* S4D time segments: 0 auto, n forced */
-/* Number of time segments the long-sequence path splits a scan into (0 = automatic: only when
- * the (batch, 64-channel) tiles cannot fill the GPU and seqlen >= 4096). Segments are scanned in
- * parallel from a zero state, their entry states chained by a carry kernel, then rescanned with
- * outputs. A measurement knob; results agree within fp32 rounding for every setting. */
+/* S4D knobs for later calls on the calling thread: path 0 auto (wave path for dstate 16), 1 the
+ * per-channel thread path; time segments 0 auto, n forced. */
+int hx_set_s4d_path(int path);
+int hx_set_s4d_segments(int nseg);
+/* Number of time segments the long-sequence path splits a scan into, for later calls on the
+ * calling thread (0 = automatic: only when the (batch, 64-channel) tiles cannot fill the GPU and
+ * seqlen >= 4096). Segments are scanned in parallel from a zero state, their entry states chained
+ * by a carry kernel, then rescanned with outputs. A measurement knob; results agree within fp32
+ * rounding for every setting. */
 int hx_set_scan_segments(int nseg);
 
 #ifdef __cplusplus

@@ -201,3 +201,72 @@ def test_decode_graph_replays_match_eager(dev):
         assert torch.equal(got, want), t
         for (a, b), (c, d) in zip(st_graph, st_eager):
             assert torch.equal(a, c) and torch.equal(b, d), t
+
+
+def test_decode_graph_survives_workspace_growth(dev):
+    """A captured decode step keeps its own workspace: a later prefill of a longer batch grows
+    (replaces) the model's shared workspace and the freed block is reused by unrelated tensors;
+    replays must still match eager decode steps bit for bit."""
+    P = lm_params(2, 64, 128, 16, 8, 4, 256, seed=11)
+    m = model_from(P, dev, dt_rank=8)
+    rng = np.random.default_rng(12)
+    tok = torch.from_numpy(rng.integers(0, 256, (4, 10)).astype(np.int32)).to(dev)
+    _, st_eager = m.prefill(tok)
+    st_graph = [(s.clone(), c.clone()) for s, c in st_eager]
+    step = m.decode_graph(st_graph)
+    # grow the shared workspace and scribble over whatever the allocator hands out next
+    big = torch.from_numpy(rng.integers(0, 256, (8, 300)).astype(np.int32)).to(dev)
+    m.prefill(big)
+    junk = [torch.full((1 << 20,), 7.0, device=dev) for _ in range(8)]
+    for t in range(4):
+        nxt = torch.from_numpy(rng.integers(0, 256, (4,)).astype(np.int32)).to(dev)
+        want = m.decode_step(nxt, st_eager).clone()
+        torch.cuda.synchronize()
+        got = step(nxt).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), t
+        for (a, b), (c, d) in zip(st_graph, st_eager):
+            assert torch.equal(a, c) and torch.equal(b, d), t
+    del junk
+
+
+def test_lm_config5_decode_batch256(dev):
+    """BASELINE config 5's decode leg at its own batch (256): the full 12-layer model prefills 24
+    tokens per sequence, then one eager decode step and one replay of the captured step (from a
+    copy of the same state). At M = 256 the projections take the small split-K GEMM path, not
+    the one batch 16 takes. The oracle checks two sequences (first and last); the eager step
+    and the graph replay agree bit for bit; decode after a 23-token prefill continues it (equals
+    the 24-token prefill's last position within the bf16 bar).
+
+    Bar: north_star's bf16-storage tolerance, 2e-2 normwise. Through 12 layers of bf16
+    intermediates a one-ulp flip anywhere propagates: on MI355X the per-sequence distance of
+    these logits from the same-rounding oracle is 0.005-0.013 on both GEMM paths (batch 16 and
+    batch 256 alike), and the two device paths are 0.005-0.011 from each other."""
+    m = ByteLM(device=dev)
+    P = m.host_params()
+    bt, T = 256, 24
+    rng = np.random.default_rng(0xC5D)
+    tok = rng.integers(0, 256, (bt, T)).astype(np.int32)
+    td = torch.from_numpy(tok).to(dev)
+    print("case config5 decode batch 256", flush=True)
+    full, _ = m.prefill(td)
+    _, state = m.prefill(td[:, :T - 1].contiguous())
+    st_graph = [(s.clone(), c.clone()) for s, c in state]
+    lg = m.decode_step(td[:, T - 1].contiguous(), state)
+    step = m.decode_graph(st_graph)
+    lg_graph = step(td[:, T - 1].contiguous()).clone()
+    torch.cuda.synchronize()
+    assert torch.isfinite(lg).all()
+    assert torch.equal(lg, lg_graph)
+    for (a, b), (c, d) in zip(st_graph, state):
+        assert torch.equal(a, c) and torch.equal(b, d)
+    err = norm_err(lg.cpu().numpy(), full[:, T - 1].cpu().numpy())
+    print(f"decode vs 24-token prefill: normwise {err:.3e}")
+    assert err <= 2e-2, err
+    sub = tok[[0, bt - 1]]
+    _, rst = oracle.lm_prefill(sub[:, :T - 1], P, m.dt_rank)
+    rl, _ = oracle.lm_decode_step(sub[:, T - 1], P, rst, m.dt_rank)
+    g = lg.cpu().numpy()[[0, bt - 1]]
+    err = norm_err(g, rl)
+    print(f"decode vs oracle: normwise {err:.3e}, elementwise {rel_err(g, rl):.3e}")
+    assert err <= 2e-2, err

@@ -205,6 +205,45 @@ def test_scan_a_zero_is_prefix_sum():
     assert rel_err(out, ref) < 1e-5
 
 
+def test_scan_dt_bias_inside_softplus_closed_form():
+    """dt_bias enters softplus(delta + dt_bias). With A = 0 the state is a prefix sum, and with
+    delta[b, t, d] = log(expm1(c[d])) - bias[d] the step size is exactly c[d] only if the bias is
+    added inside the softplus: out = (C_t . c_d sum_{s<=t} u_s B_s + D u_t) silu(z_t). A bias
+    dropped, applied after the softplus, or with the wrong sign misses by O(1)."""
+    bt, L, dim, N = 2, 30, 4, 8
+    x = inputs(bt, L, dim, N, 31)
+    x["A"][:] = 0
+    c = np.array([0.25, 0.5, 1.0, 2.0])                       # target step sizes per channel
+    bias = np.array([-1.5, 0.0, 0.75, 3.0], F)
+    x["dt_bias"] = bias
+    x["delta"] = np.broadcast_to((np.log(np.expm1(c)) - bias).astype(F), (bt, L, dim)).copy()
+    out = oracle.selective_scan(**x)
+    u, z = x["u"].astype(np.float64), x["z"].astype(np.float64)
+    H = np.cumsum(c[None, None, :, None] * u[..., None] * x["B"][:, :, None, :].astype(np.float64), axis=1)
+    y = np.einsum("bldn,bln->bld", H, x["C"].astype(np.float64)) + x["D"] * u
+    ref = y * z / (1 + np.exp(-z))
+    assert rel_err(out, ref) < 1e-5
+    # the planted mistakes this closed form catches (restated here on the CPU, not in the oracle)
+    for wrong in (np.log1p(np.exp(x["delta"].astype(np.float64))),                 # bias dropped
+                  np.log1p(np.exp(x["delta"].astype(np.float64))) + bias,          # bias after softplus
+                  np.log1p(np.exp(x["delta"].astype(np.float64) - bias))):         # wrong sign
+        Hw = np.cumsum(wrong[..., None] * u[..., None] * x["B"][:, :, None, :].astype(np.float64), axis=1)
+        yw = (np.einsum("bldn,bln->bld", Hw, x["C"].astype(np.float64)) + x["D"] * u) * z / (1 + np.exp(-z))
+        assert rel_err(out, yw) > 1e-2
+
+
+def test_scan_dt_bias_without_softplus_is_added_to_delta():
+    """delta_softplus off: dt = delta + dt_bias (no softplus), checked on the single-state
+    geometric series with the bias carrying the whole step size (delta = 0)."""
+    L, dl, A, u, Bv, Cv = 40, 0.3, -1.2, 0.8, 1.1, 0.7
+    f = lambda v, shape: np.full(shape, v, F)
+    out = oracle.selective_scan(f(u, (1, L, 1)), f(0.0, (1, L, 1)), f(A, (1, 1)), f(Bv, (1, L, 1)),
+                                f(Cv, (1, L, 1)), dt_bias=f(dl, (1,)), delta_softplus=False)
+    a = np.exp(dl * A)
+    t = np.arange(L)
+    assert rel_err(out[0, :, 0], Cv * dl * u * Bv * (1 - a ** (t + 1)) / (1 - a)) < 1e-5
+
+
 def test_scan_single_state_geometric_series():
     L, dl, A, u, Bv, Cv = 50, 0.2, -1.5, 0.7, 1.3, -0.9
     f = lambda v, shape: np.full(shape, v, F)

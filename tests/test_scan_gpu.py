@@ -16,7 +16,8 @@ from tests.util import TOL_BF16, TOL_F32, bf16_round, rel_err, scan_inputs
 
 pytestmark = pytest.mark.gpu
 
-VARIANTS = [-1, 1, 2, 4, 8, 16, 32, 33, 34, 35, 36, 40, 41, 42, 43, 44, 45]
+# -1 generic, 8 fast, 40 wave-complete, 42 its per-wave-staged form, 44 warp-specialised
+VARIANTS = [-1, 8, 40, 42, 44]
 
 
 def to_dev(x, dev, dtype=torch.float32):
@@ -64,7 +65,7 @@ def test_scan_matches_oracle(dev, shape, variant):
 @pytest.mark.parametrize("with_z", [True, False])
 @pytest.mark.parametrize("with_D", [True, False])
 @pytest.mark.parametrize("softplus", [True, False])
-@pytest.mark.parametrize("variant", [45, 44, 43, 42, 41, 40, 32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", VARIANTS)
 def test_scan_optional_operands(dev, with_z, with_D, softplus, variant):
     ssm.set_scan_variant(variant)
     x = scan_inputs(2, 70, 96, 16, seed=7, with_z=with_z, with_D=with_D)
@@ -75,7 +76,7 @@ def test_scan_optional_operands(dev, with_z, with_D, softplus, variant):
     assert rel_err(g, r) <= TOL_F32
 
 
-@pytest.mark.parametrize("variant", [0, 42, 44, 45, -1])
+@pytest.mark.parametrize("variant", [0, 42, 44, -1])
 def test_scan_softplus_all_regimes(dev, variant):
     """delta spread over softplus's regimes: e^x far below f32 resolution of 1 + e^x (x < -17,
     where softplus(x) = e^x), the log1p range, and past the x > 20 cut-over."""
@@ -92,17 +93,16 @@ def test_scan_softplus_all_regimes(dev, variant):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 def test_scan_warp_specialised_matches_wave_kernel_bitwise(dev, dtype):
-    """The warp-specialised kernel (44/45) keeps scan_wave3_kernel's (42) operation order, so the
+    """The warp-specialised kernel (44) keeps scan_wave3_kernel's (42) operation order, so the
     automatic choice between them never changes a result bit; ragged L and dim included."""
     x = scan_inputs(3, 203, 100, 16, seed=23, with_bias=True)
     init = (np.random.default_rng(24).standard_normal((3, 100, 16)) * 0.5).astype(np.float32)
     outs = {}
-    for v in (42, 44, 45):
+    for v in (42, 44):
         ssm.set_scan_variant(v)
         outs[v] = run_gpu(x, dev, dtype=dtype, init_state=init, last=True)
-    for v in (44, 45):
-        assert np.array_equal(outs[v][0], outs[42][0]), v
-        assert np.array_equal(outs[v][1], outs[42][1]), v
+    assert np.array_equal(outs[44][0], outs[42][0])
+    assert np.array_equal(outs[44][1], outs[42][1])
 
 
 def test_scan_general_A(dev):
@@ -138,7 +138,7 @@ def test_scan_zero_length_returns_initial_state(dev):
     assert np.array_equal(s, init)
 
 
-@pytest.mark.parametrize("variant", [45, 44, 43, 42, 41, 40, 32, 33, 16, 4, -1])
+@pytest.mark.parametrize("variant", VARIANTS)
 @pytest.mark.parametrize("shape", [(2, 37, 70, 16), (1, 300, 256, 16)], ids=str)
 def test_scan_bf16_storage(dev, variant, shape):
     ssm.set_scan_variant(variant)
@@ -189,7 +189,7 @@ def test_shape_errors_raise_reference_variants(dev):
                                to_dev(x["B"], dev), to_dev(x["C"], dev))
 
 
-@pytest.mark.parametrize("variant", [0, 40, 41, 42, 43, 44, 45])
+@pytest.mark.parametrize("variant", [0, 40, 42, 44])
 def test_baseline_config2_full_size(dev, variant):
     """BASELINE config 2 (batch 8, L 2048, d_inner 1536, d_state 16, fp32) end to end against the
     (multi-threaded, arithmetic-identical) CPU oracle."""
@@ -212,7 +212,7 @@ def _reset_segments(dev):
     ssm.set_scan_variant(0)
 
 
-@pytest.mark.parametrize("variant", [40, 41, 42, 43])
+@pytest.mark.parametrize("variant", [40, 42])
 @pytest.mark.parametrize("nseg", [2, 3, 7])
 @pytest.mark.parametrize("shape", [(2, 300, 128, 16), (1, 1000, 64, 16), (1, 77, 192, 16)], ids=str)
 def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape, variant):
@@ -234,7 +234,7 @@ def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape, va
     assert rel_err(glast, rlast64) <= max(TOL_F32, 1.5 * rel_err(rlast, rlast64))
 
 
-@pytest.mark.parametrize("variant", [0, 40, 41, 42, 43])
+@pytest.mark.parametrize("variant", [0, 40, 42])
 def test_baseline_config4_scan_full_size(dev, variant):
     """BASELINE config 4 scan (batch 1, L 65536, d_inner 2048, d_state 16, fp32): the automatic
     segmented path against the (multi-threaded, arithmetic-identical) CPU oracle."""
@@ -248,3 +248,32 @@ def test_baseline_config4_scan_full_size(dev, variant):
     err = rel_err(g, r)
     print(f"config4 rel err {err:.3e}")
     assert err <= TOL_F32
+
+
+def test_warp_specialised_partial_group_large_offsets(dev):
+    """dim % 48 != 0 with a batch row past 2^31 bytes (1 x 30000 x 20000 fp32, 2.4 GB per
+    operand): the lanes of the last block's channels past dim must not write anywhere. Their
+    32-bit store offsets start past the row's end; advancing them by whole chunks used to wrap
+    below it and overwrite channel 18176 (2^32 mod the row size) at early steps. Channels are
+    independent, so the oracle runs on the touched channels only, over the whole sequence."""
+    ssm.set_scan_variant(44)
+    bt, L, dim, N = 1, 30000, 20000, 16
+    g = torch.Generator(device=dev).manual_seed(0x5753)
+    u = torch.randn((bt, L, dim), generator=g, device=dev)
+    delta = torch.randn((bt, L, dim), generator=g, device=dev) * 0.5 - 4.0
+    z = torch.randn((bt, L, dim), generator=g, device=dev)
+    B = torch.randn((bt, L, N), generator=g, device=dev)
+    C = torch.randn((bt, L, N), generator=g, device=dev)
+    A = -torch.arange(1, N + 1, device=dev, dtype=torch.float32).repeat(dim, 1).contiguous()
+    D = torch.randn((dim,), generator=g, device=dev)
+    print("case 1x30000x20000 fp32 variant 44", flush=True)
+    out = ssm.selective_scan_fwd(u, delta, A, B, C, D, z)
+    torch.cuda.synchronize()
+    chans = [0, 18176, dim - 32, dim - 1]
+    cut = lambda t: np.ascontiguousarray(t[:, :, chans].cpu().numpy())  # noqa: E731
+    x = dict(u=cut(u), delta=cut(delta), z=cut(z), B=B.cpu().numpy(), C=C.cpu().numpy(),
+             A=A[chans].cpu().numpy(), D=D[chans].cpu().numpy(), dt_bias=None)
+    del u, delta, z
+    r = oracle.selective_scan(**x)
+    got = out[:, :, chans].cpu().numpy()
+    assert rel_err(got, r) <= TOL_F32
