@@ -8,7 +8,13 @@ cannot serve a step from the previous one. A "step" is one hx_selective_scan_fwd
 batch. Prints ONE JSON line.
 
   python bench.py [--steps K] [--warmup W]
-                  [--workload c2|c2bf16|c3|c4|c4s4|c4s4exact|c4s4d|c5|c5dec|copy] [--no-cpu]
+                  [--workload c1|c2|c2bf16|c3|c4|c4s4|c4s4exact|c4s4d|c5|c5dec|copy] [--no-cpu]
+
+Timing: an untimed clock-settle phase (the step back to back for SETTLE_S seconds) and W untimed
+warmup steps, then exactly K timed steps with a HIP event between consecutive steps; ms_per_step
+is the median step time ("timing" holds the mean, min, max and the settle phase).
+
+c1 = BASELINE config 1 (README SSM example shapes): exported MambaBlock MLP + S4Block, fp32.
 
 c3 = BASELINE config 3, the full Mamba block (in_proj, conv1d+SiLU, x_proj, dt_proj, fused scan,
 out_proj) at batch 4 x L 4096 x d_model 2048, bf16 storage; reported separately from the metric.
@@ -59,21 +65,62 @@ def make_scan_inputs(bt, L, dim, N, gen, dev, dtype):
     return dict(u=cast(u), delta=cast(delta), A=A, B=cast(B), C=cast(C), D=D, z=cast(z))
 
 
-def time_steps(fn, sets, steps, warmup):
-    """Runs `warmup` untimed steps then exactly `steps` timed steps, rotating over `sets` input sets;
-    HIP events on the stream the kernels are launched on (torch's current stream, which is the
-    stream handed to the C ABI). Returns ms per step."""
+SETTLE_S = 0.25  # untimed clock-settle phase before the warmup steps (seconds of launches)
+LAST_TIMING = {}
+
+
+def time_steps(fn, sets, steps, warmup, settle_s=SETTLE_S):
+    """Times exactly `steps` steps after `warmup` untimed ones, rotating over `sets` input sets.
+
+    Before the warmup the step runs back to back, untimed, for `settle_s` seconds: the GPU's
+    power management raises the shader clock over the first tens of milliseconds of load, so
+    steps timed from an idle GPU measure that ramp rather than the kernel (MI355X: config 2
+    takes 165-170 us per step in the first ~10 ms, 141-142 us after). The timed region is the
+    `steps` steps only, bracketed by synchronisation; a HIP event on the launch stream (torch's
+    current stream, the stream handed to the C ABI) separates every step, and the median step
+    time is returned (the mean is kept in LAST_TIMING)."""
+    n_settle = 0
+    if settle_s > 0:
+        t_end = time.perf_counter() + settle_s
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                fn(n_settle % sets)
+                n_settle += 1
+            torch.cuda.synchronize()
     for i in range(warmup):
         fn(i % sets)
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
     for i in range(steps):
         fn(i % sets)
-    end.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    LAST_TIMING.clear()
+    LAST_TIMING.update(median_ms=float(np.median(per)), mean_ms=float(np.mean(per)),
+                       min_ms=float(np.min(per)), max_ms=float(np.max(per)),
+                       total_ms=float(ev[0].elapsed_time(ev[-1])),
+                       clock_settle={"seconds": settle_s, "untimed_steps": n_settle})
+    return float(np.median(per))
+
+
+def host_info():
+    """The host the CPU baselines run on: nproc, lscpu model name, the OpenMP thread count used
+    (OMP_NUM_THREADS, the per-GPU CPU share on the GPU box) and OMP_PROC_BIND."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    import oracle  # test/bench infrastructure only
+    return {"nproc": os.cpu_count(), "lscpu_model": model, "omp_threads": oracle.max_threads(),
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS"),
+            "OMP_PROC_BIND": os.environ.get("OMP_PROC_BIND")}
 
 
 def cpu_baseline_scan(x_dev, sample_batches):
@@ -86,7 +133,7 @@ def cpu_baseline_scan(x_dev, sample_batches):
     t0 = time.perf_counter()
     out1 = oracle.selective_scan(**host)
     t1 = time.perf_counter()
-    threads = min(oracle.max_threads(), 16)
+    threads = oracle.max_threads()  # OMP_NUM_THREADS: the host's CPU share for this GPU
     t2 = time.perf_counter()
     oracle.selective_scan_omp(**host, threads=threads)
     t3 = time.perf_counter()
@@ -94,6 +141,7 @@ def cpu_baseline_scan(x_dev, sample_batches):
     return dict(value=toks / (t1 - t0), unit="tokens/s", cores=1, kind="port",
                 sample=f"batch rows 0..{bt - 1} of config 2 input set 0 ({bt}x{L}x{dim}x16), "
                        f"single-threaded C oracle, {t1 - t0:.2f} s",
+                host=host_info(),
                 omp=dict(value=toks / (t3 - t2), threads=threads, seconds=round(t3 - t2, 3))), out1
 
 
@@ -128,6 +176,7 @@ def bench_block(args, dev):
         ssm.mamba_block_fwd(xs[i], **prm, workspace=ws, out=outs[i])
 
     ms = time_steps(step, nsets, args.steps, args.warmup)
+    timing = dict(LAST_TIMING)
     flops = {"in_proj": 2 * M * 2 * di * dm, "x_proj": 2 * M * (r + 2 * N) * di,
              "dt_proj": 2 * M * di * r, "out_proj": 2 * M * dm * di}
     # per-stage breakdown on the block's own intermediates
@@ -152,7 +201,7 @@ def bench_block(args, dev):
     }
     breakdown = {}
     for name, fn in stages.items():
-        sms = time_steps(fn, 1, max(args.steps // 2, 3), 2)
+        sms = time_steps(fn, 1, max(args.steps // 2, 3), 2, settle_s=0.02)
         e = {"ms": sms}
         if name in flops:
             e["tflops"] = flops[name] / (sms * 1e-3) / 1e12
@@ -177,6 +226,7 @@ def bench_block(args, dev):
                      "frac": total_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
                      "traffic": None, "algorithmic_flops": total_flops, "kernel_ms": gemm_ms},
         "breakdown": breakdown,
+        "timing": timing,
         "cpu_baseline": None,
     }
     print(json.dumps(rec))
@@ -199,9 +249,14 @@ def bench_s4(args, dev):
                    C=torch.randn((M, N), generator=gen, device=dev) * 0.1,
                    D=torch.randn((M,), generator=gen, device=dev))
         par = args.workload == "c4s4"
+        # discretize(dt) once (host libm, hx_s4_discretize) and one workspace: no host round
+        # trip and no allocation inside the timed steps
+        a_disc = ssm.s4_discretize(prm["a_real"], prm["a_imag"], 0.1, device=dev)
+        fn = _ffi.lib().hx_s4_ref_parallel_workspace_size if par else _ffi.lib().hx_s4_ref_workspace_size
+        ws = torch.empty(int(fn(M, N, L)), device=dev, dtype=torch.uint8)
 
         def step(i):
-            ssm.s4_ref_fwd(xs[i], **prm, parallel=par)
+            ssm.s4_ref_fwd(xs[i], **prm, parallel=par, a=a_disc, workspace=ws)
 
         workload = ("S4Block::forward_ssm reference mode, " + ("time-parallel" if par else "bit-exact")
                     + " (d_model 2048, N 16, L 65536, A = -0.5 + i*pi*n, dt 0.1)")
@@ -220,7 +275,26 @@ def bench_s4(args, dev):
 
         workload = "S4D diagonal complex recurrence (batch 1, L 65536, d 2048, N 16, A = -0.5 + i*pi*n)"
     ms = time_steps(step, 2, args.steps, args.warmup)
+    timing = dict(LAST_TIMING)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu and args.workload in ("c4s4", "c4s4exact"):
+        # (R): S4Block::forward_ssm in the reference's execution shape (allocation per op, a
+        # copied column slice per step, single thread) on the first `ls` steps of input set 0;
+        # its cost per step does not depend on t, so tokens/s extrapolates to the full L
+        import oracle  # test/bench infrastructure only
+        ls = 4096
+        xh = xs[0][:, :ls].contiguous().cpu().numpy()
+        hp = {k: v.cpu().numpy() for k, v in prm.items()}
+        t0 = time.perf_counter()
+        yr = oracle.r_s4_forward_ssm(xh, hp["a_real"], hp["a_imag"], hp["B"], hp["C"], hp["D"])
+        t1 = time.perf_counter()
+        ref = oracle.s4_ref_fwd(xh, hp["a_real"], hp["a_imag"], hp["B"], hp["C"], hp["D"])
+        cpu = dict(value=ls / (t1 - t0), unit="tokens/s", cores=1, kind="port",
+                   sample=f"first {ls} of {L} steps of input set 0 (d_model {M}, N {N}): "
+                          f"S4Block::forward_ssm restated op by op with the reference's per-op "
+                          f"allocation (oracle/hx_oracle_ref.c), {t1 - t0:.2f} s",
+                   host=host_info(), bit_identical_to_oracle=bool(np.array_equal(yr, ref)))
     print(json.dumps({
         "metric": "S4 recurrence tokens/s (config 4), 1 GPU", "value": L * 1e3 / ms, "unit": "tokens/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
@@ -230,7 +304,73 @@ def bench_s4(args, dev):
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": gbs / PEAK_HBM_GBS, "traffic": None, "algorithmic_bytes": nbytes,
                      "kernel_ms": ms},
-        "cpu_baseline": None}))
+        "timing": timing,
+        "cpu_baseline": cpu}))
+
+
+def bench_c1(args, dev):
+    """BASELINE config 1, the README SSM example's shapes: the exported MambaBlock::forward_mamba
+    (Linear -> SiLU -> Linear, d_model 64, expand 2, crates/nn/src/lib.rs:888-906) on x [100, 64]
+    ~ U(-1, 1), and ssm::S4Block::forward_ssm (d_model 64, N 16) on x^T [64, 100], weights from the
+    reference's init distributions (seeded). A step is both forwards (latency-bound: three small
+    kernels plus the S4 chain). CPU baseline (R): the same two forwards restated in the
+    reference's execution shape (per-op allocation, oracle/hx_oracle_ref.c), one thread."""
+    import oracle  # test/bench infrastructure only
+    rng = np.random.default_rng(0x48454C49_00000001)
+    R, dm, di, N = 100, 64, 128, 16
+    f = np.float32
+    X = rng.uniform(-1, 1, (R, dm)).astype(f)
+    Wg = (rng.standard_normal((di, dm)) * np.sqrt(2 / dm)).astype(f)
+    Wo = (rng.standard_normal((dm, di)) * np.sqrt(2 / di)).astype(f)
+    bg, bo = np.zeros(di, f), np.zeros(dm, f)
+    ar, ai = np.zeros(N, f), rng.standard_normal(N).astype(f)
+    B = (rng.standard_normal((N, dm)) * 0.1).astype(f)
+    C = (rng.standard_normal((dm, N)) * 0.1).astype(f)
+    D = np.zeros(dm, f)
+    xs = np.ascontiguousarray(X.T)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    gX, gWg, gWo, gbg, gbo, gxs, gB, gC, gD = map(d, (X, Wg, Wo, bg, bo, xs, B, C, D))
+    gar, gai = d(ar), d(ai)
+    a_disc = ssm.s4_discretize(gar, gai, 0.1, device=dev)
+    ws = torch.empty(int(_ffi.lib().hx_s4_ref_workspace_size(dm, N, R)), device=dev, dtype=torch.uint8)
+    out = {}
+
+    def step(i):
+        h = ssm.linear(gX, gWg, gbg, act=1)
+        out["mlp"] = ssm.linear(h, gWo, gbo)
+        out["s4"] = ssm.s4_ref_fwd(gxs, gar, gai, gB, gC, gD, a=a_disc, workspace=ws)
+
+    ms = time_steps(step, 1, args.steps, args.warmup)
+    timing = dict(LAST_TIMING)
+    torch.cuda.synchronize()
+    ref_mlp = oracle.mamba_mlp(X, Wg, bg, Wo, bo)
+    ref_s4 = oracle.s4_ref_fwd(xs, ar, ai, B, C, D)
+    g_mlp, g_s4 = out["mlp"].cpu().numpy(), out["s4"].cpu().numpy()
+    floor = lambda r: 1e-3 * np.abs(r).max()  # noqa: E731
+    err_mlp = float((np.abs(g_mlp - ref_mlp) / np.maximum(np.abs(ref_mlp), floor(ref_mlp))).max())
+    cpu = None
+    if not args.no_cpu:
+        reps = 200
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            oracle.r_mamba_mlp(X, Wg, bg, Wo, bo)
+            oracle.r_s4_forward_ssm(xs, ar, ai, B, C, D)
+        t1 = time.perf_counter()
+        cpu = dict(value=R * reps / (t1 - t0), unit="tokens/s", cores=1, kind="port",
+                   sample=f"{reps} repetitions of both config-1 forwards in the reference's "
+                          f"execution shape (oracle/hx_oracle_ref.c), {t1 - t0:.2f} s",
+                   host=host_info())
+    print(json.dumps({
+        "metric": "config-1 forwards (exported MambaBlock MLP [100, 64] + S4Block::forward_ssm "
+                  "[64, 100]) tokens/s, 1 GPU",
+        "value": R * 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (x ~ U(-1,1), the reference's init distributions, seeded)",
+        "config": {"workload": "config1: MambaBlock MLP d_model 64 expand 2 on [100, 64] + "
+                               "S4Block d_model 64 N 16 on [64, 100]"},
+        "parity": {"mlp_max_rel_err": err_mlp, "s4_bit_exact": bool(np.array_equal(g_s4, ref_s4))},
+        "timing": timing, "cpu_baseline": cpu}))
 
 
 def bench_lm(args, dev):
@@ -273,6 +413,7 @@ def bench_lm(args, dev):
         tokens = bt
         workload = "byte LM recurrent decode step (HIP graph), 12 layers d_model 512, batch 256"
         extra = {}
+    extra["timing"] = dict(LAST_TIMING)
     rec = {
         "metric": ("byte LM prefill tokens/s (config 5), 1 GPU" if args.workload == "c5"
                    else "byte LM decode tokens/s (config 5, one step at batch 256), 1 GPU"),
@@ -292,8 +433,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c2bf16", "c4", "c3", "c4s4", "c4s4exact", "c4s4d", "c5", "c5dec",
-                             "copy"],
+                    choices=["c1", "c2", "c2bf16", "c4", "c3", "c4s4", "c4s4exact", "c4s4d", "c5",
+                             "c5dec", "copy"],
                     help="copy = plain device copy of 512 MiB (HBM ceiling and counter calibration)")
     ap.add_argument("--variant", type=int, default=0, help="scan kernel variant (hx_set_scan_variant)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -311,6 +452,9 @@ def main():
     if args.variant:
         ssm.set_scan_variant(args.variant)
 
+    if args.workload == "c1":
+        bench_c1(args, dev)
+        return
     if args.workload == "copy":
         n = 512 * 2**20 // 4
         src = [torch.randn(n, device=dev) for _ in range(2)]
@@ -350,6 +494,7 @@ def main():
         ssm.selective_scan_fwd(**sets[i], out=outs[i])
 
     ms = time_steps(step, nsets, args.steps, args.warmup)
+    timing = dict(LAST_TIMING)
     tokens = bt * L
     nbytes = scan_bytes(bt, L, dim, N, es)
     achieved = nbytes / (ms * 1e-3) / 1e9
@@ -392,6 +537,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "algorithmic_bytes": nbytes, "kernel_ms": ms},
+        "timing": timing,
         "cpu_baseline": cpu,
         "parity_max_rel_err": parity,
     }

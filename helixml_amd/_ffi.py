@@ -87,10 +87,16 @@ SIGNATURES = {
     "hx_device_info": [_int, ctypes.POINTER(_int), ctypes.POINTER(_sz)],
     "hx_last_error": [],
     "hx_selective_scan_fwd": [_i64, _i64, _i64, _i64, _int, _int] + [_p] * 11 + [_p],
+    "hx_selective_scan_workspace_size": [_i64, _i64, _i64, _i64, _int],
+    "hx_selective_scan_fwd_ws": [_i64, _i64, _i64, _i64, _int, _int] + [_p] * 11 + [_p, _sz, _p],
     "hx_selective_state_update": [_i64, _i64, _i64, _int, _int] + [_p] * 10 + [_p],
-    "hx_s4_ref_fwd": [_i64, _i64, _i64, _f] + [_p] * 8 + [_p],
-    "hx_s4_ref_fwd_parallel": [_i64, _i64, _i64, _f] + [_p] * 8 + [_p],
-    "hx_s4d_complex_fwd": [_i64, _i64, _i64, _i64] + [_p] * 10 + [_p],
+    "hx_s4_discretize": [_i64, _f, _p, _p, _p],
+    "hx_s4_ref_workspace_size": [_i64, _i64, _i64],
+    "hx_s4_ref_fwd": [_i64, _i64, _i64, _f] + [_p] * 7 + [_p, _sz, _p],
+    "hx_s4_ref_parallel_workspace_size": [_i64, _i64, _i64],
+    "hx_s4_ref_fwd_parallel": [_i64, _i64, _i64, _f] + [_p] * 7 + [_p, _sz, _p],
+    "hx_s4d_workspace_size": [_i64, _i64, _i64, _i64],
+    "hx_s4d_complex_fwd": [_i64, _i64, _i64, _i64] + [_p] * 10 + [_p, _sz, _p],
     "hx_linear_f32": [_i64, _i64, _i64, _p, _p, _p, _int, _p, _p],
     "hx_matmul_f32": [_i64, _i64, _i64, _p, _p, _p, _p],
     "hx_gemm_bf16": [_i64, _i64, _i64, _p, _i64, _p, _i64, _p, _int, _int,

@@ -415,7 +415,7 @@ template <bool VEC>
 __global__ __launch_bounds__(64 * kPWaves) void s4p_proj_kernel(int64_t M, int64_t L,
                                                        const float* __restrict__ x,
                                                        const float* __restrict__ BdT,
-                                                       const float* __restrict__ a,
+                                                       const float* __restrict__ a, int64_t N,
                                                        float* __restrict__ H,
                                                        float* __restrict__ E) {
     __shared__ __attribute__((aligned(16))) float part[kPWaves][16][kPChunk];
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(64 * kPWaves) void s4p_proj_kernel(int64_t M, int64
     // scans steps [16q, 16q + 16)
     const bool scanner = tid < 256;
     const int n = tid & 15, q = (tid >> 4) & 15;
-    const float an = a[n];
+    const float an = n < N ? a[n] : 0.0f;  // states past N: zero decay on zero input
     float u[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -515,13 +515,11 @@ __global__ __launch_bounds__(64 * kPWaves) void s4p_proj_kernel(int64_t M, int64
     }
 }
 
-// Discretisation on the device: a[n] = exp(dt*a_real[n]) * cos(dt*a_imag[n]); BdT[m][n] =
-// B[n][m]*dt (n < N, else 0); pw[j][n] = a[n]^(j+1) for j < kPChunk.
+// BdT[m][n] = B[n][m]*dt (n < N, else 0); pw[j][n] = a[n]^(j+1) for j < kPChunk, where a is
+// the discretisation the caller computed with the reference's libm expf/cosf (hx_s4_discretize).
 __global__ __launch_bounds__(256) void s4p_setup_kernel(int64_t M, int64_t N, float dt,
-                                                        const float* __restrict__ a_real,
-                                                        const float* __restrict__ a_imag,
+                                                        const float* __restrict__ a,
                                                         const float* __restrict__ B,
-                                                        float* __restrict__ a,
                                                         float* __restrict__ BdT,
                                                         float* __restrict__ pw) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -530,14 +528,10 @@ __global__ __launch_bounds__(256) void s4p_setup_kernel(int64_t M, int64_t N, fl
         BdT[i] = n < N ? B[n * M + m] * dt : 0.0f;
     }
     if (blockIdx.x == 0 && threadIdx.x < 16) {
-        // a in double from the reference's f32 products tr = a_real*dt, ti = a_imag*dt, rounded
-        // once; the powers are those of the rounded a, formed in double and rounded once, so the
-        // carry applies exactly the decay the chunk scans apply step by step.
+        // the powers are those of the rounded a, formed in double and rounded once, so the carry
+        // applies exactly the decay the chunk scans apply step by step
         const int n = threadIdx.x;
-        const float tr = n < N ? a_real[n] * dt : 0.0f;
-        const float ti = n < N ? a_imag[n] * dt : 0.0f;
-        const float an = n < N ? (float)(exp((double)tr) * cos((double)ti)) : 0.0f;
-        a[n] = an;
+        const float an = n < N ? a[n] : 0.0f;
         double p = an;
         for (int j = 0; j < kPChunk; ++j) {
             pw[j * 16 + n] = (float)p;
@@ -655,10 +649,43 @@ __global__ __launch_bounds__(256) void s4p_output_kernel(int64_t M, int64_t L, i
 }  // namespace
 }  // namespace hx
 
+namespace hx {
+namespace {
+// Workspace layout of the reference-mode path: Bd [N][M] | H [L][N], each 256-byte aligned.
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+size_t s4_ref_ws_bytes(int64_t M, int64_t N, int64_t L) {
+    return align256((size_t)N * M * sizeof(float)) + align256((size_t)L * N * sizeof(float));
+}
+}  // namespace
+}  // namespace hx
+
+extern "C" int hx_s4_discretize(int64_t dstate, float dt, const float* a_real, const float* a_imag,
+                                float* a) {
+    using namespace hx;
+    HX_REQUIRE(dstate >= 0 && dstate <= kMaxState, HX_ERR_UNSUPPORTED,
+               "s4_discretize: dstate=%lld not supported (0..%d)", (long long)dstate, kMaxState);
+    if (dstate == 0) return HX_OK;
+    HX_REQUIRE(a_real && a_imag && a, HX_ERR_INVALID_INPUT,
+               "s4_discretize: a_real, a_imag and a must be non-NULL host pointers");
+    // discretize(dt) (ssm.rs:113-120): tr = a_real*dt; ti = a_imag*dt (mul_scalar, each rounded
+    // to f32), a = exp(tr) * cos(ti) with the libm the reference's f32::exp / f32::cos call
+    for (int64_t n = 0; n < dstate; ++n) {
+        volatile float tr = a_real[n] * dt;
+        volatile float ti = a_imag[n] * dt;
+        a[n] = expf(tr) * cosf(ti);
+    }
+    return HX_OK;
+}
+
+extern "C" size_t hx_s4_ref_workspace_size(int64_t d_model, int64_t dstate, int64_t seqlen) {
+    if (d_model <= 0 || dstate <= 0 || seqlen <= 0) return 0;
+    return hx::s4_ref_ws_bytes(d_model, dstate, seqlen);
+}
+
 extern "C" int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, float dt,
-                             const float* x, const float* a_real, const float* a_imag,
-                             const float* B, const float* C, const float* D, const float* gate,
-                             float* y, void* stream) {
+                             const float* x, const float* a, const float* B, const float* C,
+                             const float* D, const float* gate, float* y, void* workspace,
+                             size_t workspace_bytes, void* stream) {
     using namespace hx;
     HX_REQUIRE(d_model >= 0 && seqlen >= 0, HX_ERR_INVALID_DIMENSION,
                "s4_ref: negative size (d_model=%lld seqlen=%lld)", (long long)d_model,
@@ -666,63 +693,37 @@ extern "C" int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, fl
     HX_REQUIRE(dstate >= 1 && dstate <= kMaxState, HX_ERR_UNSUPPORTED,
                "s4_ref: dstate=%lld not supported (1..%d)", (long long)dstate, kMaxState);
     if (d_model == 0 || seqlen == 0) return HX_OK;
-    HX_REQUIRE(x && a_real && a_imag && B && C && D && y, HX_ERR_INVALID_INPUT,
-               "s4_ref: x, a_real, a_imag, B, C, D and y must be non-NULL");
+    HX_REQUIRE(x && a && B && C && D && y, HX_ERR_INVALID_INPUT,
+               "s4_ref: x, a, B, C, D and y must be non-NULL");
     HX_REQUIRE((seqlen + kTileT - 1) / kTileT <= 65535, HX_ERR_UNSUPPORTED,
                "s4_ref: seqlen %lld too long for one launch", (long long)seqlen);
+    const size_t need = s4_ref_ws_bytes(d_model, dstate, seqlen);
+    HX_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256), HX_ERR_INVALID_INPUT,
+               "s4_ref: workspace of %zu bytes (256-byte aligned) needed, %zu given", need,
+               workspace ? workspace_bytes : (size_t)0);
     hipStream_t s = as_stream(stream);
-
-    // discretize(dt) (ssm.rs:113-120) on the host with libm, exactly as the reference:
-    // tr = a_real*dt; ti = a_imag*dt; a = expf(tr) * cosf(ti). This synchronises with `stream`
-    // (the parameters are read back), which reference mode accepts for bit-faithfulness.
-    float ar[kMaxState], ai[kMaxState], a[kMaxState];
-    HX_HIP_CHECK(hipStreamSynchronize(s));
-    HX_HIP_CHECK(hipMemcpy(ar, a_real, dstate * sizeof(float), hipMemcpyDeviceToHost));
-    HX_HIP_CHECK(hipMemcpy(ai, a_imag, dstate * sizeof(float), hipMemcpyDeviceToHost));
-    for (int64_t n = 0; n < dstate; ++n) {
-        volatile float tr = ar[n] * dt;
-        volatile float ti = ai[n] * dt;
-        a[n] = expf(tr) * cosf(ti);
-    }
-
-    // scratch: a [N] | Bd [N*M] | H [L*N]
-    const size_t n_a = 64, n_bd = (size_t)dstate * d_model, n_h = (size_t)seqlen * dstate;
-    float* scratch = nullptr;
-    HX_HIP_CHECK(hipMallocAsync((void**)&scratch, (n_a + n_bd + n_h) * sizeof(float), s));
-    float* a_dev = scratch;
-    float* Bd = scratch + n_a;
-    float* H = Bd + n_bd;
-    int rc = HX_OK;
-    hipError_t e = hipMemcpyAsync(a_dev, a, dstate * sizeof(float), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);  // `a` is a stack buffer
-    if (e != hipSuccess) {
-        rc = set_error(HX_ERR_BACKEND, "s4_ref: upload of discretised A failed: %s",
-                       hipGetErrorString(e));
-    } else {
-        hipLaunchKernelGGL(s4_scale_kernel, dim3((unsigned)((n_bd + 255) / 256)), dim3(256), 0, s,
-                           (int64_t)n_bd, dt, B, Bd);
-        dim3 g1((unsigned)((seqlen + 255) / 256));
-        if (dstate <= 16)
-            hipLaunchKernelGGL(s4_input_proj_kernel<16>, g1, dim3(256), 0, s, d_model, seqlen,
-                               dstate, x, Bd, H);
-        else
-            hipLaunchKernelGGL(s4_input_proj_kernel<kMaxState>, g1, dim3(256), 0, s, d_model,
-                               seqlen, dstate, x, Bd, H);
-        hipLaunchKernelGGL(s4_scan_seq_kernel, dim3(1), dim3(64), 0, s, seqlen, dstate, a_dev, H);
-        dim3 g3((unsigned)((d_model + kTileM - 1) / kTileM),
-                (unsigned)((seqlen + kTileT - 1) / kTileT));
-        if (dstate <= 16)
-            hipLaunchKernelGGL(s4_output_kernel<16>, g3, dim3(256), 0, s, d_model, seqlen, dstate,
-                               x, H, C, D, gate, y);
-        else
-            hipLaunchKernelGGL(s4_output_kernel<kMaxState>, g3, dim3(256), 0, s, d_model, seqlen,
-                               dstate, x, H, C, D, gate, y);
-        hipError_t le = hipGetLastError();
-        if (le != hipSuccess)
-            rc = set_error(HX_ERR_BACKEND, "s4_ref: launch failed: %s", hipGetErrorString(le));
-    }
-    (void)hipFreeAsync(scratch, s);
-    return rc;
+    float* Bd = (float*)workspace;
+    float* H = (float*)((char*)workspace + align256((size_t)dstate * d_model * sizeof(float)));
+    const size_t n_bd = (size_t)dstate * d_model;
+    hipLaunchKernelGGL(s4_scale_kernel, dim3((unsigned)((n_bd + 255) / 256)), dim3(256), 0, s,
+                       (int64_t)n_bd, dt, B, Bd);
+    dim3 g1((unsigned)((seqlen + 255) / 256));
+    if (dstate <= 16)
+        hipLaunchKernelGGL(s4_input_proj_kernel<16>, g1, dim3(256), 0, s, d_model, seqlen, dstate,
+                           x, Bd, H);
+    else
+        hipLaunchKernelGGL(s4_input_proj_kernel<kMaxState>, g1, dim3(256), 0, s, d_model, seqlen,
+                           dstate, x, Bd, H);
+    hipLaunchKernelGGL(s4_scan_seq_kernel, dim3(1), dim3(64), 0, s, seqlen, dstate, a, H);
+    dim3 g3((unsigned)((d_model + kTileM - 1) / kTileM), (unsigned)((seqlen + kTileT - 1) / kTileT));
+    if (dstate <= 16)
+        hipLaunchKernelGGL(s4_output_kernel<16>, g3, dim3(256), 0, s, d_model, seqlen, dstate, x,
+                           H, C, D, gate, y);
+    else
+        hipLaunchKernelGGL(s4_output_kernel<kMaxState>, g3, dim3(256), 0, s, d_model, seqlen,
+                           dstate, x, H, C, D, gate, y);
+    HX_LAUNCH_CHECK();
+    return HX_OK;
 }
 
 namespace hx {
@@ -732,27 +733,41 @@ namespace {
 thread_local int g_s4d_path = 0;  // per calling thread (hx_set_s4d_path)
 thread_local int g_s4d_segments = 0;  // per calling thread (hx_set_s4d_segments)
 
-int launch_s4d_wave(int64_t Bt, int64_t L, int64_t Dm, const float* x, const float* dt,
-                    const float* a_re, const float* a_im, const float* B_re, const float* B_im,
-                    const float* C_re, const float* C_im, const float* D, float* y, hipStream_t s) {
-    const int ntiles = (int)((Dm + 63) / 64);
-    const int64_t pairs = (int64_t)ntiles * Bt;
+// Time segments of the S4D wave path: about 2048 waves (two per SIMD), segments of at least 512
+// steps, 16-step aligned. Returns the segment count and sets seg_len.
+int64_t s4d_segments(int64_t Bt, int64_t L, int64_t Dm, int64_t* seg_len_out) {
+    const int64_t pairs = (int64_t)((Dm + 63) / 64) * Bt;
     int64_t nseg = g_s4d_segments;
     if (nseg <= 0) {
-        // about 2048 waves (two per SIMD); segments of at least 512 steps
         nseg = (512 + pairs - 1) / pairs;
         const int64_t cap = L / 512 > 1 ? L / 512 : 1;
         nseg = nseg < cap ? nseg : cap;
     }
     int64_t seg_len = (L + nseg - 1) / nseg;
     seg_len = (seg_len + 15) / 16 * 16;
-    nseg = (L + seg_len - 1) / seg_len;
+    *seg_len_out = seg_len;
+    return (L + seg_len - 1) / seg_len;
+}
+bool s4d_wave_ok(int64_t dim, int64_t dstate, const float* x, const float* y) {
+    return dstate == 16 && dim % 4 == 0 && aligned(x, 16) && aligned(y, 16) && g_s4d_path != 1;
+}
+// Segment end and entry states, [nseg][B][D][16] complex each.
+size_t s4d_ws_bytes(int64_t Bt, int64_t Dm, int64_t nseg) {
+    return nseg > 1 ? 2 * (size_t)nseg * Bt * Dm * 16 * 2 * sizeof(float) : 0;
+}
+
+int launch_s4d_wave(int64_t Bt, int64_t L, int64_t Dm, const float* x, const float* dt,
+                    const float* a_re, const float* a_im, const float* B_re, const float* B_im,
+                    const float* C_re, const float* C_im, const float* D, float* y,
+                    float* scratch, hipStream_t s) {
+    const int ntiles = (int)((Dm + 63) / 64);
+    const int64_t pairs = (int64_t)ntiles * Bt;
+    int64_t seg_len = 0;
+    const int64_t nseg = s4d_segments(Bt, L, Dm, &seg_len);
     HX_REQUIRE(pairs * nseg <= 0x7fffffff, HX_ERR_UNSUPPORTED, "s4d_complex: grid too large");
     S4dSeg sg{seg_len, (int)nseg, nullptr, nullptr};
-    float* scratch = nullptr;
     if (nseg > 1) {
         const size_t per = (size_t)nseg * Bt * Dm * 16 * 2;
-        HX_HIP_CHECK(hipMallocAsync((void**)&scratch, 2 * per * sizeof(float), s));
         sg.seg_end = scratch;
         sg.seg_init = scratch + per;
         hipLaunchKernelGGL(s4d_wave_kernel<true>, dim3((unsigned)(pairs * nseg)), dim3(256), 0, s, L,
@@ -763,30 +778,38 @@ int launch_s4d_wave(int64_t Bt, int64_t L, int64_t Dm, const float* x, const flo
     }
     hipLaunchKernelGGL(s4d_wave_kernel<false>, dim3((unsigned)(pairs * nseg)), dim3(256), 0, s, L,
                        Dm, ntiles, Bt, x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D, y, sg);
-    hipError_t le = hipGetLastError();
-    if (scratch) (void)hipFreeAsync(scratch, s);
-    if (le != hipSuccess)
-        return set_error(HX_ERR_BACKEND, "s4d_complex: launch failed: %s", hipGetErrorString(le));
+    HX_LAUNCH_CHECK();
     return HX_OK;
 }
 }  // namespace
 }  // namespace hx
 
 extern "C" int hx_set_s4d_path(int path) {
+    HX_REQUIRE(path == 0 || path == 1, HX_ERR_INVALID_INPUT, "hx_set_s4d_path: %d is not 0 or 1", path);
     hx::g_s4d_path = path;
     return HX_OK;
 }
 
 extern "C" int hx_set_s4d_segments(int nseg) {
+    HX_REQUIRE(nseg >= 0 && nseg <= 4096, HX_ERR_INVALID_INPUT,
+               "hx_set_s4d_segments: %d outside 0..4096", nseg);
     hx::g_s4d_segments = nseg;
     return HX_OK;
+}
+
+extern "C" size_t hx_s4d_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate) {
+    using namespace hx;
+    if (batch <= 0 || seqlen <= 0 || dim <= 0 || dstate != 16 || dim % 4 != 0 || g_s4d_path == 1)
+        return 0;
+    int64_t seg_len = 0;
+    return s4d_ws_bytes(batch, dim, s4d_segments(batch, seqlen, dim, &seg_len));
 }
 
 extern "C" int hx_s4d_complex_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
                                   const float* x, const float* dt, const float* a_re,
                                   const float* a_im, const float* B_re, const float* B_im,
                                   const float* C_re, const float* C_im, const float* D, float* y,
-                                  void* stream) {
+                                  void* workspace, size_t workspace_bytes, void* stream) {
     using namespace hx;
     HX_REQUIRE(batch >= 0 && seqlen >= 0 && dim >= 0, HX_ERR_INVALID_DIMENSION,
                "s4d_complex: negative size");
@@ -796,10 +819,16 @@ extern "C" int hx_s4d_complex_fwd(int64_t batch, int64_t seqlen, int64_t dim, in
     HX_REQUIRE(x && dt && a_re && a_im && B_re && B_im && C_re && C_im && y, HX_ERR_INVALID_INPUT,
                "s4d_complex: a required pointer is NULL");
     hipStream_t s = as_stream(stream);
-    const bool wave_ok = dstate == 16 && dim % 4 == 0 && aligned(x, 16) && aligned(y, 16) &&
-                         g_s4d_path != 1;
-    if (wave_ok) return launch_s4d_wave(batch, seqlen, dim, x, dt, a_re, a_im, B_re, B_im, C_re,
-                                        C_im, D, y, s);
+    if (s4d_wave_ok(dim, dstate, x, y)) {
+        int64_t seg_len = 0;
+        const size_t need = s4d_ws_bytes(batch, dim, s4d_segments(batch, seqlen, dim, &seg_len));
+        HX_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
+                   HX_ERR_INVALID_INPUT,
+                   "s4d_complex: workspace of %zu bytes (16-byte aligned) needed, %zu given "
+                   "(hx_s4d_workspace_size)", need, workspace ? workspace_bytes : (size_t)0);
+        return launch_s4d_wave(batch, seqlen, dim, x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D, y,
+                               (float*)workspace, s);
+    }
     const int64_t total = batch * dim;
     dim3 grid((unsigned)((total + 127) / 128));
     if (dstate <= 16)
@@ -812,10 +841,27 @@ extern "C" int hx_s4d_complex_fwd(int64_t batch, int64_t seqlen, int64_t dim, in
     return HX_OK;
 }
 
+namespace hx {
+namespace {
+// Workspace of the time-parallel path: pw [kPChunk][16] | BdT [M][16] | H [L][16] | E [nch][16] |
+// carry [nch][16], each 256-byte aligned.
+size_t s4p_ws_bytes(int64_t M, int64_t L) {
+    const size_t nch = (size_t)((L + kPChunk - 1) / kPChunk);
+    return align256((size_t)kPChunk * 16 * 4) + align256((size_t)M * 16 * 4) +
+           align256((size_t)L * 16 * 4) + 2 * align256(nch * 16 * 4);
+}
+}  // namespace
+}  // namespace hx
+
+extern "C" size_t hx_s4_ref_parallel_workspace_size(int64_t d_model, int64_t dstate, int64_t seqlen) {
+    if (d_model <= 0 || dstate <= 0 || seqlen <= 0) return 0;
+    return hx::s4p_ws_bytes(d_model, seqlen);
+}
+
 extern "C" int hx_s4_ref_fwd_parallel(int64_t d_model, int64_t dstate, int64_t seqlen, float dt,
-                                      const float* x, const float* a_real, const float* a_imag,
-                                      const float* B, const float* C, const float* D,
-                                      const float* gate, float* y, void* stream) {
+                                      const float* x, const float* a, const float* B,
+                                      const float* C, const float* D, const float* gate, float* y,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
     using namespace hx;
     HX_REQUIRE(d_model >= 0 && seqlen >= 0, HX_ERR_INVALID_DIMENSION,
                "s4_ref_parallel: negative size (d_model=%lld seqlen=%lld)", (long long)d_model,
@@ -823,34 +869,37 @@ extern "C" int hx_s4_ref_fwd_parallel(int64_t d_model, int64_t dstate, int64_t s
     HX_REQUIRE(dstate >= 1 && dstate <= 16, HX_ERR_UNSUPPORTED,
                "s4_ref_parallel: dstate=%lld not supported (1..16)", (long long)dstate);
     if (d_model == 0 || seqlen == 0) return HX_OK;
-    HX_REQUIRE(x && a_real && a_imag && B && C && D && y, HX_ERR_INVALID_INPUT,
-               "s4_ref_parallel: x, a_real, a_imag, B, C, D and y must be non-NULL");
+    HX_REQUIRE(x && a && B && C && D && y, HX_ERR_INVALID_INPUT,
+               "s4_ref_parallel: x, a, B, C, D and y must be non-NULL");
     HX_REQUIRE((seqlen + kOTile - 1) / kOTile <= 65535, HX_ERR_UNSUPPORTED,
                "s4_ref_parallel: seqlen %lld too long for one launch", (long long)seqlen);
+    const size_t need = s4p_ws_bytes(d_model, seqlen);
+    HX_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256), HX_ERR_INVALID_INPUT,
+               "s4_ref_parallel: workspace of %zu bytes (256-byte aligned) needed, %zu given", need,
+               workspace ? workspace_bytes : (size_t)0);
     hipStream_t s = as_stream(stream);
     const int64_t nch = (seqlen + kPChunk - 1) / kPChunk;
-    // scratch: a [16] | pw [kPChunk*16] | BdT [M*16] | H [L*16] | E [nch*16] | carry [nch*16]
-    const size_t n_a = 64, n_pw = kPChunk * 16, n_bd = (size_t)d_model * 16,
-                 n_h = (size_t)seqlen * 16, n_e = (size_t)nch * 16;
-    float* scratch = nullptr;
-    HX_HIP_CHECK(hipMallocAsync((void**)&scratch, (n_a + n_pw + n_bd + n_h + 2 * n_e) * sizeof(float), s));
-    float* a_dev = scratch;
-    float* pw = a_dev + n_a;
-    float* BdT = pw + n_pw;
-    float* H = BdT + n_bd;
-    float* E = H + n_h;
-    float* carry = E + n_e;
-    hipLaunchKernelGGL(s4p_setup_kernel, dim3((unsigned)((n_bd + 255) / 256)), dim3(256), 0, s,
-                       d_model, dstate, dt, a_real, a_imag, B, a_dev, BdT, pw);
+    char* w = (char*)workspace;
+    float* pw = (float*)w;
+    w += align256((size_t)kPChunk * 16 * 4);
+    float* BdT = (float*)w;
+    w += align256((size_t)d_model * 16 * 4);
+    float* H = (float*)w;
+    w += align256((size_t)seqlen * 16 * 4);
+    float* E = (float*)w;
+    w += align256((size_t)nch * 16 * 4);
+    float* carry = (float*)w;
+    hipLaunchKernelGGL(s4p_setup_kernel, dim3((unsigned)((d_model * 16 + 255) / 256)), dim3(256), 0, s,
+                       d_model, dstate, dt, a, B, BdT, pw);
     const bool vec = seqlen % 4 == 0 && aligned(x, 16);
     const bool vec_out = vec && aligned(C, 16);
     dim3 g1((unsigned)nch);
     if (vec)
         hipLaunchKernelGGL(s4p_proj_kernel<true>, g1, dim3(64 * kPWaves), 0, s, d_model, seqlen, x,
-                           BdT, a_dev, H, E);
+                           BdT, a, dstate, H, E);
     else
         hipLaunchKernelGGL(s4p_proj_kernel<false>, g1, dim3(64 * kPWaves), 0, s, d_model, seqlen, x,
-                           BdT, a_dev, H, E);
+                           BdT, a, dstate, H, E);
     hipLaunchKernelGGL(s4p_carry_kernel, dim3(1), dim3(256), 0, s, nch, pw, E, carry);
     dim3 g3((unsigned)((d_model + kOTile - 1) / kOTile), (unsigned)((seqlen + kOTile - 1) / kOTile));
     if (vec_out)
@@ -859,9 +908,6 @@ extern "C" int hx_s4_ref_fwd_parallel(int64_t d_model, int64_t dstate, int64_t s
     else
         hipLaunchKernelGGL(s4p_output_kernel<false>, g3, dim3(256), 0, s, d_model, seqlen, dstate, x,
                            H, carry, pw, C, D, gate, y);
-    hipError_t le = hipGetLastError();
-    (void)hipFreeAsync(scratch, s);
-    if (le != hipSuccess)
-        return set_error(HX_ERR_BACKEND, "s4_ref_parallel: launch failed: %s", hipGetErrorString(le));
+    HX_LAUNCH_CHECK();
     return HX_OK;
 }

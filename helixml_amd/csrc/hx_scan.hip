@@ -1161,7 +1161,35 @@ struct ScanArgs {
     const float* init_state;
     float* last_state;
     hipStream_t stream;
+    void* ws = nullptr;      // caller workspace for the segmented long-sequence path (nullable:
+    size_t ws_bytes = 0;     // without one the sequence is never segmented)
 };
+
+// Time segments of the wave path: only when the (batch, 64-channel tile) pairs alone cannot fill
+// the GPU (about 512 blocks, segments of at least 1024 steps), or as forced by
+// hx_set_scan_segments; 16-step aligned. Returns the count and sets *seg_len.
+int64_t scan_segments(const ScanArgs& a, int64_t* seg_len_out) {
+    const int64_t pairs = ((a.Dm + 63) / 64) * a.Bt;
+    int64_t nseg = 1;
+    if (g_scan_segments > 0) {
+        nseg = g_scan_segments;
+    } else if (pairs < 256 && a.L >= 4096) {
+        const int64_t want = (512 + pairs - 1) / pairs;
+        const int64_t cap = a.L / 1024;
+        nseg = want < cap ? want : cap;
+        if (nseg < 1) nseg = 1;
+    }
+    int64_t seg_len = (a.L + nseg - 1) / nseg;
+    seg_len = (seg_len + 15) / 16 * 16;
+    *seg_len_out = seg_len;
+    return (a.L + seg_len - 1) / seg_len;
+}
+// Scratch of a segmented scan: end states and entry states [nseg][B][D][16], total dt [nseg][B][D].
+size_t scan_seg_bytes(int64_t Bt, int64_t Dm, int64_t nseg) {
+    if (nseg <= 1) return 0;
+    const size_t per = (size_t)Bt * Dm * 16;
+    return (size_t)nseg * (2 * per + (size_t)Bt * Dm) * sizeof(float);
+}
 
 template <typename T, int W, int TCH, bool HAS_Z, bool SP>
 int launch_fast(const ScanArgs& a) {
@@ -1209,42 +1237,23 @@ int launch_wave_one(const ScanArgs& a, const WaveSeg& sg) {
 
 template <typename T, int PF, bool HAS_Z, bool SP, int VER>
 int launch_wave(const ScanArgs& a) {
-    // Segment the sequence when the (batch, 64-channel tile) pairs alone cannot fill the GPU.
-    const int64_t ntiles = (a.Dm + 63) / 64;
-    const int64_t pairs = ntiles * a.Bt;
-    int nseg = 1;
-    if (g_scan_segments > 0) {
-        nseg = g_scan_segments;
-    } else if (pairs < 256 && a.L >= 4096) {
-        const int64_t want = (512 + pairs - 1) / pairs;          // ~512 blocks
-        const int64_t cap = a.L / 1024;                           // segments >= 1024 steps
-        nseg = (int)(want < cap ? want : cap);
-        if (nseg < 1) nseg = 1;
-    }
-    int64_t seg_len = (a.L + nseg - 1) / nseg;
-    seg_len = (seg_len + 15) / 16 * 16;
-    nseg = (int)((a.L + seg_len - 1) / seg_len);
+    int64_t seg_len = a.L;
+    const int64_t nseg = a.ws ? scan_segments(a, &seg_len) : 1;
     if (nseg <= 1) return launch_wave_one<T, PF, HAS_Z, SP, false, VER>(a, WaveSeg{a.L, 1, nullptr, nullptr, nullptr});
-
+    const size_t need = scan_seg_bytes(a.Bt, a.Dm, nseg);
+    HX_REQUIRE(a.ws_bytes >= need && aligned(a.ws, 16), HX_ERR_INVALID_INPUT,
+               "selective scan: workspace of %zu bytes (16-byte aligned) needed, %zu given "
+               "(hx_selective_scan_workspace_size)", need, a.ws_bytes);
     const size_t per = (size_t)a.Bt * a.Dm * 16;
-    const size_t nfloat = (size_t)nseg * (2 * per + (size_t)a.Bt * a.Dm);
-    float* scratch = nullptr;
-    HX_HIP_CHECK(hipMallocAsync((void**)&scratch, nfloat * sizeof(float), a.stream));
-    float* hend = scratch;
+    float* hend = (float*)a.ws;
     float* seg_init = hend + (size_t)nseg * per;
     float* sumdt = seg_init + (size_t)nseg * per;
-    int rc = launch_wave_one<T, PF, false, SP, true, VER>(a, WaveSeg{seg_len, nseg, nullptr, hend, sumdt});
-    if (rc == HX_OK) {
-        hipLaunchKernelGGL(scan_seg_carry_kernel, dim3((unsigned)((per + 255) / 256)), dim3(256), 0,
-                           a.stream, a.Bt, a.Dm, nseg, a.A, a.init_state, hend, sumdt, seg_init);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess)
-            rc = set_error(HX_ERR_BACKEND, "scan carry launch failed: %s", hipGetErrorString(e));
-    }
-    if (rc == HX_OK)
-        rc = launch_wave_one<T, PF, HAS_Z, SP, false, VER>(a, WaveSeg{seg_len, nseg, seg_init, nullptr, nullptr});
-    (void)hipFreeAsync(scratch, a.stream);
-    return rc;
+    int rc = launch_wave_one<T, PF, false, SP, true, VER>(a, WaveSeg{seg_len, (int)nseg, nullptr, hend, sumdt});
+    if (rc != HX_OK) return rc;
+    hipLaunchKernelGGL(scan_seg_carry_kernel, dim3((unsigned)((per + 255) / 256)), dim3(256), 0,
+                       a.stream, a.Bt, a.Dm, (int)nseg, a.A, a.init_state, hend, sumdt, seg_init);
+    HX_LAUNCH_CHECK();
+    return launch_wave_one<T, PF, HAS_Z, SP, false, VER>(a, WaveSeg{seg_len, (int)nseg, seg_init, nullptr, nullptr});
 }
 
 template <typename T, int PF, int VER = 1>
@@ -1395,6 +1404,17 @@ int run_scan(const ScanArgs& a) {
     return dispatch_fast<T, 8, 16>(a);
 }
 
+// Workspace bytes the dispatch of run_scan would use for these sizes (pointers assumed aligned;
+// a path that needs none leaves a given workspace unused).
+size_t scan_workspace_bytes(const ScanArgs& a, size_t es) {
+    const int v = g_scan_variant;
+    if (a.N != 16 || a.Dm % 4 != 0 || a.L <= 0 || a.Bt <= 0 || a.Dm <= 0) return 0;
+    if (v != 0 && v != 40 && v != 42) return 0;  // generic, fast and warp-specialised: none
+    if (v == 0 && ws_preferred(a, es)) return 0;
+    int64_t seg_len = 0;
+    return scan_seg_bytes(a.Bt, a.Dm, scan_segments(a, &seg_len));
+}
+
 int check_common(int64_t Bt, int64_t L, int64_t Dm, int64_t N, int dtype) {
     HX_REQUIRE(Bt >= 0 && L >= 0 && Dm >= 0, HX_ERR_INVALID_DIMENSION,
                "selective scan: negative size (batch=%lld seqlen=%lld dim=%lld)", (long long)Bt,
@@ -1411,13 +1431,14 @@ int check_common(int64_t Bt, int64_t L, int64_t Dm, int64_t N, int dtype) {
 }  // namespace
 }  // namespace hx
 
-extern "C" int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
-                                     int dtype, int delta_softplus, const void* u,
-                                     const void* delta, const float* A, const void* B,
-                                     const void* C, const float* D, const void* z,
-                                     const float* dt_bias, void* out, const float* init_state,
-                                     float* last_state, void* stream) {
-    if (int rc = hx::check_common(batch, seqlen, dim, dstate, dtype)) return rc;
+namespace hx {
+namespace {
+int scan_entry(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, int dtype,
+               int delta_softplus, const void* u, const void* delta, const float* A, const void* B,
+               const void* C, const float* D, const void* z, const float* dt_bias, void* out,
+               const float* init_state, float* last_state, void* workspace, size_t workspace_bytes,
+               void* stream) {
+    if (int rc = check_common(batch, seqlen, dim, dstate, dtype)) return rc;
     if (batch == 0 || dim == 0) return HX_OK;
     HX_REQUIRE(A != nullptr, HX_ERR_INVALID_INPUT, "selective scan: A is NULL");
     if (seqlen == 0) {
@@ -1426,19 +1447,51 @@ extern "C" int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim,
             const size_t bytes = (size_t)batch * dim * dstate * sizeof(float);
             if (init_state)
                 HX_HIP_CHECK(hipMemcpyAsync(last_state, init_state, bytes, hipMemcpyDeviceToDevice,
-                                            hx::as_stream(stream)));
+                                            as_stream(stream)));
             else
-                HX_HIP_CHECK(hipMemsetAsync(last_state, 0, bytes, hx::as_stream(stream)));
+                HX_HIP_CHECK(hipMemsetAsync(last_state, 0, bytes, as_stream(stream)));
         }
         return HX_OK;
     }
     HX_REQUIRE(u && delta && B && C && out, HX_ERR_INVALID_INPUT,
                "selective scan: u, delta, B, C and out must be non-NULL");
-    hx::ScanArgs a{batch, seqlen, dim,     dstate,     delta_softplus != 0,
-                   u,     delta,  A,       B,          C,
-                   D,     z,      dt_bias, out,        init_state,
-                   last_state,    hx::as_stream(stream)};
-    return dtype == HX_F32 ? hx::run_scan<float>(a) : hx::run_scan<uint16_t>(a);
+    ScanArgs a{batch, seqlen, dim, dstate, delta_softplus != 0, u, delta, A, B, C, D, z, dt_bias,
+               out, init_state, last_state, as_stream(stream), workspace, workspace_bytes};
+    return dtype == HX_F32 ? run_scan<float>(a) : run_scan<uint16_t>(a);
+}
+}  // namespace
+}  // namespace hx
+
+extern "C" int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
+                                     int dtype, int delta_softplus, const void* u,
+                                     const void* delta, const float* A, const void* B,
+                                     const void* C, const float* D, const void* z,
+                                     const float* dt_bias, void* out, const float* init_state,
+                                     float* last_state, void* stream) {
+    return hx::scan_entry(batch, seqlen, dim, dstate, dtype, delta_softplus, u, delta, A, B, C, D,
+                          z, dt_bias, out, init_state, last_state, nullptr, 0, stream);
+}
+
+extern "C" size_t hx_selective_scan_workspace_size(int64_t batch, int64_t seqlen, int64_t dim,
+                                                   int64_t dstate, int dtype) {
+    if (dtype != HX_F32 && dtype != HX_BF16) return 0;
+    hx::ScanArgs a{batch, seqlen, dim, dstate, 1, nullptr, nullptr, nullptr, nullptr, nullptr,
+                   nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    return hx::scan_workspace_bytes(a, dtype == HX_F32 ? 4 : 2);
+}
+
+extern "C" int hx_selective_scan_fwd_ws(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
+                                        int dtype, int delta_softplus, const void* u,
+                                        const void* delta, const float* A, const void* B,
+                                        const void* C, const float* D, const void* z,
+                                        const float* dt_bias, void* out, const float* init_state,
+                                        float* last_state, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+    HX_REQUIRE(workspace != nullptr || workspace_bytes == 0, HX_ERR_INVALID_INPUT,
+               "selective scan: NULL workspace with %zu bytes", workspace_bytes);
+    return hx::scan_entry(batch, seqlen, dim, dstate, dtype, delta_softplus, u, delta, A, B, C, D,
+                          z, dt_bias, out, init_state, last_state,
+                          workspace_bytes ? workspace : nullptr, workspace_bytes, stream);
 }
 
 extern "C" int hx_set_scan_variant(int variant) {

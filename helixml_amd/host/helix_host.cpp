@@ -268,11 +268,27 @@ HipTensor S4Block::forward_ssm(const HipTensor& x, const HipTensor* gate, bool p
     // y memory is [L, d_model]; the reference's shape field is [d_model, L] (CpuTensor::stack(., 1),
     // backend-cpu/src/lib.rs:277-296), or [d_model] when L == 1 (lib.rs:261-263)
     HipTensor y(L == 1 ? Shape({M}) : Shape({M, L}), Storage::F32, 0);
+    const float dt = 0.1f;  // ssm.rs:151
+    if (!a_disc_.defined() || a_src_[0] != A_real.data() || a_src_[1] != A_imag.data()) {
+        // discretize(dt) (ssm.rs:113-120) on the host with the reference's libm, once per
+        // parameter buffer rather than per forward
+        const std::vector<float> ar = A_real.to_host(), ai = A_imag.to_host();
+        std::vector<float> a(d_state_);
+        check(hx_s4_discretize((int64_t)d_state_, dt, ar.data(), ai.data(), a.data()),
+              "hx_s4_discretize");
+        a_disc_ = HipTensor::from_host(a, Shape({d_state_}), Storage::F32, 0);
+        a_src_[0] = A_real.data();
+        a_src_[1] = A_imag.data();
+    }
+    const size_t need = parallel ? hx_s4_ref_parallel_workspace_size((int64_t)M, (int64_t)d_state_, (int64_t)L)
+                                 : hx_s4_ref_workspace_size((int64_t)M, (int64_t)d_state_, (int64_t)L);
+    if (!workspace_.defined() || workspace_.nbytes() < need)
+        workspace_ = HipTensor(Shape({(need + 3) / 4}), Storage::F32, 0);
     auto fn = parallel ? hx_s4_ref_fwd_parallel : hx_s4_ref_fwd;
-    check(fn((int64_t)M, (int64_t)d_state_, (int64_t)L, 0.1f, (const float*)x.data(),
-             (const float*)A_real.data(), (const float*)A_imag.data(), (const float*)B.data(),
-             (const float*)C.data(), (const float*)D.data(),
-             gate ? (const float*)gate->data() : nullptr, (float*)y.data(), nullptr),
+    check(fn((int64_t)M, (int64_t)d_state_, (int64_t)L, dt, (const float*)x.data(),
+             (const float*)a_disc_.data(), (const float*)B.data(), (const float*)C.data(),
+             (const float*)D.data(), gate ? (const float*)gate->data() : nullptr, (float*)y.data(),
+             workspace_.data(), workspace_.nbytes(), nullptr),
           parallel ? "hx_s4_ref_fwd_parallel" : "hx_s4_ref_fwd");
     return y;
 }

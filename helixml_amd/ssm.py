@@ -13,6 +13,8 @@ from __future__ import annotations
 
 from typing import Optional
 
+import numpy as np
+
 import torch
 
 from . import _ffi
@@ -44,10 +46,18 @@ def _need(t: Optional[torch.Tensor], name: str, shape, dtype) -> None:
         raise InvalidInput(f"{name} must be contiguous")
 
 
+def selective_scan_workspace_size(batch, seqlen, dim, dstate, dtype=torch.float32):
+    """Bytes of scratch hx_selective_scan_fwd_ws needs (0 when the sequence is not segmented)."""
+    return int(_ffi.lib().hx_selective_scan_workspace_size(batch, seqlen, dim, dstate, _STORAGE[dtype]))
+
+
 def selective_scan_fwd(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_softplus=True,
-                       init_state=None, return_last_state=False, out=None, stream=None):
-    """Fused selective scan (hx_selective_scan_fwd). u, delta, z: [batch, L, dim];
-    B, C: [batch, L, dstate]; A: [dim, dstate] fp32; D, dt_bias: [dim] fp32."""
+                       init_state=None, return_last_state=False, out=None, workspace=None,
+                       stream=None):
+    """Fused selective scan (hx_selective_scan_fwd_ws). u, delta, z: [batch, L, dim];
+    B, C: [batch, L, dstate]; A: [dim, dstate] fp32; D, dt_bias: [dim] fp32. ``workspace``: a
+    uint8 device tensor of at least selective_scan_workspace_size(...) bytes for the segmented
+    long-sequence path; allocated here (by torch, outside the library) when not given."""
     if u.dim() != 3:
         raise ShapeMismatch(f"u: expected 3 dims [batch, seqlen, dim], got {list(u.shape)}")
     bt, L, dim = u.shape
@@ -70,9 +80,14 @@ def selective_scan_fwd(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_so
         out = torch.empty_like(u)
     _need(out, "out", (bt, L, dim), st)
     last = torch.empty((bt, dim, N), device=u.device, dtype=torch.float32) if return_last_state else None
-    _ffi.call("hx_selective_scan_fwd", bt, L, dim, N, _STORAGE[st], int(bool(delta_softplus)),
+    need = selective_scan_workspace_size(bt, L, dim, N, st)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, device=u.device, dtype=torch.uint8)
+    nbytes = workspace.numel() if (need and workspace is not None) else 0
+    _ffi.call("hx_selective_scan_fwd_ws", bt, L, dim, N, _STORAGE[st], int(bool(delta_softplus)),
               _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(dt_bias),
-              _ptr(out), _ptr(init_state), _ptr(last), _stream(stream))
+              _ptr(out), _ptr(init_state), _ptr(last), _ptr(workspace) if nbytes else None, nbytes,
+              _stream(stream))
     return (out, last) if return_last_state else out
 
 
@@ -101,11 +116,26 @@ def selective_state_update(state, u, delta, A, B, C, D=None, z=None, dt_bias=Non
     return out
 
 
-def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, parallel=False, stream=None):
+def s4_discretize(a_real, a_imag, dt=0.1, device=None):
+    """S4Block::discretize's decay (crates/nn/src/ssm.rs:113-120) through hx_s4_discretize:
+    a = expf(a_real*dt) * cosf(a_imag*dt) computed on the host with the reference's libm, returned
+    as a float32 device tensor. Reads a_real/a_imag back if they live on the device (one copy);
+    callers that run many forwards with the same parameters compute it once."""
+    ar = np.ascontiguousarray(a_real.detach().float().cpu().numpy())
+    ai = np.ascontiguousarray(a_imag.detach().float().cpu().numpy())
+    n = ar.shape[0]
+    a = np.empty(n, np.float32)
+    _ffi.call("hx_s4_discretize", n, float(dt), ar.ctypes.data, ai.ctypes.data, a.ctypes.data)
+    return torch.from_numpy(a).to(device if device is not None else a_real.device)
+
+
+def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, parallel=False, a=None,
+               workspace=None, stream=None):
     """Reference-mode S4Block::forward_ssm (crates/nn/src/ssm.rs:138-186) on x [d_model, L];
     returns y with memory [L, d_model] (the reference's shape field is [d_model, L]).
     parallel=False: bit-identical to CpuTensor (hx_s4_ref_fwd); parallel=True: time-parallel
-    chunked recurrence for long L, equal to rounding (hx_s4_ref_fwd_parallel, dstate <= 16)."""
+    chunked recurrence for long L, equal to rounding (hx_s4_ref_fwd_parallel, dstate <= 16).
+    ``a``: the discretised decay (s4_discretize(a_real, a_imag, dt)); computed here when None."""
     M, L = x.shape
     N = a_real.shape[0]
     f = torch.float32
@@ -116,9 +146,17 @@ def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, parallel=False, st
     _need(C, "C", (M, N), f)
     _need(D, "D", (M,), f)
     _need(gate, "gate", (M,), f)
+    if a is None:
+        a = s4_discretize(a_real, a_imag, dt, device=x.device)
+    _need(a, "a", (N,), f)
     y = torch.empty((L, M), device=x.device, dtype=f)
-    _ffi.call("hx_s4_ref_fwd_parallel" if parallel else "hx_s4_ref_fwd", M, N, L, float(dt), _ptr(x), _ptr(a_real), _ptr(a_imag), _ptr(B),
-              _ptr(C), _ptr(D), _ptr(gate), _ptr(y), _stream(stream))
+    size_fn = "hx_s4_ref_parallel_workspace_size" if parallel else "hx_s4_ref_workspace_size"
+    need = int(getattr(_ffi.lib(), size_fn)(M, N, L))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
+    _ffi.call("hx_s4_ref_fwd_parallel" if parallel else "hx_s4_ref_fwd", M, N, L, float(dt), _ptr(x),
+              _ptr(a), _ptr(B), _ptr(C), _ptr(D), _ptr(gate), _ptr(y), _ptr(workspace),
+              workspace.numel(), _stream(stream))
     return y
 
 
@@ -134,8 +172,11 @@ def s4d_complex_fwd(x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D=None, stream=No
         _need(t, name, (dim, N), f)
     _need(D, "D", (dim,), f)
     y = torch.empty_like(x)
+    need = int(_ffi.lib().hx_s4d_workspace_size(bt, L, dim, N))
+    ws = torch.empty(need, device=x.device, dtype=torch.uint8) if need else None
     _ffi.call("hx_s4d_complex_fwd", bt, L, dim, N, _ptr(x), _ptr(dt), _ptr(a_re), _ptr(a_im),
-              _ptr(B_re), _ptr(B_im), _ptr(C_re), _ptr(C_im), _ptr(D), _ptr(y), _stream(stream))
+              _ptr(B_re), _ptr(B_im), _ptr(C_re), _ptr(C_im), _ptr(D), _ptr(y), _ptr(ws), need,
+              _stream(stream))
     return y
 
 

@@ -212,6 +212,11 @@ public:
 
 private:
     size_t d_model_, d_state_;
+    // discretize(dt)'s decay (hx_s4_discretize, host libm) for the A_real / A_imag buffers it was
+    // computed from (parameters are immutable buffers, so their addresses identify them)
+    mutable HipTensor a_disc_;
+    mutable const void* a_src_[2] = {nullptr, nullptr};
+    mutable HipTensor workspace_;
 };
 
 // nn::ssm::MambaBlock::forward_mamba (ssm.rs:435-464): delta = X . delta_proj; y =

@@ -5,9 +5,9 @@
  * This is the drop-in boundary a Rust `crates/backend-hip` binds with an `extern "C"` block.
  * Every entry point takes plain pointers, sizes and
  * enums: no HIP, torch or C++ types cross it. Inputs and outputs are allocated by the caller
- * (hx_malloc, or any HIP allocation on the same device). Block and layer entry points take a
- * caller-owned workspace (sizes from the *_workspace_size functions); the long-sequence scan
- * and the S4 paths take stream-ordered scratch (hipMallocAsync / hipFreeAsync on `stream`).
+ * (hx_malloc, or any HIP allocation on the same device). No compute entry point allocates:
+ * scratch memory is a caller-owned workspace whose size the matching *_workspace_size function
+ * returns (the block and layer forwards, the long-sequence scan, the S4 paths).
  * A `stream` argument is a hipStream_t passed as void*
  * (NULL = the legacy default stream). All compute entry points are stream-ordered and
  * asynchronous; they validate shapes on the host before any launch and return a status code.
@@ -85,7 +85,8 @@ const char* hx_last_error(void);
  *   y     = sum_n C[b,t,n]*h[n] + D[d]*u
  *   out   = y * silu(z)                       (if z != NULL)
  * dtype selects the storage type of u, delta, z, B, C and out; A, D, dt_bias, state are fp32.
- * init_state (nullable) seeds h; last_state (nullable) receives h after the last step. */
+ * init_state (nullable) seeds h; last_state (nullable) receives h after the last step.
+ * Uses no scratch memory: a sequence is never cut into time segments here (see _ws below). */
 int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
                           int dtype, int delta_softplus,
                           const void* u, const void* delta, const float* A,
@@ -93,6 +94,23 @@ int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t ds
                           const void* z, const float* dt_bias,
                           void* out, const float* init_state, float* last_state,
                           void* stream);
+
+/* hx_selective_scan_fwd with a caller workspace for the long-sequence path: when the
+ * (batch, channel) tiles alone cannot fill the GPU (few channels, long seqlen), the sequence is
+ * cut into time segments scanned in parallel from a zero state, their entry states chained by a
+ * carry kernel, then rescanned with outputs (results agree with the unsegmented scan to fp32
+ * rounding). workspace: device memory of at least hx_selective_scan_workspace_size(...) bytes,
+ * 16-byte aligned (0 bytes: no segments); it holds no state between calls. Same reference
+ * counterpart as hx_selective_scan_fwd (the per-step loop of ssm.rs:166-182). */
+size_t hx_selective_scan_workspace_size(int64_t batch, int64_t seqlen, int64_t dim,
+                                        int64_t dstate, int dtype);
+int hx_selective_scan_fwd_ws(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
+                             int dtype, int delta_softplus,
+                             const void* u, const void* delta, const float* A,
+                             const void* B, const void* C, const float* D,
+                             const void* z, const float* dt_bias,
+                             void* out, const float* init_state, float* last_state,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* Single-step recurrent decode (state update only), for token-by-token generation:
  * the same arithmetic as one time step of hx_selective_scan_fwd with seqlen 1, updating
@@ -106,8 +124,15 @@ int hx_selective_state_update(int64_t batch, int64_t dim, int64_t dstate,
                               void* stream);
 
 /* ------------------------------------------------------------------ S4 recurrences */
-/* Reference-faithful nn::ssm::S4Block::forward_ssm (crates/nn/src/ssm.rs:138-186) with
- * discretize(dt) (ssm.rs:103-135): a[n] = exp(dt*a_real[n])*cos(dt*a_imag[n]), Bd = dt*B,
+/* nn::ssm::S4Block::discretize(dt)'s real decay (crates/nn/src/ssm.rs:113-120) on HOST arrays:
+ * a[n] = expf(a_real[n]*dt) * cosf(a_imag[n]*dt), each product rounded to f32 first, with the
+ * libm the reference's f32::exp / f32::cos call, so the result is the reference's bit for bit.
+ * The caller uploads `a` (dstate floats) for hx_s4_ref_fwd / hx_s4_ref_fwd_parallel: the
+ * discretisation needs no device round trip per forward. dstate <= 64. */
+int hx_s4_discretize(int64_t dstate, float dt, const float* a_real, const float* a_imag, float* a);
+
+/* Reference-faithful nn::ssm::S4Block::forward_ssm (crates/nn/src/ssm.rs:138-186) given the
+ * discretised decay a (device, [dstate], from hx_s4_discretize) and Bd = dt*B (ssm.rs:127-130),
  * one state h[dstate] SHARED by all channels:
  *   h = a (.) h + Bd . x[:, t];   y[t][m] = (C . h)[m] + D[m] * x[m][t]
  * x: [d_model, seqlen] row-major (column t is u_t, ssm.rs:168-169).
@@ -115,35 +140,43 @@ int hx_selective_state_update(int64_t batch, int64_t dim, int64_t dstate,
  *    order, backend-cpu/src/lib.rs:277-296; the shape field it reports is [d_model, seqlen]).
  * gate (nullable) [d_model]: y[t][m] *= gate[m] — fuses nn::ssm::MambaBlock's gating
  *    (ssm.rs:460-461, broadcast_to repeat-rows, backend-cpu/src/lib.rs:1388-1404).
- * B: [dstate, d_model], C: [d_model, dstate], D: [d_model]. dstate <= 64. */
+ * B: [dstate, d_model], C: [d_model, dstate], D: [d_model]. dstate <= 64.
+ * workspace: at least hx_s4_ref_workspace_size(...) bytes of device memory, 256-byte aligned.
+ * Asynchronous on `stream` (no host round trip). */
+size_t hx_s4_ref_workspace_size(int64_t d_model, int64_t dstate, int64_t seqlen);
 int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, float dt,
-                  const float* x, const float* a_real, const float* a_imag,
-                  const float* B, const float* C, const float* D, const float* gate,
-                  float* y, void* stream);
+                  const float* x, const float* a, const float* B, const float* C, const float* D,
+                  const float* gate, float* y, void* workspace, size_t workspace_bytes,
+                  void* stream);
 
 /* Time-parallel variant of hx_s4_ref_fwd for long sequences (same arguments and layouts,
- * dstate <= 16): the 16 state recurrences are solved in 64-step chunks with a carry chain, the
- * discretisation runs on the device, and products may contract to FMA, so results agree with
- * reference mode to rounding (within 1e-4) instead of bit for bit. Asynchronous on `stream`
- * (no host round trip). Replaces the per-step loop of S4Block::forward_ssm
- * (crates/nn/src/ssm.rs:166-182) for L in the tens of thousands. */
+ * dstate <= 16): the 16 state recurrences are solved in 256-step chunks with a carry chain (the
+ * chunk decay a^256 formed from the same rounded a) and products may contract to FMA, so results
+ * agree with reference mode to rounding (within 1e-4) instead of bit for bit. workspace: at
+ * least hx_s4_ref_parallel_workspace_size(...) bytes, 256-byte aligned. Replaces the per-step
+ * loop of S4Block::forward_ssm (crates/nn/src/ssm.rs:166-182) for L in the tens of thousands. */
+size_t hx_s4_ref_parallel_workspace_size(int64_t d_model, int64_t dstate, int64_t seqlen);
 int hx_s4_ref_fwd_parallel(int64_t d_model, int64_t dstate, int64_t seqlen, float dt,
-                           const float* x, const float* a_real, const float* a_imag,
-                           const float* B, const float* C, const float* D, const float* gate,
-                           float* y, void* stream);
+                           const float* x, const float* a, const float* B, const float* C,
+                           const float* D, const float* gate, float* y, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /* S4D diagonal complex recurrence (per-channel state, S4D discretisation with the same
  * ZOH-on-A / Euler-on-B choice as ssm.rs:108-130), the complex form of what
  * S4Block::discretize computes and then drops (A_d_imag, ssm.rs:121-125):
  *   Abar[d,n] = exp(dt[d]*(a_re[d,n] + i*a_im[d,n])), Bbar = dt[d]*B[d,n] (complex)
  *   h[d,n] = Abar*h + Bbar*x[b,t,d];  y[b,t,d] = 2*Re(sum_n C[d,n]*h[d,n]) + D[d]*x[b,t,d]
- * x, y: [batch, seqlen, dim] fp32. a_re, a_im, B_re, B_im, C_re, C_im: [dim, dstate]; dt, D: [dim]. */
+ * x, y: [batch, seqlen, dim] fp32. a_re, a_im, B_re, B_im, C_re, C_im: [dim, dstate]; dt, D: [dim].
+ * workspace: at least hx_s4d_workspace_size(...) bytes (segment states of the long-sequence
+ * path; 0 when the sequence is not segmented), 16-byte aligned. */
+size_t hx_s4d_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate);
 int hx_s4d_complex_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
                        const float* x, const float* dt,
                        const float* a_re, const float* a_im,
                        const float* B_re, const float* B_im,
                        const float* C_re, const float* C_im,
-                       const float* D, float* y, void* stream);
+                       const float* D, float* y, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /* ------------------------------------------------------------------ dense */
 /* nn::Linear::forward (crates/nn/src/lib.rs:120-134): Y[r][o] = sum_k X[r][k]*W[o][k] + bias[o],

@@ -29,6 +29,9 @@ Pinning status of each function (how tests/test_oracle.py pins it):
                         bf16 rounding at the storage points; cross-checked against
                         numpy_mamba_block (float64, same storage rounding)
   s4d_complex           impulse response 2*Re(sum C Abar^t Bbar), constant-input steady state
+  r_s4_forward_ssm,     the reference's execution shape (allocation per op, copying slices,
+  r_mamba_mlp           reshapes and stack, hx_oracle_ref.c) for the CPU-baseline timing;
+                        bit-identical to s4_ref_fwd / mamba_mlp (checked in tests)
 """
 from __future__ import annotations
 
@@ -78,6 +81,8 @@ def lib() -> ctypes.CDLL:
             "oracle_selective_scan_omp": [_i64, _i64, _i64, _i64, _int] + [_p] * 9 + [_int],
             "oracle_max_threads": [],
             "oracle_conv1d_silu": [_i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
+            "oracle_r_s4_forward_ssm": [_i64, _i64, _i64, _f] + [_p] * 9,
+            "oracle_r_mamba_mlp": [_i64, _i64, _i64] + [_p] * 6,
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -209,6 +214,31 @@ def selective_scan_omp(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_so
                                     _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(dt_bias),
                                     _ptr(out), int(threads))
     return out
+
+
+def r_s4_forward_ssm(x, a_real, a_imag, B, C, D, delta=None, lam=None, dt=0.1):
+    """S4Block::forward_ssm in the reference's execution shape (hx_oracle_ref.c): x [M, L] ->
+    y memory [L, M]; same values as s4_ref_fwd, bit for bit."""
+    x, a_real, a_imag, B, C, D = map(_f32, (x, a_real, a_imag, B, C, D))
+    M, L = x.shape
+    N = a_real.shape[0]
+    delta = _f32(delta) if delta is not None else np.zeros(M, np.float32)
+    lam = _f32(lam) if lam is not None else np.zeros(N, np.float32)
+    y = np.empty((L, M), np.float32)
+    lib().oracle_r_s4_forward_ssm(M, N, L, dt, _ptr(x), _ptr(a_real), _ptr(a_imag), _ptr(B),
+                                  _ptr(C), _ptr(D), _ptr(delta), _ptr(lam), _ptr(y))
+    return y
+
+
+def r_mamba_mlp(X, Wg, bg, Wo, bo):
+    """Exported MambaBlock::forward_mamba in the reference's execution shape (hx_oracle_ref.c);
+    same values as mamba_mlp, bit for bit."""
+    X, Wg, bg, Wo, bo = map(_f32, (X, Wg, bg, Wo, bo))
+    R, dm = X.shape
+    di = Wg.shape[0]
+    Y = np.empty((R, dm), np.float32)
+    lib().oracle_r_mamba_mlp(R, dm, di, _ptr(X), _ptr(Wg), _ptr(bg), _ptr(Wo), _ptr(bo), _ptr(Y))
+    return Y
 
 
 def max_threads() -> int:

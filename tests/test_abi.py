@@ -4,6 +4,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from helixml_amd import _ffi
@@ -66,9 +67,50 @@ def test_scan_null_pointers_rejected():
 
 def test_s4_ref_rejects():
     L = _ffi.lib()
-    assert L.hx_s4_ref_fwd(4, 0, 4, 0.1, *([None] * 8), None) == _ffi.UnsupportedOperation.status
-    assert L.hx_s4_ref_fwd(4, 16, 4, 0.1, *([None] * 8), None) == _ffi.InvalidInput.status
-    assert L.hx_s4_ref_fwd(0, 16, 4, 0.1, *([None] * 8), None) == 0
+    assert L.hx_s4_ref_fwd(4, 0, 4, 0.1, *([None] * 7), None, 0, None) == _ffi.UnsupportedOperation.status
+    assert L.hx_s4_ref_fwd(4, 16, 4, 0.1, *([None] * 7), None, 0, None) == _ffi.InvalidInput.status
+    assert L.hx_s4_ref_fwd(0, 16, 4, 0.1, *([None] * 7), None, 0, None) == 0
+
+
+def test_s4_discretize_is_the_reference_libm_formula():
+    """hx_s4_discretize (host) = expf(f32(a_real*dt)) * cosf(f32(a_imag*dt)) in f32, as
+    S4Block::discretize (crates/nn/src/ssm.rs:113-120) computes it; the oracle's restatement of
+    the same function is pinned by the S4 reference-mode tests."""
+    rng = np.random.default_rng(5)
+    ar = rng.standard_normal(16).astype(np.float32)
+    ai = rng.standard_normal(16).astype(np.float32) * np.float32(3)
+    a = np.empty(16, np.float32)
+    assert _ffi.lib().hx_s4_discretize(16, 0.1, ar.ctypes.data, ai.ctypes.data, a.ctypes.data) == 0
+    tr = (ar * np.float32(0.1)).astype(np.float32)
+    ti = (ai * np.float32(0.1)).astype(np.float32)
+    ref = (np.exp(tr.astype(np.float64)) * np.cos(ti.astype(np.float64)))
+    assert np.abs(a - ref).max() <= 2e-7 * np.abs(ref).max()
+    # A_real = 0 (the reference's default init, ssm.rs:42): a = cos(dt * A_imag) exactly as f32 cosf
+    ar0 = np.zeros(16, np.float32)
+    assert _ffi.lib().hx_s4_discretize(16, 0.1, ar0.ctypes.data, ai.ctypes.data, a.ctypes.data) == 0
+    assert np.abs(a - np.cos(ti.astype(np.float64))).max() <= 1.2e-7
+    assert _ffi.lib().hx_s4_discretize(65, 0.1, None, None, None) == _ffi.UnsupportedOperation.status
+    assert _ffi.lib().hx_s4_discretize(4, 0.1, None, None, None) == _ffi.InvalidInput.status
+
+
+def test_workspace_sizes():
+    L = _ffi.lib()
+    # config 4 scan (batch 1, L 65536, d 2048): segmented, 16 segments x (2 x 32768 + 2048) floats
+    assert L.hx_selective_scan_workspace_size(1, 65536, 2048, 16, 0) == 16 * (2 * 2048 * 16 + 2048) * 4
+    # config 2 (batch 8, L 2048, d 1536) fills the GPU unsegmented: no workspace
+    assert L.hx_selective_scan_workspace_size(8, 2048, 1536, 16, 0) == 0
+    assert L.hx_selective_scan_workspace_size(1, 8192, 64, 7, 0) == 0  # generic kernel
+    assert L.hx_s4_ref_workspace_size(64, 16, 100) >= (16 * 64 + 100 * 16) * 4
+    assert L.hx_s4_ref_parallel_workspace_size(2048, 16, 65536) >= (2048 + 65536) * 16 * 4
+    assert L.hx_s4d_workspace_size(1, 65536, 2048, 16) > 0
+    assert L.hx_s4d_workspace_size(1, 100, 64, 8) == 0
+
+
+def test_scan_ws_rejects_short_workspace():
+    buf = (ctypes.c_uint8 * 64)()
+    rc = _ffi.lib().hx_selective_scan_fwd_ws(1, 4, 4, 16, 0, 1, *([None] * 11), None, 64, None)
+    assert rc == _ffi.InvalidInput.status  # NULL workspace with a size
+    del buf
 
 
 def test_linear_rejects_bad_act():

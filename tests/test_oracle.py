@@ -494,3 +494,23 @@ def test_planted_mistakes_are_caught():
     rb = oracle.numpy_mamba_block(**pb, dt_rank=8)
     swapped = dict(pb, w_in=np.concatenate([pb["w_in"][32:], pb["w_in"][:32]]))
     assert rel_err(oracle.mamba_block(**swapped, dt_rank=8), rb) > 1e-1
+
+
+def test_reference_execution_shape_restatement_is_bit_identical():
+    """The (R) CPU-baseline restatement (allocation per op, copied slices, stack) computes the
+    same f32 operations in the same order as the pinned oracle: equal bit for bit."""
+    rng = np.random.default_rng(41)
+    M, N, L = 24, 16, 37
+    x = rng.standard_normal((M, L)).astype(F)
+    ar = np.full(N, -0.5, F)
+    ai = (np.pi * np.arange(N)).astype(F)
+    B = (rng.standard_normal((N, M)) * 0.1).astype(F)
+    C = (rng.standard_normal((M, N)) * 0.1).astype(F)
+    D = rng.standard_normal(M).astype(F)
+    assert np.array_equal(oracle.r_s4_forward_ssm(x, ar, ai, B, C, D), oracle.s4_ref_fwd(x, ar, ai, B, C, D))
+    X = rng.uniform(-1, 1, (100, 64)).astype(F)
+    Wg = (rng.standard_normal((128, 64)) * np.sqrt(2 / 64)).astype(F)
+    Wo = (rng.standard_normal((64, 128)) * np.sqrt(2 / 128)).astype(F)
+    bg = rng.standard_normal(128).astype(F) * np.float32(0.1)
+    bo = rng.standard_normal(64).astype(F) * np.float32(0.1)
+    assert np.array_equal(oracle.r_mamba_mlp(X, Wg, bg, Wo, bo), oracle.mamba_mlp(X, Wg, bg, Wo, bo))
