@@ -89,6 +89,7 @@ SIGNATURES = {
     "hx_selective_scan_fwd": [_i64, _i64, _i64, _i64, _int, _int] + [_p] * 11 + [_p],
     "hx_selective_scan_workspace_size": [_i64, _i64, _i64, _i64, _int],
     "hx_selective_scan_fwd_ws": [_i64, _i64, _i64, _i64, _int, _int] + [_p] * 11 + [_p, _sz, _p],
+    "hx_selective_scan_fwd_noalloc": [_i64, _i64, _i64, _i64, _int, _int] + [_p] * 11 + [_p],
     "hx_selective_state_update": [_i64, _i64, _i64, _int, _int] + [_p] * 10 + [_p],
     "hx_s4_discretize": [_i64, _f, _p, _p, _p],
     "hx_s4_ref_workspace_size": [_i64, _i64, _i64],

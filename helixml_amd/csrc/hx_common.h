@@ -19,6 +19,10 @@ namespace hx {
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
 
+// Resolves the current device's address of the no-allocation scan's device scratch (once per
+// device; hx_init calls it). *out (nullable) receives the address.
+int scan_scratch_setup(void** out);
+
 #define HX_HIP_CHECK(expr)                                                                   \
     do {                                                                                     \
         hipError_t hx_e_ = (expr);                                                           \

@@ -34,6 +34,7 @@ int hx_init(int device) {
     HX_REQUIRE(device >= 0 && device < n, HX_ERR_INVALID_INPUT,
                "hx_init: device %d out of range (%d visible)", device, n);
     HX_HIP_CHECK(hipSetDevice(device));
+    if (int rc = hx::scan_scratch_setup(nullptr)) return rc;
     hx::clear_error();
     return HX_OK;
 }

@@ -19,6 +19,8 @@
 // state-update, which is why it runs on VALU and not MFMA.
 #include <type_traits>
 
+#include <mutex>
+
 #include "hx_common.h"
 #include "hx_wave.h"
 
@@ -1492,6 +1494,62 @@ extern "C" int hx_selective_scan_fwd_ws(int64_t batch, int64_t seqlen, int64_t d
     return hx::scan_entry(batch, seqlen, dim, dstate, dtype, delta_softplus, u, delta, A, B, C, D,
                           z, dt_bias, out, init_state, last_state,
                           workspace_bytes ? workspace : nullptr, workspace_bytes, stream);
+}
+
+// ------------------------------------------------------------------ no-allocation entry point
+// Scratch of hx_selective_scan_fwd_noalloc: the segmented long-sequence path's end states, entry
+// states and segment dt totals (the same layout a caller workspace holds for
+// hx_selective_scan_fwd_ws). One copy per device, resident until the process ends. Nothing in it
+// has to start at zero: the end-state pass writes every end state and dt total the carry kernel
+// reads, and the carry kernel writes every entry state the output pass reads.
+constexpr size_t kScanScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kScanScratchBytes];
+
+namespace hx {
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_dev[64] = {};  // device address of `scratch`, per device
+}  // namespace
+
+// Looks up the current device's address of `scratch` once per device (hipGetSymbolAddress with
+// that device current). Host code passes this address, never the array's name, to kernels.
+int scan_scratch_setup(void** out) {
+    int dev = 0;
+    HX_HIP_CHECK(hipGetDevice(&dev));
+    HX_REQUIRE(dev >= 0 && dev < 64, HX_ERR_UNSUPPORTED, "scan scratch: device %d >= 64", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_dev[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        HX_REQUIRE(e == hipSuccess && p != nullptr, HX_ERR_BACKEND,
+                   "scan scratch: hipGetSymbolAddress failed on device %d: %s", dev,
+                   hipGetErrorString(e));
+        g_scratch_dev[dev] = p;
+    }
+    if (out) *out = g_scratch_dev[dev];
+    return HX_OK;
+}
+}  // namespace hx
+
+extern "C" int hx_selective_scan_fwd_noalloc(int64_t batch, int64_t seqlen, int64_t dim,
+                                             int64_t dstate, int dtype, int delta_softplus,
+                                             const void* u, const void* delta, const float* A,
+                                             const void* B, const void* C, const float* D,
+                                             const void* z, const float* dt_bias, void* out,
+                                             const float* init_state, float* last_state,
+                                             void* stream) {
+    if (int rc = hx::check_common(batch, seqlen, dim, dstate, dtype)) return rc;
+    const size_t need = hx_selective_scan_workspace_size(batch, seqlen, dim, dstate, dtype);
+    HX_REQUIRE(need <= kScanScratchBytes, HX_ERR_UNSUPPORTED,
+               "selective scan (no-alloc): %zu bytes of scratch needed, the device scratch holds "
+               "%zu (use hx_selective_scan_fwd_ws with a caller workspace)",
+               need, kScanScratchBytes);
+    void* ws = nullptr;
+    if (need > 0)
+        if (int rc = hx::scan_scratch_setup(&ws)) return rc;
+    return hx::scan_entry(batch, seqlen, dim, dstate, dtype, delta_softplus, u, delta, A, B, C, D,
+                          z, dt_bias, out, init_state, last_state, ws,
+                          need > 0 ? kScanScratchBytes : 0, stream);
 }
 
 extern "C" int hx_set_scan_variant(int variant) {

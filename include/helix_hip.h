@@ -112,6 +112,24 @@ int hx_selective_scan_fwd_ws(int64_t batch, int64_t seqlen, int64_t dim, int64_t
                              void* out, const float* init_state, float* last_state,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* hx_selective_scan_fwd_ws without the workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc): the segmented
+ * long-sequence path uses an 8 MiB device-resident scratch array of the library instead (one per
+ * device, held until the process ends; hx_init or the first call on a device resolves its
+ * address). Calls nothing that allocates. Shapes whose segmented path needs more than 8 MiB
+ * (hx_selective_scan_workspace_size > 8 MiB, e.g. with hx_set_scan_segments forcing thousands of
+ * segments) are rejected with HX_ERR_UNSUPPORTED. Every call on a device shares that scratch:
+ * calls that overlap on one device (concurrent streams or threads) race; stream-ordered calls on
+ * one stream do not. No counterpart in the reference (which has no device path): it exists for
+ * callers that cannot allocate. Results are identical to hx_selective_scan_fwd_ws's. */
+int hx_selective_scan_fwd_noalloc(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
+                                  int dtype, int delta_softplus,
+                                  const void* u, const void* delta, const float* A,
+                                  const void* B, const void* C, const float* D,
+                                  const void* z, const float* dt_bias,
+                                  void* out, const float* init_state, float* last_state,
+                                  void* stream);
+
 /* Single-step recurrent decode (state update only), for token-by-token generation:
  * the same arithmetic as one time step of hx_selective_scan_fwd with seqlen 1, updating
  * `state` [batch, dim, dstate] in place. u, delta, z, out: [batch, dim]; B, C: [batch, dstate].
