@@ -85,6 +85,7 @@ SIGNATURES = {
     "hx_memcpy_d2d": [_p, _p, _sz, _p],
     "hx_sync": [],
     "hx_device_info": [_int, ctypes.POINTER(_int), ctypes.POINTER(_sz)],
+    "hx_device_utilization": [_int, ctypes.POINTER(ctypes.c_double)],
     "hx_last_error": [],
     "hx_selective_scan_fwd": [_i64, _i64, _i64, _i64, _int, _int] + [_p] * 11 + [_p],
     "hx_selective_scan_workspace_size": [_i64, _i64, _i64, _i64, _int],
@@ -113,6 +114,12 @@ SIGNATURES = {
     "hx_mamba_layer_workspace_size": [_i64] * 6,
     "hx_mamba_layer_fwd": [_i64] * 7 + [_p, _p, _f] + [_p] * 11 + [_p, _sz, _p],
     "hx_mamba_layer_decode": [_i64] * 6 + [_p, _p, _f] + [_p] * 11 + [_p, _sz, _p],
+    "hx_binary_f32": [_int, _i64, _p, _p, _p, _p],
+    "hx_unary_f32": [_int, _i64, _p, _f, _p, _p],
+    "hx_mean_axis_f32": [_i64, _i64, _i64, _int, _p, _p, _p],
+    "hx_copy_strided_f32": [_int, _p, _p, _p, _p, _p, _p],
+    "hx_fill_f32": [_i64, _f, _p, _p],
+    "hx_eye_f32": [_i64, _p, _p],
     "hx_set_scan_variant": [_int],
     "hx_set_scan_segments": [_int],
     "hx_set_gemm_kernel": [_int],

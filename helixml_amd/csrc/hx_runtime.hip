@@ -1,5 +1,7 @@
 // hx_runtime.hip — device selection, allocation, copies and error reporting for the C ABI.
+#include <cctype>
 #include <cstdarg>
+#include <cstdio>
 #include <cstring>
 
 #include "hx_common.h"
@@ -89,6 +91,25 @@ int hx_device_info(int device, int* compute_units, size_t* memory_bytes) {
     HX_HIP_CHECK(hipGetDeviceProperties(&prop, device));
     if (compute_units) *compute_units = prop.multiProcessorCount;
     if (memory_bytes) *memory_bytes = prop.totalGlobalMem;
+    return HX_OK;
+}
+
+int hx_device_utilization(int device, double* busy_fraction) {
+    HX_REQUIRE(busy_fraction != nullptr, HX_ERR_INVALID_INPUT, "hx_device_utilization: NULL output");
+    *busy_fraction = 0.0;
+    char bus[64] = {0};
+    HX_HIP_CHECK(hipDeviceGetPCIBusId(bus, (int)sizeof(bus), device));
+    for (char* c = bus; *c; ++c) *c = (char)tolower((unsigned char)*c);  // sysfs names are lower case
+    char path[160];
+    snprintf(path, sizeof(path), "/sys/bus/pci/devices/%s/gpu_busy_percent", bus);
+    FILE* f = fopen(path, "r");
+    HX_REQUIRE(f != nullptr, HX_ERR_UNSUPPORTED, "hx_device_utilization: %s is not readable", path);
+    int pct = -1;
+    const int got = fscanf(f, "%d", &pct);
+    fclose(f);
+    HX_REQUIRE(got == 1 && pct >= 0 && pct <= 100, HX_ERR_BACKEND,
+               "hx_device_utilization: unexpected contents of %s", path);
+    *busy_fraction = pct / 100.0;
     return HX_OK;
 }
 

@@ -8,6 +8,7 @@
 #include <fstream>
 
 #include "helix_hip.h"
+#include "helix_detail.h"
 
 namespace helix {
 
@@ -34,16 +35,7 @@ void check(int status, const char* what) {
 }
 
 namespace {
-[[noreturn]] void shape_mismatch(const std::vector<size_t>& expected, const std::vector<size_t>& actual) {
-    auto fmt = [](const std::vector<size_t>& v) {
-        std::string s = "[";
-        for (size_t i = 0; i < v.size(); ++i) s += (i ? ", " : "") + std::to_string(v[i]);
-        return s + "]";
-    };
-    // the reference's message: "Shape mismatch: expected {expected:?}, got {actual:?}"
-    throw TensorError(ErrorKind::ShapeMismatch, "Shape mismatch: expected " + fmt(expected) +
-                                                    ", got " + fmt(actual));
-}
+using detail::shape_mismatch;
 
 uint16_t f32_to_bf16(float f) {
     uint32_t x;
@@ -181,24 +173,6 @@ HipTensor HipTensor::clone() const {
     HipTensor t(shape_, storage_, device_);
     if (numel()) check(hx_memcpy_d2d(t.data(), data(), nbytes(), nullptr), "hx_memcpy_d2d");
     return t;
-}
-
-HipTensor HipTensor::matmul(const HipTensor& b) const {
-    // CpuTensor::matmul 2-D x 2-D (backend-cpu/src/lib.rs:644-678); other ranks are outside the
-    // path (the reference errors for > 2-D, lib.rs:749-755)
-    if (shape_.ndim() != 2 || b.shape_.ndim() != 2)
-        throw TensorError(ErrorKind::UnsupportedOperation,
-                          "Operation not supported: matmul of rank " + std::to_string(shape_.ndim()) +
-                              " x " + std::to_string(b.shape_.ndim()));
-    const size_t M = shape_.dim(0), K = shape_.dim(1), K2 = b.shape_.dim(0), N = b.shape_.dim(1);
-    if (K != K2) shape_mismatch({K}, {K2});
-    if (storage_ != Storage::F32 || b.storage_ != Storage::F32)
-        throw TensorError(ErrorKind::DTypeMismatch, "DType mismatch: expected F32 storage");
-    HipTensor y(Shape({M, N}), Storage::F32, device_);
-    check(hx_matmul_f32((int64_t)M, (int64_t)K, (int64_t)N, (const float*)data(),
-                        (const float*)b.data(), (float*)y.data(), nullptr),
-          "hx_matmul_f32");
-    return y;
 }
 
 // ----------------------------------------------------------------------------- nn
@@ -530,146 +504,6 @@ std::pair<std::string, std::vector<HipTensor>> load_checkpoint(const std::string
     std::vector<HipTensor> out;
     for (const HostTensor& t : h) out.push_back(HipTensor::from_host(t.values, Shape(t.shape), Storage::F32, device));
     return {meta, std::move(out)};
-}
-
-// ----------------------------------------------------------------------------- hal backend
-RocmBackend::RocmBackend(int device) : device_(device) {
-    check(hx_init(device), "hx_init");
-    caps_.device_type = DeviceType::ROCm;
-    caps_.device_id = device_id();
-    caps_.supported_operations = {OperationType::MatMul, OperationType::SSMForward,
-                                  OperationType::StateUpdate};
-    caps_.supported_precisions = {DataType::F32, DataType::BF16};
-    int cus = 0;
-    size_t mem = 0;
-    check(hx_device_info(device, &cus, &mem), "hx_device_info");
-    caps_.compute_units = (size_t)cus;
-    caps_.memory_bytes = mem;
-    caps_.memory_bandwidth_gbs = 8000.0;  // MI355X HBM3E, published
-}
-
-RocmBackend::~RocmBackend() {
-    for (auto& kv : live_) (void)hx_free(kv.second);
-}
-
-std::string RocmBackend::device_id() const { return "rocm:" + std::to_string(device_); }
-
-bool RocmBackend::supports_operation(OperationType op) const {
-    for (OperationType o : caps_.supported_operations)
-        if (o == op) return true;
-    return false;
-}
-
-size_t RocmBackend::optimal_batch_size() const {
-    // the scan runs one block per (batch row, 64 channels): at d_inner 1536 (24 tiles per row)
-    // compute_units / 32 rows (8 on 256 CUs) give every CU a tile
-    return caps_.compute_units >= 32 ? caps_.compute_units / 32 : 1;
-}
-
-MemoryHandle RocmBackend::allocate(size_t size, DataType dtype) {
-    void* p = nullptr;
-    check(hx_malloc(&p, size ? size : 4), "hx_malloc");
-    MemoryHandle h;
-    h.id = next_id_++;
-    h.size = size;
-    h.dtype = dtype;
-    h.address = (uintptr_t)p;
-    live_[h.id] = p;
-    return h;
-}
-
-void RocmBackend::deallocate(const MemoryHandle& h) {
-    auto it = live_.find(h.id);
-    if (it == live_.end())
-        throw TensorError(ErrorKind::InvalidInput, "Invalid input: unknown memory handle");
-    check(hx_free(it->second), "hx_free");
-    live_.erase(it);
-}
-
-void RocmBackend::copy_from_host(const MemoryHandle& dst, const void* src, size_t bytes) {
-    if (bytes > dst.size) throw TensorError(ErrorKind::InvalidInput, "Invalid input: copy past handle");
-    check(hx_memcpy_h2d((void*)dst.address, src, bytes), "hx_memcpy_h2d");
-}
-
-void RocmBackend::copy_to_host(void* dst, const MemoryHandle& src, size_t bytes) const {
-    if (bytes > src.size) throw TensorError(ErrorKind::InvalidInput, "Invalid input: copy past handle");
-    check(hx_sync(), "hx_sync");
-    check(hx_memcpy_d2h(dst, (const void*)src.address, bytes), "hx_memcpy_d2h");
-}
-
-bool RocmBackend::is_available() const { return hx_init(device_) == HX_OK; }
-
-void RocmBackend::synchronize() { check(hx_sync(), "hx_sync"); }
-
-MemoryHandle RocmBackend::execute_op(const Operation& op) {
-    auto param = [&](const char* k, double dflt, bool required) {
-        auto it = op.params.find(k);
-        if (it == op.params.end()) {
-            if (required)
-                throw TensorError(ErrorKind::InvalidInput, std::string("Invalid input: missing parameter ") + k);
-            return dflt;
-        }
-        return it->second;
-    };
-    auto ptr = [&](size_t i) -> void* {
-        return i < op.inputs.size() && op.inputs[i].address ? (void*)op.inputs[i].address : nullptr;
-    };
-    auto out_for = [&](size_t bytes, DataType dt) {
-        if (op.output) {
-            if (op.output->size < bytes)
-                throw TensorError(ErrorKind::InvalidInput, "Invalid input: output handle too small");
-            return *op.output;
-        }
-        return allocate(bytes, dt);
-    };
-    switch (op.op_type) {
-        case OperationType::MatMul: {
-            if (op.inputs.size() != 2) throw TensorError(ErrorKind::InvalidInput, "Invalid input: MatMul takes a, b");
-            const auto& a = op.inputs[0].shape;
-            const auto& b = op.inputs[1].shape;
-            if (a.size() != 2 || b.size() != 2)
-                throw TensorError(ErrorKind::UnsupportedOperation, "Operation not supported: MatMul rank");
-            if (a[1] != b[0]) shape_mismatch({a[1]}, {b[0]});
-            MemoryHandle o = out_for(a[0] * b[1] * 4, DataType::F32);
-            o.shape = {a[0], b[1]};
-            check(hx_matmul_f32((int64_t)a[0], (int64_t)a[1], (int64_t)b[1], (const float*)ptr(0),
-                                (const float*)ptr(1), (float*)o.address, nullptr),
-                  "hx_matmul_f32");
-            return o;
-        }
-        case OperationType::SSMForward: {
-            if (op.inputs.size() < 5)
-                throw TensorError(ErrorKind::InvalidInput, "Invalid input: SSMForward takes u, delta, A, B, C[, D, z, dt_bias]");
-            const int64_t bt = (int64_t)param("batch", 0, true), L = (int64_t)param("seqlen", 0, true);
-            const int64_t dim = (int64_t)param("dim", 0, true), N = (int64_t)param("dstate", 16, false);
-            const int sp = (int)param("softplus", 1, false);
-            const bool bf = op.inputs[0].dtype == DataType::BF16;
-            MemoryHandle o = out_for((size_t)(bt * L * dim) * (bf ? 2 : 4), op.inputs[0].dtype);
-            o.shape = {(size_t)bt, (size_t)L, (size_t)dim};
-            check(hx_selective_scan_fwd(bt, L, dim, N, bf ? HX_BF16 : HX_F32, sp, ptr(0), ptr(1),
-                                        (const float*)ptr(2), ptr(3), ptr(4), (const float*)ptr(5), ptr(6),
-                                        (const float*)ptr(7), (void*)o.address, nullptr, nullptr, nullptr),
-                  "hx_selective_scan_fwd");
-            return o;
-        }
-        case OperationType::StateUpdate: {
-            if (op.inputs.size() < 6)
-                throw TensorError(ErrorKind::InvalidInput, "Invalid input: StateUpdate takes state, u, delta, A, B, C[, D, z, dt_bias]");
-            const int64_t bt = (int64_t)param("batch", 0, true), dim = (int64_t)param("dim", 0, true);
-            const int64_t N = (int64_t)param("dstate", 16, false);
-            const int sp = (int)param("softplus", 1, false);
-            const bool bf = op.inputs[1].dtype == DataType::BF16;
-            MemoryHandle o = out_for((size_t)(bt * dim) * (bf ? 2 : 4), op.inputs[1].dtype);
-            o.shape = {(size_t)bt, (size_t)dim};
-            check(hx_selective_state_update(bt, dim, N, bf ? HX_BF16 : HX_F32, sp, (float*)ptr(0), ptr(1),
-                                            ptr(2), (const float*)ptr(3), ptr(4), ptr(5), (const float*)ptr(6),
-                                            ptr(7), (const float*)ptr(8), (void*)o.address, nullptr),
-                  "hx_selective_state_update");
-            return o;
-        }
-        default:  // SiLU and the rest are fused into the kernels above, not standalone ops here
-            throw TensorError(ErrorKind::UnsupportedOperation, "Operation not supported on ROCm backend");
-    }
 }
 
 }  // namespace helix

@@ -12,8 +12,9 @@
 //                 u32 big-endian metadata length, metadata JSON, then bincode 1.x of
 //                 Vec<CpuTensor> — HipTensors are written in exactly the bytes a CpuTensor with
 //                 the same values writes, and read back from them;
-//   hal:          ComputeBackend for ROCm (crates/hal/src/backend.rs:13-70) with SSMForward,
-//                 StateUpdate and MatMul operations (hal/src/device.rs:129-210).
+//   hal:          ComputeBackend (crates/hal/src/backend.rs:13-70) and ComputeGraph
+//                 (hal/src/operations.rs:87-230) for ROCm, the full OperationType enum
+//                 (hal/src/device.rs:129-210).
 //
 // Errors are thrown as helix::TensorError carrying the reference's variant; nothing here
 // computes on the host: every value comes from the HIP kernels behind include/helix_hip.h.
@@ -138,8 +139,48 @@ public:
     HipTensor reshape(Shape s) const;  // shares storage
     HipTensor clone() const;
 
-    // Tensor ops on the path (TensorOps, tensor.rs:62-134)
-    HipTensor matmul(const HipTensor& other) const;  // 2-D x 2-D, CpuTensor::matmul bit-exact
+    // ---- TensorOps (tensor.rs:62-134) with CpuTensor's semantics and errors
+    // (backend-cpu/src/lib.rs); fp32 storage. Values come from the device primitives of
+    // helix_hip.h (hx_binary_f32, hx_unary_f32, hx_mean_axis_f32, hx_copy_strided_f32, ...).
+    // matmul: 2-D x 2-D, 1-D x 2-D, 2-D x 1-D (lib.rs:634-757), bit-exact; other ranks
+    // UnsupportedOperation as the reference.
+    HipTensor matmul(const HipTensor& other) const;
+    HipTensor add(const HipTensor& o) const;  // equal shapes (lib.rs:570-632), bit-exact
+    HipTensor sub(const HipTensor& o) const;
+    HipTensor mul(const HipTensor& o) const;
+    HipTensor div(const HipTensor& o) const;
+    HipTensor add_scalar(float s) const;  // lib.rs:916-922
+    HipTensor mul_scalar(float s) const;  // lib.rs:925-932
+    HipTensor neg() const;                // lib.rs:895-902
+    HipTensor abs() const;                // lib.rs:822-828
+    HipTensor sqrt() const;               // lib.rs:768-775 (correctly rounded)
+    HipTensor exp() const;                // lib.rs:777-784 (device libm: within a few ulp)
+    HipTensor log() const;                // lib.rs:786-793
+    HipTensor sin() const;                // lib.rs:795-801
+    HipTensor cos() const;                // lib.rs:803-809
+    float to_scalar() const;              // lib.rs:966-974: one element, else InvalidInput
+    static HipTensor from_scalar(float value, Shape shape, int device = 0);  // lib.rs:904-914
+    static HipTensor eye(size_t n, int device = 0);                          // lib.rs:1303-1323
+    // ---- TensorActivation (tensor.rs:191-209)
+    HipTensor silu() const;     // x / (1 + exp(-x)), lib.rs:1154-1170
+    HipTensor sigmoid() const;  // lib.rs:1172-1178
+    // ---- TensorReduce::mean (lib.rs:995-1010): dims (all when null) are removed one by one in
+    // reverse order of the list (keepdim is ignored, as in the reference), each by ndarray's
+    // mean_axis with its summation order (bit-exact).
+    HipTensor mean(const std::vector<size_t>* dims = nullptr, bool keepdim = false) const;
+    // ---- TensorBroadcast::broadcast_to (lib.rs:1352-1518; other ranks through the generic
+    // index map of lib.rs:511-560, reproduced as written)
+    HipTensor broadcast_to(const Shape& shape) const;
+    // ---- Tensor shape operations (tensor.rs:7-59): exact copies
+    HipTensor transpose(size_t dim0, size_t dim1) const;  // lib.rs:115-137 (materialised)
+    HipTensor slice(const std::vector<size_t>& start, const std::vector<size_t>& end) const;  // 2-D, lib.rs:139-183
+    static HipTensor cat(const std::vector<HipTensor>& ts, size_t dim);    // 1-D, lib.rs:185-252
+    // lib.rs:254-335: for 1..3-D inputs the data are concatenated in input order whatever `dim`,
+    // and `dim` only places the count in the shape field; 0-D and >= 4-D inputs are placed by
+    // the generic stack (lib.rs:390-467)
+    static HipTensor stack(const std::vector<HipTensor>& ts, size_t dim);
+    HipTensor contiguous() const { return clone(); }  // device tensors are always row-major
+    bool is_contiguous() const { return true; }
 
 private:
     struct Buffer {
@@ -203,6 +244,16 @@ public:
     // and shape field [d_model, L]. parallel = the time-parallel form (equal to rounding).
     HipTensor forward_ssm(const HipTensor& x, const HipTensor* gate = nullptr,
                           bool parallel = false) const;
+    // Module::forward (ssm.rs:269-273) = forward_conv (ssm.rs:189-229) with compute_conv_kernel
+    // (ssm.rs:232-251), written as the reference writes them over HipTensor ops, so every shape
+    // gives the reference's result or error: input [batch, seq_len] (2-D slices), kernel
+    // K_0 = C.B, K_k = C.(A_real^k).B through 2-D x 1-D products. As in the reference, no input
+    // shape completes (the k = 1 product needs d_model == d_state, k = 2 is a 1-D x 1-D matmul,
+    // the stack of K_0 [d, d] with K_1 [d] mismatches, and the L = 1 path reshapes a [1, 1]
+    // slice to [d_model] then slices the 2-D kernel with one index); an input of rank < 2
+    // (where the reference's unwrap panics) raises InvalidDimension.
+    HipTensor forward(const HipTensor& x) const { return forward_conv(x); }
+    HipTensor forward_conv(const HipTensor& x) const;
     // checkpoint()/restore() (ssm.rs:331-360): A_real, A_imag, B, C, D, delta, Lambda.
     std::vector<HipTensor> checkpoint() const;
     void restore(const std::vector<HipTensor>& ck);
@@ -218,6 +269,42 @@ private:
     mutable const void* a_src_[2] = {nullptr, nullptr};
     mutable HipTensor workspace_;
 };
+
+// The exported nn::S4Block (crates/nn/src/lib.rs:674-773): A [d_state, d_state] ~ N(0, 0.1),
+// B [d_state, d_model] ~ N(0, 0.1), C [d_model, d_state] ~ N(0, 0.1), D zeros [d_model], delta
+// [d_model] ~ U(0.001, 0.1), Lambda [d_state] ~ N(0, 1) (lib.rs:687-726, in that draw order).
+// forward = forward_ssm (lib.rs:770-772) returns its input unchanged (a clone, lib.rs:742-756):
+// the README's S4 example. dim(0) and dim(1) are read first, so an input of rank < 2 (a panic
+// in the reference) raises InvalidDimension.
+class ExportedS4Block {
+public:
+    ExportedS4Block(size_t d_model, size_t d_state, Rng& rng, int device = 0);
+    HipTensor forward_ssm(const HipTensor& x) const;
+    HipTensor forward(const HipTensor& x) const { return forward_ssm(x); }
+    std::vector<const HipTensor*> parameters() const { return {&A, &B, &C, &D, &delta, &Lambda}; }
+    size_t d_model() const { return d_model_; }
+    size_t d_state() const { return d_state_; }
+    HipTensor A, B, C, D, delta, Lambda;
+
+private:
+    size_t d_model_, d_state_;
+};
+
+// The reference's nn code over the HipTensor primitives alone, each written as the reference
+// writes it (the generic Module<T> bodies instantiated for T = HipTensor, no fused kernel):
+//   linear       Linear::forward (lib.rs:120-134): x.matmul(W.transpose(0,1)) + broadcast(bias)
+//   mamba_mlp    exported MambaBlock::forward_mamba (lib.rs:888-906): linear -> silu -> linear
+//   rmsnorm      RMSNorm::forward (lib.rs:258-285) with eps' = eps (the reference draws
+//                U[eps, eps + 1e-8) per row)
+//   s4_forward_ssm  ssm::S4Block::discretize + forward_ssm (ssm.rs:103-186): per-step slices,
+//                GEMVs and stack(., 1)
+// They show the primitives are a complete drop-in; the fused entry points are the fast path.
+namespace generic {
+HipTensor linear(const HipTensor& x, const HipTensor& weight, const HipTensor* bias);
+HipTensor mamba_mlp(const HipTensor& x, const Linear& gate, const Linear& out_proj);
+HipTensor rmsnorm(const HipTensor& x, const HipTensor& weight, float eps);
+HipTensor s4_forward_ssm(const S4Block& s4, const HipTensor& x);
+}  // namespace generic
 
 // nn::ssm::MambaBlock::forward_mamba (ssm.rs:435-464): delta = X . delta_proj; y =
 // S4.forward_ssm(delta) gated by `gate`. X must be [d_model, d_model] as in the reference.
@@ -269,29 +356,77 @@ std::pair<std::string, std::vector<HipTensor>> load_checkpoint(const std::string
                                                                int device = 0);
 
 // ----------------------------------------------------------------------------- hal
-// hal::DeviceType and DataType (hal/src/device.rs:8-100) in the reference's declaration order;
-// OperationType (device.rs:129-210) holds the reference's names for the operations on this path.
+// hal::DeviceType and DataType (hal/src/device.rs:8-100) in the reference's declaration order.
 enum class DeviceType { CPU, CUDA, Metal, ROCm, NPU, TPU, QPU, BCI };
 enum class DataType { I8, I16, I32, I64, U8, U16, U32, U64, F16, F32, F64, BF8, BF16, C32, C64, Bool };
-enum class OperationType { Add, MatMul, Conv1D, SiLU, SSMForward, SSMBackward, StateUpdate };
+// hal::OperationType (hal/src/device.rs:129-210), every variant in the reference's order.
+enum class OperationType {
+    Add, Sub, Mul, Div, Pow, Sqrt, Abs,
+    Sin, Cos, Tan, Asin, Acos, Atan,
+    Exp, Log, Log2, Log10,
+    MatMul, Transpose, Inverse, Determinant, Eigenvalues, SVD,
+    Conv1D, Conv2D, Conv3D, MaxPool, AvgPool,
+    FFT, IFFT, RFFT, IRFFT,
+    Sum, Mean, Max, Min, Var, Std,
+    ReLU, Sigmoid, Tanh, SiLU, GELU, Softmax,
+    SSMForward, SSMBackward, StateUpdate,
+    TopologicalAnalysis, MotifDetection, CycleDetection, StabilityCalculation,
+    QuantumGate, QuantumMeasurement, QuantumEntanglement,
+    SpikeEncoding, SpikeDecoding, SignalFiltering,
+};
+const char* operation_name(OperationType op);  // the variant's name (Debug formatting)
 
 // hal::MemoryHandle (hal/src/memory.rs:11-24).
 struct MemoryHandle {
     uint64_t id = 0;
     DeviceType device = DeviceType::ROCm;
-    size_t size = 0;
+    size_t size = 0;  // bytes
     DataType dtype = DataType::F32;
     uintptr_t address = 0;
-    std::vector<size_t> shape;  // logical shape of the buffer
+    std::vector<size_t> shape;  // logical shape of the buffer (empty: size / element bytes, 1-D)
 };
 
 // hal::Operation (hal/src/operations.rs:9-28): type, inputs, output, numeric parameters.
 struct Operation {
     OperationType op_type;
     std::vector<MemoryHandle> inputs;
-    MemoryHandle* output = nullptr;  // optional preallocated output
+    MemoryHandle* output = nullptr;  // optional output: used as the destination when it has memory
+                                     // (address != 0); its id names the result in a ComputeGraph
     std::map<std::string, double> params;
     explicit Operation(OperationType t) : op_type(t) {}
+};
+
+// hal::ComputeGraph (hal/src/operations.rs:88-231): nodes, dependency edges from -> to,
+// build() finds input nodes (no incoming edge) and output nodes (no outgoing edge),
+// topological_sort() is the reference's DFS (reverse post-order) and raises on a cycle.
+class ComputeGraph {
+public:
+    size_t add_operation(Operation op);
+    void add_dependency(size_t from, size_t to);  // InvalidInput for an unknown node
+    const std::vector<Operation>& nodes() const { return nodes_; }
+    const std::vector<size_t>* dependencies(size_t node) const;
+    void build();
+    std::vector<size_t> topological_sort() const;
+    const std::vector<size_t>& input_nodes() const { return inputs_; }
+    const std::vector<size_t>& output_nodes() const { return outputs_; }
+
+private:
+    std::vector<Operation> nodes_;
+    std::map<size_t, std::vector<size_t>> deps_;
+    std::vector<size_t> inputs_, outputs_;
+};
+
+// hal::TopologicalFeatures / AsyncHandle (hal/src/backend.rs:73-123).
+struct TopologicalFeatures {
+    std::vector<uint64_t> motif_hashes;
+    std::vector<std::vector<size_t>> cycles;
+    double stability = 0.0;
+    double entropy = 0.0;
+};
+struct AsyncHandle {
+    uint64_t id = 0;
+    std::string device_id;
+    OperationType operation = OperationType::Add;
 };
 
 struct DeviceCapabilities {
@@ -301,39 +436,81 @@ struct DeviceCapabilities {
     std::vector<DataType> supported_precisions;
     size_t compute_units = 0;
     size_t memory_bytes = 0;
+    size_t available_memory = 0;
     double memory_bandwidth_gbs = 0.0;
+    bool supports_async = true;
 };
 
-// hal::ComputeBackend (hal/src/backend.rs:13-70) for one ROCm device.
-class RocmBackend {
+// hal::ComputeBackend (hal/src/backend.rs:13-70), every method of the trait.
+class ComputeBackend {
+public:
+    virtual ~ComputeBackend() = default;
+    virtual DeviceType device_type() const = 0;
+    virtual std::string device_id() const = 0;
+    virtual const DeviceCapabilities& capabilities() const = 0;
+    virtual bool supports_operation(OperationType op) const = 0;
+    virtual size_t optimal_batch_size() const = 0;
+    virtual std::vector<DataType> supported_precisions() const = 0;
+    virtual double memory_bandwidth() const = 0;
+    virtual size_t compute_units() const = 0;
+    virtual MemoryHandle allocate(size_t size, DataType dtype) = 0;
+    virtual void deallocate(const MemoryHandle& h) = 0;
+    virtual void copy_from_host(const MemoryHandle& dst, const void* src, size_t bytes) = 0;
+    virtual void copy_to_host(void* dst, const MemoryHandle& src, size_t bytes) const = 0;
+    virtual MemoryHandle copy_to(const MemoryHandle& src, ComputeBackend& dst) = 0;
+    virtual MemoryHandle execute_op(const Operation& op) = 0;
+    virtual std::vector<MemoryHandle> execute_graph(const ComputeGraph& graph) = 0;
+    virtual TopologicalFeatures compute_topological_features(const MemoryHandle& data) = 0;
+    virtual AsyncHandle execute_async(const Operation& op) = 0;
+    virtual MemoryHandle wait(const AsyncHandle& h) = 0;
+    virtual bool is_available() const = 0;
+    virtual double utilization() const = 0;
+    virtual void synchronize() = 0;
+};
+
+// ComputeBackend for one ROCm device. execute_op runs on the device:
+//   Add/Sub/Mul/Div (2 equal-size inputs), Sqrt/Abs/Sin/Cos/Exp/Log/Sigmoid/SiLU (1 input),
+//   Mean (all elements -> 1), Transpose (2-D, shape from the input handle), MatMul (a [M,K],
+//   b [K,N] from the handles' shapes), SSMForward (u, delta, A, B, C[, D, z, dt_bias]; params
+//   batch, seqlen, dim, dstate, softplus), StateUpdate (state, u, delta, A, B, C[, D, z,
+//   dt_bias]; params batch, dim, dstate, softplus). Others: UnsupportedOperation.
+// execute_async launches the operation on the device stream and returns at once; wait() blocks
+// until it has finished and returns its output. execute_graph runs the nodes in topological
+// order, feeding a node's output to the nodes whose inputs carry that output's id, and returns
+// the outputs of the output nodes (the reference's substitution rule, operations.rs + the CPU
+// backend's execute_graph). utilization() reads the device's busy percentage from sysfs.
+class RocmBackend : public ComputeBackend {
 public:
     explicit RocmBackend(int device = 0);
-    ~RocmBackend();
-    DeviceType device_type() const { return DeviceType::ROCm; }
-    std::string device_id() const;
-    const DeviceCapabilities& capabilities() const { return caps_; }
-    bool supports_operation(OperationType op) const;
-    size_t optimal_batch_size() const;
-    std::vector<DataType> supported_precisions() const { return caps_.supported_precisions; }
-    double memory_bandwidth() const { return caps_.memory_bandwidth_gbs; }
-    size_t compute_units() const { return caps_.compute_units; }
-    MemoryHandle allocate(size_t size, DataType dtype);
-    void deallocate(const MemoryHandle& h);
-    void copy_from_host(const MemoryHandle& dst, const void* src, size_t bytes);
-    void copy_to_host(void* dst, const MemoryHandle& src, size_t bytes) const;
-    // SSMForward: inputs u, delta, A, B, C [, D, z, dt_bias as present] with params batch, seqlen,
-    // dim, dstate, softplus; StateUpdate: state, u, delta, A, B, C [, D, z, dt_bias];
-    // MatMul: a [M,K], b [K,N] (fp32). The output is allocated unless op.output is given.
-    MemoryHandle execute_op(const Operation& op);
-    bool is_available() const;
-    double utilization() const { return 0.0; }
-    void synchronize();
+    ~RocmBackend() override;
+    DeviceType device_type() const override { return DeviceType::ROCm; }
+    std::string device_id() const override;
+    const DeviceCapabilities& capabilities() const override { return caps_; }
+    bool supports_operation(OperationType op) const override;
+    size_t optimal_batch_size() const override;
+    std::vector<DataType> supported_precisions() const override { return caps_.supported_precisions; }
+    double memory_bandwidth() const override { return caps_.memory_bandwidth_gbs; }
+    size_t compute_units() const override { return caps_.compute_units; }
+    MemoryHandle allocate(size_t size, DataType dtype) override;
+    void deallocate(const MemoryHandle& h) override;
+    void copy_from_host(const MemoryHandle& dst, const void* src, size_t bytes) override;
+    void copy_to_host(void* dst, const MemoryHandle& src, size_t bytes) const override;
+    MemoryHandle copy_to(const MemoryHandle& src, ComputeBackend& dst) override;
+    MemoryHandle execute_op(const Operation& op) override;
+    std::vector<MemoryHandle> execute_graph(const ComputeGraph& graph) override;
+    TopologicalFeatures compute_topological_features(const MemoryHandle& data) override;
+    AsyncHandle execute_async(const Operation& op) override;
+    MemoryHandle wait(const AsyncHandle& h) override;
+    bool is_available() const override;
+    double utilization() const override;
+    void synchronize() override;
 
 private:
     int device_;
     DeviceCapabilities caps_;
     uint64_t next_id_ = 1;
     std::map<uint64_t, void*> live_;
+    std::map<uint64_t, MemoryHandle> pending_;  // execute_async outputs by handle id
 };
 
 }  // namespace helix

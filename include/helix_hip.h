@@ -70,6 +70,10 @@ int hx_sync(void);
 /* Compute units and global memory bytes of `device` (for hal::ComputeBackend::compute_units and
  * capabilities, hal/src/backend.rs:31-35). */
 int hx_device_info(int device, int* compute_units, size_t* memory_bytes);
+/* Fraction of time `device` was busy over the driver's last sampling window (amdgpu's
+ * gpu_busy_percent in sysfs, 0..1), for hal::ComputeBackend::utilization (hal/src/backend.rs:
+ * 65-66). HX_ERR_UNSUPPORTED where the driver does not expose it. */
+int hx_device_utilization(int device, double* busy_fraction);
 /* Text of the last error raised on the calling thread ("" if none). Becomes the message of
  * TensorError::BackendError / the variant matching the status. */
 const char* hx_last_error(void);
@@ -306,6 +310,53 @@ int hx_mamba_layer_decode(int64_t batch, int64_t d_model, int64_t d_inner, int64
 /* CpuTensor::matmul 2-D x 2-D (crates/backend-cpu/src/lib.rs:644-678): Y = A[M,K] . B[K,N]. */
 int hx_matmul_f32(int64_t M, int64_t K, int64_t N, const float* A, const float* B, float* Y,
                   void* stream);
+
+/* ------------------------------------------------------------------ tensor primitives */
+/* The CpuTensor operations a HipTensor needs to implement the reference's traits on the device
+ * (crates/tensor-core/src/tensor.rs:7-209), fp32, row-major. Shape checks and the reference's
+ * error variants are the caller's (the HipTensor layer): only element counts cross here. */
+
+/* Equal-shape elementwise y = a op b over n elements: CpuTensor::add/sub/mul/div
+ * (crates/backend-cpu/src/lib.rs:570-632). One IEEE operation per element (bit-exact). */
+typedef enum { HX_ADD = 0, HX_SUB = 1, HX_MUL = 2, HX_DIV = 3 } hx_binary_op;
+int hx_binary_f32(int op, int64_t n, const float* a, const float* b, float* y, void* stream);
+
+/* Elementwise y = f(x[, scalar]) over n elements (crates/backend-cpu/src/lib.rs):
+ * HX_EXP exp (777-784), HX_COS cos (803-809), HX_SIN sin (795-801), HX_SQRT sqrt (768-775,
+ * correctly rounded), HX_SILU x / (1 + exp(-x)) (1154-1170), HX_NEG -x (895-902), HX_MUL_SCALAR
+ * x * scalar (925-932), HX_ADD_SCALAR x + scalar (916-922), HX_ABS |x| (822-828), HX_LOG ln x
+ * (786-793), HX_SIGMOID 1 / (1 + exp(-x)) (1172-1178). exp/cos/sin/log use the device math
+ * library where the reference calls host libm (results within a few ulp). */
+typedef enum {
+    HX_EXP = 0, HX_COS = 1, HX_SIN = 2, HX_SQRT = 3, HX_SILU = 4, HX_NEG = 5, HX_MUL_SCALAR = 6,
+    HX_ADD_SCALAR = 7, HX_ABS = 8, HX_LOG = 9, HX_SIGMOID = 10
+} hx_unary_op;
+int hx_unary_f32(int op, int64_t n, const float* x, float scalar, float* y, void* stream);
+
+/* Mean over the middle axis of x viewed as [outer, len, inner]: y[o][i] = sum_l x[o][l][i] / len
+ * (TensorReduce::mean of one axis, crates/backend-cpu/src/lib.rs:995-1010, i.e. ndarray 0.15's
+ * mean_axis = sum_axis / len), bit-exact with ndarray's summation order: lane_fold = 1 (the
+ * reduced axis is the array's last, minimum-stride axis; requires inner == 1) sums each lane with
+ * eight partial sums over elements k mod 8 combined as ((p0+p4) + (p1+p5) + (p2+p6) + (p3+p7)) and
+ * then the len mod 8 trailing elements; lane_fold = 0 adds the len sub-views in axis order.
+ * len == 0 is rejected (the reference unwraps ndarray's None there). */
+int hx_mean_axis_f32(int64_t outer, int64_t len, int64_t inner, int lane_fold, const float* x,
+                     float* y, void* stream);
+
+/* Exact strided copy of a logical block of `shape` (ndim <= HX_MAX_DIMS, strides in elements,
+ * a source stride may be 0): dst[sum_j c_j*dst_strides[j]] = src[sum_j c_j*src_strides[j]]. The
+ * HipTensor layer expresses reshape/contiguous (94-113), transpose (115-137), slice (139-183),
+ * cat (185-252), stack (254-335, 390-467) and broadcast_to (1352-1518, 511-560) with it. */
+#define HX_MAX_DIMS 8
+int hx_copy_strided_f32(int ndim, const int64_t* shape, const float* src,
+                        const int64_t* src_strides, float* dst, const int64_t* dst_strides,
+                        void* stream);
+
+/* y[0..n) = value: Tensor zeros / ones / from_scalar (crates/backend-cpu/src/lib.rs:1273-1301,
+ * 904-914). */
+int hx_fill_f32(int64_t n, float value, float* y, void* stream);
+/* n x n identity: TensorRandom::eye (crates/backend-cpu/src/lib.rs:1303-1316). */
+int hx_eye_f32(int64_t n, float* y, void* stream);
 
 /* ------------------------------------------------------------------ tuning */
 /* Selects the selective-scan kernel variant for later calls on the calling thread: 0 = auto

@@ -29,6 +29,16 @@ Pinning status of each function (how tests/test_oracle.py pins it):
                         bf16 rounding at the storage points; cross-checked against
                         numpy_mamba_block (float64, same storage rounding)
   s4d_complex           impulse response 2*Re(sum C Abar^t Bbar), constant-input steady state
+  unary                 special values (exp 0 = 1, cos 0 = 1, sin 0 = 0, log 1 = 0, sqrt of
+                        squares), float64 within one f32 ulp, silu/sigmoid formulas
+  mean_axis             constant and small-integer rows (exact); the summation order by a
+                        crafted row whose sum is 6 in ndarray's eight-accumulator fold and 3 in
+                        sequential order (hand-derived from the fold), and the same values as a
+                        column (sequential order off the contiguous axis: 3)
+  rmsnorm_ref           composition of unary/mean (pinned above); equals rmsnorm to rounding
+  broadcast_to, stack,  numpy's broadcast_to / concatenate / stack / transpose / slicing on the
+  transpose, slice2d,   cases the reference computes correctly; the generic broadcast's stride
+  cat1d                 quirk on a hand-derived case (src [2, 3] -> [1, 1, 2, 3])
   r_s4_forward_ssm,     the reference's execution shape (allocation per op, copying slices,
   r_mamba_mlp           reshapes and stack, hx_oracle_ref.c) for the CPU-baseline timing;
                         bit-identical to s4_ref_fwd / mamba_mlp (checked in tests)
@@ -83,6 +93,9 @@ def lib() -> ctypes.CDLL:
             "oracle_conv1d_silu": [_i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
             "oracle_r_s4_forward_ssm": [_i64, _i64, _i64, _f] + [_p] * 9,
             "oracle_r_mamba_mlp": [_i64, _i64, _i64] + [_p] * 6,
+            "oracle_unary": [_int, _i64, _p, _f, _p],
+            "oracle_mean_axis": [_i64, _i64, _i64, _int, _p, _p],
+            "oracle_rmsnorm_ref": [_i64, _i64, _p, _p, _f, _p, _p],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -459,3 +472,123 @@ def numpy_mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, 
     dt = r(dtlo @ r(w_dt).T).reshape(Bt, L, di)
     y, _ = numpy_selective_scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True)
     return r(r(y).reshape(-1, di) @ r(w_out).T).reshape(Bt, L, dm)
+
+
+# ------------------------------------------------------------------ tensor primitives
+# Restatements of CpuTensor's primitives (crates/backend-cpu/src/lib.rs) that HipTensor's
+# device primitives (hx_binary_f32, hx_unary_f32, hx_mean_axis_f32, hx_copy_strided_f32) are
+# checked against. Elementwise add/sub/mul/div are single IEEE float32 operations, so numpy's
+# float32 arithmetic is their restatement.
+
+UNARY = {"exp": 0, "cos": 1, "sin": 2, "sqrt": 3, "silu": 4, "neg": 5, "mul_scalar": 6,
+         "add_scalar": 7, "abs": 8, "log": 9, "sigmoid": 10}
+
+
+def unary(op, x, s=0.0):
+    """libm maps of CpuTensor (lib.rs:768-932, 1154-1178); op as in UNARY."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().oracle_unary(UNARY[op], x.size, _ptr(x), s, _ptr(y))
+    return y
+
+
+def mean_axis(x, axis):
+    """ndarray 0.15 mean_axis (TensorReduce::mean of one axis, lib.rs:995-1010) of a row-major
+    array, with ndarray's summation order (the lane fold on the last axis)."""
+    x = _f32(x)
+    d = x.shape
+    outer = int(np.prod(d[:axis], dtype=np.int64))
+    inner = int(np.prod(d[axis + 1:], dtype=np.int64))
+    y = np.empty(d[:axis] + d[axis + 1:], np.float32)
+    lane = 1 if axis == len(d) - 1 else 0
+    lib().oracle_mean_axis(outer, d[axis], inner, lane, _ptr(x), _ptr(y))
+    return y
+
+
+def rmsnorm_ref(X, w, eps):
+    """nn::RMSNorm::forward (lib.rs:258-285) in its primitives' order (eps' = eps)."""
+    X, w = _f32(X), _f32(w)
+    R, Dm = X.shape
+    Y = np.empty_like(X)
+    work = np.empty(Dm, np.float32)
+    lib().oracle_rmsnorm_ref(R, Dm, _ptr(X), _ptr(w), eps, _ptr(Y), _ptr(work))
+    return Y
+
+
+def _row_major_strides(dims):
+    s = [1] * len(dims)
+    for i in range(len(dims) - 1, 0, -1):
+        s[i - 1] = s[i] * dims[i]
+    return s
+
+
+def broadcast_to(x, shape):
+    """CpuTensor::broadcast_to (lib.rs:1352-1518): the (1,2) / (2,3) / (1,3) cases, and the
+    generic index map of lib.rs:511-560 as written for every other rank pair (target dim j reads
+    the source with the source's own stride at index j, 1 past its rank). Raises ValueError where
+    the reference returns ShapeMismatch."""
+    x = np.asarray(x, np.float32)
+    s, t = list(x.shape), list(shape)
+    if len(s) > len(t):
+        raise ValueError("ShapeMismatch")
+    if s == t:
+        return x.copy()
+    padded = [1] * (len(t) - len(s)) + s
+    for pd, td in zip(padded, t):
+        if pd != 1 and pd != td:
+            raise ValueError("ShapeMismatch")
+    flat = x.reshape(-1)
+    if (len(s), len(t)) == (1, 2):
+        if s[0] == t[1]:
+            return np.tile(flat, (t[0], 1))
+        if s[0] == t[0]:
+            return np.repeat(flat, t[1]).reshape(t)
+        raise ValueError("ShapeMismatch")
+    if (len(s), len(t)) == (2, 3):
+        if s == t[1:] or (s[0] == 1 and s[1] == t[2]):
+            return np.broadcast_to(x, t).copy()
+        raise ValueError("ShapeMismatch")
+    if (len(s), len(t)) == (1, 3):
+        if s[0] == t[2]:
+            return np.broadcast_to(x, t).copy()
+        raise ValueError("ShapeMismatch")
+    ss = _row_major_strides(s)
+    out = np.empty(int(np.prod(t, dtype=np.int64)), np.float32)
+    for i in range(out.size):   # small cases only: the reference's loop, element by element
+        idx, rem = 0, i
+        for j in range(len(t) - 1, -1, -1):
+            c = rem % t[j]
+            rem //= t[j]
+            sc = c % padded[j] if padded[j] != 1 else 0
+            idx += sc * (ss[j] if j < len(ss) else 1)
+        out[i] = flat[idx]
+    return out.reshape(t)
+
+
+def stack(tensors, dim):
+    """CpuTensor::stack (lib.rs:254-335, generic 390-467): returns (data, shape field). For 1..3-D
+    inputs the data are the inputs back to back whatever `dim`; the shape field inserts the count
+    at `dim`. Other ranks: a true stack along `dim`."""
+    arrs = [np.asarray(a, np.float32) for a in tensors]
+    if len(arrs) == 1:
+        return arrs[0].copy(), list(arrs[0].shape)
+    shape = list(arrs[0].shape)
+    field = shape[:dim] + [len(arrs)] + shape[dim:]
+    if 1 <= len(shape) <= 3:
+        return np.concatenate([a.reshape(-1) for a in arrs]).reshape(field), field
+    return np.stack(arrs, axis=dim), field
+
+
+def transpose(x, d0, d1):
+    """CpuTensor::transpose (lib.rs:115-137): logical axis swap."""
+    return np.ascontiguousarray(np.swapaxes(np.asarray(x, np.float32), d0, d1))
+
+
+def slice2d(x, start, end):
+    """CpuTensor::slice of a 2-D tensor (lib.rs:158-175)."""
+    return np.asarray(x, np.float32)[start[0]:end[0], start[1]:end[1]].copy()
+
+
+def cat1d(tensors):
+    """CpuTensor::cat of 1-D tensors (lib.rs:229-246)."""
+    return np.concatenate([np.asarray(a, np.float32) for a in tensors])

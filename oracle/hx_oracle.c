@@ -322,3 +322,81 @@ void oracle_conv1d_silu(int64_t Bt, int64_t L, int64_t Dd, int64_t W, const floa
                 y[(b * L + t) * Dd + d] = silu_ref(acc);
             }
 }
+
+/* ---------------------------------------------------------------- tensor primitives */
+
+/* CpuTensor's elementwise maps (backend-cpu/src/lib.rs): op codes of include/helix_hip.h's
+ * hx_unary_op. Rust's f32::{exp, ln, sin, cos, sqrt, abs} lower to libm's expf/logf/sinf/cosf and
+ * the correctly rounded square root; silu = x / (1 + exp(-x)) (lib.rs:1158-1162), sigmoid =
+ * 1 / (1 + exp(-x)) (lib.rs:1172-1178). */
+void oracle_unary(int op, int64_t n, const float* x, float s, float* y) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        float r;
+        switch (op) {
+            case 0: r = expf(v); break;
+            case 1: r = cosf(v); break;
+            case 2: r = sinf(v); break;
+            case 3: r = sqrtf(v); break;
+            case 4: r = v / (1.0f + expf(-v)); break;
+            case 5: r = -v; break;
+            case 6: r = v * s; break;
+            case 7: r = v + s; break;
+            case 8: r = fabsf(v); break;
+            case 9: r = logf(v); break;
+            default: r = 1.0f / (1.0f + expf(-v)); break;
+        }
+        y[i] = r;
+    }
+}
+
+/* ndarray 0.15's unrolled fold over a contiguous slice (numeric_util::unrolled_fold, what
+ * ArrayBase::sum uses for a contiguous lane): eight partial sums p_k over elements i = k mod 8
+ * of the first 8*floor(n/8), acc = 0 + (p0+p4), + (p1+p5), + (p2+p6), + (p3+p7), then the
+ * n mod 8 trailing elements in order. */
+static float unrolled_sum(const float* x, int64_t n) {
+    float p[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int64_t body = n / 8 * 8;
+    for (int64_t i = 0; i < body; i += 8)
+        for (int k = 0; k < 8; ++k) p[k] = p[k] + x[i + k];
+    float acc = 0.0f;
+    acc = acc + (p[0] + p[4]);
+    acc = acc + (p[1] + p[5]);
+    acc = acc + (p[2] + p[6]);
+    acc = acc + (p[3] + p[7]);
+    for (int64_t i = body; i < n; ++i) acc = acc + x[i];
+    return acc;
+}
+
+/* TensorReduce::mean over one axis (backend-cpu/src/lib.rs:995-1010 -> ndarray mean_axis =
+ * sum_axis / len) of x viewed as [outer, len, inner]. ndarray's sum_axis sums each lane with the
+ * unrolled fold when the axis is the array's minimum-stride axis (lane_fold = 1, inner == 1),
+ * else adds the len sub-views in axis order from zero. */
+void oracle_mean_axis(int64_t outer, int64_t len, int64_t inner, int lane_fold, const float* x,
+                      float* y) {
+    for (int64_t o = 0; o < outer; ++o) {
+        if (lane_fold) {
+            y[o] = unrolled_sum(x + o * len, len) / (float)len;
+            continue;
+        }
+        for (int64_t i = 0; i < inner; ++i) {
+            float acc = 0.0f;
+            for (int64_t l = 0; l < len; ++l) acc = acc + x[(o * len + l) * inner + i];
+            y[o * inner + i] = acc / (float)len;
+        }
+    }
+}
+
+/* nn::RMSNorm::forward (crates/nn/src/lib.rs:258-285) as its primitives compute it, with
+ * eps' = eps: ms = mean(x*x, last axis) by the unrolled fold; rms = sqrt(ms + eps);
+ * y = (x / rms) * w. (oracle_rmsnorm above sums the squares sequentially: the two differ by
+ * rounding only.) */
+void oracle_rmsnorm_ref(int64_t R, int64_t Dm, const float* X, const float* w, float eps, float* Y,
+                        float* work) {
+    for (int64_t r = 0; r < R; ++r) {
+        for (int64_t j = 0; j < Dm; ++j) work[j] = X[r * Dm + j] * X[r * Dm + j];
+        const float ms = unrolled_sum(work, Dm) / (float)Dm;
+        const float rms = sqrtf(ms + eps);
+        for (int64_t j = 0; j < Dm; ++j) Y[r * Dm + j] = (X[r * Dm + j] / rms) * w[j];
+    }
+}

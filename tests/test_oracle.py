@@ -465,6 +465,77 @@ def test_rmsnorm_random_eps_is_below_resolution():
         assert rel_err(oracle.rmsnorm(x, w, ej), y0) < 1e-6
 
 
+# ------------------------------------------------------------------ tensor primitives
+
+def test_unary_special_values_and_f64():
+    z = np.zeros(3, F)
+    assert np.all(oracle.unary("exp", z) == 1) and np.all(oracle.unary("cos", z) == 1)
+    assert np.all(oracle.unary("sin", z) == 0) and np.all(oracle.unary("log", np.ones(3, F)) == 0)
+    sq = np.array([0, 1, 4, 9, 1 << 20], F)
+    assert np.array_equal(oracle.unary("sqrt", sq * sq), sq)
+    x = np.random.default_rng(4).standard_normal(10000).astype(F) * F(3)
+    for op, f in (("exp", np.exp), ("sin", np.sin), ("cos", np.cos)):
+        r = f(x.astype(np.float64))
+        g = oracle.unary(op, x).astype(np.float64)
+        ulp = np.spacing(np.abs(r).astype(F)).astype(np.float64)
+        assert np.all(np.abs(g - r) <= ulp), op          # within one f32 ulp of the exact value
+    xd = x.astype(np.float64)
+    assert rel_err(oracle.unary("silu", x), xd / (1 + np.exp(-xd))) < 1e-6
+    assert rel_err(oracle.unary("sigmoid", x), 1 / (1 + np.exp(-xd))) < 1e-6
+    assert np.array_equal(oracle.unary("mul_scalar", x, 0.5), x * F(0.5))
+    assert np.array_equal(oracle.unary("neg", x), -x)
+
+
+def test_mean_axis_closed_forms_and_order():
+    # constant rows and small integers: exact in any order
+    assert np.all(oracle.mean_axis(np.full((3, 24), 2.5, F), 1) == F(2.5))
+    ints = np.arange(40, dtype=F).reshape(4, 10)
+    assert np.array_equal(oracle.mean_axis(ints, 1), ints.sum(1) / F(10))
+    assert np.array_equal(oracle.mean_axis(ints, 0), ints.sum(0) / F(4))
+    # summation order, derived by hand from ndarray's fold: row [1e8, 1, 1, 1, -1e8, 1, 1, 1, 0]
+    # folds to p0 + p4 = 0, then + 2 + 2 + 2 = 6 (sequentially 1e8 absorbs the first three ones: 3)
+    row = np.array([1e8, 1, 1, 1, -1e8, 1, 1, 1, 0], F)
+    assert oracle.mean_axis(row[None, :], 1)[0] == F(6) / F(9)
+    assert oracle.mean_axis(row[:, None], 0)[0] == F(3) / F(9)
+    x = np.random.default_rng(2).standard_normal((5, 37)).astype(F)
+    assert rel_err(oracle.mean_axis(x, 1), x.astype(np.float64).mean(1)) < 1e-5
+
+
+def test_rmsnorm_ref_matches_rmsnorm_to_rounding():
+    x = np.random.default_rng(3).standard_normal((8, 64)).astype(F)
+    w = np.random.default_rng(4).standard_normal(64).astype(F)
+    assert rel_err(oracle.rmsnorm_ref(x, w, 1e-5), oracle.rmsnorm(x, w, 1e-5)) < 1e-6
+
+
+def test_broadcast_to_restatement():
+    rng = np.random.default_rng(6)
+    for src, dst in [((5,), (3, 5)), ((4, 5), (3, 4, 5)), ((1, 5), (2, 3, 5)), ((5,), (2, 3, 5)),
+                     ((2, 3, 1), (2, 3, 7)), ((3,), (2, 2, 2, 3)), ((1, 2, 1, 3), (2, 2, 4, 3))]:
+        x = rng.standard_normal(src).astype(F)
+        assert np.array_equal(oracle.broadcast_to(x, dst), np.broadcast_to(x, dst)), (src, dst)
+    # (1,2) with len == rows == 1: the repeat-columns branch (lib.rs:1405-1419)
+    assert np.array_equal(oracle.broadcast_to(np.array([7], F), (1, 4)), np.full((1, 4), 7, F))
+    # generic index map with a rank gap and a >1 source rank (lib.rs:531-546): target dim j reads
+    # stride self_strides[j] or 1 past the source rank; for [2, 3] -> [1, 1, 2, 3] both source
+    # dims get stride 1, so out[..., r, c] = src_flat[r + c]
+    x = np.arange(6, dtype=F).reshape(2, 3)
+    assert np.array_equal(oracle.broadcast_to(x, (1, 1, 2, 3)).reshape(2, 3),
+                          np.array([[0, 1, 2], [1, 2, 3]], F))
+    with pytest.raises(ValueError):
+        oracle.broadcast_to(np.ones(4, F), (3, 5))
+    with pytest.raises(ValueError):
+        oracle.broadcast_to(np.ones(1, F), (3, 5))   # size-1 vector, R and C > 1
+
+
+def test_stack_restatement():
+    a, b = np.arange(3, dtype=F), np.arange(3, 6, dtype=F)
+    data, field = oracle.stack([a, b], 1)
+    assert field == [3, 2] and np.array_equal(data.reshape(-1), np.arange(6, dtype=F))
+    xs = [np.random.default_rng(k).standard_normal((2, 3, 2, 2)).astype(F) for k in range(3)]
+    data, field = oracle.stack(xs, 2)
+    assert field == [2, 3, 3, 2, 2] and np.array_equal(data, np.stack(xs, 2))
+
+
 def test_planted_mistakes_are_caught():
     x = inputs(1, 50, 4, 16, 6)
     good = oracle.selective_scan(**x)
