@@ -206,6 +206,241 @@ struct BlockWeights {
     const float *conv_w, *conv_b, *dt_bias, *A, *D;
 };
 
+// ----------------------------------------------------------------------------- fused decode
+using namespace ::hx;
+
+// The SSM half of one recurrent decode step of a layer, one block of 512 threads per sequence:
+// the conv window step, x_proj (dt_lo | B | C), dt_proj, the state update with the D skip and
+// the SiLU(z) gate — four launches of the unfused step in one, with every intermediate in LDS or
+// registers instead of HBM. Rounding points are the unfused path's (xc, dt_lo, B, C and dt are
+// rounded to bf16 where that path stores them), so the two differ only in the order of the
+// x_proj and dt_proj sums. A thread owns channel pairs (c, c + 1), c = 2 * tid + 1024 * i.
+//   pass 1: xc = silu(conv_b + sum_j conv_w[c][j] * window[j]) -> LDS; window advanced
+//   x_proj: per 64 outputs j, each thread sums w_x[j][c] * xc[c] over its channels, a butterfly
+//           reduce-scatter leaves output j on lane j of every wave, the 8 waves add through LDS
+//   pass 2: dt[c] = sum_r w_dt[c][r] * dt_lo[r]; dl = softplus(dt + dt_bias); per state n:
+//           h = exp(dl * A[c][n]) * h + dl * xc * B[n]; y = (sum_n C[n] * h + D * xc) * silu(z)
+// State [batch][d_inner][16] fp32 and conv window [batch][d_conv-1][d_inner] fp32 in place.
+constexpr int kDecThreads = 512;
+
+__device__ inline float bf16r(float v) { return bf16_bits_to_f32(Storage<uint16_t>::round(v)); }
+
+template <int KC>
+__global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
+    int d_inner, int dt_rank, const uint16_t* __restrict__ xpart, const uint16_t* __restrict__ z,
+    const float* __restrict__ conv_w, const float* __restrict__ conv_b,
+    float* __restrict__ conv_state, const uint16_t* __restrict__ w_x,
+    const uint16_t* __restrict__ w_dt, const float* __restrict__ dt_bias,
+    const float* __restrict__ A, const float* __restrict__ Dv, float* __restrict__ ssm_state,
+    uint16_t* __restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) float s_dec[];
+    const int J = dt_rank + 32;
+    const int Jp = (J + 63) / 64 * 64;
+    float* s_xc = s_dec;                 // [d_inner]
+    float* s_aux = s_xc + d_inner;       // [3][d_inner]: dt_bias, D, z (staged in pass 1)
+    float* s_dbc = s_aux + 3 * d_inner;  // [Jp]: dt_lo | B | C, bf16-rounded
+    float* s_red = s_dbc + Jp;           // [8][64]
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint16_t* xr = xpart + b * (int64_t)d_inner;
+    float* cst = conv_state + b * (int64_t)(KC - 1) * d_inner;
+
+    // Pass-2 operands of a round of UC channels per group of four lanes (lane part k4 = states
+    // 4k4..4k4+3 and dt_proj ranks 8k4..8k4+7 of the first 32): state, A and the first 16 bytes
+    // of the dt_proj row. The first round is loaded here, before anything else.
+    constexpr int UC = 8;
+    constexpr int CSTEP = kDecThreads / 4;
+    const int k4 = tid & 3;
+    const bool vec_dt = (dt_rank & 31) == 0;
+    float4 hq[UC], aq[UC];
+    uint4 wq[UC];
+    auto load_round = [&](int ch0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int ch = ch0 + u * CSTEP < d_inner ? ch0 + u * CSTEP : d_inner - 1;  // clamped: unused
+            hq[u] = reinterpret_cast<const float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4];
+            aq[u] = reinterpret_cast<const float4*>(A + (int64_t)ch * 16)[k4];
+            if (vec_dt) wq[u] = *reinterpret_cast<const uint4*>(w_dt + (int64_t)ch * dt_rank + 8 * k4);
+        }
+    };
+    load_round(tid >> 2);
+
+    // pass 1: conv window step
+    for (int c = 2 * tid; c < d_inner; c += 2 * kDecThreads) {
+        const uint32_t xw = *reinterpret_cast<const uint32_t*>(xr + c);
+        const float xv[2] = {__uint_as_float(xw << 16), __uint_as_float(xw & 0xffff0000u)};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int ch = c + e;
+            float acc = conv_b ? conv_b[ch] : 0.0f;
+            float wk[KC];
+            if constexpr (KC == 4) {
+                const float4 w4 = reinterpret_cast<const float4*>(conv_w)[ch];
+                wk[0] = w4.x; wk[1] = w4.y; wk[2] = w4.z; wk[3] = w4.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < KC; ++j) wk[j] = conv_w[ch * KC + j];
+            }
+            float prev[KC > 1 ? KC - 1 : 1];
+#pragma unroll
+            for (int j = 0; j < KC - 1; ++j) {
+                prev[j] = cst[(int64_t)j * d_inner + ch];
+                acc = fmaf(wk[j], prev[j], acc);
+            }
+            acc = fmaf(wk[KC - 1], xv[e], acc);
+#pragma unroll
+            for (int j = 0; j + 1 < KC - 1; ++j) cst[(int64_t)j * d_inner + ch] = prev[j + 1];
+            if (KC > 1) cst[(int64_t)(KC - 2) * d_inner + ch] = xv[e];
+            s_xc[ch] = bf16r(silu(acc));
+        }
+        const uint32_t zw = *reinterpret_cast<const uint32_t*>(z + b * (int64_t)d_inner + c);
+        s_aux[c] = dt_bias ? dt_bias[c] : 0.0f;
+        s_aux[c + 1] = dt_bias ? dt_bias[c + 1] : 0.0f;
+        s_aux[d_inner + c] = Dv ? Dv[c] : 0.0f;
+        s_aux[d_inner + c + 1] = Dv ? Dv[c + 1] : 0.0f;
+        s_aux[2 * d_inner + c] = __uint_as_float(zw << 16);
+        s_aux[2 * d_inner + c + 1] = __uint_as_float(zw & 0xffff0000u);
+    }
+    __syncthreads();
+
+    // x_proj: 64 outputs at a time
+    for (int j0 = 0; j0 < J; j0 += 64) {
+        float acc[64];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) acc[j] = 0.0f;
+        for (int c = 2 * tid; c < d_inner; c += 2 * kDecThreads) {
+            const float x0 = s_xc[c], x1 = s_xc[c + 1];
+            // rows past J are clamped to the last one (no branch, so all 64 loads issue at once);
+            // their sums are never stored
+            uint32_t w2[64];
+#pragma unroll
+            for (int j = 0; j < 64; ++j) {
+                const int jr = j0 + j < J ? j0 + j : J - 1;
+                w2[j] = *reinterpret_cast<const uint32_t*>(w_x + (int64_t)jr * d_inner + c);
+            }
+#pragma unroll
+            for (int j = 0; j < 64; ++j) {
+                acc[j] = fmaf(__uint_as_float(w2[j] << 16), x0, acc[j]);
+                acc[j] = fmaf(__uint_as_float(w2[j] & 0xffff0000u), x1, acc[j]);
+            }
+        }
+        // butterfly reduce-scatter across the wave: lane l ends with the wave's sum for j = l
+#pragma unroll
+        for (int k = 32; k >= 1; k >>= 1) {
+            const bool up = (lane & k) != 0;
+#pragma unroll
+            for (int i = 0; i < k; ++i) {
+                const float send = up ? acc[i] : acc[i + k];
+                const float keep = up ? acc[i + k] : acc[i];
+                acc[i] = keep + __shfl_xor(send, k, 64);
+            }
+        }
+        s_red[wave * 64 + lane] = acc[0];
+        __syncthreads();
+        if (tid < 64 && j0 + tid < J) {
+            float t = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kDecThreads / 64; ++w) t += s_red[w * 64 + tid];
+            s_dbc[j0 + tid] = bf16r(t);
+        }
+        __syncthreads();
+    }
+
+    // pass 2: dt_proj, state update, skip and gate (the first round's operands were loaded at
+    // the start of the kernel, under pass 1 and x_proj).
+    const float* dtlo = s_dbc;
+    const float* Bn = s_dbc + dt_rank;
+    const float* Cn = Bn + 16;
+    float bk[4], ck[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { bk[i] = Bn[4 * k4 + i]; ck[i] = Cn[4 * k4 + i]; }
+    for (int ch0 = tid >> 2; ch0 < d_inner; ch0 += UC * CSTEP) {
+        if (ch0 != (tid >> 2)) load_round(ch0);
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int ch = ch0 + u * CSTEP;
+            const int chc = ch < d_inner ? ch : d_inner - 1;
+            float d = 0.0f;
+            if (vec_dt) {
+                const uint32_t ws[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    d = fmaf(__uint_as_float(ws[i] << 16), dtlo[8 * k4 + 2 * i], d);
+                    d = fmaf(__uint_as_float(ws[i] & 0xffff0000u), dtlo[8 * k4 + 2 * i + 1], d);
+                }
+                const uint16_t* wr = w_dt + (int64_t)chc * dt_rank;
+                for (int r0 = 8 * k4 + 32; r0 < dt_rank; r0 += 32) {
+                    const uint4 wv = *reinterpret_cast<const uint4*>(wr + r0);
+                    const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        d = fmaf(__uint_as_float(w4[i] << 16), dtlo[r0 + 2 * i], d);
+                        d = fmaf(__uint_as_float(w4[i] & 0xffff0000u), dtlo[r0 + 2 * i + 1], d);
+                    }
+                }
+            } else {
+                const uint16_t* wr = w_dt + (int64_t)chc * dt_rank;
+                for (int r = k4; r < dt_rank; r += 4) d = fmaf(bf16_bits_to_f32(wr[r]), dtlo[r], d);
+            }
+            d += __shfl_xor(d, 1, 64);
+            d += __shfl_xor(d, 2, 64);
+            if (ch >= d_inner) continue;  // uniform per lane group
+            float dl = bf16r(d) + s_aux[ch];
+            dl = softplus(dl);
+            const float uv = s_xc[ch];
+            const float du = dl * uv;
+            float h4[4] = {hq[u].x, hq[u].y, hq[u].z, hq[u].w};
+            const float a4[4] = {aq[u].x, aq[u].y, aq[u].z, aq[u].w};
+            float yy = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float ab = fast_exp2(dl * (a4[i] * kLog2e));
+                h4[i] = fmaf(ab, h4[i], du * bk[i]);
+                yy = fmaf(ck[i], h4[i], yy);
+            }
+            reinterpret_cast<float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4] =
+                make_float4(h4[0], h4[1], h4[2], h4[3]);
+            yy += __shfl_xor(yy, 1, 64);
+            yy += __shfl_xor(yy, 2, 64);
+            if (k4 == 0) {
+                if (Dv) yy = fmaf(s_aux[d_inner + ch], uv, yy);
+                y[b * (int64_t)d_inner + ch] = Storage<uint16_t>::round(yy * silu(s_aux[2 * d_inner + ch]));
+            }
+        }
+    }
+}
+
+size_t ssm_decode_lds(int64_t d_inner, int64_t dt_rank) {
+    const int64_t J = dt_rank + 32, Jp = (J + 63) / 64 * 64;
+    return (size_t)(4 * d_inner + Jp + 8 * 64) * sizeof(float);
+}
+
+int launch_ssm_decode(int64_t batch, int64_t d_inner, int64_t dt_rank, int64_t d_conv,
+                      const void* xpart, const void* z, const float* conv_w, const float* conv_b,
+                      float* conv_state, const void* w_x, const void* w_dt, const float* dt_bias,
+                      const float* A, const float* D, float* ssm_state, void* y, void* stream) {
+    const size_t lds = ssm_decode_lds(d_inner, dt_rank);
+    HX_REQUIRE(batch <= 0x7fffffff, HX_ERR_UNSUPPORTED, "mamba_layer_decode: batch %lld too large",
+               (long long)batch);
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024 &&
+            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return set_error(HX_ERR_UNSUPPORTED, "mamba_layer_decode: %zu bytes of LDS unavailable", lds);
+        hipLaunchKernelGGL(kern, dim3((unsigned)batch), dim3(kDecThreads), lds, as_stream(stream),
+                           (int)d_inner, (int)dt_rank, (const uint16_t*)xpart, (const uint16_t*)z,
+                           conv_w, conv_b, conv_state, (const uint16_t*)w_x, (const uint16_t*)w_dt,
+                           dt_bias, A, D, ssm_state, (uint16_t*)y);
+        HX_LAUNCH_CHECK();
+        return (int)HX_OK;
+    };
+    switch (d_conv) {
+        case 1: return go(ssm_decode_kernel<1>);
+        case 2: return go(ssm_decode_kernel<2>);
+        case 3: return go(ssm_decode_kernel<3>);
+        default: return go(ssm_decode_kernel<4>);
+    }
+}
+
 struct BlockBufs {
     void *xpart, *z, *xconv, *dt, *y, *dtlo, *B, *C;
 };
@@ -363,18 +598,14 @@ extern "C" int hx_mamba_layer_decode(int64_t batch, int64_t d_model, int64_t d_i
                            HX_BF16, b.xpart, d_inner, d_inner, b.z, d_inner, 2 * d_inner, nullptr,
                            0, stream)))
         return rc;
-    if ((rc = hx_conv1d_step(batch, d_inner, d_conv, HX_BF16, b.xpart, d_inner, w.conv_w, w.conv_b,
-                             conv_state, b.xconv, stream)))
-        return rc;
-    if ((rc = hx_gemm_bf16(batch, dt_rank + 2 * dstate, d_inner, b.xconv, d_inner, w.w_x, d_inner,
-                           nullptr, 0, HX_BF16, b.dtlo, dt_rank, dt_rank, b.B, dstate,
-                           dt_rank + dstate, b.C, dstate, stream)))
-        return rc;
-    if ((rc = hx_gemm_bf16(batch, d_inner, dt_rank, b.dtlo, dt_rank, w.w_dt, dt_rank, nullptr, 0,
-                           HX_BF16, b.dt, d_inner, d_inner, nullptr, 0, d_inner, nullptr, 0, stream)))
-        return rc;
-    if ((rc = hx_selective_state_update(batch, d_inner, dstate, HX_BF16, 1, ssm_state, b.xconv, b.dt,
-                                        w.A, b.B, b.C, w.D, b.z, w.dt_bias, b.y, stream)))
+    // conv step, x_proj, dt_proj, state update and gate in one launch (ssm_decode_kernel)
+    HX_REQUIRE(aligned(ssm_state, 16) && aligned(w.A, 16) && aligned(w.w_x, 4) &&
+                   aligned(w.w_dt, 16) && aligned(w.conv_w, 16),
+               HX_ERR_INVALID_INPUT,
+               "mamba_layer_decode: ssm_state, A, w_dt and conv_w must be 16-byte aligned");
+    if ((rc = launch_ssm_decode(batch, d_inner, dt_rank, d_conv, b.xpart, b.z, w.conv_w, w.conv_b,
+                                conv_state, w.w_x, w.w_dt, w.dt_bias, w.A, w.D, ssm_state, b.y,
+                                stream)))
         return rc;
     return hx_gemm_bf16(batch, d_model, d_inner, b.y, d_inner, w.w_out, d_inner, nullptr, 2, HX_F32,
                         resid, d_model, d_model, nullptr, 0, d_model, nullptr, 0, stream);
