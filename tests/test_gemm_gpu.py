@@ -176,15 +176,21 @@ def test_gemm_splitk_rejects(dev):
                   _ffi.HX_F32, Y.data_ptr(), 32, 32, None, 0, 32, None, 0, 2, ws.data_ptr(), 64, None)
 
 
-@pytest.mark.parametrize("gemm_kernel", [5], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [2, 4, 5], indirect=True)
 @pytest.mark.parametrize("M,N,K", [(2048, 512, 64), (8192, 1024, 256), (12288, 512, 128)])
 def test_gemm_grouped_tile_order(dev, gemm_kernel, M, N, K):
     """Grids whose tiles split evenly into whole row panels per XCD take the grouped tile order
-    (groups of up to 4 row panels; 12288 x 512 gives each XCD 6 panels: a group of 4 and one of
-    2): every output tile is computed exactly once, against the fp32 reference."""
+    (groups of up to 4 row panels; 12288 x 512 gives each XCD 6 panels of 256 rows: a group of 4
+    and one of 2) in the 256 x 256 kernel and both 256 x 128 kernels: every output tile is written
+    (the output starts as NaN) and matches the fp32 reference."""
+    from helixml_amd import _ffi
     g = torch.Generator().manual_seed(M + N + K)
     X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
     W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
-    y = ssm.gemm_bf16(X, W, out_dtype=torch.float32)
+    y = torch.full((M, N), float("nan"), device=dev)
+    _ffi.call("hx_gemm_bf16", M, N, K, X.data_ptr(), K, W.data_ptr(), K, None, 0, _ffi.HX_F32,
+              y.data_ptr(), N, N, None, 0, N, None, 0, None)
     torch.cuda.synchronize()
-    assert norm_err(y.cpu().numpy(), ref(X, W)) <= 1e-5
+    yh = y.cpu().numpy()
+    assert not np.isnan(yh).any()
+    assert norm_err(yh, ref(X, W)) <= 1e-5
