@@ -214,18 +214,44 @@ using namespace ::hx;
 // the SiLU(z) gate — four launches of the unfused step in one, with every intermediate in LDS or
 // registers instead of HBM. Rounding points are the unfused path's (xc, dt_lo, B, C and dt are
 // rounded to bf16 where that path stores them), so the two differ only in the order of the
-// x_proj and dt_proj sums. A thread owns channel pairs (c, c + 1), c = 2 * tid + 1024 * i.
+// x_proj and dt_proj sums.
 //   pass 1: xc = silu(conv_b + sum_j conv_w[c][j] * window[j]) -> LDS; window advanced
-//   x_proj: per 64 outputs j, each thread sums w_x[j][c] * xc[c] over its channels, a butterfly
-//           reduce-scatter leaves output j on lane j of every wave, the 8 waves add through LDS
+//           (a thread owns channel pairs c = 2 tid + 1024 i)
+//   x_proj: 64 outputs at a time; thread (quad q = tid % 256, group g = tid / 256) sums
+//           w_x[j][4q..4q+3] * xc over its channels for 32 outputs j, a butterfly reduce-scatter
+//           leaves one output per lane pair, the 4 waves of a group add through LDS
 //   pass 2: dt[c] = sum_r w_dt[c][r] * dt_lo[r]; dl = softplus(dt + dt_bias); per state n:
 //           h = exp(dl * A[c][n]) * h + dl * xc * B[n]; y = (sum_n C[n] * h + D * xc) * silu(z)
+// The step is a chain of dependent phases, so its time is load latency, not bandwidth: the
+// global loads of the first pass-1 pair, the first x_proj chunk and the first pass-2 round's
+// state are issued at the start, in the order the phases use them (a wait for one load also
+// waits for every memory operation issued before it); A and the dt_proj rows, read by every
+// block and so L2-hot, follow once the x_proj products are done (fewer live registers); the
+// stores all come after those loads.
 // State [batch][d_inner][16] fp32 and conv window [batch][d_conv-1][d_inner] fp32 in place.
 constexpr int kDecThreads = 512;
 
 __device__ inline float bf16r(float v) { return bf16_bits_to_f32(Storage<uint16_t>::round(v)); }
 
-template <int KC>
+// One level of a butterfly reduce-scatter across the wave: K values in acc[0..K) become K / 2,
+// the lanes with bit K set keeping the upper half of the pairwise sums (K a template argument so
+// every index is a constant and acc stays in registers).
+template <int K>
+__device__ inline void rs_level(float* acc, int lane) {
+    const bool up = (lane & K) != 0;
+#pragma unroll
+    for (int i = 0; i < K / 2; ++i) {
+        const float send = up ? acc[i] : acc[i + K / 2];
+        const float keep = up ? acc[i + K / 2] : acc[i];
+        acc[i] = keep + __shfl_xor(send, K, 64);
+    }
+}
+
+// ONE: d_inner <= 1024 and dt_rank <= 32, so each thread has one channel pair in pass 1, one
+// x_proj chunk and one pass-2 round: straight-line code with the loads placed as above. Other
+// shapes loop, and load each pass-2 round's operands at the start of the round (the registers
+// the early loads would hold across the loops are not there).
+template <int KC, bool ONE>
 __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
     int d_inner, int dt_rank, const uint16_t* __restrict__ xpart, const uint16_t* __restrict__ z,
     const float* __restrict__ conv_w, const float* __restrict__ conv_b,
@@ -239,111 +265,141 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
     float* s_xc = s_dec;                 // [d_inner]
     float* s_aux = s_xc + d_inner;       // [3][d_inner]: dt_bias, D, z (staged in pass 1)
     float* s_dbc = s_aux + 3 * d_inner;  // [Jp]: dt_lo | B | C, bf16-rounded
-    float* s_red = s_dbc + Jp;           // [8][64]
+    float* s_red = s_dbc + Jp;           // [8][32]: x_proj wave sums
     const int64_t b = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint16_t* xr = xpart + b * (int64_t)d_inner;
+    const uint16_t* zr = z + b * (int64_t)d_inner;
     float* cst = conv_state + b * (int64_t)(KC - 1) * d_inner;
 
+    // pass-1 operands of channel pair (c, c + 1) (c clamped into range: values then unused)
+    uint32_t p_xw, p_zw;
+    float p_wk[2][KC], p_cb[2], p_prev[KC > 1 ? KC - 1 : 1][2], p_dtb[2], p_dv[2];
+    auto load_p1 = [&](int c) __attribute__((always_inline)) {
+        c = c < d_inner ? c : d_inner - 2;
+        p_xw = *reinterpret_cast<const uint32_t*>(xr + c);
+        p_zw = *reinterpret_cast<const uint32_t*>(zr + c);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            if constexpr (KC == 4) {
+                const float4 w4 = reinterpret_cast<const float4*>(conv_w)[c + e];
+                p_wk[e][0] = w4.x; p_wk[e][1] = w4.y; p_wk[e][2] = w4.z; p_wk[e][3] = w4.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < KC; ++j) p_wk[e][j] = conv_w[(c + e) * KC + j];
+            }
+            p_cb[e] = conv_b ? conv_b[c + e] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < KC - 1; ++j) p_prev[j][e] = cst[(int64_t)j * d_inner + c + e];
+            p_dtb[e] = dt_bias ? dt_bias[c + e] : 0.0f;
+            p_dv[e] = Dv ? Dv[c + e] : 0.0f;
+        }
+    };
+    // x_proj operands: rows j0 + 32 g + jj (clamped to J - 1: sums never stored) of channels
+    // cb + 4q .. +3 (clamped into range: not summed)
+    const int xq = tid & 255, xg = tid >> 8;
+    uint2 wxq[32];
+    auto load_wx = [&](int j0, int cb) __attribute__((always_inline)) {
+        const int c = cb + 4 * xq < d_inner ? cb + 4 * xq : d_inner - 4;
+#pragma unroll
+        for (int jj = 0; jj < 32; ++jj) {
+            const int jr = j0 + 32 * xg + jj < J ? j0 + 32 * xg + jj : J - 1;
+            wxq[jj] = *reinterpret_cast<const uint2*>(w_x + (int64_t)jr * d_inner + c);
+        }
+    };
     // Pass-2 operands of a round of UC channels per group of four lanes (lane part k4 = states
     // 4k4..4k4+3 and dt_proj ranks 8k4..8k4+7 of the first 32): state, A and the first 16 bytes
-    // of the dt_proj row. The first round is loaded here, before anything else.
+    // of the dt_proj row.
     constexpr int UC = 8;
     constexpr int CSTEP = kDecThreads / 4;
     const int k4 = tid & 3;
     const bool vec_dt = (dt_rank & 31) == 0;
     float4 hq[UC], aq[UC];
     uint4 wq[UC];
-    auto load_round = [&](int ch0) __attribute__((always_inline)) {
+    auto load_state = [&](int ch0) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < UC; ++u) {
             const int ch = ch0 + u * CSTEP < d_inner ? ch0 + u * CSTEP : d_inner - 1;  // clamped: unused
             hq[u] = reinterpret_cast<const float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4];
+        }
+    };
+    auto load_aw = [&](int ch0) __attribute__((always_inline)) {  // shared by all blocks: L2-hot
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int ch = ch0 + u * CSTEP < d_inner ? ch0 + u * CSTEP : d_inner - 1;
             aq[u] = reinterpret_cast<const float4*>(A + (int64_t)ch * 16)[k4];
             if (vec_dt) wq[u] = *reinterpret_cast<const uint4*>(w_dt + (int64_t)ch * dt_rank + 8 * k4);
         }
     };
-    load_round(tid >> 2);
+    load_p1(2 * tid);
+    load_wx(0, 0);
+    if constexpr (ONE) load_state(tid >> 2);
 
     // pass 1: conv window step
     for (int c = 2 * tid; c < d_inner; c += 2 * kDecThreads) {
-        const uint32_t xw = *reinterpret_cast<const uint32_t*>(xr + c);
-        const float xv[2] = {__uint_as_float(xw << 16), __uint_as_float(xw & 0xffff0000u)};
+        if (!ONE && c != 2 * tid) load_p1(c);
+        const float xv[2] = {__uint_as_float(p_xw << 16), __uint_as_float(p_xw & 0xffff0000u)};
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const int ch = c + e;
-            float acc = conv_b ? conv_b[ch] : 0.0f;
-            float wk[KC];
-            if constexpr (KC == 4) {
-                const float4 w4 = reinterpret_cast<const float4*>(conv_w)[ch];
-                wk[0] = w4.x; wk[1] = w4.y; wk[2] = w4.z; wk[3] = w4.w;
-            } else {
+            float acc = p_cb[e];
 #pragma unroll
-                for (int j = 0; j < KC; ++j) wk[j] = conv_w[ch * KC + j];
-            }
-            float prev[KC > 1 ? KC - 1 : 1];
+            for (int j = 0; j < KC - 1; ++j) acc = fmaf(p_wk[e][j], p_prev[j][e], acc);
+            acc = fmaf(p_wk[e][KC - 1], xv[e], acc);
 #pragma unroll
-            for (int j = 0; j < KC - 1; ++j) {
-                prev[j] = cst[(int64_t)j * d_inner + ch];
-                acc = fmaf(wk[j], prev[j], acc);
-            }
-            acc = fmaf(wk[KC - 1], xv[e], acc);
-#pragma unroll
-            for (int j = 0; j + 1 < KC - 1; ++j) cst[(int64_t)j * d_inner + ch] = prev[j + 1];
-            if (KC > 1) cst[(int64_t)(KC - 2) * d_inner + ch] = xv[e];
-            s_xc[ch] = bf16r(silu(acc));
+            for (int j = 0; j + 1 < KC - 1; ++j) cst[(int64_t)j * d_inner + c + e] = p_prev[j + 1][e];
+            if (KC > 1) cst[(int64_t)(KC - 2) * d_inner + c + e] = xv[e];
+            s_xc[c + e] = bf16r(silu(acc));
+            s_aux[c + e] = p_dtb[e];
+            s_aux[d_inner + c + e] = p_dv[e];
         }
-        const uint32_t zw = *reinterpret_cast<const uint32_t*>(z + b * (int64_t)d_inner + c);
-        s_aux[c] = dt_bias ? dt_bias[c] : 0.0f;
-        s_aux[c + 1] = dt_bias ? dt_bias[c + 1] : 0.0f;
-        s_aux[d_inner + c] = Dv ? Dv[c] : 0.0f;
-        s_aux[d_inner + c + 1] = Dv ? Dv[c + 1] : 0.0f;
-        s_aux[2 * d_inner + c] = __uint_as_float(zw << 16);
-        s_aux[2 * d_inner + c + 1] = __uint_as_float(zw & 0xffff0000u);
+        s_aux[2 * d_inner + c] = __uint_as_float(p_zw << 16);
+        s_aux[2 * d_inner + c + 1] = __uint_as_float(p_zw & 0xffff0000u);
+        if constexpr (ONE) break;
     }
     __syncthreads();
 
     // x_proj: 64 outputs at a time
+    const int jj_lane = (((lane >> 5) & 1) << 4) | (((lane >> 4) & 1) << 3) | (((lane >> 3) & 1) << 2) |
+                        (((lane >> 2) & 1) << 1) | ((lane >> 1) & 1);
     for (int j0 = 0; j0 < J; j0 += 64) {
-        float acc[64];
+        float acc[32];
 #pragma unroll
-        for (int j = 0; j < 64; ++j) acc[j] = 0.0f;
-        for (int c = 2 * tid; c < d_inner; c += 2 * kDecThreads) {
-            const float x0 = s_xc[c], x1 = s_xc[c + 1];
-            // rows past J are clamped to the last one (no branch, so all 64 loads issue at once);
-            // their sums are never stored
-            uint32_t w2[64];
+        for (int jj = 0; jj < 32; ++jj) acc[jj] = 0.0f;
+        for (int cb = 0; cb < d_inner; cb += 1024) {
+            if (!ONE && (j0 != 0 || cb != 0)) load_wx(j0, cb);
+            const int c = cb + 4 * xq;
+            if (c < d_inner) {
+                const float4 x4 = *reinterpret_cast<const float4*>(s_xc + c);
 #pragma unroll
-            for (int j = 0; j < 64; ++j) {
-                const int jr = j0 + j < J ? j0 + j : J - 1;
-                w2[j] = *reinterpret_cast<const uint32_t*>(w_x + (int64_t)jr * d_inner + c);
+                for (int jj = 0; jj < 32; ++jj) {
+                    acc[jj] = fmaf(__uint_as_float(wxq[jj].x << 16), x4.x, acc[jj]);
+                    acc[jj] = fmaf(__uint_as_float(wxq[jj].x & 0xffff0000u), x4.y, acc[jj]);
+                    acc[jj] = fmaf(__uint_as_float(wxq[jj].y << 16), x4.z, acc[jj]);
+                    acc[jj] = fmaf(__uint_as_float(wxq[jj].y & 0xffff0000u), x4.w, acc[jj]);
+                }
             }
-#pragma unroll
-            for (int j = 0; j < 64; ++j) {
-                acc[j] = fmaf(__uint_as_float(w2[j] << 16), x0, acc[j]);
-                acc[j] = fmaf(__uint_as_float(w2[j] & 0xffff0000u), x1, acc[j]);
-            }
+            if constexpr (ONE) break;
         }
-        // butterfly reduce-scatter across the wave: lane l ends with the wave's sum for j = l
-#pragma unroll
-        for (int k = 32; k >= 1; k >>= 1) {
-            const bool up = (lane & k) != 0;
-#pragma unroll
-            for (int i = 0; i < k; ++i) {
-                const float send = up ? acc[i] : acc[i + k];
-                const float keep = up ? acc[i + k] : acc[i];
-                acc[i] = keep + __shfl_xor(send, k, 64);
-            }
-        }
-        s_red[wave * 64 + lane] = acc[0];
+        if constexpr (ONE) load_aw(tid >> 2);  // under the reductions and barriers that follow
+        // butterfly reduce-scatter across the wave: the lane pair (2i, 2i + 1) ends with the
+        // wave's sum for output jj_lane
+        rs_level<32>(acc, lane);
+        rs_level<16>(acc, lane);
+        rs_level<8>(acc, lane);
+        rs_level<4>(acc, lane);
+        rs_level<2>(acc, lane);
+        acc[0] += __shfl_xor(acc[0], 1, 64);
+        if ((lane & 1) == 0) s_red[wave * 32 + jj_lane] = acc[0];
         __syncthreads();
         if (tid < 64 && j0 + tid < J) {
-            float t = 0.0f;
+            const int g = tid >> 5, jj = tid & 31;
+            float t = s_red[(4 * g) * 32 + jj];
 #pragma unroll
-            for (int w = 0; w < kDecThreads / 64; ++w) t += s_red[w * 64 + tid];
+            for (int w = 1; w < 4; ++w) t += s_red[(4 * g + w) * 32 + jj];
             s_dbc[j0 + tid] = bf16r(t);
         }
         __syncthreads();
+        if constexpr (ONE) break;
     }
 
     // pass 2: dt_proj, state update, skip and gate (the first round's operands were loaded at
@@ -355,7 +411,10 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) { bk[i] = Bn[4 * k4 + i]; ck[i] = Cn[4 * k4 + i]; }
     for (int ch0 = tid >> 2; ch0 < d_inner; ch0 += UC * CSTEP) {
-        if (ch0 != (tid >> 2)) load_round(ch0);
+        if constexpr (!ONE) {  // general shapes: each round's operands at its start
+            load_state(ch0);
+            load_aw(ch0);
+        }
 #pragma unroll
         for (int u = 0; u < UC; ++u) {
             const int ch = ch0 + u * CSTEP;
@@ -369,7 +428,7 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
                     d = fmaf(__uint_as_float(ws[i] & 0xffff0000u), dtlo[8 * k4 + 2 * i + 1], d);
                 }
                 const uint16_t* wr = w_dt + (int64_t)chc * dt_rank;
-                for (int r0 = 8 * k4 + 32; r0 < dt_rank; r0 += 32) {
+                for (int r0 = 8 * k4 + 32; !ONE && r0 < dt_rank; r0 += 32) {
                     const uint4 wv = *reinterpret_cast<const uint4*>(wr + r0);
                     const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
@@ -407,12 +466,13 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
                 y[b * (int64_t)d_inner + ch] = Storage<uint16_t>::round(yy * silu(s_aux[2 * d_inner + ch]));
             }
         }
+        if constexpr (ONE) break;
     }
 }
 
 size_t ssm_decode_lds(int64_t d_inner, int64_t dt_rank) {
     const int64_t J = dt_rank + 32, Jp = (J + 63) / 64 * 64;
-    return (size_t)(4 * d_inner + Jp + 8 * 64) * sizeof(float);
+    return (size_t)(4 * d_inner + Jp + 8 * 32) * sizeof(float);
 }
 
 int launch_ssm_decode(int64_t batch, int64_t d_inner, int64_t dt_rank, int64_t d_conv,
@@ -433,11 +493,19 @@ int launch_ssm_decode(int64_t batch, int64_t d_inner, int64_t dt_rank, int64_t d
         HX_LAUNCH_CHECK();
         return (int)HX_OK;
     };
+    if (d_inner <= 2 * kDecThreads && dt_rank <= 32) {
+        switch (d_conv) {
+            case 1: return go(ssm_decode_kernel<1, true>);
+            case 2: return go(ssm_decode_kernel<2, true>);
+            case 3: return go(ssm_decode_kernel<3, true>);
+            default: return go(ssm_decode_kernel<4, true>);
+        }
+    }
     switch (d_conv) {
-        case 1: return go(ssm_decode_kernel<1>);
-        case 2: return go(ssm_decode_kernel<2>);
-        case 3: return go(ssm_decode_kernel<3>);
-        default: return go(ssm_decode_kernel<4>);
+        case 1: return go(ssm_decode_kernel<1, false>);
+        case 2: return go(ssm_decode_kernel<2, false>);
+        case 3: return go(ssm_decode_kernel<3, false>);
+        default: return go(ssm_decode_kernel<4, false>);
     }
 }
 
@@ -599,10 +667,10 @@ extern "C" int hx_mamba_layer_decode(int64_t batch, int64_t d_model, int64_t d_i
                            0, stream)))
         return rc;
     // conv step, x_proj, dt_proj, state update and gate in one launch (ssm_decode_kernel)
-    HX_REQUIRE(aligned(ssm_state, 16) && aligned(w.A, 16) && aligned(w.w_x, 4) &&
+    HX_REQUIRE(aligned(ssm_state, 16) && aligned(w.A, 16) && aligned(w.w_x, 8) &&
                    aligned(w.w_dt, 16) && aligned(w.conv_w, 16),
                HX_ERR_INVALID_INPUT,
-               "mamba_layer_decode: ssm_state, A, w_dt and conv_w must be 16-byte aligned");
+               "mamba_layer_decode: ssm_state, A, w_dt and conv_w must be 16-byte aligned, w_x 8-byte");
     if ((rc = launch_ssm_decode(batch, d_inner, dt_rank, d_conv, b.xpart, b.z, w.conv_w, w.conv_b,
                                 conv_state, w.w_x, w.w_dt, w.dt_bias, w.A, w.D, ssm_state, b.y,
                                 stream)))
