@@ -14,6 +14,11 @@ Timing: an untimed clock-settle phase (the step back to back for SETTLE_S second
 warmup steps, then exactly K timed steps with a HIP event between consecutive steps; ms_per_step
 is the median step time ("timing" holds the mean, min, max and the settle phase).
 
+Rooflines on the config-2 line: "roofline" = algorithmic bytes per launch / live launch time
+against 8 TB/s, with "traffic" the HBM bytes per launch rocprofv3 measured (profiles/traffic.json);
+"issue_roofline" = the kernel's VALU-busy issue slots per launch (rocprofv3 SQ_ACTIVE_INST_VALU,
+profiles/issue.json) / live launch time, against 1024 SIMDs x 2.4 GHz / 4 cycles per slot.
+
 c1 = BASELINE config 1 (README SSM example shapes): exported MambaBlock MLP + S4Block, fp32.
 
 c3 = BASELINE config 3, the full Mamba block (in_proj, conv1d+SiLU, x_proj, dt_proj, fused scan,
@@ -512,11 +517,32 @@ def main():
         parity = float((np.abs(g - r) / np.maximum(np.abs(r), floor)).max())
 
     traffic = None
+    issue = None
     tfile = os.path.join(ROOT, "profiles", "traffic.json")
-    if args.workload == "c2" and args.variant == 0 and os.path.exists(tfile):
+    tkey = {"c2": SCAN_KERNEL + "@config2", "c4": "selective_scan_fwd@config4"}.get(args.workload)
+    if tkey and args.variant == 0 and os.path.exists(tfile):
         # measured HBM bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)
-        rec_t = json.load(open(tfile)).get(SCAN_KERNEL + "@config2")
+        rec_t = json.load(open(tfile)).get(tkey)
         traffic = rec_t["traffic_bytes"] if rec_t else None
+    ifile = os.path.join(ROOT, "profiles", "issue.json")
+    if args.workload == "c2" and args.variant == 0 and os.path.exists(ifile):
+        # VALU issue roofline: the kernel's VALU-busy issue slots per launch (rocprofv3
+        # SQ_ACTIVE_INST_VALU, 4-cycle units; a transcendental holds 2) over the slots 1024 SIMDs
+        # offer in this launch's live duration at the published peak engine clock (and at the
+        # clock the profiling run measured)
+        rec_i = json.load(open(ifile)).get(SCAN_KERNEL + "@config2")
+        if rec_i:
+            slots = rec_i["valu_busy_slots"]
+            pl = rec_i["per_launch"]
+            clk = pl["SQ_BUSY_CYCLES"] / rec_i["shader_engines"] / (pl["duration_us"] * 1e-6) / 1e9
+            peak = rec_i["simds"] * rec_i["peak_clock_ghz"] / 4  # G slots/s
+            got = slots / (ms * 1e-3) / 1e9
+            issue = {"bound": "valu-issue", "achieved": got, "peak": peak, "unit": "G VALU slots/s",
+                     "frac": got / peak, "slots_per_launch": slots,
+                     "valu_insts_per_launch": pl["SQ_INSTS_VALU"],
+                     "trans_insts_per_launch": pl["SQ_INSTS_VALU_TRANS_F32"],
+                     "measured_clock_ghz": clk,
+                     "frac_at_measured_clock": got / (rec_i["simds"] * clk / 4)}
 
     rec = {
         "metric": "Mamba selective-scan fwd tokens/s + achieved HBM GB/s (% of peak), 1 GPU",
@@ -537,6 +563,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "algorithmic_bytes": nbytes, "kernel_ms": ms},
+        "issue_roofline": issue,
         "timing": timing,
         "cpu_baseline": cpu,
         "parity_max_rel_err": parity,
