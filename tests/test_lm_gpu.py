@@ -148,6 +148,31 @@ def test_lm_prefill_and_decode_vs_oracle(dev):
     assert err <= 1e-2, err
 
 
+@pytest.mark.parametrize("dm,di,r,K", [(640, 1280, 40, 4), (512, 1024, 64, 3)])
+def test_lm_decode_general_shapes(dev, dm, di, r, K):
+    """The fused decode step's general form: d_inner above 1024 (two pass-1 pairs and two pass-2
+    rounds per thread, two x_proj channel blocks) with a dt_rank that is no multiple of 32 (element
+    dt_proj loads), and dt_rank 64 (two x_proj output chunks, 16-byte dt_proj rows over two rank
+    blocks) with a width-3 conv. Two decode steps against the oracle; decode continues the
+    prefill."""
+    P = lm_params(2, dm, di, 16, r, K, 256, seed=dm + r)
+    m = model_from(P, dev, dt_rank=r, K=K)
+    tok = np.random.default_rng(di).integers(0, 256, (3, 8)).astype(np.int32)
+    td = torch.from_numpy(tok).to(dev)
+    print(f"case decode d_model {dm} d_inner {di} dt_rank {r} conv {K}", flush=True)
+    _, state = m.prefill(td[:, :6])
+    _, rstate = oracle.lm_prefill(tok[:, :6], P, r)
+    for t in (6, 7):
+        lg = m.decode_step(td[:, t].contiguous(), state)
+        torch.cuda.synchronize()
+        rl, rstate = oracle.lm_decode_step(tok[:, t], P, rstate, r)
+        err = norm_err(lg.cpu().numpy(), rl)
+        assert err <= 1e-2, (t, err)
+    full, _ = m.prefill(td)
+    err = norm_err(lg.cpu().numpy(), full[:, 7].cpu().numpy())
+    assert err <= 1e-2, err
+
+
 def test_lm_config5_full_size(dev):
     """12 layers, d_model 512, d_inner 1024, N 16, dt_rank 32, conv 4, vocab
     256, batch 16 x L 8192 prefill, then one decode step for all 16 sequences. The oracle checks
