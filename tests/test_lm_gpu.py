@@ -258,8 +258,8 @@ def test_decode_graph_survives_workspace_growth(dev):
 def test_lm_config5_decode_batch256(dev):
     """BASELINE config 5's decode leg at its own batch (256): the full 12-layer model prefills 24
     tokens per sequence, then one eager decode step and one replay of the captured step (from a
-    copy of the same state). At M = 256 the projections take the small split-K GEMM path, not
-    the one batch 16 takes. The oracle checks two sequences (first and last); the eager step
+    copy of the same state). At M = 256 in_proj takes the small-M GEMM's 64-wide tiles (batch 16
+    takes its 32-wide ones). The oracle checks two sequences (first and last); the eager step
     and the graph replay agree bit for bit; decode after a 23-token prefill continues it (equals
     the 24-token prefill's last position within the bf16 bar).
 
