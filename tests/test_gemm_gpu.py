@@ -74,9 +74,10 @@ def gemm_kernel(dev, request):
                                    (600, 136, 128)])
 @pytest.mark.parametrize("act", [0, 1])
 def test_gemm_tile_kernels_fp32_out(dev, gemm_kernel, M, N, K, act):
-    """Each tile kernel (128 x 128 x 32, 256 x 128 x 64 register-staged, split-K 32 x 64, 256 x
-    128 x 64 direct-to-LDS) on aligned and ragged shapes; the direct-to-LDS kernel takes the
-    shapes with K % 64 == 0 (1, 2, 3 and more K tiles) and falls back on the others."""
+    """Each tile kernel (128 x 128 x 32, 256 x 128 x 64 register-staged, the small-M kernel's
+    32 x 32 / 32 x 64 tiles with K split over 4 waves, 256 x 128 x 64 direct-to-LDS, 256 x 256)
+    on aligned and ragged shapes; the direct-to-LDS kernels take the shapes with K % 64 (or 32)
+    == 0 (1, 2, 3 and more K tiles) and fall back on the others."""
     g = torch.Generator().manual_seed(M + N + K)
     X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
     W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
