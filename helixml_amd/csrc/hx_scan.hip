@@ -1450,8 +1450,8 @@ int scan_entry(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, int d
             if (init_state)
                 HX_HIP_CHECK(hipMemcpyAsync(last_state, init_state, bytes, hipMemcpyDeviceToDevice,
                                             as_stream(stream)));
-            else
-                HX_HIP_CHECK(hipMemsetAsync(last_state, 0, bytes, as_stream(stream)));
+            else  // a fill kernel, not a memset (this call may be captured into a graph)
+                return hx_fill_f32((int64_t)(bytes / sizeof(float)), 0.0f, last_state, stream);
         }
         return HX_OK;
     }

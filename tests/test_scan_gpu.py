@@ -138,6 +138,23 @@ def test_scan_zero_length_returns_initial_state(dev):
     assert np.array_equal(s, init)
 
 
+def test_scan_zero_length_without_initial_state_writes_zeros(dev):
+    """No initial state: the final state is zero, written by a fill kernel (the output starts as
+    NaN, so a skipped write shows), through the plain and the no-allocation entry points."""
+    from helixml_amd import _ffi
+    x = {k: to_dev(v, dev) for k, v in scan_inputs(2, 0, 8, 16, seed=12).items()}
+    out = torch.empty((2, 0, 8), device=dev)
+    for entry in ("hx_selective_scan_fwd", "hx_selective_scan_fwd_noalloc"):
+        last = torch.full((2, 8, 16), float("nan"), device=dev)
+        args = [2, 0, 8, 16, _ffi.HX_F32, 1] + [x[k].data_ptr() if x[k] is not None else None
+                                                for k in ("u", "delta", "A", "B", "C", "D", "z",
+                                                          "dt_bias")]
+        _ffi.call(entry, *args, out.data_ptr(), None, last.data_ptr(),
+                  torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(last, torch.zeros_like(last)), entry
+
+
 @pytest.mark.parametrize("variant", VARIANTS)
 @pytest.mark.parametrize("shape", [(2, 37, 70, 16), (1, 300, 256, 16)], ids=str)
 def test_scan_bf16_storage(dev, variant, shape):
