@@ -31,34 +31,196 @@ constexpr int kMaxState = 64;
 
 // ---------------------------------------------------------------- ref mode, step 1
 // U[t][n] = sum_m Bd[n][m] * x[m][t], m ascending (CpuTensor 2-D x 1-D matmul,
-// backend-cpu/src/lib.rs:728-735). One thread per t; Bd rows are wave-uniform (scalar loads).
-template <int NS>
-__global__ __launch_bounds__(256) void s4_input_proj_kernel(int64_t M, int64_t L, int64_t N,
-                                                            const float* __restrict__ x,
-                                                            const float* __restrict__ Bd,
-                                                            float* __restrict__ U) {
-#pragma clang fp contract(off)
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= L) return;
-    float acc[NS];
-#pragma unroll
-    for (int n = 0; n < NS; ++n) acc[n] = 0.0f;
-    for (int64_t m = 0; m < M; ++m) {
-        const float xv = x[m * L + t];
-#pragma unroll
-        for (int n = 0; n < NS; ++n)
-            if (n < N) acc[n] = __fadd_rn(acc[n], __fmul_rn(Bd[n * M + m], xv));
-    }
-#pragma unroll
-    for (int n = 0; n < NS; ++n)
-        if (n < N) U[t * N + n] = acc[n];
+// backend-cpu/src/lib.rs:728-735); every product and sum rounded separately.
+// A block owns 256 steps (one per thread) and one group of 8 states (blockIdx.y). Rows of x
+// stream through a 4-slot LDS ring of 16 rows x 256 steps, loaded straight to LDS three slots
+// ahead. Bd arrives transposed and zero-padded to whole groups ([m][Np], Np = 8 x groups), so a
+// row's 8 values are one uniform (scalar) load. A 16-state model runs as two blocks per CU:
+// each SIMD holds two waves that cover each other's waits.
+constexpr int kPjRows = 16, kPjSlots = 4, kPjT = 256;
+
+typedef float hx_f32x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)p; }
+
+// v[k] = the float at LDS byte offset a + (R0 + k) * 1024, k < 4 (rows R0..R0+3 of a ring slot).
+// Written as inline asm that completes inside the statement: a compiler-visible LDS read would
+// make the compiler wait for every outstanding global_load_lds first (vmcnt(0)), draining the
+// ring; the ring is ordered by the explicit vmcnt waits and barriers instead.
+template <int R0>
+__device__ inline void lds_rows4(uint32_t a, float (&v)[4]) {
+    hx_f32x2 r0, r1;
+    asm volatile(
+        "ds_read2st64_b32 %0, %2 offset0:%3 offset1:%4\n\t"
+        "ds_read2st64_b32 %1, %2 offset0:%5 offset1:%6\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r0), "=&v"(r1)
+        : "v"(a), "n"(4 * R0), "n"(4 * R0 + 4), "n"(4 * R0 + 8), "n"(4 * R0 + 12)
+        : "memory");
+    v[0] = r0[0]; v[1] = r0[1]; v[2] = r1[0]; v[3] = r1[1];
+}
+__device__ inline float lds_row1(uint32_t a) {
+    float v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a) : "memory");
+    return v;
 }
 
-// Bd = B * dt (mul_scalar, ssm.rs:130), rounded once like the reference.
-__global__ void s4_scale_kernel(int64_t n, float dt, const float* __restrict__ B,
-                                float* __restrict__ Bd) {
+// VB = bytes per lane of each global_load_lds: 16 (L % 4 == 0, x 16-byte aligned) or 4.
+template <int VB>
+__global__ __launch_bounds__(256) void s4_input_proj_kernel(int64_t M, int64_t L, int64_t N,
+                                                            int64_t Np,
+                                                            const float* __restrict__ x,
+                                                            const float* __restrict__ BdT,
+                                                            float* __restrict__ U) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float ring[kPjSlots][kPjRows][kPjT];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t t0 = (int64_t)blockIdx.x * kPjT;
+    const int g = blockIdx.y;
+    const float* bd = BdT + 8 * g;
+    const int nch = (int)((M + kPjRows - 1) / kPjRows);
+    // loads per wave per chunk: wave w fills rows 4w..4w+3 (VB 16: one 1 KB load per row, VB 4:
+    // four 256-byte loads per row). Every chunk index issues the same number (rows past M are
+    // clamped to row M-1), so one wait count serves every chunk.
+    constexpr int P = VB == 16 ? 4 : 16;
+    constexpr int WAITN = P * (kPjSlots - 2);
+    static_assert(WAITN <= 63, "vmcnt range");
+    // chunks are issued in order q = 0, 1, 2, ...: the wave's first row of chunk q is xr, moved
+    // on 16 rows per chunk; rows past M read row M-1
+    const float* xr = x + (int64_t)(4 * w) * L;
+    const float* const xlast = x + (M - 1) * L;
+    int64_t loff[VB == 16 ? 1 : 4];  // lane's column offsets (floats), clamped into the row
+    if constexpr (VB == 16) {
+        loff[0] = min(t0 + 4 * lane, L - 4);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) loff[j] = min(t0 + 64 * j + lane, L - 1);
+    }
+    auto issue = [&](int q) __attribute__((always_inline)) {
+        float* dst = &ring[q % kPjSlots][4 * w][0];
+        const float* src = xr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float* row = src > xlast ? xlast : src;
+            if constexpr (VB == 16) {
+                __builtin_amdgcn_global_load_lds((gvoid_t*)(row + loff[0]), (lvoid_t*)dst, 16, 0, 0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    __builtin_amdgcn_global_load_lds((gvoid_t*)(row + loff[j]), (lvoid_t*)(dst + 64 * j),
+                                                     4, 0, 0);
+            }
+            src += L;
+            dst += kPjT;
+        }
+        xr += kPjRows * L;
+    };
+#pragma unroll
+    for (int q = 0; q < kPjSlots - 1; ++q) issue(q);
+    float acc[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc[n] = 0.0f;
+    // Bd rows as uniform loads through the constant address space, which the compiler always
+    // turns into scalar loads (a global pointer is only scalar-loaded where it can prove no
+    // store in the kernel clobbers it, and gives up on long loop bodies).
+    typedef float f32x8 __attribute__((ext_vector_type(8)));
+    typedef const __attribute__((address_space(4))) float cfloat;
+    typedef const __attribute__((address_space(4))) f32x8 cf32x8;
+    auto rows4 = [&](const cfloat* r, f32x8 (&b)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = *(const cf32x8*)(r + j * Np);
+    };
+    // The LDS read of a group also waits for the group's Bd rows (loaded before it); this
+    // empty asm tells the compiler so, or it would wait again after the next group's loads.
+    auto landed = [&](const f32x8 (&b)[4]) __attribute__((always_inline)) {
+        asm volatile("" ::"s"(b[0]), "s"(b[1]), "s"(b[2]), "s"(b[3]));
+    };
+    // the next group's row pointer comes out of an empty asm placed after the current group's
+    // LDS read, so its loads are not hoisted further; the empty asm after each group's sums
+    // keeps them before the next LDS read. At most two groups of Bd rows live in scalar registers.
+    auto next_rows = [&](const cfloat*& r) __attribute__((always_inline)) {
+        r += 4 * Np;
+        asm volatile("" : "+s"(r));
+    };
+    auto acc4 = [&](const f32x8 (&b)[4], const float (&xv)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // a row's 8 products, then its 8 sums: no add waits on the product just issued
+            float pr[8];
+#pragma unroll
+            for (int n = 0; n < 8; ++n) pr[n] = __fmul_rn(b[j][n], xv[j]);
+            asm volatile("" : "+v"(pr[0]), "+v"(pr[1]), "+v"(pr[2]), "+v"(pr[3]), "+v"(pr[4]),
+                         "+v"(pr[5]), "+v"(pr[6]), "+v"(pr[7]));
+#pragma unroll
+            for (int n = 0; n < 8; ++n) acc[n] = __fadd_rn(acc[n], pr[n]);
+        }
+        asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]),
+                     "+v"(acc[5]), "+v"(acc[6]), "+v"(acc[7]));
+    };
+    const uint32_t xbase = lds_off(&ring[0][0][tid]);
+    for (int c = 0; c < nch; ++c) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");  // own loads of chunk c
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // everyone's; c-1 read
+        issue(c + kPjSlots - 1);  // into the slot of chunk c-1
+        const uint32_t a = xbase + (uint32_t)(c % kPjSlots) * (kPjRows * kPjT * 4);
+        const int64_t m0 = (int64_t)c * kPjRows;
+        if (m0 + kPjRows <= M) {
+            f32x8 bA[4], bB[4];
+            float xv[4];
+            const cfloat* r = (const cfloat*)(bd + m0 * Np);
+            rows4(r, bA);
+            lds_rows4<0>(a, xv);
+            landed(bA);
+            next_rows(r);
+            rows4(r, bB);
+            __builtin_amdgcn_sched_barrier(0);  // the scalar loads issue before the sums
+            acc4(bA, xv);
+            lds_rows4<4>(a, xv);
+            landed(bB);
+            next_rows(r);
+            rows4(r, bA);
+            __builtin_amdgcn_sched_barrier(0);
+            acc4(bB, xv);
+            lds_rows4<8>(a, xv);
+            landed(bA);
+            next_rows(r);
+            rows4(r, bB);
+            __builtin_amdgcn_sched_barrier(0);
+            acc4(bA, xv);
+            lds_rows4<12>(a, xv);
+            landed(bB);
+            acc4(bB, xv);
+        } else {
+            for (int r = 0; m0 + r < M; ++r) {
+                const float xv = lds_row1(a + r * (kPjT * 4));
+                const float* br = bd + (m0 + r) * Np;
+#pragma unroll
+                for (int n = 0; n < 8; ++n) acc[n] = __fadd_rn(acc[n], __fmul_rn(br[n], xv));
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load still writing LDS at exit
+    const int64_t t = t0 + tid;
+    if (t >= L) return;
+    float* u = U + t * N + 8 * g;
+    if ((N & 3) == 0 && 8 * g + 8 <= N) {
+        reinterpret_cast<float4*>(u)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        reinterpret_cast<float4*>(u)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    } else {
+#pragma unroll
+        for (int n = 0; n < 8; ++n)
+            if (8 * g + n < N) u[n] = acc[n];
+    }
+}
+
+// BdT[m][n] = B[n][m] * dt for n < N, 0 for N <= n < Np (mul_scalar, ssm.rs:130), rounded once
+// like the reference; transposed and padded for the projection's scalar loads.
+__global__ void s4_scale_kernel(int64_t M, int64_t N, int64_t Np, float dt,
+                                const float* __restrict__ B, float* __restrict__ BdT) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) Bd[i] = __fmul_rn(B[i], dt);
+    if (i >= M * Np) return;
+    const int64_t m = i / Np, n = i % Np;
+    BdT[i] = n < N ? __fmul_rn(B[n * M + m], dt) : 0.0f;
 }
 
 // ---------------------------------------------------------------- ref mode, step 2
@@ -87,6 +249,122 @@ __global__ __launch_bounds__(64) void s4_scan_seq_kernel(int64_t L, int64_t N,
     for (; t < L; ++t) {
         h = __fadd_rn(__fmul_rn(an, h), H[t * N + n]);
         H[t * N + n] = h;
+    }
+}
+
+// The same recurrence with its operands kept in LDS (N a power of two <= 64, L * N % 4 == 0).
+// Wave 0 runs the N chains, one lane per state, with the same rounded a*h then +u per step;
+// the chain is bound by the latency of its dependent multiply and add, so everything else it
+// issues is kept to one 16-byte LDS read and one write per 4 steps. Waves 1 and 2 (each on its
+// own SIMD) stream H through a 3-slot LDS ring of 4096-float chunks (CH = 4096 / N steps),
+// transposed to state-major rows [n][t] (row stride CH + 4) so a chain lane reads and writes
+// 4 steps per LDS access, and write finished chunks back step-major. Between barriers i and
+// i+1 the chain runs chunk i in place while the helpers write chunk i-1 back, move chunk i+1
+// (loaded two chunks earlier) from registers into its slot, and issue the loads of chunk i+3.
+constexpr int kChunkF = 4096, kChainHelpers = 2;
+constexpr int kSlotF = kChunkF + 4 * 64;  // N rows of CH + 4 floats, N <= 64
+constexpr int kHelperF4 = kChunkF / 4 / (64 * kChainHelpers);  // float4 per helper lane per chunk
+
+__global__ __launch_bounds__(64 * (1 + kChainHelpers)) void s4_scan_stream_kernel(
+    int64_t L, int lgN, const float* __restrict__ a, float* __restrict__ H) {
+#pragma clang fp contract(off)
+    // 32 floats past the last slot: the chain's read-ahead past the end of a row stays inside
+    __shared__ __attribute__((aligned(16))) float ring[3 * kSlotF + 32];
+    const int N = 1 << lgN, CH = kChunkF >> lgN, S = CH + 4;
+    const int tid = threadIdx.x;
+    const int64_t total = L << lgN;  // floats of H
+    const int nch = (int)((total + kChunkF - 1) / kChunkF);
+    if (tid < 64) {
+        const int n = tid;
+        const float an = a[min(n, N - 1)];
+        asm volatile("" ::"v"(an));  // the load completes here, not inside the step loop
+        float h = 0.0f;
+        lds_barrier();  // chunk 0 in its slot
+        for (int i = 0; i < nch; ++i) {
+            if (n < N) {
+                // Steps past L at the end of the last chunk run on stale values and are not
+                // stored. The read-ahead of the last 32 steps of a row reads the next row or
+                // slot (values unused).
+                float* row = (float*)__builtin_assume_aligned(ring + (i % 3) * kSlotF + n * S, 16);
+                float4 A[4], B[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    A[k] = *reinterpret_cast<const float4*>(row + 4 * k);
+                    B[k] = *reinterpret_cast<const float4*>(row + 16 + 4 * k);
+                }
+                // 16 steps from U in place at row + tt, then U takes the 16 steps 32 on
+                auto batch = [&](float4 (&U)[4], int tt) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        float4 o;
+                        h = __fadd_rn(__fmul_rn(an, h), U[k].x); o.x = h;
+                        h = __fadd_rn(__fmul_rn(an, h), U[k].y); o.y = h;
+                        h = __fadd_rn(__fmul_rn(an, h), U[k].z); o.z = h;
+                        h = __fadd_rn(__fmul_rn(an, h), U[k].w); o.w = h;
+                        *reinterpret_cast<float4*>(row + tt + 4 * k) = o;
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        U[k] = *reinterpret_cast<const float4*>(row + tt + 32 + 4 * k);
+                };
+                for (int tt = 0; tt < CH; tt += 32) {
+                    batch(A, tt);
+                    batch(B, tt + 16);
+                }
+            }
+            lds_barrier();
+        }
+        return;
+    }
+    const int hl = tid - 64;  // float4 j = hl + 64 * kChainHelpers * k of a chunk
+    float4 ra[kHelperF4], rb[kHelperF4];  // registers of even / odd chunks
+    auto fidx = [&](int k) { return 4 * (hl + 64 * kChainHelpers * k); };
+    auto load = [&](float4 (&r)[kHelperF4], int q) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < kHelperF4; ++k) {
+            // past the end: a clamped in-bounds load; those steps are never stored
+            const int64_t f = min((int64_t)q * kChunkF + fidx(k), total - 4);
+            r[k] = *reinterpret_cast<const float4*>(H + f);
+        }
+    };
+    auto put = [&](const float4 (&r)[kHelperF4], int q) __attribute__((always_inline)) {
+        float* slot = ring + (q % 3) * kSlotF;
+#pragma unroll
+        for (int k = 0; k < kHelperF4; ++k) {
+            const int j = fidx(k);
+            const float v[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) slot[((j + e) & (N - 1)) * S + ((j + e) >> lgN)] = v[e];
+        }
+    };
+    auto flush = [&](int q) __attribute__((always_inline)) {
+        const float* slot = ring + (q % 3) * kSlotF;
+#pragma unroll
+        for (int k = 0; k < kHelperF4; ++k) {
+            const int j = fidx(k);
+            const int64_t f = (int64_t)q * kChunkF + j;
+            if (f >= total) continue;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = slot[((j + e) & (N - 1)) * S + ((j + e) >> lgN)];
+            *reinterpret_cast<float4*>(H + f) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    };
+    // iteration i, cur = registers of chunk i+1 (parity of i+1)
+    auto iter = [&](int i, float4 (&cur)[kHelperF4]) __attribute__((always_inline)) {
+        if (i + 1 < nch) put(cur, i + 1);
+        load(cur, i + 3);
+        if (i >= 1) flush(i - 1);
+        if (i < nch) lds_barrier();
+    };
+    load(ra, 0);
+    load(rb, 1);
+    put(ra, 0);
+    load(ra, 2);
+    lds_barrier();
+    for (int i = 0; i <= nch; i += 2) {
+        iter(i, rb);
+        if (i + 1 <= nch) iter(i + 1, ra);
     }
 }
 
@@ -139,6 +417,68 @@ __global__ __launch_bounds__(256) void s4_output_kernel(int64_t M, int64_t L, in
         float v = __fadd_rn(o, __fmul_rn(dd, sx[mm][tt]));
         if (gate) v = __fmul_rn(v, g);
         y[t * M + m] = v;
+    }
+}
+
+// The same sums with H rows as scalar operands (N = 4, 8 or 16, L % 4 == 0, x 16-byte
+// aligned): a block owns 64 channels x 64 steps; lane = channel holds C[m][0..N-1] in
+// registers, x is transposed through LDS, and a wave reads the H rows of each group of 4 steps
+// as uniform (scalar) loads, so no LDS traffic is spent broadcasting them.
+constexpr int kOutM = 64, kOutT = 64, kOutS = kOutT + 4;
+
+template <int N>
+__global__ __launch_bounds__(256) void s4_output_sgpr_kernel(int64_t M, int64_t L,
+                                                             const float* __restrict__ x,
+                                                             const float* __restrict__ H,
+                                                             const float* __restrict__ C,
+                                                             const float* __restrict__ D,
+                                                             const float* __restrict__ gate,
+                                                             float* __restrict__ y) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float sx[kOutM][kOutS];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t m0 = (int64_t)blockIdx.x * kOutM, t0 = (int64_t)blockIdx.y * kOutT;
+#pragma unroll
+    for (int k = 0; k < kOutM * kOutT / 4 / 256; ++k) {
+        const int i = tid + 256 * k;
+        const int r = i / (kOutT / 4), q = i % (kOutT / 4);
+        const int64_t m = m0 + r, t = t0 + 4 * q;
+        const float4 v = (m < M && t < L) ? *reinterpret_cast<const float4*>(x + m * L + t)
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4*>(&sx[r][4 * q]) = v;
+    }
+    __syncthreads();
+    const int64_t m = m0 + lane;
+    const bool live = m < M;
+    const int64_t mc = live ? m : M - 1;
+    float c[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) c[n] = C[mc * N + n];
+    const float dd = D[mc];
+    const float g = gate ? gate[mc] : 1.0f;
+    for (int gi = w; gi < kOutT / 4; gi += 4) {
+        const int64_t tb = t0 + 4 * gi;
+        if (tb >= L) break;
+        const float4 x4 = *reinterpret_cast<const float4*>(&sx[lane][4 * gi]);
+        const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+        // L % 4 == 0, so all 4 steps of a group are in range; the 4 sums run interleaved
+        float hv[4][N];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int n = 0; n < N; ++n) hv[e][n] = H[(tb + e) * N + n];
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = __fadd_rn(o[e], __fmul_rn(c[n], hv[e][n]));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float v = __fadd_rn(o[e], __fmul_rn(dd, xv[e]));
+            if (gate) v = __fmul_rn(v, g);
+            if (live) y[(tb + e) * M + m] = v;
+        }
     }
 }
 
@@ -653,8 +993,11 @@ namespace hx {
 namespace {
 // Workspace layout of the reference-mode path: Bd [N][M] | H [L][N], each 256-byte aligned.
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+// states padded to whole groups of 8 (the projection's transposed Bd rows)
+int64_t s4_ref_np(int64_t N) { return 8 * ((N + 7) / 8); }
 size_t s4_ref_ws_bytes(int64_t M, int64_t N, int64_t L) {
-    return align256((size_t)N * M * sizeof(float)) + align256((size_t)L * N * sizeof(float));
+    return align256((size_t)s4_ref_np(N) * M * sizeof(float)) +
+           align256((size_t)L * N * sizeof(float));
 }
 }  // namespace
 }  // namespace hx
@@ -702,26 +1045,52 @@ extern "C" int hx_s4_ref_fwd(int64_t d_model, int64_t dstate, int64_t seqlen, fl
                "s4_ref: workspace of %zu bytes (256-byte aligned) needed, %zu given", need,
                workspace ? workspace_bytes : (size_t)0);
     hipStream_t s = as_stream(stream);
-    float* Bd = (float*)workspace;
-    float* H = (float*)((char*)workspace + align256((size_t)dstate * d_model * sizeof(float)));
-    const size_t n_bd = (size_t)dstate * d_model;
+    const int64_t Np = s4_ref_np(dstate);
+    float* BdT = (float*)workspace;
+    float* H = (float*)((char*)workspace + align256((size_t)Np * d_model * sizeof(float)));
+    const size_t n_bd = (size_t)Np * d_model;
     hipLaunchKernelGGL(s4_scale_kernel, dim3((unsigned)((n_bd + 255) / 256)), dim3(256), 0, s,
-                       (int64_t)n_bd, dt, B, Bd);
-    dim3 g1((unsigned)((seqlen + 255) / 256));
-    if (dstate <= 16)
+                       d_model, dstate, Np, dt, B, BdT);
+    const dim3 g1((unsigned)((seqlen + kPjT - 1) / kPjT), (unsigned)(Np / 8));
+    if (seqlen % 4 == 0 && aligned(x, 16))
         hipLaunchKernelGGL(s4_input_proj_kernel<16>, g1, dim3(256), 0, s, d_model, seqlen, dstate,
-                           x, Bd, H);
+                           Np, x, BdT, H);
     else
-        hipLaunchKernelGGL(s4_input_proj_kernel<kMaxState>, g1, dim3(256), 0, s, d_model, seqlen,
-                           dstate, x, Bd, H);
-    hipLaunchKernelGGL(s4_scan_seq_kernel, dim3(1), dim3(64), 0, s, seqlen, dstate, a, H);
-    dim3 g3((unsigned)((d_model + kTileM - 1) / kTileM), (unsigned)((seqlen + kTileT - 1) / kTileT));
-    if (dstate <= 16)
-        hipLaunchKernelGGL(s4_output_kernel<16>, g3, dim3(256), 0, s, d_model, seqlen, dstate, x,
-                           H, C, D, gate, y);
-    else
-        hipLaunchKernelGGL(s4_output_kernel<kMaxState>, g3, dim3(256), 0, s, d_model, seqlen,
-                           dstate, x, H, C, D, gate, y);
+        hipLaunchKernelGGL(s4_input_proj_kernel<4>, g1, dim3(256), 0, s, d_model, seqlen, dstate,
+                           Np, x, BdT, H);
+    const bool pow2 = (dstate & (dstate - 1)) == 0;
+    if (pow2 && (seqlen * dstate) % 4 == 0) {
+        int lgN = 0;
+        while ((1 << lgN) < dstate) ++lgN;
+        hipLaunchKernelGGL(s4_scan_stream_kernel, dim3(1), dim3(64 * (1 + kChainHelpers)), 0, s,
+                           seqlen, lgN, a, H);
+    } else {
+        hipLaunchKernelGGL(s4_scan_seq_kernel, dim3(1), dim3(64), 0, s, seqlen, dstate, a, H);
+    }
+    const bool fast_out = seqlen % 4 == 0 && aligned(x, 16) &&
+                          (dstate == 4 || dstate == 8 || dstate == 16);
+    if (fast_out) {
+        const dim3 g3((unsigned)((d_model + kOutM - 1) / kOutM),
+                      (unsigned)((seqlen + kOutT - 1) / kOutT));
+        if (dstate == 4)
+            hipLaunchKernelGGL(s4_output_sgpr_kernel<4>, g3, dim3(256), 0, s, d_model, seqlen, x,
+                               H, C, D, gate, y);
+        else if (dstate == 8)
+            hipLaunchKernelGGL(s4_output_sgpr_kernel<8>, g3, dim3(256), 0, s, d_model, seqlen, x,
+                               H, C, D, gate, y);
+        else
+            hipLaunchKernelGGL(s4_output_sgpr_kernel<16>, g3, dim3(256), 0, s, d_model, seqlen, x,
+                               H, C, D, gate, y);
+    } else {
+        const dim3 g3((unsigned)((d_model + kTileM - 1) / kTileM),
+                      (unsigned)((seqlen + kTileT - 1) / kTileT));
+        if (dstate <= 16)
+            hipLaunchKernelGGL(s4_output_kernel<16>, g3, dim3(256), 0, s, d_model, seqlen, dstate,
+                               x, H, C, D, gate, y);
+        else
+            hipLaunchKernelGGL(s4_output_kernel<kMaxState>, g3, dim3(256), 0, s, d_model, seqlen,
+                               dstate, x, H, C, D, gate, y);
+    }
     HX_LAUNCH_CHECK();
     return HX_OK;
 }

@@ -81,6 +81,36 @@ def test_s4_ref_bit_exact(dev, M, N, L):
     assert np.array_equal(g, r), f"max abs diff {np.abs(g - r).max()}"
 
 
+# Each case takes a different route through hx_s4_ref_fwd's kernels: the projection's 16- or
+# 4-byte ring loads (L % 4, alignment of x) and its tail chunk (M % 16); the streamed
+# recurrence (N a power of two, L*N % 4 == 0; several ring wraps at L*N >> 3 x 4096) or the
+# per-lane one; the scalar-operand output kernel (N in {4, 8, 16}, L % 4 == 0) or the LDS one.
+@pytest.mark.parametrize("M,N,L,offset", [
+    (64, 16, 4096, 0),    # all fast paths, 16 recurrence chunks
+    (300, 4, 3000, 0),    # 18 full projection chunks + a 12-row tail, N 4 output kernel
+    (37, 8, 1003, 0),     # odd L: 4-byte ring loads, streamed recurrence, LDS output kernel
+    (19, 2, 6000, 0),     # N 2: 2048-step recurrence chunks
+    (19, 1, 2050, 0),     # N 1, L*N % 4 != 0: per-lane recurrence
+    (65, 32, 520, 0),     # 4 state groups, 128-step chunks
+    (5, 16, 7, 0),        # fewer rows and steps than one tile
+    (64, 16, 4096, 1),    # x not 16-byte aligned: 4-byte ring loads, LDS output kernel
+    (48, 12, 900, 0),     # N 12: padded state group, per-lane recurrence
+])
+def test_s4_ref_bit_exact_paths(dev, M, N, L, offset):
+    p = s4_inputs(M, N, L, seed=11 + M + N + L, a_real=np.full(N, -0.01))
+    gate = (np.random.default_rng(3).standard_normal(M) * 0.1).astype(F)
+    print(f"case s4_ref_paths M={M} N={N} L={L} offset={offset}", flush=True)
+    d = {k: dv(v, dev) for k, v in p.items()}
+    if offset:
+        flat = torch.empty(M * L + offset, device=dev, dtype=torch.float32)
+        d["x"] = flat[offset:].view(M, L)
+        d["x"].copy_(torch.from_numpy(p["x"]))
+        assert d["x"].data_ptr() % 16 != 0
+    g = ssm.s4_ref_fwd(**d, gate=dv(gate, dev)).cpu().numpy()
+    r = oracle.s4_ref_fwd(**p, gate=gate)
+    assert np.array_equal(g, r), f"max abs diff {np.abs(g - r).max()}"
+
+
 # ------------------------------------------------------------------ time-parallel reference mode
 
 @pytest.mark.parametrize("M,N,L", [(64, 16, 100), (8, 4, 16), (5, 3, 1), (130, 16, 513),
