@@ -478,6 +478,64 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
     const float bias = dt_bias ? dt_bias[dc] : 0.0f;
     float sumdt = 0.0f;
 
+    // END_ONLY with softplus (dt > 0) and every A < 0: start the segment's run from zero at the
+    // latest 16-step boundary tw from which the decay to the segment's end, exp(A * sum of dt
+    // over [tw, tend)), is below 2^-60 for every state of the wave's channels. What is dropped
+    // is that decay times the state at tw (and times the carried entry state, whose decay over
+    // the whole segment is smaller still): 2^-60 of values the recurrence itself only holds to
+    // 2^-24. The carry then takes no decay from such a segment (its sum of dt is published as
+    // +inf). The sums of dt are read backwards from the segment's end, 16 chunks per batch,
+    // each chunk's softplus summed over the wave's 4 step rows and scaled down by 1e-5 so that
+    // the approximate softplus can only make the window longer.
+    int64_t tstart = tbeg;
+    bool windowed = false;
+    if constexpr (END_ONLY && SOFTPLUS) {
+        float am = fmaxf(fmaxf(A2[0], A2[1]), fmaxf(A2[2], A2[3]));
+        {
+            float t1 = am, t2 = am;
+            swap16(t1, t2);
+            const float m2 = fmaxf(t1, t2);
+            float t3 = m2, t4 = m2;
+            swap32(t3, t4);
+            am = fmaxf(t3, t4);  // max of A*log2(e) over the channel's 16 states
+        }
+        const float need = !dvalid ? 0.0f : (am < 0.0f ? 60.5f / -am : INFINITY);
+        if (__ballot(!(need < INFINITY)) == 0) {
+            constexpr int NB = 16;
+            const T* dcol = db + (uint32_t)dc;
+            float S = 0.0f;
+            for (int64_t t_hi = tend; t_hi > tbeg && !windowed; t_hi -= NB * TCH) {
+                float v[NB][4];
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t t = t_hi - (j + 1) * TCH + r + 4 * i;
+                        v[j][i] = Storage<T>::load(dcol + (uint32_t)(t > tbeg ? t : tbeg) * D32);
+                    }
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const int64_t tw = t_hi - (j + 1) * TCH;
+                    if (tw < tbeg) break;  // uniform
+                    float cs = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) cs += softplus(v[j][i] + bias);
+                    float t1 = cs, t2 = cs;
+                    swap16(t1, t2);
+                    const float c2 = t1 + t2;
+                    float t3 = c2, t4 = c2;
+                    swap32(t3, t4);
+                    S += (t3 + t4) * 0.99999f;
+                    if (__ballot(S < need) == 0) {
+                        tstart = tw;
+                        windowed = tw > tbeg;
+                        break;
+                    }
+                }
+            }
+        }
+    }
+
     float4 ru[PF], rd[PF], rz[PF], rb[PF], rc[PF];
     auto fetch = [&](int k) __attribute__((always_inline)) {
         const uint32_t xo = x_next < x_last ? x_next : x_last;
@@ -580,12 +638,14 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
         }
     };
 
+    x_next = (uint32_t)(tstart + mrow) * D32 + mcol;
+    bc_next = (uint32_t)(tstart + c) * NS + 4 * r;
 #pragma unroll
     for (int k = 0; k < PF; ++k) fetch(k);
     stage_in(0, 0);
     float4 B4 = rb[0], C4 = rc[0];
     fetch(0);
-    for (int64_t tb0 = tbeg; tb0 < tend; tb0 += PF * TCH) {
+    for (int64_t tb0 = tstart; tb0 < tend; tb0 += PF * TCH) {
         StepLoop<PF>::run([&](auto kc) __attribute__((always_inline)) {
             constexpr int k = decltype(kc)::value;
             constexpr int kn = (k + 1) % PF;
@@ -618,7 +678,7 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
         float sa = t1 + t2;
         float t3 = sa, t4 = sa;
         swap32(t3, t4);
-        sumdt = t3 + t4;
+        sumdt = windowed ? INFINITY : t3 + t4;
         if (dvalid) {
             float* he = sg.seg_hend + (int64_t)seg * Bt * Dm * NS;
 #pragma unroll
