@@ -198,10 +198,10 @@ __global__ __launch_bounds__(64 * W) void scan_fwd_kernel(
 //     (12 swaps + 12 adds per 16 steps), leaving each lane the sums of its own 4 steps.
 
 // Segments: for long sequences with few (batch, channel-tile) pairs the sequence is cut into
-// nseg segments of seg_len steps, each its own block. END_ONLY blocks run a segment from a zero
-// state and publish its end state and the segment's total dt (the decay over the segment is
-// exp(A * sum dt)); a carry kernel chains the segments' entry states; full blocks then run each
-// segment from its entry state (seg_init) and write the outputs.
+// nseg segments of seg_len steps, each its own block. END_ONLY blocks compute a segment's end
+// state from a zero entry state and the decay over the segment (per state); a carry kernel
+// chains the segments' entry states; full blocks then run each segment from its entry state
+// (seg_init) and write the outputs.
 // Number of time segments for the wave kernel: 0 = automatic; set by hx_set_scan_segments.
 thread_local int g_scan_segments = 0;
 
@@ -210,7 +210,7 @@ struct WaveSeg {
     int nseg;
     const float* seg_init;  // [nseg][B][D][16] entry states (full mode, nseg > 1)
     float* seg_hend;        // [nseg][B][D][16] end state from zero (END_ONLY)
-    float* seg_sumdt;       // [nseg][B][D]     total dt of the segment (END_ONLY)
+    float* seg_decay;       // [nseg][B][D][16] decay over the segment (END_ONLY; 0 = dropped)
 };
 
 template <typename T, int PF, bool HAS_Z, bool SOFTPLUS, bool END_ONLY>
@@ -393,9 +393,12 @@ __global__ __launch_bounds__(256) void scan_wave_kernel(
         sumdt = t3 + t4;
         if (dvalid) {
             float* he = sg.seg_hend + (int64_t)seg * Bt * Dm * NS;
+            float* de = sg.seg_decay + (int64_t)seg * Bt * Dm * NS;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) he[(b * Dm + d) * NS + 4 * r + k] = h[k];
-            if (r == 0) sg.seg_sumdt[((int64_t)seg * Bt + b) * Dm + d] = sumdt;
+            for (int k = 0; k < 4; ++k) {
+                he[(b * Dm + d) * NS + 4 * r + k] = h[k];
+                de[(b * Dm + d) * NS + 4 * r + k] = fast_exp2(A2[k] * sumdt);
+            }
         }
     }
 }
@@ -462,8 +465,11 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
     const uint32_t mcol = (uint32_t)(mvalid ? mch : 0);
     const uint32_t x_last = (uint32_t)(tend - 1) * D32 + mcol;          // clamp of tile offsets
     const uint32_t bc_last = (uint32_t)(tend - 1) * NS + 4 * r;         // clamp of B/C offsets
-    uint32_t x_next = (uint32_t)(tbeg + mrow) * D32 + mcol;             // next tile fetch
-    uint32_t bc_next = (uint32_t)(tbeg + c) * NS + 4 * r;               // next B/C fetch
+    const uint32_t x_first = (uint32_t)(tbeg + mrow) * D32 + mcol;      // first chunk's offsets
+    const uint32_t bc_first = (uint32_t)(tbeg + c) * NS + 4 * r;
+    // next fetch: forwards from the segment's first chunk, or (END_ONLY) backwards from its last
+    uint32_t x_next = (uint32_t)((END_ONLY ? tend - TCH : tbeg) + mrow) * D32 + mcol;
+    uint32_t bc_next = (uint32_t)((END_ONLY ? tend - TCH : tbeg) + c) * NS + 4 * r;
     const uint32_t x_step = TCH * D32, bc_step = TCH * NS;
 
     float A2[4], h[4];
@@ -476,65 +482,8 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
     }
     const float Dd = Dv ? Dv[dc] : 0.0f;
     const float bias = dt_bias ? dt_bias[dc] : 0.0f;
-    float sumdt = 0.0f;
-
-    // END_ONLY with softplus (dt > 0) and every A < 0: start the segment's run from zero at the
-    // latest 16-step boundary tw from which the decay to the segment's end, exp(A * sum of dt
-    // over [tw, tend)), is below 2^-60 for every state of the wave's channels. What is dropped
-    // is that decay times the state at tw (and times the carried entry state, whose decay over
-    // the whole segment is smaller still): 2^-60 of values the recurrence itself only holds to
-    // 2^-24. The carry then takes no decay from such a segment (its sum of dt is published as
-    // +inf). The sums of dt are read backwards from the segment's end, 16 chunks per batch,
-    // each chunk's softplus summed over the wave's 4 step rows and scaled down by 1e-5 so that
-    // the approximate softplus can only make the window longer.
-    int64_t tstart = tbeg;
-    bool windowed = false;
-    if constexpr (END_ONLY && SOFTPLUS) {
-        float am = fmaxf(fmaxf(A2[0], A2[1]), fmaxf(A2[2], A2[3]));
-        {
-            float t1 = am, t2 = am;
-            swap16(t1, t2);
-            const float m2 = fmaxf(t1, t2);
-            float t3 = m2, t4 = m2;
-            swap32(t3, t4);
-            am = fmaxf(t3, t4);  // max of A*log2(e) over the channel's 16 states
-        }
-        const float need = !dvalid ? 0.0f : (am < 0.0f ? 60.5f / -am : INFINITY);
-        if (__ballot(!(need < INFINITY)) == 0) {
-            constexpr int NB = 16;
-            const T* dcol = db + (uint32_t)dc;
-            float S = 0.0f;
-            for (int64_t t_hi = tend; t_hi > tbeg && !windowed; t_hi -= NB * TCH) {
-                float v[NB][4];
-#pragma unroll
-                for (int j = 0; j < NB; ++j)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int64_t t = t_hi - (j + 1) * TCH + r + 4 * i;
-                        v[j][i] = Storage<T>::load(dcol + (uint32_t)(t > tbeg ? t : tbeg) * D32);
-                    }
-#pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const int64_t tw = t_hi - (j + 1) * TCH;
-                    if (tw < tbeg) break;  // uniform
-                    float cs = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) cs += softplus(v[j][i] + bias);
-                    float t1 = cs, t2 = cs;
-                    swap16(t1, t2);
-                    const float c2 = t1 + t2;
-                    float t3 = c2, t4 = c2;
-                    swap32(t3, t4);
-                    S += (t3 + t4) * 0.99999f;
-                    if (__ballot(S < need) == 0) {
-                        tstart = tw;
-                        windowed = tw > tbeg;
-                        break;
-                    }
-                }
-            }
-        }
-    }
+    // END_ONLY: decay from the segment's end back to the step reached, per state
+    float Q[4] = {1.0f, 1.0f, 1.0f, 1.0f};
 
     float4 ru[PF], rd[PF], rz[PF], rb[PF], rc[PF];
     auto fetch = [&](int k) __attribute__((always_inline)) {
@@ -545,8 +494,13 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
         const uint32_t bo = bc_next < bc_last ? bc_next : bc_last;
         rb[k] = Vec4<T>::load(Bb + bo);
         rc[k] = END_ONLY ? make_float4(0, 0, 0, 0) : Vec4<T>::load(Cb + bo);
-        x_next += x_step;
-        bc_next += bc_step;
+        if constexpr (END_ONLY) {  // backwards; past the segment's start the first chunk repeats
+            x_next = x_next >= x_first + x_step ? x_next - x_step : x_first;
+            bc_next = bc_next >= bc_first + bc_step ? bc_next - bc_step : bc_first;
+        } else {
+            x_next += x_step;
+            bc_next += bc_step;
+        }
     };
     auto stage_in = [&](int k, int buf) __attribute__((always_inline)) {
         *reinterpret_cast<float4*>(&s_in[w][buf][0][mrow][mcl]) = ru[k];
@@ -579,7 +533,6 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
             if (!FULL) x = s < nvalid ? x : 0.0f;  // steps past the end leave the state unchanged
             dl[i] = x;
             du[i] = x * uu[i];
-            if (END_ONLY) sumdt += x;
         }
         // row all-gather through LDS: lane (r, c) holds steps r + 4i, stored step-major
         // (s_g[.][cb][s], s = 4i + r) so the float4 at [4g] is exactly the steps of group g and
@@ -601,6 +554,31 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
         const float bk[4] = {B4.x, B4.y, B4.z, B4.w};
         const float ck[4] = {C4.x, C4.y, C4.z, C4.w};
         float P[16];
+        if constexpr (END_ONLY) {
+            // steps 15..0: h += Q * B*dt*u, then Q *= exp(dt*A); h is the end state from a zero
+            // state at the step reached, Q the decay from there to the end
+            StepLoop<4>::run([&](auto gc) {
+                constexpr int g = decltype(gc)::value;
+                float ab[4][4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int s = 15 - (4 * g + e);
+                        ab[e][k] = fast_exp2(gdl[s & 3][s >> 2] * A2[k]);
+                    }
+                StepLoop<4>::run([&](auto ec) {
+                    constexpr int e = decltype(ec)::value;
+                    constexpr int s = 15 - (4 * g + e);
+                    const float dus = gdu[s & 3][s >> 2];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        h[k] = fmaf(Q[k], dpp<kDppBcast<s>>(bk[k]) * dus, h[k]);
+                        Q[k] *= ab[e][k];
+                    }
+                });
+            });
+        } else {
         StepLoop<4>::run([&](auto gc) {
             constexpr int g = decltype(gc)::value;
             float ab[4][4];
@@ -625,6 +603,7 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
                 }
             });
         });
+        }
         if constexpr (!END_ONLY) {
             float Y[4];
             rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i
@@ -638,14 +617,47 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
         }
     };
 
-    x_next = (uint32_t)(tstart + mrow) * D32 + mcol;
-    bc_next = (uint32_t)(tstart + c) * NS + 4 * r;
 #pragma unroll
     for (int k = 0; k < PF; ++k) fetch(k);
     stage_in(0, 0);
     float4 B4 = rb[0], C4 = rc[0];
     fetch(0);
-    for (int64_t tb0 = tstart; tb0 < tend; tb0 += PF * TCH) {
+    // END_ONLY: the segment's chunks from the last back to the first (all whole: segment lengths
+    // are multiples of 16 and the last, possibly partial, segment has no end-state pass). It
+    // stops after the first chunk at which every state of the wave's channels has decayed below
+    // 2^-48 on its way to the segment's end: what is left out is that decay times the state at
+    // that step (and times the entry state, whose decay over the whole segment is smaller
+    // still), 2^-48 of values the recurrence holds to 2^-24 (a NaN or growing decay never
+    // stops it). The segment then publishes a decay of 0, so its entry state is not carried.
+    bool dropped = false;
+    if constexpr (END_ONLY) {
+        bool stop = false;  // uniform
+        for (int64_t q0 = 0; !stop; q0 += PF) {
+            StepLoop<PF>::run([&](auto kc) __attribute__((always_inline)) {
+                constexpr int k = decltype(kc)::value;
+                constexpr int kn = (k + 1) % PF;
+                constexpr int buf = k & 1;  // PF is even
+                if (stop) return;
+                const int64_t t0 = tend - (q0 + k + 1) * TCH;
+                if (t0 < tbeg) {
+                    stop = true;
+                    return;
+                }
+                stage_in(kn, buf ^ 1);
+                const float4 Bn = rb[kn];
+                fetch(kn);
+                compute(t0, buf, B4, C4, std::true_type{});
+                B4 = Bn;
+                __builtin_amdgcn_wave_barrier();
+                const float qm = fmaxf(fmaxf(Q[0], Q[1]), fmaxf(Q[2], Q[3]));
+                if (__ballot(dvalid && !(qm < 0x1p-48f)) == 0) {
+                    stop = true;
+                    dropped = t0 > tbeg;
+                }
+            });
+        }
+    }
+    for (int64_t tb0 = tbeg; !END_ONLY && tb0 < tend; tb0 += PF * TCH) {
         StepLoop<PF>::run([&](auto kc) __attribute__((always_inline)) {
             constexpr int k = decltype(kc)::value;
             constexpr int kn = (k + 1) % PF;
@@ -673,39 +685,32 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
             for (int k = 0; k < 4; ++k) last_state[(b * Dm + d) * NS + 4 * r + k] = h[k];
         }
     } else {
-        float t1 = sumdt, t2 = sumdt;
-        swap16(t1, t2);
-        float sa = t1 + t2;
-        float t3 = sa, t4 = sa;
-        swap32(t3, t4);
-        sumdt = windowed ? INFINITY : t3 + t4;
         if (dvalid) {
             float* he = sg.seg_hend + (int64_t)seg * Bt * Dm * NS;
+            float* de = sg.seg_decay + (int64_t)seg * Bt * Dm * NS;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) he[(b * Dm + d) * NS + 4 * r + k] = h[k];
-            if (r == 0) sg.seg_sumdt[((int64_t)seg * Bt + b) * Dm + d] = sumdt;
+            for (int k = 0; k < 4; ++k) {
+                he[(b * Dm + d) * NS + 4 * r + k] = h[k];
+                de[(b * Dm + d) * NS + 4 * r + k] = dropped ? 0.0f : Q[k];
+            }
         }
     }
 }
 
 
-// Entry state of every segment: h_in[0] = init (or 0); h_in[k] = exp(A * sumdt[k-1]) * h_in[k-1]
-// + hend[k-1], per (b, d, n). Writes seg_init[k] for k = 0..nseg-1 (reads hend/sumdt of the
-// first nseg-1 segments only).
+// Entry state of every segment: h_in[0] = init (or 0); h_in[k] = decay[k-1] * h_in[k-1] +
+// hend[k-1], per (b, d, n). Writes seg_init[k] for k = 0..nseg-1 (reads hend/decay of the first
+// nseg-1 segments only).
 __global__ __launch_bounds__(256) void scan_seg_carry_kernel(
-    int64_t Bt, int64_t Dm, int nseg, const float* __restrict__ A,
-    const float* __restrict__ init_state, const float* __restrict__ hend,
-    const float* __restrict__ sumdt, float* __restrict__ seg_init) {
+    int64_t Bt, int64_t Dm, int nseg, const float* __restrict__ init_state,
+    const float* __restrict__ hend, const float* __restrict__ decay, float* __restrict__ seg_init) {
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t per = Bt * Dm * 16;
     if (gid >= per) return;
-    const int64_t bd = gid / 16, n = gid % 16;
-    const int64_t dd = bd % Dm;
-    const float a2 = A[dd * 16 + n] * kLog2e;
     float hc = init_state ? init_state[gid] : 0.0f;
     seg_init[gid] = hc;
     for (int k = 0; k + 1 < nseg; ++k) {  // the last segment's end state is not produced
-        hc = fmaf(fast_exp2(a2 * sumdt[(int64_t)k * Bt * Dm + bd]), hc, hend[(int64_t)k * per + gid]);
+        hc = fmaf(decay[(int64_t)k * per + gid], hc, hend[(int64_t)k * per + gid]);
         seg_init[(int64_t)(k + 1) * per + gid] = hc;
     }
 }
@@ -1246,11 +1251,11 @@ int64_t scan_segments(const ScanArgs& a, int64_t* seg_len_out) {
     *seg_len_out = seg_len;
     return (a.L + seg_len - 1) / seg_len;
 }
-// Scratch of a segmented scan: end states and entry states [nseg][B][D][16], total dt [nseg][B][D].
+// Scratch of a segmented scan: end states, entry states and decays, each [nseg][B][D][16].
 size_t scan_seg_bytes(int64_t Bt, int64_t Dm, int64_t nseg) {
     if (nseg <= 1) return 0;
     const size_t per = (size_t)Bt * Dm * 16;
-    return (size_t)nseg * (2 * per + (size_t)Bt * Dm) * sizeof(float);
+    return (size_t)nseg * 3 * per * sizeof(float);
 }
 
 template <typename T, int W, int TCH, bool HAS_Z, bool SP>
@@ -1309,11 +1314,11 @@ int launch_wave(const ScanArgs& a) {
     const size_t per = (size_t)a.Bt * a.Dm * 16;
     float* hend = (float*)a.ws;
     float* seg_init = hend + (size_t)nseg * per;
-    float* sumdt = seg_init + (size_t)nseg * per;
-    int rc = launch_wave_one<T, PF, false, SP, true, VER>(a, WaveSeg{seg_len, (int)nseg, nullptr, hend, sumdt});
+    float* decay = seg_init + (size_t)nseg * per;
+    int rc = launch_wave_one<T, PF, false, SP, true, VER>(a, WaveSeg{seg_len, (int)nseg, nullptr, hend, decay});
     if (rc != HX_OK) return rc;
     hipLaunchKernelGGL(scan_seg_carry_kernel, dim3((unsigned)((per + 255) / 256)), dim3(256), 0,
-                       a.stream, a.Bt, a.Dm, (int)nseg, a.A, a.init_state, hend, sumdt, seg_init);
+                       a.stream, a.Bt, a.Dm, (int)nseg, a.init_state, hend, decay, seg_init);
     HX_LAUNCH_CHECK();
     return launch_wave_one<T, PF, HAS_Z, SP, false, VER>(a, WaveSeg{seg_len, (int)nseg, seg_init, nullptr, nullptr});
 }
@@ -1558,9 +1563,9 @@ extern "C" int hx_selective_scan_fwd_ws(int64_t batch, int64_t seqlen, int64_t d
 
 // ------------------------------------------------------------------ no-allocation entry point
 // Scratch of hx_selective_scan_fwd_noalloc: the segmented long-sequence path's end states, entry
-// states and segment dt totals (the same layout a caller workspace holds for
+// states and segment decays (the same layout a caller workspace holds for
 // hx_selective_scan_fwd_ws). One copy per device, resident until the process ends. Nothing in it
-// has to start at zero: the end-state pass writes every end state and dt total the carry kernel
+// has to start at zero: the end-state pass writes every end state and decay the carry kernel
 // reads, and the carry kernel writes every entry state the output pass reads.
 constexpr size_t kScanScratchBytes = (size_t)8 << 20;
 static __device__ __align__(256) unsigned char scratch[kScanScratchBytes];

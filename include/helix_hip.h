@@ -101,9 +101,10 @@ int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t ds
 
 /* hx_selective_scan_fwd with a caller workspace for the long-sequence path: when the
  * (batch, channel) tiles alone cannot fill the GPU (few channels, long seqlen), the sequence is
- * cut into time segments scanned in parallel from a zero state, their entry states chained by a
- * carry kernel, then rescanned with outputs (results agree with the unsegmented scan to fp32
- * rounding). workspace: device memory of at least hx_selective_scan_workspace_size(...) bytes,
+ * cut into time segments whose end states (from a zero state) are accumulated backwards from
+ * each segment's end until every state's decay to the end is below 2^-48, their entry states
+ * chained by a carry kernel, then rescanned with outputs (results agree with the unsegmented
+ * scan to fp32 rounding). workspace: device memory of at least hx_selective_scan_workspace_size(...) bytes,
  * 16-byte aligned (0 bytes: no segments); it holds no state between calls. Same reference
  * counterpart as hx_selective_scan_fwd (the per-step loop of ssm.rs:166-182). */
 size_t hx_selective_scan_workspace_size(int64_t batch, int64_t seqlen, int64_t dim,

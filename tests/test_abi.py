@@ -95,8 +95,9 @@ def test_s4_discretize_is_the_reference_libm_formula():
 
 def test_workspace_sizes():
     L = _ffi.lib()
-    # config 4 scan (batch 1, L 65536, d 2048): segmented, 16 segments x (2 x 32768 + 2048) floats
-    assert L.hx_selective_scan_workspace_size(1, 65536, 2048, 16, 0) == 16 * (2 * 2048 * 16 + 2048) * 4
+    # config 4 scan (batch 1, L 65536, d 2048): segmented, 16 segments x 3 x 32768 floats (end
+    # states, entry states, decays)
+    assert L.hx_selective_scan_workspace_size(1, 65536, 2048, 16, 0) == 16 * 3 * 2048 * 16 * 4
     # config 2 (batch 8, L 2048, d 1536) fills the GPU unsegmented: no workspace
     assert L.hx_selective_scan_workspace_size(8, 2048, 1536, 16, 0) == 0
     assert L.hx_selective_scan_workspace_size(1, 8192, 64, 7, 0) == 0  # generic kernel
