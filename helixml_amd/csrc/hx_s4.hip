@@ -606,6 +606,30 @@ __global__ __launch_bounds__(256) void s4d_wave_kernel(
     }
     const float Dd = Dv ? Dv[dc] : 0.0f;
 
+    // END_ONLY: the system is time-invariant, so the steps after which |Abar|^k < 2^-48 for every
+    // state of the block's channels are known up front (k >= 48 / -(dt a_re log2 e), with half a
+    // bit of margin for expf's rounding of |Abar|); the end state from zero then starts that many
+    // steps (whole chunks) before the segment's end. What is left out is |Abar|^k times the
+    // state at that step, 2^-48 of quantities the fp32 recurrence holds to 2^-24. The carry
+    // still applies the segment's own transfer Abar^seg_len, which is smaller still.
+    int64_t tstart = tbeg;
+    if constexpr (END_ONLY) {
+        __shared__ int s_win;
+        if (tid == 0) s_win = 0;
+        lds_barrier();
+        int wl = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float l2 = dt * a_re[dc * NS + 4 * r + k] * kLog2e;  // log2 |Abar|
+            const float wf = 48.5f / -l2;
+            wl = max(wl, l2 < 0.0f && wf < 1.0e9f ? (int)ceilf(wf) : 0x7fffffff);
+        }
+        atomicMax(&s_win, dvalid ? wl : 0);
+        lds_barrier();
+        const int64_t win = s_win;
+        if (win < tend - tbeg) tstart = tend - (win + TCH - 1) / TCH * TCH;
+    }
+
     // prefetch ring of PF = 2 chunks in two named registers (an indexed array of float4 was
     // placed in scratch memory by the compiler)
     float4 rx0, rx1;
@@ -663,12 +687,12 @@ __global__ __launch_bounds__(256) void s4d_wave_kernel(
     };
 
     static_assert(PF == 2, "two-slot ring");
-    fetch(rx0, tbeg);
-    fetch(rx1, tbeg + TCH);
+    fetch(rx0, tstart);
+    fetch(rx1, tstart + TCH);
     stage_in(rx0, 0);
-    fetch(rx0, tbeg + (int64_t)PF * TCH);
+    fetch(rx0, tstart + (int64_t)PF * TCH);
     lds_barrier();
-    for (int64_t tb0 = tbeg; tb0 < tend; tb0 += PF * TCH) {
+    for (int64_t tb0 = tstart; tb0 < tend; tb0 += PF * TCH) {
         StepLoop<PF>::run([&](auto kc) __attribute__((always_inline)) {
             constexpr int k = decltype(kc)::value;
             constexpr int buf = k & 1;
