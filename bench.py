@@ -46,7 +46,7 @@ from helixml_amd import _ffi, ssm  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
 # the kernel the automatic dispatch runs for config 2 (the name rocprofv3 reports)
-SCAN_KERNEL = "scan_ws_kernel<float, 2, true, true>"
+SCAN_KERNEL = "scan_ws2_kernel<float, 3, true, true>"
 
 
 def scan_bytes(bt, L, dim, N, es, with_z=True, with_D=True):

@@ -811,6 +811,43 @@ template <int OPB> struct RingRead<uint16_t, 2, OPB> {
     }
 };
 
+// r[m][o] = the fp32 words at a + o * OPB + 64 m and 768 bytes further (one channel at two steps
+// 4 rows of 48 channels apart), o < NOP (2 or 3), m < 3: ds_read2_b32 with dword offsets 16m and
+// 16m + 192.
+template <int NOP, int OPB> struct RingRead2 {
+    __device__ static inline void run(uint32_t a, float2 (&r)[3][3]) {
+        const uint32_t a1 = a + OPB, a2 = a + 2 * OPB;
+        hx_u32x2 v[3][3];
+        if constexpr (NOP == 3) {
+            asm volatile(
+                "ds_read2_b32 %0, %9 offset1:192\n\tds_read2_b32 %1, %10 offset1:192\n\tds_read2_b32 %2, %11 offset1:192\n\t"
+                "ds_read2_b32 %3, %9 offset0:16 offset1:208\n\tds_read2_b32 %4, %10 offset0:16 offset1:208\n\t"
+                "ds_read2_b32 %5, %11 offset0:16 offset1:208\n\t"
+                "ds_read2_b32 %6, %9 offset0:32 offset1:224\n\tds_read2_b32 %7, %10 offset0:32 offset1:224\n\t"
+                "ds_read2_b32 %8, %11 offset0:32 offset1:224\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(v[0][2]), "=&v"(v[1][0]), "=&v"(v[1][1]), "=&v"(v[1][2]),
+                  "=&v"(v[2][0]), "=&v"(v[2][1]), "=&v"(v[2][2])
+                : "v"(a), "v"(a1), "v"(a2)
+                : "memory");
+        } else {
+            (void)a2;
+            asm volatile(
+                "ds_read2_b32 %0, %6 offset1:192\n\tds_read2_b32 %1, %7 offset1:192\n\t"
+                "ds_read2_b32 %2, %6 offset0:16 offset1:208\n\tds_read2_b32 %3, %7 offset0:16 offset1:208\n\t"
+                "ds_read2_b32 %4, %6 offset0:32 offset1:224\n\tds_read2_b32 %5, %7 offset0:32 offset1:224\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(v[1][0]), "=&v"(v[1][1]), "=&v"(v[2][0]), "=&v"(v[2][1])
+                : "v"(a), "v"(a1)
+                : "memory");
+        }
+#pragma unroll
+        for (int m = 0; m < 3; ++m)
+#pragma unroll
+            for (int o = 0; o < NOP; ++o) r[m][o] = make_float2(__uint_as_float(v[m][o][0]), __uint_as_float(v[m][o][1]));
+    }
+};
+
 // One element stored through a raw buffer resource: offsets at or past the resource's size are
 // dropped by the hardware, so a store needs no branch (and the compiler's wait counts stay exact).
 __device__ inline void buf_store(float v, __amdgpu_buffer_rsrc_t rs, uint32_t off, float*) {
@@ -1093,6 +1130,308 @@ __global__ __launch_bounds__(256) void scan_ws_kernel(
     }
 }
 
+// ----------------------------------------------------------------------------- split-state form
+// Warp-specialised scan with every SIMD running two waves, so one wave's waits (hand-over
+// barrier, B/C loads, LDS reads, dependent issue) overlap the other's issue. A block of 8 waves
+// owns 48 channels of one batch row (fp32 storage):
+//   * waves 0..2 and 4..6 are state waves: wave w < 3 holds states 0..7 of channel group w,
+//     wave w > 3 states 8..15 of group w - 4 (lane (r, c): channel c, states 8h + 2r, 8h + 2r + 1;
+//     B/C of step t0 + j in lane j of row r). Each reduce-scatters its 8 states' readouts
+//     across rows; the lower half hands its partials to the upper half through LDS, which adds
+//     them in the next phase (after the chunk barrier), then D*u, the gate and the stores;
+//   * waves 3 and 7 are element waves, each preparing half of every chunk's steps for all 48
+//     channels (softplus(delta + bias), dt*u, u, SiLU(z)).
+// Waves of a block are placed on SIMDs round-robin, so waves w and w + 4 share a SIMD: SIMDs
+// 0..2 each run a lower and an upper state wave, SIMD 3 the two element waves. The hand-over
+// buffers hold each channel's 16 steps in the order 4 (s % 4) + s / 4 for all four operands.
+// The readout is summed as (states 0..7) + (states 8..15), so results match scan_ws_kernel to
+// rounding, not bit for bit. Requires Dm % 4 == 0, 16-byte rows, (L + 48) * Dm * 4 < 2^32.
+template <typename T> struct Pair;
+template <> struct Pair<float> {
+    __device__ static inline float2 load(const float* p) { return *reinterpret_cast<const float2*>(p); }
+};
+template <> struct Pair<uint16_t> {
+    __device__ static inline float2 load(const uint16_t* p) {
+        const uint32_t r = *reinterpret_cast<const uint32_t*>(p);
+        return make_float2(__uint_as_float(r << 16), __uint_as_float(r & 0xffff0000u));
+    }
+};
+
+template <typename T, int NR, bool HAS_Z, bool SOFTPLUS>
+__global__ __launch_bounds__(512) void scan_ws2_kernel(
+    int64_t L, int64_t Dm, int ngrp,
+    const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
+    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ Dv,
+    const T* __restrict__ z, const float* __restrict__ dt_bias, T* __restrict__ out,
+    const float* __restrict__ init_state, float* __restrict__ last_state) {
+    constexpr int NS = 16, TCH = 16, GCH = 48, DS = 20;
+    constexpr int NOP = HAS_Z ? 3 : 2;
+    constexpr int OPB = 2048;                 // ring slot of one operand of a half chunk (8 steps x
+                                              // 48 channels = 1536 bytes, padded to two full loads)
+    constexpr int STB = NOP * OPB;            // one ring stage
+    constexpr int RING = 2 * NR * STB;        // both element waves' rings
+    // All LDS is the dynamic allocation, rings first: the LDS base of a load to LDS is a 16-bit
+    // byte address, so the rings must lie below 64 KiB. Then the hand-over buffers
+    // s_x[buf][dt | dt*u | u | SiLU(z)][ch][20] and the lower halves' readouts s_y[2][group][lane].
+    extern __shared__ __attribute__((aligned(16))) char s_dyn[];
+    static_assert(RING <= 65536 - 1024, "rings below 64 KiB");
+    auto& s_x = *reinterpret_cast<float(*)[3][4][GCH][DS]>(s_dyn + RING);
+    auto& s_y = *reinterpret_cast<float4(*)[2][3][64]>(s_dyn + RING + sizeof(float) * 3 * 4 * GCH * DS);
+
+    const int nblk = gridDim.x;
+    int id = blockIdx.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);  // XCD-aware order
+    const int grp = id % ngrp;
+    const int64_t b = id / ngrp;
+    const int64_t cblk = (int64_t)grp * GCH;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nch = (int)((L + TCH - 1) / TCH);
+    const uint32_t D32 = (uint32_t)Dm;
+
+    auto state_wave = [&](auto hc) __attribute__((always_inline)) {
+        constexpr int HH = decltype(hc)::value;  // 0: states 0..7, 1: states 8..15
+        const int g = HH ? w - 4 : w;
+        const int r = lane >> 4, c = lane & 15;
+        const int lch = 16 * g + c;
+        const int st0 = 8 * HH + 2 * r;
+        const int64_t d = cblk + lch;
+        const bool dvalid = d < Dm;
+        const int64_t dc = dvalid ? d : Dm - 1;
+        float A2[2], h[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            A2[k] = A[dc * NS + st0 + k] * kLog2e;
+            h[k] = init_state ? init_state[(b * Dm + dc) * NS + st0 + k] : 0.0f;
+        }
+        const float Dd = Dv ? Dv[dc] : 0.0f;
+        const T* Bb = Bm + b * L * NS;
+        const T* Cb = Cm + b * L * NS;
+        const uint32_t bc_last = (uint32_t)(L - 1) * NS + st0;
+        uint32_t bc_next = (uint32_t)c * NS + st0;
+        float2 rb[2], rc[2];
+        auto fetch = [&](int k) __attribute__((always_inline)) {
+            const uint32_t bo = bc_next < bc_last ? bc_next : bc_last;
+            rb[k] = Pair<T>::load(Bb + bo);
+            rc[k] = Pair<T>::load(Cb + bo);
+            bc_next += TCH * NS;
+        };
+        const uint32_t nrec = (uint32_t)(L * Dm * (int64_t)sizeof(T));
+        const uint32_t row_bytes = D32 * (uint32_t)sizeof(T);
+        const uint32_t lane_off = dvalid ? ((uint32_t)r * D32 + (uint32_t)d) * (uint32_t)sizeof(T) : nrec;
+        const __amdgpu_buffer_rsrc_t ors =
+            __builtin_amdgcn_make_buffer_rsrc(out + b * L * Dm, (short)0, (int)nrec, kBufRsrcWord3);
+        float dl[2][16], du[2][16];
+        auto read_dt = [&](auto kc, int b3) __attribute__((always_inline)) {
+            constexpr int k = decltype(kc)::value;
+            const float* p0 = &s_x[b3][0][lch][0];
+            const float* p1 = &s_x[b3][1][lch][0];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 a = *reinterpret_cast<const float4*>(p0 + 4 * i);
+                const float4 q = *reinterpret_cast<const float4*>(p1 + 4 * i);
+                // index 4i + j of a channel row holds step 4j + i
+                dl[k][i] = a.x; dl[k][4 + i] = a.y; dl[k][8 + i] = a.z; dl[k][12 + i] = a.w;
+                du[k][i] = q.x; du[k][4 + i] = q.y; du[k][8 + i] = q.z; du[k][12 + i] = q.w;
+            }
+        };
+        // upper half: this wave's readouts, u and SiLU(z) of the chunk whose outputs are pending
+        float Yp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, fup[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float fzp[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        auto finish = [&](int p) __attribute__((always_inline)) {
+            const float4 o = s_y[p & 1][g][lane];
+            const float ov[4] = {o.x, o.y, o.z, o.w};
+            // step r + 4i of chunk p sits at lane_off + (16p + 4i) * row bytes; steps past the
+            // end land at or past nrec and are dropped; lanes of channels past Dm stay at nrec
+            const uint32_t chunk_off = dvalid ? lane_off + (uint32_t)p * (uint32_t)TCH * row_bytes : nrec;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float y = fmaf(Dd, fup[i], ov[i] + Yp[i]);
+                if (HAS_Z) y *= fzp[i];
+                buf_store(y, ors, chunk_off + 4 * i * row_bytes, (T*)nullptr);
+            }
+        };
+        fetch(0);
+        fetch(1);
+        lds_barrier();  // chunks 0 and 1 prepared
+        read_dt(std::integral_constant<int, 0>{}, 0);
+        int b3 = 0;  // p % 3
+        for (int p0 = 0; p0 < nch; p0 += 2) {
+            StepLoop<2>::run([&](auto kc) __attribute__((always_inline)) {
+                constexpr int k = decltype(kc)::value;  // = p & 1: dt register set and B/C slot
+                const int p = p0 + k;
+                if (p >= nch) return;  // uniform
+                const int b3n = b3 == 2 ? 0 : b3 + 1;
+                if (p + 1 < nch) read_dt(std::integral_constant<int, k ^ 1>{}, b3n);
+                if (HH && p > 0) finish(p - 1);
+                const float bk[2] = {rb[k].x, rb[k].y};
+                const float ck[2] = {rc[k].x, rc[k].y};
+                float P[16];
+                StepLoop<4>::run([&](auto gc) __attribute__((always_inline)) {
+                    constexpr int g4 = decltype(gc)::value;
+                    float ab[4][2];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk) ab[e][kk] = fast_exp2(dl[k][4 * g4 + e] * A2[kk]);
+                    StepLoop<4>::run([&](auto ec) __attribute__((always_inline)) {
+                        constexpr int e = decltype(ec)::value;
+                        constexpr int s = 4 * g4 + e;
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk)
+                            h[kk] = fmaf(ab[e][kk], h[kk], dpp<kDppBcast<s>>(bk[kk]) * du[k][s]);
+                        float acc = dpp<kDppBcast<s>>(ck[0]) * h[0];
+                        acc = fmac_bcast<s>(acc, ck[1], h[1]);
+                        P[(s >> 2) + 4 * (s & 3)] = acc;  // j = i + 4*rr for s = rr + 4*i
+                    });
+                });
+                fetch(k);  // chunk p + 2, into the slot this chunk's B/C came from
+                float Y[4];
+                rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i, this half's 8 states
+                if (HH) {
+                    const float4 fu = *reinterpret_cast<const float4*>(&s_x[b3][2][lch][4 * r]);
+                    const float4 fz = HAS_Z ? *reinterpret_cast<const float4*>(&s_x[b3][3][lch][4 * r])
+                                            : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+                    Yp[0] = Y[0]; Yp[1] = Y[1]; Yp[2] = Y[2]; Yp[3] = Y[3];
+                    fup[0] = fu.x; fup[1] = fu.y; fup[2] = fu.z; fup[3] = fu.w;
+                    fzp[0] = fz.x; fzp[1] = fz.y; fzp[2] = fz.z; fzp[3] = fz.w;
+                } else {
+                    s_y[p & 1][g][lane] = make_float4(Y[0], Y[1], Y[2], Y[3]);
+                }
+                b3 = b3n;
+                lds_barrier();
+            });
+        }
+        if (HH && nch > 0) finish(nch - 1);
+        if (last_state && dvalid) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) last_state[(b * Dm + d) * NS + st0 + k] = h[k];
+        }
+    };
+
+    if (w == 3 || w == 7) {
+        // ------------------------------------------------------------ element waves
+        // wave 3 prepares steps 0..7 of every chunk, wave 7 steps 8..15, for all 48 channels.
+        // Each streams its 8 steps of u/delta/z straight into its own NR-deep LDS ring with
+        // buffer loads to LDS (2 x 64 lanes x 16 bytes per operand, the last 512 bytes padding;
+        // reads past the end of the batch row return zeros). Every chunk issues the same LPC
+        // full-wave loads, with no branch the compiler could split, so the explicit vmcnt waits
+        // count exactly. Lane (c, s2) then handles channels c, c + 16, c + 32 at
+        // steps s2 and s2 + 4 of the wave's half: ring reads and hand-over writes of a wave
+        // instruction touch distinct banks.
+        const int e = w >> 2;
+        constexpr int ROWB = GCH * 4;      // one step of 48 channels
+        constexpr int LPC = NOP * 2;       // loads per chunk
+        constexpr int WAITN = (NR - 1) * LPC;
+        static_assert(WAITN <= 63, "vmcnt range");
+        char* ring = s_dyn + e * NR * STB;  // [NR][op][8 steps][48 ch]
+        const uint32_t nrec = (uint32_t)(L * Dm * 4);
+        const __amdgpu_buffer_rsrc_t rs_u =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(u + b * L * Dm), (short)0, (int)nrec, kBufRsrcWord3);
+        const __amdgpu_buffer_rsrc_t rs_d =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(delta + b * L * Dm), (short)0, (int)nrec, kBufRsrcWord3);
+        const __amdgpu_buffer_rsrc_t rs_z = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(HAS_Z ? z + b * L * Dm : u + b * L * Dm), (short)0, (int)nrec, kBufRsrcWord3);
+        // load instruction i, lane q: bytes 1024 i + 16 q of the half chunk = step 8e + (64 i + q) / 12,
+        // channels 4 ((64 i + q) % 12) ..; pieces of channels past Dm read channel 0 (never used);
+        // lanes q >= 96 fill the slot's padding with chunk data that is never read
+        uint32_t loff[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = 64 * i + lane;
+            const int64_t ch = cblk + (q % 12) * 4;
+            loff[i] = q < 96 ? (uint32_t)((8 * e + q / 12) * Dm + (ch < Dm ? ch : 0)) * 4u : 0u;
+        }
+        const uint32_t chunk_bytes = (uint32_t)(TCH * Dm * 4);
+        auto issue = [&](int stage, int qc) __attribute__((always_inline)) {
+            char* dst = ring + stage * STB;
+            const uint32_t cb = (uint32_t)qc * chunk_bytes;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lvoid_t*)dst, 16, loff[0] + cb, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_d, (lvoid_t*)(dst + OPB), 16, loff[0] + cb, 0, 0, 0);
+            if (HAS_Z) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_z, (lvoid_t*)(dst + 2 * OPB), 16, loff[0] + cb, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lvoid_t*)(dst + 1024), 16, loff[1] + cb, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_d, (lvoid_t*)(dst + OPB + 1024), 16, loff[1] + cb, 0, 0, 0);
+            if (HAS_Z)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_z, (lvoid_t*)(dst + 2 * OPB + 1024), 16, loff[1] + cb, 0, 0, 0);
+        };
+        const int c = lane & 15, s2 = lane >> 4;
+        float bias_r[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            const int64_t ch = cblk + c + 16 * m;
+            bias_r[m] = (dt_bias && ch < Dm) ? dt_bias[ch] : 0.0f;
+        }
+        // chunk qc from ring stage `stage` into hand-over buffer b3: steps 8e + s2 + 4i (i < 2)
+        // go to index 4 s2 + 2e + i of each channel row (the state waves' step order)
+        auto prepare = [&](int stage, int b3, int qc) __attribute__((always_inline)) {
+            const uint32_t a0 = lds_off(ring + stage * STB + s2 * ROWB + c * 4);
+            float2 raw[3][3];  // [m][u | delta | z], .x step s2, .y step s2 + 4
+            RingRead2<NOP, OPB>::run(a0, raw);
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                const int ch = c + 16 * m;
+                float x[2], xu[2], uv[2], fz[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const bool tv = (int64_t)qc * TCH + 8 * e + s2 + 4 * i < L;
+                    const float uu = i ? raw[m][0].y : raw[m][0].x;
+                    float v = (i ? raw[m][1].y : raw[m][1].x) + bias_r[m];
+                    if (SOFTPLUS) v = softplus(v);
+                    v = tv ? v : 0.0f;
+                    x[i] = v;
+                    xu[i] = v * uu;
+                    uv[i] = uu;
+                    fz[i] = HAS_Z ? silu(i ? raw[m][NOP - 1].y : raw[m][NOP - 1].x) : 1.0f;
+                }
+                // inline-asm stores: for compiler-visible LDS stores the compiler would first wait
+                // for every buffer load still writing the ring (vmcnt(0)); the barrier that ends
+                // the phase waits for these stores (lgkmcnt(0))
+                const uint32_t ha = lds_off(&s_x[b3][0][ch][4 * s2 + 2 * e]);
+                const hx_u32x2 vx = {__float_as_uint(x[0]), __float_as_uint(x[1])};
+                const hx_u32x2 vxu = {__float_as_uint(xu[0]), __float_as_uint(xu[1])};
+                const hx_u32x2 vu = {__float_as_uint(uv[0]), __float_as_uint(uv[1])};
+                const hx_u32x2 vz = {__float_as_uint(fz[0]), __float_as_uint(fz[1])};
+                constexpr int OPS = GCH * DS * 4;  // bytes between the hand-over operands
+                asm volatile("ds_write_b64 %0, %1\n\tds_write_b64 %0, %2 offset:%5\n\tds_write_b64 %0, %3 offset:%6"
+                             :: "v"(ha), "v"(vx), "v"(vxu), "v"(vu), "v"(vz), "n"(OPS), "n"(2 * OPS) : "memory");
+                if (HAS_Z) asm volatile("ds_write_b64 %0, %1 offset:%2" :: "v"(ha), "v"(vz), "n"(3 * OPS) : "memory");
+            }
+        };
+        auto wait_loads = [&]() __attribute__((always_inline)) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
+        };
+        auto barrier = [&]() __attribute__((always_inline)) {
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        };
+        // ring stage of chunk q is q % NR; every chunk index issues exactly LPC loads, so the
+        // wait count is the same before every prepare. The ring reads complete inside
+        // prepare, so the stage is refilled right after it.
+#pragma unroll
+        for (int k = 0; k < NR; ++k) issue(k, k);
+        int stage = 0, b3 = 0, q = 0;
+        auto step = [&]() __attribute__((always_inline)) {
+            wait_loads();
+            prepare(stage, b3, q);
+            issue(stage, q + NR);
+            stage = stage + 1 == NR ? 0 : stage + 1;
+            b3 = b3 == 2 ? 0 : b3 + 1;
+            ++q;
+        };
+        step();               // chunk 0
+        if (nch > 1) step();  // chunk 1
+        barrier();
+        for (int p = 0; p < nch; ++p) {
+            if (p + 2 < nch) step();  // chunk p + 2
+            barrier();
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load still writing LDS at exit
+    } else if (w < 3) {
+        state_wave(std::integral_constant<int, 0>{});
+    } else {
+        state_wave(std::integral_constant<int, 1>{});
+    }
+}
+
 // ----------------------------------------------------------------------------- generic path
 // One thread per (b, d), states in registers, any dstate <= NMAX, no alignment assumptions.
 template <typename T, int NMAX>
@@ -1337,12 +1676,20 @@ int dispatch_wave(const ScanArgs& a) {
 // runs two of its blocks: one wave per SIMD, the element wave on a SIMD of its own. Granted per
 // kernel and device through hipFuncSetAttribute (cached).
 constexpr size_t kWsStaticLds = 3 * 4 * 48 * 20 * 4;
-size_t ws_dyn_lds(int NR, bool has_z, size_t es) {
+// scan_ws2_kernel: 2 element waves x NR stages x operands x 2048-byte slots, then the
+// hand-over buffers and the readout buffers; at least 84 KB so that one block runs per CU
+size_t ws2_dyn_lds(int NR, bool has_z) {
+    const size_t need = (size_t)2 * NR * (has_z ? 3 : 2) * 2048 + kWsStaticLds + 2 * 3 * 64 * 16;
+    return need > 84 * 1024 ? need : 84 * 1024;
+}
+// scan_ws_kernel: its ring starts right after the static hand-over buffers and, like every LDS
+// target of a load to LDS, must end below 64 KiB (46080 + 2 x 3 x 3072 = 64512 at fp32)
+size_t ws_dyn_lds(int NR, bool has_z, size_t es, size_t stat) {
     const size_t ring = (size_t)NR * (has_z ? 3 : 2) * 16 * 48 * es;
-    const size_t need = 84 * 1024 - kWsStaticLds;
+    const size_t need = 84 * 1024 - stat;
     return ring > need ? ring : need;
 }
-bool ws_lds_ok(const void* fn, size_t bytes) {
+bool ws_lds_ok(const void* fn, size_t bytes, size_t stat) {
     struct Entry { const void* fn; int dev; int ok; };
     static Entry cache[64];
     static int n = 0;
@@ -1352,38 +1699,46 @@ bool ws_lds_ok(const void* fn, size_t bytes) {
         if (cache[i].fn == fn && cache[i].dev == dev) return cache[i].ok != 0;
     int v = 0;
     const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
-                    (size_t)v >= bytes + kWsStaticLds &&
+                    (size_t)v >= bytes + stat &&
                     hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
     (void)hipGetLastError();
     if (n < 64) cache[n++] = Entry{fn, dev, ok ? 1 : 0};
     return ok;
 }
 
-template <typename T, int NR, bool HAS_Z, bool SP>
+template <typename T, int NR, bool HAS_Z, bool SP, bool SPLIT>
 int launch_ws(const ScanArgs& a) {
     const int64_t ngrp = (a.Dm + 47) / 48;
     HX_REQUIRE(ngrp * a.Bt <= 0x7fffffff, HX_ERR_UNSUPPORTED,
                "selective scan: %lld blocks exceed the grid", (long long)(ngrp * a.Bt));
-    const void* fn = (const void*)scan_ws_kernel<T, NR, HAS_Z, SP>;
-    const size_t dyn = ws_dyn_lds(NR, HAS_Z, sizeof(T));
-    HX_REQUIRE(ws_lds_ok(fn, dyn), HX_ERR_UNSUPPORTED,
-               "selective scan: the device does not grant %zu bytes of LDS per block",
-               dyn + kWsStaticLds);
-    hipLaunchKernelGGL((scan_ws_kernel<T, NR, HAS_Z, SP>), dim3((unsigned)(ngrp * a.Bt)), dim3(256), dyn,
-                       a.stream, a.L, a.Dm, (int)ngrp, (const T*)a.u, (const T*)a.delta, a.A,
-                       (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
-                       a.init_state, a.last_state);
+    const void* fn = SPLIT ? (const void*)scan_ws2_kernel<T, NR, HAS_Z, SP>
+                           : (const void*)scan_ws_kernel<T, NR, HAS_Z, SP>;
+    // the split kernel keeps all its LDS in the dynamic allocation (rings, hand-over, readouts)
+    const size_t stat = SPLIT ? 0 : kWsStaticLds;
+    const size_t dyn = SPLIT ? ws2_dyn_lds(NR, HAS_Z) : ws_dyn_lds(NR, HAS_Z, sizeof(T), stat);
+    HX_REQUIRE(ws_lds_ok(fn, dyn, stat), HX_ERR_UNSUPPORTED,
+               "selective scan: the device does not grant %zu bytes of LDS per block", dyn + stat);
+    if constexpr (SPLIT)
+        hipLaunchKernelGGL((scan_ws2_kernel<T, NR, HAS_Z, SP>), dim3((unsigned)(ngrp * a.Bt)), dim3(512),
+                           dyn, a.stream, a.L, a.Dm, (int)ngrp, (const T*)a.u, (const T*)a.delta, a.A,
+                           (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
+                           a.init_state, a.last_state);
+    else
+        hipLaunchKernelGGL((scan_ws_kernel<T, NR, HAS_Z, SP>), dim3((unsigned)(ngrp * a.Bt)), dim3(256),
+                           dyn, a.stream, a.L, a.Dm, (int)ngrp, (const T*)a.u, (const T*)a.delta, a.A,
+                           (const T*)a.B, (const T*)a.C, a.D, (const T*)a.z, a.dt_bias, (T*)a.out,
+                           a.init_state, a.last_state);
     HX_LAUNCH_CHECK();
     return HX_OK;
 }
 
-template <typename T, int NR>
+template <typename T, int NR, bool SPLIT = false>
 int dispatch_ws(const ScanArgs& a) {
     const bool hz = a.z != nullptr;
-    if (hz && a.softplus) return launch_ws<T, NR, true, true>(a);
-    if (hz) return launch_ws<T, NR, true, false>(a);
-    if (a.softplus) return launch_ws<T, NR, false, true>(a);
-    return launch_ws<T, NR, false, false>(a);
+    if (hz && a.softplus) return launch_ws<T, NR, true, true, SPLIT>(a);
+    if (hz) return launch_ws<T, NR, true, false, SPLIT>(a);
+    if (a.softplus) return launch_ws<T, NR, false, true, SPLIT>(a);
+    return launch_ws<T, NR, false, false, SPLIT>(a);
 }
 
 template <typename T, int NMAX>
@@ -1438,7 +1793,8 @@ bool ws_preferred(const ScanArgs& a, size_t es) {
 }
 
 // Kernel variant of the calling thread: 0 = auto, -1 = generic, 8 = the fast kernel, 40 =
-// scan_wave_kernel, 42 = scan_wave3_kernel, 44 = the warp-specialised kernel (set by
+// scan_wave_kernel, 42 = scan_wave3_kernel, 44 = the warp-specialised kernel, 46 = its
+// split-state form (fp32 storage; other dtypes fall back to the fast kernel) (set by
 // hx_set_scan_variant; a measurement knob, per thread so concurrent callers do not see each
 // other's setting).
 thread_local int g_scan_variant = 0;
@@ -1455,7 +1811,12 @@ int run_scan(const ScanArgs& a) {
                          a.Bt * ((a.Dm + 63) / 64) <= 0x7fffffff;
     if (v == 0) {  // auto: the wave-complete kernels where their float4 access is legal
         if (tile_ok) {
-            if (ws_preferred(a, sizeof(T))) return dispatch_ws<T, 2>(a);
+            if (ws_preferred(a, sizeof(T))) {
+                // fp32: the split-state form (two waves per SIMD); bf16 keeps the 4-wave form
+                if constexpr (std::is_same<T, float>::value)
+                    if ((a.L + 48) * a.Dm * 4 < (1LL << 32)) return dispatch_ws<T, 3, true>(a);
+                return dispatch_ws<T, 2>(a);
+            }
             return a.L * a.Dm < (1LL << 31) ? dispatch_wave<T, 2, 3>(a) : dispatch_wave<T, 2>(a);
         }
         return dispatch_fast<T, 8, 16>(a);
@@ -1465,6 +1826,11 @@ int run_scan(const ScanArgs& a) {
         case 42: if (tile_ok && a.L * a.Dm < (1LL << 31)) return dispatch_wave<T, 2, 3>(a); break;
         case 44:
             if (tile_ok && (a.L + 16) * a.Dm * (int64_t)sizeof(T) < (1LL << 32)) return dispatch_ws<T, 2>(a);
+            break;
+        case 46:
+            if constexpr (std::is_same<T, float>::value)
+                if (tile_ok && (a.L + 48) * a.Dm * (int64_t)sizeof(T) < (1LL << 32))
+                    return dispatch_ws<T, 3, true>(a);
             break;
         default: break;
     }
@@ -1619,8 +1985,8 @@ extern "C" int hx_selective_scan_fwd_noalloc(int64_t batch, int64_t seqlen, int6
 
 extern "C" int hx_set_scan_variant(int variant) {
     HX_REQUIRE(variant == 0 || variant == -1 || variant == 8 || variant == 40 || variant == 42 ||
-                   variant == 44,
-               HX_ERR_INVALID_INPUT, "hx_set_scan_variant: %d is not one of 0, -1, 8, 40, 42, 44",
+                   variant == 44 || variant == 46,
+               HX_ERR_INVALID_INPUT, "hx_set_scan_variant: %d is not one of 0, -1, 8, 40, 42, 44, 46",
                variant);
     hx::g_scan_variant = variant;
     return HX_OK;

@@ -365,8 +365,10 @@ int hx_eye_f32(int64_t n, float* y, void* stream);
  * needs), 8 = the fast kernel (8 waves split the states of 64 channels), 40 = the wave-complete
  * kernel (a wave owns 16 channels x 16 states; 64-bit row offsets), 42 = its leaner form with
  * per-wave staging, 44 = the warp-specialised kernel (3 state waves + 1 element wave per CU, 48
- * channels per block). A measurement knob with no reference counterpart; results agree within
- * fp32 rounding for every variant. */
+ * channels per block), 46 = its split-state form for fp32 storage (6 state waves holding half of
+ * each channel's states + 2 element waves; the automatic choice for fp32 wherever 44 would be).
+ * A measurement knob with no reference counterpart; results agree within fp32 rounding for
+ * every variant. */
 int hx_set_scan_variant(int variant);
 /* Selects the bf16 GEMM kernel for later calls on the calling thread: 0 auto, 1 128x128 tiles, 2 256x128 tiles, 3 small-M
  * 32x32 / 32x64 tiles with K split over 4 waves (K % 8 == 0),

@@ -16,8 +16,9 @@ from tests.util import TOL_BF16, TOL_F32, bf16_round, rel_err, scan_inputs
 
 pytestmark = pytest.mark.gpu
 
-# -1 generic, 8 fast, 40 wave-complete, 42 its per-wave-staged form, 44 warp-specialised
-VARIANTS = [-1, 8, 40, 42, 44]
+# -1 generic, 8 fast, 40 wave-complete, 42 its per-wave-staged form, 44 warp-specialised,
+# 46 its split-state form (fp32)
+VARIANTS = [-1, 8, 40, 42, 44, 46]
 
 
 def to_dev(x, dev, dtype=torch.float32):
@@ -76,7 +77,7 @@ def test_scan_optional_operands(dev, with_z, with_D, softplus, variant):
     assert rel_err(g, r) <= TOL_F32
 
 
-@pytest.mark.parametrize("variant", [0, 42, 44, -1])
+@pytest.mark.parametrize("variant", [0, 42, 44, 46, -1])
 def test_scan_softplus_all_regimes(dev, variant):
     """delta spread over softplus's regimes: e^x far below f32 resolution of 1 + e^x (x < -17,
     where softplus(x) = e^x), the log1p range, and past the x > 20 cut-over."""
@@ -206,7 +207,7 @@ def test_shape_errors_raise_reference_variants(dev):
                                to_dev(x["B"], dev), to_dev(x["C"], dev))
 
 
-@pytest.mark.parametrize("variant", [0, 40, 42, 44])
+@pytest.mark.parametrize("variant", [0, 40, 42, 44, 46])
 def test_baseline_config2_full_size(dev, variant):
     """BASELINE config 2 (batch 8, L 2048, d_inner 1536, d_state 16, fp32) end to end against the
     (multi-threaded, arithmetic-identical) CPU oracle."""
