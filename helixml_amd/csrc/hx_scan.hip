@@ -848,6 +848,45 @@ template <int NOP, int OPB> struct RingRead2 {
     }
 };
 
+// Output-stage reads of scan_ws2_kernel's element waves, as inline asm (see RingRead): for
+// m < 3, y0/y1[m] = the float2 at ay + 1024 m (+ 3072 for the upper half's partials), uu[m] =
+// the float2 at ax + 1280 m (u), gz[m] the same OPS bytes further (SiLU(z)) when HZ.
+template <bool HZ, int OPS> struct HandoverRead {
+    __device__ static inline void run(uint32_t ay, uint32_t ax, float2 (&y0)[3], float2 (&y1)[3],
+                                      float2 (&uu)[3], float2 (&gz)[3]) {
+        hx_u32x2 a[3], bq[3], u[3], zz[3];
+        if constexpr (HZ) {
+            asm volatile(
+                "ds_read_b64 %0, %12\n\tds_read_b64 %1, %12 offset:1024\n\tds_read_b64 %2, %12 offset:2048\n\t"
+                "ds_read_b64 %3, %12 offset:3072\n\tds_read_b64 %4, %12 offset:4096\n\tds_read_b64 %5, %12 offset:5120\n\t"
+                "ds_read_b64 %6, %13\n\tds_read_b64 %7, %13 offset:1280\n\tds_read_b64 %8, %13 offset:2560\n\t"
+                "ds_read_b64 %9, %13 offset:%14\n\tds_read_b64 %10, %13 offset:%15\n\tds_read_b64 %11, %13 offset:%16\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(bq[0]), "=&v"(bq[1]), "=&v"(bq[2]),
+                  "=&v"(u[0]), "=&v"(u[1]), "=&v"(u[2]), "=&v"(zz[0]), "=&v"(zz[1]), "=&v"(zz[2])
+                : "v"(ay), "v"(ax), "n"(OPS), "n"(OPS + 1280), "n"(OPS + 2560)
+                : "memory");
+        } else {
+            asm volatile(
+                "ds_read_b64 %0, %9\n\tds_read_b64 %1, %9 offset:1024\n\tds_read_b64 %2, %9 offset:2048\n\t"
+                "ds_read_b64 %3, %9 offset:3072\n\tds_read_b64 %4, %9 offset:4096\n\tds_read_b64 %5, %9 offset:5120\n\t"
+                "ds_read_b64 %6, %10\n\tds_read_b64 %7, %10 offset:1280\n\tds_read_b64 %8, %10 offset:2560\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(bq[0]), "=&v"(bq[1]), "=&v"(bq[2]),
+                  "=&v"(u[0]), "=&v"(u[1]), "=&v"(u[2])
+                : "v"(ay), "v"(ax)
+                : "memory");
+        }
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            y0[m] = make_float2(__uint_as_float(a[m][0]), __uint_as_float(a[m][1]));
+            y1[m] = make_float2(__uint_as_float(bq[m][0]), __uint_as_float(bq[m][1]));
+            uu[m] = make_float2(__uint_as_float(u[m][0]), __uint_as_float(u[m][1]));
+            gz[m] = HZ ? make_float2(__uint_as_float(zz[m][0]), __uint_as_float(zz[m][1])) : make_float2(1.0f, 1.0f);
+        }
+    }
+};
+
 // One element stored through a raw buffer resource: offsets at or past the resource's size are
 // dropped by the hardware, so a store needs no branch (and the compiler's wait counts stay exact).
 __device__ inline void buf_store(float v, __amdgpu_buffer_rsrc_t rs, uint32_t off, float*) {
@@ -1176,7 +1215,7 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
     extern __shared__ __attribute__((aligned(16))) char s_dyn[];
     static_assert(RING <= 65536 - 1024, "rings below 64 KiB");
     auto& s_x = *reinterpret_cast<float(*)[3][4][GCH][DS]>(s_dyn + RING);
-    auto& s_y = *reinterpret_cast<float4(*)[2][3][64]>(s_dyn + RING + sizeof(float) * 3 * 4 * GCH * DS);
+    auto& s_y = *reinterpret_cast<float4(*)[2][2][3][64]>(s_dyn + RING + sizeof(float) * 3 * 4 * GCH * DS);
 
     const int nblk = gridDim.x;
     int id = blockIdx.x;
@@ -1187,7 +1226,6 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nch = (int)((L + TCH - 1) / TCH);
-    const uint32_t D32 = (uint32_t)Dm;
 
     auto state_wave = [&](auto hc) __attribute__((always_inline)) {
         constexpr int HH = decltype(hc)::value;  // 0: states 0..7, 1: states 8..15
@@ -1204,7 +1242,6 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
             A2[k] = A[dc * NS + st0 + k] * kLog2e;
             h[k] = init_state ? init_state[(b * Dm + dc) * NS + st0 + k] : 0.0f;
         }
-        const float Dd = Dv ? Dv[dc] : 0.0f;
         const T* Bb = Bm + b * L * NS;
         const T* Cb = Cm + b * L * NS;
         const uint32_t bc_last = (uint32_t)(L - 1) * NS + st0;
@@ -1216,11 +1253,6 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
             rc[k] = Pair<T>::load(Cb + bo);
             bc_next += TCH * NS;
         };
-        const uint32_t nrec = (uint32_t)(L * Dm * (int64_t)sizeof(T));
-        const uint32_t row_bytes = D32 * (uint32_t)sizeof(T);
-        const uint32_t lane_off = dvalid ? ((uint32_t)r * D32 + (uint32_t)d) * (uint32_t)sizeof(T) : nrec;
-        const __amdgpu_buffer_rsrc_t ors =
-            __builtin_amdgcn_make_buffer_rsrc(out + b * L * Dm, (short)0, (int)nrec, kBufRsrcWord3);
         float dl[2][16], du[2][16];
         auto read_dt = [&](auto kc, int b3) __attribute__((always_inline)) {
             constexpr int k = decltype(kc)::value;
@@ -1235,22 +1267,6 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
                 du[k][i] = q.x; du[k][4 + i] = q.y; du[k][8 + i] = q.z; du[k][12 + i] = q.w;
             }
         };
-        // upper half: this wave's readouts, u and SiLU(z) of the chunk whose outputs are pending
-        float Yp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, fup[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        float fzp[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-        auto finish = [&](int p) __attribute__((always_inline)) {
-            const float4 o = s_y[p & 1][g][lane];
-            const float ov[4] = {o.x, o.y, o.z, o.w};
-            // step r + 4i of chunk p sits at lane_off + (16p + 4i) * row bytes; steps past the
-            // end land at or past nrec and are dropped; lanes of channels past Dm stay at nrec
-            const uint32_t chunk_off = dvalid ? lane_off + (uint32_t)p * (uint32_t)TCH * row_bytes : nrec;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float y = fmaf(Dd, fup[i], ov[i] + Yp[i]);
-                if (HAS_Z) y *= fzp[i];
-                buf_store(y, ors, chunk_off + 4 * i * row_bytes, (T*)nullptr);
-            }
-        };
         fetch(0);
         fetch(1);
         lds_barrier();  // chunks 0 and 1 prepared
@@ -1263,7 +1279,6 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
                 if (p >= nch) return;  // uniform
                 const int b3n = b3 == 2 ? 0 : b3 + 1;
                 if (p + 1 < nch) read_dt(std::integral_constant<int, k ^ 1>{}, b3n);
-                if (HH && p > 0) finish(p - 1);
                 const float bk[2] = {rb[k].x, rb[k].y};
                 const float ck[2] = {rc[k].x, rc[k].y};
                 float P[16];
@@ -1288,21 +1303,11 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
                 fetch(k);  // chunk p + 2, into the slot this chunk's B/C came from
                 float Y[4];
                 rows_reduce_scatter(P, Y);  // Y[i]: step r + 4i, this half's 8 states
-                if (HH) {
-                    const float4 fu = *reinterpret_cast<const float4*>(&s_x[b3][2][lch][4 * r]);
-                    const float4 fz = HAS_Z ? *reinterpret_cast<const float4*>(&s_x[b3][3][lch][4 * r])
-                                            : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-                    Yp[0] = Y[0]; Yp[1] = Y[1]; Yp[2] = Y[2]; Yp[3] = Y[3];
-                    fup[0] = fu.x; fup[1] = fu.y; fup[2] = fu.z; fup[3] = fu.w;
-                    fzp[0] = fz.x; fzp[1] = fz.y; fzp[2] = fz.z; fzp[3] = fz.w;
-                } else {
-                    s_y[p & 1][g][lane] = make_float4(Y[0], Y[1], Y[2], Y[3]);
-                }
+                s_y[p & 1][HH][g][lane] = make_float4(Y[0], Y[1], Y[2], Y[3]);  // the element waves finish it
                 b3 = b3n;
                 lds_barrier();
             });
         }
-        if (HH && nch > 0) finish(nch - 1);
         if (last_state && dvalid) {
 #pragma unroll
             for (int k = 0; k < 2; ++k) last_state[(b * Dm + d) * NS + st0 + k] = h[k];
@@ -1397,33 +1402,72 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
                 if (HAS_Z) asm volatile("ds_write_b64 %0, %1 offset:%2" :: "v"(ha), "v"(vz), "n"(3 * OPS) : "memory");
             }
         };
-        auto wait_loads = [&]() __attribute__((always_inline)) {
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
+        // outputs of chunk pc (its readouts published in phase pc, read in phase pc + 1): lane
+        // (c, s2) sums both halves' partials for channels c + 16m at steps 8e + s2 + 4i, adds D*u,
+        // applies the gate and stores; steps past the end fall at or past nrec (dropped), lanes of
+        // channels past Dm stay at nrec
+        float Dd[3];
+        uint32_t obase[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            const int64_t ch = cblk + c + 16 * m;
+            Dd[m] = (Dv && ch < Dm) ? Dv[ch] : 0.0f;
+            obase[m] = ch < Dm ? (uint32_t)((8 * e + s2) * Dm + ch) * 4u : nrec;
+        }
+        const __amdgpu_buffer_rsrc_t ors =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(out + b * L * Dm), (short)0, (int)nrec, kBufRsrcWord3);
+        const uint32_t row4 = (uint32_t)(4 * Dm * 4);  // 4 steps
+        auto finish = [&](int pc) __attribute__((always_inline)) {
+            const uint32_t ay = lds_off(&s_y[pc & 1][0][0][s2 * 16 + c]) + 8 * e;
+            const uint32_t ax = lds_off(&s_x[pc % 3][2][c][4 * s2 + 2 * e]);
+            float2 y0[3], y1[3], uu[3], gz[3];
+            HandoverRead<HAS_Z, GCH * DS * 4>::run(ay, ax, y0, y1, uu, gz);
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                const uint32_t o = obase[m] < nrec ? obase[m] + (uint32_t)pc * chunk_bytes : nrec;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    float y = fmaf(Dd[m], i ? uu[m].y : uu[m].x, (i ? y0[m].y : y0[m].x) + (i ? y1[m].y : y1[m].x));
+                    if (HAS_Z) y *= i ? gz[m].y : gz[m].x;
+                    buf_store(y, ors, o + (uint32_t)i * row4, (float*)nullptr);
+                }
+            }
         };
+
         auto barrier = [&]() __attribute__((always_inline)) {
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         };
-        // ring stage of chunk q is q % NR; every chunk index issues exactly LPC loads, so the
-        // wait count is the same before every prepare. The ring reads complete inside
-        // prepare, so the stage is refilled right after it.
+        // ring stage of chunk q is q % NR; every chunk index issues exactly LPC loads and every
+        // finish exactly 6 stores (stores count in vmcnt too). The wait before preparing chunk q
+        // lets through what was issued after chunk q's loads: NR - 1 chunks of loads, plus, from
+        // phase NR on, NR finishes' stores; before that, fewer stores were issued and the
+        // smaller count only waits longer. The ring reads complete inside prepare, so the stage
+        // is refilled right after it.
+        constexpr int WAITS = WAITN + NR * 6;
+        static_assert(WAITS <= 63, "vmcnt range");
 #pragma unroll
         for (int k = 0; k < NR; ++k) issue(k, k);
         int stage = 0, b3 = 0, q = 0;
-        auto step = [&]() __attribute__((always_inline)) {
-            wait_loads();
+        auto step = [&](auto wc) __attribute__((always_inline)) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(decltype(wc)::value) : "memory");
             prepare(stage, b3, q);
             issue(stage, q + NR);
             stage = stage + 1 == NR ? 0 : stage + 1;
             b3 = b3 == 2 ? 0 : b3 + 1;
             ++q;
         };
-        step();               // chunk 0
-        if (nch > 1) step();  // chunk 1
+        step(std::integral_constant<int, WAITN>{});                // chunk 0
+        if (nch > 1) step(std::integral_constant<int, WAITN>{});  // chunk 1
         barrier();
         for (int p = 0; p < nch; ++p) {
-            if (p + 2 < nch) step();  // chunk p + 2
+            if (p > 0) finish(p - 1);  // before chunk p + 2 overwrites that chunk's u and SiLU(z)
+            if (p + 2 < nch) {         // chunk p + 2
+                if (p >= NR) step(std::integral_constant<int, WAITS>{});
+                else step(std::integral_constant<int, WAITN>{});
+            }
             barrier();
         }
+        if (nch > 0) finish(nch - 1);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load still writing LDS at exit
     } else if (w < 3) {
         state_wave(std::integral_constant<int, 0>{});
@@ -1679,7 +1723,7 @@ constexpr size_t kWsStaticLds = 3 * 4 * 48 * 20 * 4;
 // scan_ws2_kernel: 2 element waves x NR stages x operands x 2048-byte slots, then the
 // hand-over buffers and the readout buffers; at least 84 KB so that one block runs per CU
 size_t ws2_dyn_lds(int NR, bool has_z) {
-    const size_t need = (size_t)2 * NR * (has_z ? 3 : 2) * 2048 + kWsStaticLds + 2 * 3 * 64 * 16;
+    const size_t need = (size_t)2 * NR * (has_z ? 3 : 2) * 2048 + kWsStaticLds + 2 * 2 * 3 * 64 * 16;
     return need > 84 * 1024 ? need : 84 * 1024;
 }
 // scan_ws_kernel: its ring starts right after the static hand-over buffers and, like every LDS
