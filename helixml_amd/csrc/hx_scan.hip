@@ -848,6 +848,47 @@ template <int NOP, int OPB> struct RingRead2 {
     }
 };
 
+// bf16 ring of scan_ws2_kernel: r[m][o] = the bf16 channel `odd` of the dword at
+// a + o * OPB + 32 m and of the dword 384 bytes further (one channel pair at two steps 4 rows of
+// 48 bf16 channels apart), widened to fp32; ds_read2_b32 with dword offsets 8m and 8m + 96.
+template <int NOP, int OPB> struct RingRead2Bf16 {
+    __device__ static inline void run(uint32_t a, int odd, float2 (&r)[3][3]) {
+        const uint32_t a1 = a + OPB, a2 = a + 2 * OPB;
+        hx_u32x2 v[3][3];
+        if constexpr (NOP == 3) {
+            asm volatile(
+                "ds_read2_b32 %0, %9 offset1:96\n\tds_read2_b32 %1, %10 offset1:96\n\tds_read2_b32 %2, %11 offset1:96\n\t"
+                "ds_read2_b32 %3, %9 offset0:8 offset1:104\n\tds_read2_b32 %4, %10 offset0:8 offset1:104\n\t"
+                "ds_read2_b32 %5, %11 offset0:8 offset1:104\n\t"
+                "ds_read2_b32 %6, %9 offset0:16 offset1:112\n\tds_read2_b32 %7, %10 offset0:16 offset1:112\n\t"
+                "ds_read2_b32 %8, %11 offset0:16 offset1:112\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(v[0][2]), "=&v"(v[1][0]), "=&v"(v[1][1]), "=&v"(v[1][2]),
+                  "=&v"(v[2][0]), "=&v"(v[2][1]), "=&v"(v[2][2])
+                : "v"(a), "v"(a1), "v"(a2)
+                : "memory");
+        } else {
+            (void)a2;
+            asm volatile(
+                "ds_read2_b32 %0, %6 offset1:96\n\tds_read2_b32 %1, %7 offset1:96\n\t"
+                "ds_read2_b32 %2, %6 offset0:8 offset1:104\n\tds_read2_b32 %3, %7 offset0:8 offset1:104\n\t"
+                "ds_read2_b32 %4, %6 offset0:16 offset1:112\n\tds_read2_b32 %5, %7 offset0:16 offset1:112\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(v[1][0]), "=&v"(v[1][1]), "=&v"(v[2][0]), "=&v"(v[2][1])
+                : "v"(a), "v"(a1)
+                : "memory");
+        }
+#pragma unroll
+        for (int m = 0; m < 3; ++m)
+#pragma unroll
+            for (int o = 0; o < NOP; ++o) {
+                const uint32_t x = v[m][o][0], y = v[m][o][1];
+                r[m][o] = make_float2(__uint_as_float(odd ? (x & 0xffff0000u) : (x << 16)),
+                                      __uint_as_float(odd ? (y & 0xffff0000u) : (y << 16)));
+            }
+    }
+};
+
 // Output-stage reads of scan_ws2_kernel's element waves, as inline asm (see RingRead): for
 // m < 3, y0/y1[m] = the float2 at ay + 1024 m (+ 3072 for the upper half's partials), uu[m] =
 // the float2 at ax + 1280 m (u), gz[m] the same OPS bytes further (SiLU(z)) when HZ.
@@ -1172,7 +1213,7 @@ __global__ __launch_bounds__(256) void scan_ws_kernel(
 // ----------------------------------------------------------------------------- split-state form
 // Warp-specialised scan with every SIMD running two waves, so one wave's waits (hand-over
 // barrier, B/C loads, LDS reads, dependent issue) overlap the other's issue. A block of 8 waves
-// owns 48 channels of one batch row (fp32 storage):
+// owns 48 channels of one batch row (fp32 or bf16 storage; the arithmetic is fp32):
 //   * waves 0..2 and 4..6 are state waves: wave w < 3 holds states 0..7 of channel group w,
 //     wave w > 3 states 8..15 of group w - 4 (lane (r, c): channel c, states 8h + 2r, 8h + 2r + 1;
 //     B/C of step t0 + j in lane j of row r). Each reduce-scatters its 8 states' readouts
@@ -1184,7 +1225,8 @@ __global__ __launch_bounds__(256) void scan_ws_kernel(
 // 0..2 each run a lower and an upper state wave, SIMD 3 the two element waves. The hand-over
 // buffers hold each channel's 16 steps in the order 4 (s % 4) + s / 4 for all four operands.
 // The readout is summed as (states 0..7) + (states 8..15), so results match scan_ws_kernel to
-// rounding, not bit for bit. Requires Dm % 4 == 0, 16-byte rows, (L + 48) * Dm * 4 < 2^32.
+// rounding, not bit for bit. Requires Dm % 4 == 0 (Dm % 8 == 0 for bf16 storage), 16-byte rows,
+// (L + 48) * Dm * es < 2^32.
 template <typename T> struct Pair;
 template <> struct Pair<float> {
     __device__ static inline float2 load(const float* p) { return *reinterpret_cast<const float2*>(p); }
@@ -1205,8 +1247,10 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
     const float* __restrict__ init_state, float* __restrict__ last_state) {
     constexpr int NS = 16, TCH = 16, GCH = 48, DS = 20;
     constexpr int NOP = HAS_Z ? 3 : 2;
-    constexpr int OPB = 2048;                 // ring slot of one operand of a half chunk (8 steps x
-                                              // 48 channels = 1536 bytes, padded to two full loads)
+    constexpr int ES = (int)sizeof(T);
+    constexpr int NLD = ES / 2;               // 64-lane x 16-byte loads per operand of a half chunk
+    constexpr int OPB = NLD * 1024;           // ring slot of one operand of a half chunk (8 steps x
+                                              // 48 channels = 1536 or 768 bytes, padded to whole loads)
     constexpr int STB = NOP * OPB;            // one ring stage
     constexpr int RING = 2 * NR * STB;        // both element waves' rings
     // All LDS is the dynamic allocation, rings first: the LDS base of a load to LDS is a 16-bit
@@ -1325,39 +1369,42 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
         // steps s2 and s2 + 4 of the wave's half: ring reads and hand-over writes of a wave
         // instruction touch distinct banks.
         const int e = w >> 2;
-        constexpr int ROWB = GCH * 4;      // one step of 48 channels
-        constexpr int LPC = NOP * 2;       // loads per chunk
+        constexpr int ROWB = GCH * ES;     // one step of 48 channels
+        constexpr int LPR = ROWB / 16;     // load lanes per step row
+        constexpr int EPP = 16 / ES;       // channels per 16-byte piece
+        constexpr int LPC = NOP * NLD;     // loads per chunk
         constexpr int WAITN = (NR - 1) * LPC;
         static_assert(WAITN <= 63, "vmcnt range");
         char* ring = s_dyn + e * NR * STB;  // [NR][op][8 steps][48 ch]
-        const uint32_t nrec = (uint32_t)(L * Dm * 4);
+        const uint32_t nrec = (uint32_t)(L * Dm * ES);
         const __amdgpu_buffer_rsrc_t rs_u =
             __builtin_amdgcn_make_buffer_rsrc((void*)(u + b * L * Dm), (short)0, (int)nrec, kBufRsrcWord3);
         const __amdgpu_buffer_rsrc_t rs_d =
             __builtin_amdgcn_make_buffer_rsrc((void*)(delta + b * L * Dm), (short)0, (int)nrec, kBufRsrcWord3);
         const __amdgpu_buffer_rsrc_t rs_z = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(HAS_Z ? z + b * L * Dm : u + b * L * Dm), (short)0, (int)nrec, kBufRsrcWord3);
-        // load instruction i, lane q: bytes 1024 i + 16 q of the half chunk = step 8e + (64 i + q) / 12,
-        // channels 4 ((64 i + q) % 12) ..; pieces of channels past Dm read channel 0 (never used);
-        // lanes q >= 96 fill the slot's padding with chunk data that is never read
-        uint32_t loff[2];
+        // load instruction i, lane q: bytes 1024 i + 16 q of the half chunk = step 8e + (64 i + q) / LPR,
+        // channels EPP ((64 i + q) % LPR) ..; pieces of channels past Dm read channel 0 (never
+        // used); lanes past the 8 rows fill the slot's padding with chunk data that is never read
+        uint32_t loff[2];  // NLD <= 2 used (a bound that depends on T, captured by the lambdas
+                           // below, makes the host pass drop the kernels' launch stubs)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NLD; ++i) {
             const int q = 64 * i + lane;
-            const int64_t ch = cblk + (q % 12) * 4;
-            loff[i] = q < 96 ? (uint32_t)((8 * e + q / 12) * Dm + (ch < Dm ? ch : 0)) * 4u : 0u;
+            const int64_t ch = cblk + (q % LPR) * EPP;
+            loff[i] = q < 8 * LPR ? (uint32_t)(((8 * e + q / LPR) * Dm + (ch < Dm ? ch : 0)) * ES) : 0u;
         }
-        const uint32_t chunk_bytes = (uint32_t)(TCH * Dm * 4);
+        const uint32_t chunk_bytes = (uint32_t)(TCH * Dm * ES);
         auto issue = [&](int stage, int qc) __attribute__((always_inline)) {
             char* dst = ring + stage * STB;
             const uint32_t cb = (uint32_t)qc * chunk_bytes;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lvoid_t*)dst, 16, loff[0] + cb, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_d, (lvoid_t*)(dst + OPB), 16, loff[0] + cb, 0, 0, 0);
-            if (HAS_Z) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_z, (lvoid_t*)(dst + 2 * OPB), 16, loff[0] + cb, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lvoid_t*)(dst + 1024), 16, loff[1] + cb, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_d, (lvoid_t*)(dst + OPB + 1024), 16, loff[1] + cb, 0, 0, 0);
-            if (HAS_Z)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_z, (lvoid_t*)(dst + 2 * OPB + 1024), 16, loff[1] + cb, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < NLD; ++i) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lvoid_t*)(dst + 1024 * i), 16, loff[i] + cb, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_d, (lvoid_t*)(dst + OPB + 1024 * i), 16, loff[i] + cb, 0, 0, 0);
+                if (HAS_Z)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_z, (lvoid_t*)(dst + 2 * OPB + 1024 * i), 16, loff[i] + cb, 0, 0, 0);
+            }
         };
         const int c = lane & 15, s2 = lane >> 4;
         float bias_r[3];
@@ -1369,9 +1416,13 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
         // chunk qc from ring stage `stage` into hand-over buffer b3: steps 8e + s2 + 4i (i < 2)
         // go to index 4 s2 + 2e + i of each channel row (the state waves' step order)
         auto prepare = [&](int stage, int b3, int qc) __attribute__((always_inline)) {
-            const uint32_t a0 = lds_off(ring + stage * STB + s2 * ROWB + c * 4);
             float2 raw[3][3];  // [m][u | delta | z], .x step s2, .y step s2 + 4
-            RingRead2<NOP, OPB>::run(a0, raw);
+            if constexpr (ES == 4) {
+                RingRead2<NOP, OPB>::run(lds_off(ring + stage * STB + s2 * ROWB + c * 4), raw);
+            } else {
+                // the dword holding channels c & ~1 and c | 1; this lane's half by c's parity
+                RingRead2Bf16<NOP, OPB>::run(lds_off(ring + stage * STB + s2 * ROWB + (c >> 1) * 4), c & 1, raw);
+            }
 #pragma unroll
             for (int m = 0; m < 3; ++m) {
                 const int ch = c + 16 * m;
@@ -1412,11 +1463,11 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
         for (int m = 0; m < 3; ++m) {
             const int64_t ch = cblk + c + 16 * m;
             Dd[m] = (Dv && ch < Dm) ? Dv[ch] : 0.0f;
-            obase[m] = ch < Dm ? (uint32_t)((8 * e + s2) * Dm + ch) * 4u : nrec;
+            obase[m] = ch < Dm ? (uint32_t)(((8 * e + s2) * Dm + ch) * ES) : nrec;
         }
         const __amdgpu_buffer_rsrc_t ors =
             __builtin_amdgcn_make_buffer_rsrc((void*)(out + b * L * Dm), (short)0, (int)nrec, kBufRsrcWord3);
-        const uint32_t row4 = (uint32_t)(4 * Dm * 4);  // 4 steps
+        const uint32_t row4 = (uint32_t)(4 * Dm * ES);  // 4 steps
         auto finish = [&](int pc) __attribute__((always_inline)) {
             const uint32_t ay = lds_off(&s_y[pc & 1][0][0][s2 * 16 + c]) + 8 * e;
             const uint32_t ax = lds_off(&s_x[pc % 3][2][c][4 * s2 + 2 * e]);
@@ -1429,7 +1480,7 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
                 for (int i = 0; i < 2; ++i) {
                     float y = fmaf(Dd[m], i ? uu[m].y : uu[m].x, (i ? y0[m].y : y0[m].x) + (i ? y1[m].y : y1[m].x));
                     if (HAS_Z) y *= i ? gz[m].y : gz[m].x;
-                    buf_store(y, ors, o + (uint32_t)i * row4, (float*)nullptr);
+                    buf_store(y, ors, o + (uint32_t)i * row4, (T*)nullptr);
                 }
             }
         };
@@ -1722,8 +1773,8 @@ int dispatch_wave(const ScanArgs& a) {
 constexpr size_t kWsStaticLds = 3 * 4 * 48 * 20 * 4;
 // scan_ws2_kernel: 2 element waves x NR stages x operands x 2048-byte slots, then the
 // hand-over buffers and the readout buffers; at least 84 KB so that one block runs per CU
-size_t ws2_dyn_lds(int NR, bool has_z) {
-    const size_t need = (size_t)2 * NR * (has_z ? 3 : 2) * 2048 + kWsStaticLds + 2 * 2 * 3 * 64 * 16;
+size_t ws2_dyn_lds(int NR, bool has_z, size_t es) {
+    const size_t need = (size_t)2 * NR * (has_z ? 3 : 2) * (es == 4 ? 2048 : 1024) + kWsStaticLds + 2 * 2 * 3 * 64 * 16;
     return need > 84 * 1024 ? need : 84 * 1024;
 }
 // scan_ws_kernel: its ring starts right after the static hand-over buffers and, like every LDS
@@ -1759,7 +1810,7 @@ int launch_ws(const ScanArgs& a) {
                            : (const void*)scan_ws_kernel<T, NR, HAS_Z, SP>;
     // the split kernel keeps all its LDS in the dynamic allocation (rings, hand-over, readouts)
     const size_t stat = SPLIT ? 0 : kWsStaticLds;
-    const size_t dyn = SPLIT ? ws2_dyn_lds(NR, HAS_Z) : ws_dyn_lds(NR, HAS_Z, sizeof(T), stat);
+    const size_t dyn = SPLIT ? ws2_dyn_lds(NR, HAS_Z, sizeof(T)) : ws_dyn_lds(NR, HAS_Z, sizeof(T), stat);
     HX_REQUIRE(ws_lds_ok(fn, dyn, stat), HX_ERR_UNSUPPORTED,
                "selective scan: the device does not grant %zu bytes of LDS per block", dyn + stat);
     if constexpr (SPLIT)
@@ -1836,9 +1887,16 @@ bool ws_preferred(const ScanArgs& a, size_t es) {
     return (double)ws_rounds * 0.89 < (double)w3_rounds;
 }
 
+// Whether scan_ws2_kernel takes these sizes: byte offsets of a batch row with the ring's lead in
+// 32 bits, and for bf16 whole 8-channel pieces per row (no 16-byte load straddles the row's end).
+template <typename T>
+bool ws2_ok(const ScanArgs& a) {
+    return (a.L + 48) * a.Dm * (int64_t)sizeof(T) < (1LL << 32) && (sizeof(T) == 4 || a.Dm % 8 == 0);
+}
+
 // Kernel variant of the calling thread: 0 = auto, -1 = generic, 8 = the fast kernel, 40 =
 // scan_wave_kernel, 42 = scan_wave3_kernel, 44 = the warp-specialised kernel, 46 = its
-// split-state form (fp32 storage; other dtypes fall back to the fast kernel) (set by
+// split-state form (where ws2_ok holds; otherwise the fast kernel) (set by
 // hx_set_scan_variant; a measurement knob, per thread so concurrent callers do not see each
 // other's setting).
 thread_local int g_scan_variant = 0;
@@ -1856,9 +1914,10 @@ int run_scan(const ScanArgs& a) {
     if (v == 0) {  // auto: the wave-complete kernels where their float4 access is legal
         if (tile_ok) {
             if (ws_preferred(a, sizeof(T))) {
-                // fp32: the split-state form (two waves per SIMD); bf16 keeps the 4-wave form
+                // fp32: the split-state form (two waves per SIMD; config 2 132.5 vs 145.4 us).
+                // bf16 keeps the 4-wave form, which measured faster there (154.9 vs 162.1 us).
                 if constexpr (std::is_same<T, float>::value)
-                    if ((a.L + 48) * a.Dm * 4 < (1LL << 32)) return dispatch_ws<T, 3, true>(a);
+                    if (ws2_ok<T>(a)) return dispatch_ws<T, 3, true>(a);
                 return dispatch_ws<T, 2>(a);
             }
             return a.L * a.Dm < (1LL << 31) ? dispatch_wave<T, 2, 3>(a) : dispatch_wave<T, 2>(a);
@@ -1872,9 +1931,7 @@ int run_scan(const ScanArgs& a) {
             if (tile_ok && (a.L + 16) * a.Dm * (int64_t)sizeof(T) < (1LL << 32)) return dispatch_ws<T, 2>(a);
             break;
         case 46:
-            if constexpr (std::is_same<T, float>::value)
-                if (tile_ok && (a.L + 48) * a.Dm * (int64_t)sizeof(T) < (1LL << 32))
-                    return dispatch_ws<T, 3, true>(a);
+            if (tile_ok && ws2_ok<T>(a)) return dispatch_ws<T, 3, true>(a);
             break;
         default: break;
     }

@@ -365,8 +365,9 @@ int hx_eye_f32(int64_t n, float* y, void* stream);
  * needs), 8 = the fast kernel (8 waves split the states of 64 channels), 40 = the wave-complete
  * kernel (a wave owns 16 channels x 16 states; 64-bit row offsets), 42 = its leaner form with
  * per-wave staging, 44 = the warp-specialised kernel (3 state waves + 1 element wave per CU, 48
- * channels per block), 46 = its split-state form for fp32 storage (6 state waves holding half of
- * each channel's states + 2 element waves; the automatic choice for fp32 wherever 44 would be).
+ * channels per block), 46 = its split-state form (6 state waves holding half of each channel's
+ * states + 2 element waves; bf16 storage needs dim % 8 == 0; the automatic choice for fp32
+ * wherever 44 would be, while bf16 keeps 44).
  * A measurement knob with no reference counterpart; results agree within fp32 rounding for
  * every variant. */
 int hx_set_scan_variant(int variant);
