@@ -23,6 +23,13 @@ void clear_error();
 // device; hx_init calls it). *out (nullable) receives the address.
 int scan_scratch_setup(void** out);
 
+// Whether the current device grants kernel `fn` `dyn_bytes` of dynamic LDS next to `static_bytes`
+// of static LDS; the first query per (kernel, device, size) raises the kernel's dynamic-LDS limit
+// (hipFuncSetAttribute), later ones return the stored answer. Thread-safe.
+bool grant_dynamic_lds(const void* fn, size_t dyn_bytes, size_t static_bytes);
+// Compute units of the current device (stored per device; 256 if the query fails). Thread-safe.
+int device_cus();
+
 #define HX_HIP_CHECK(expr)                                                                   \
     do {                                                                                     \
         hipError_t hx_e_ = (expr);                                                           \

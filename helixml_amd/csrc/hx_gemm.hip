@@ -519,129 +519,13 @@ __device__ inline void tile_of(int nbx, int nb, int bid, int& tm, int& tn) {
     }
 }
 
-// ----------------------------------------------------------------------------- large tiles
-// Block tile 256 x 128 x 64, 4 waves in 2 x 2, each wave 128 x 64 = 4 x 2 tiles of
-// v_mfma_f32_32x32x16_bf16 (8 MFMAs per 6 LDS fragment reads, vs 4 per 4 in the 128 x 128 kernel).
-// Global -> registers -> LDS, double-buffered, rows padded by 16 bytes. The epilogue stages each
-// wave's 32 x 64 sub-tiles through LDS and writes rows as 16-byte vectors (8 bf16 or 4 fp32 per
-// lane), applying bias, SiLU and accumulate; a vector that would straddle a column split or the
-// N edge falls back to element stores.
+// ----------------------------------------------------------------------------- 256 x 128 tiles
 constexpr int LBM = 256, LBN = 128, LBK = 64;
-constexpr int LLDK = LBK + 8;  // padded row: 144 bytes
-
-template <bool VEC>
-__global__ __launch_bounds__(256) void gemm_bf16_nt_large_kernel(int64_t M, int64_t N, int64_t K,
-                                                                 const uint16_t* __restrict__ X,
-                                                                 int64_t ldx,
-                                                                 const uint16_t* __restrict__ W,
-                                                                 int64_t ldw,
-                                                                 const float* __restrict__ bias,
-                                                                 GemmOut o) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    uint16_t* sA = smem;                        // [2][LBM][LLDK]
-    uint16_t* sB = smem + 2 * LBM * LLDK;       // [2][LBN][LLDK]
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    // XCD-aware, L2-grouped tile order (tile_of)
-    const int nbx = gridDim.x, nby = gridDim.y;
-    const int nb = nbx * nby;
-    int tm, tn;
-    tile_of(nbx, nb, blockIdx.y * nbx + blockIdx.x, tm, tn);
-    const int64_t m0 = (int64_t)tm * LBM, n0 = (int64_t)tn * LBN;
-
-    // per K-step: A 256 x 64 (2048 16-byte pieces, 8 per thread), B 128 x 64 (1024, 4 per thread)
-    uint4 ra[8], rb[4];
-    auto gload = [&](int64_t k0) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int e = tid + j * 256;
-            const int row = e >> 3, kc = (e & 7) * 8;
-            ra[j] = load16_guard<VEC>(X, m0 + row, M, k0 + kc, K, ldx);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = tid + j * 256;
-            const int row = e >> 3, kc = (e & 7) * 8;
-            rb[j] = load16_guard<VEC>(W, n0 + row, N, k0 + kc, K, ldw);
-        }
-    };
-    auto sstore = [&](int buf) __attribute__((always_inline)) {
-        uint16_t* a = sA + buf * LBM * LLDK;
-        uint16_t* bb = sB + buf * LBN * LLDK;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int e = tid + j * 256;
-            *reinterpret_cast<uint4*>(a + (e >> 3) * LLDK + (e & 7) * 8) = ra[j];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = tid + j * 256;
-            *reinterpret_cast<uint4*>(bb + (e >> 3) * LLDK + (e & 7) * 8) = rb[j];
-        }
-    };
-
-    f32x16 acc[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    const int fr = lane & 31;
-    const int fk = (lane >> 5) * 8;
-    const int64_t nk = (K + LBK - 1) / LBK;
-    gload(0);
-    sstore(0);
-    if (nk > 1) gload(LBK);
-    __syncthreads();
-    for (int64_t kt = 0; kt < nk; ++kt) {
-        const int buf = (int)(kt & 1);
-        const uint16_t* a = sA + buf * LBM * LLDK + (wm * 128 + fr) * LLDK + fk;
-        const uint16_t* bb = sB + buf * LBN * LLDK + (wn * 64 + fr) * LLDK + fk;
-#pragma unroll
-        for (int kk = 0; kk < LBK; kk += 16) {
-            bf16x8 af[4], bf[2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(a + i * 32 * LLDK + kk);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(bb + j * 32 * LLDK + kk);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < nk) {
-            sstore(buf ^ 1);
-            if (kt + 2 < nk) gload((kt + 2) * LBK);
-        }
-        __syncthreads();
-    }
-
-    // epilogue: per wave, 4 row groups of 32 x 64 staged in a private 32 x 64 fp32 LDS tile
-    float* st = reinterpret_cast<float*>(smem) + wave * (32 * 68);  // row stride 68 floats
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                st[row * 68 + j * 32 + (lane & 31)] = acc[i][j][r];
-            }
-        __builtin_amdgcn_wave_barrier();
-        store_tile_rows(o, bias, st, M, N, m0 + wm * 128 + i * 32, n0 + wn * 64, lane);
-        __builtin_amdgcn_wave_barrier();
-    }
-}
 
 // ----------------------------------------------------------------------------- direct-to-LDS
-// Same 256 x 128 x 64 tiling and epilogue as gemm_bf16_nt_large_kernel, but tiles move from
-// global memory straight into LDS with gfx950's global_load_lds_dwordx4 (64 lanes x 16 bytes into
+// Block tile 256 x 128 x 64, 4 waves in 2 x 2, each wave 128 x 64 = 4 x 2 tiles of
+// v_mfma_f32_32x32x16_bf16. Tiles move from global memory straight into LDS with gfx950's
+// global_load_lds_dwordx4 (64 lanes x 16 bytes into
 // one contiguous KiB of LDS per instruction): no register staging, a 3-stage LDS ring, and the
 // loads of tile kt+2 issued while tile kt is multiplied. Each KiB holds 8 tile rows of 128 bytes;
 // within a row the 16-byte K-chunks are XOR-swizzled (chunk c of row r sits in slot c ^ (r & 7))
@@ -1023,42 +907,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(int64_t M, int64_t N
 }  // namespace hx
 
 namespace {
-// The 256 x 128 kernel needs 108 KB of LDS per block: use it only where the device grants that
-// (the MI355X's CUs have 160 KB); the result is cached per device.
-bool large_lds_ok(size_t bytes) {
-    static int cached[64] = {0};  // 0 unknown, 1 yes, 2 no
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    if (cached[dev] == 0) {
-        int v = 0;
-        const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
-                            hipSuccess &&
-                        (size_t)v >= bytes &&
-                        hipFuncSetAttribute((const void*)hx::gemm_bf16_nt_large_kernel<true>,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            (int)bytes) == hipSuccess;
-        cached[dev] = ok ? 1 : 2;
-    }
-    return cached[dev] == 1;
-}
-
 template <int KB, int NST>
 bool d256_ok() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    if (cached[dev] == 0) {
-        const size_t bytes = (size_t)NST * (hx::XBM + hx::XBN) * KB * 2;
-        int v = 0;
-        const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
-                            hipSuccess &&
-                        (size_t)v >= bytes &&
-                        hipFuncSetAttribute((const void*)hx::gemm_bf16_nt_d256_kernel<KB, NST>,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            (int)bytes) == hipSuccess;
-        cached[dev] = ok ? 1 : 2;
-    }
-    return cached[dev] == 1;
+    const size_t bytes = (size_t)NST * (hx::XBM + hx::XBN) * KB * 2;
+    return hx::grant_dynamic_lds((const void*)hx::gemm_bf16_nt_d256_kernel<KB, NST>, bytes, 0);
 }
 
 template <int KB, int NST>
@@ -1073,22 +925,7 @@ int launch_d256(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, con
     return HX_OK;
 }
 
-bool dlds_ok(size_t bytes) {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    if (cached[dev] == 0) {
-        int v = 0;
-        const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
-                            hipSuccess &&
-                        (size_t)v >= bytes &&
-                        hipFuncSetAttribute((const void*)hx::gemm_bf16_nt_dlds_kernel,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            (int)bytes) == hipSuccess;
-        cached[dev] = ok ? 1 : 2;
-    }
-    return cached[dev] == 1;
-}
+bool dlds_ok(size_t bytes) { return hx::grant_dynamic_lds((const void*)hx::gemm_bf16_nt_dlds_kernel, bytes, 0); }
 }  // namespace
 
 extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
@@ -1140,17 +977,8 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
         HX_LAUNCH_CHECK();
         return HX_OK;
     }
-    const size_t lds = (size_t)2 * (LBM + LBN) * LLDK * sizeof(uint16_t);
-    if (vec && g_gemm_kernel != 1 && g_gemm_kernel != 3 &&
-        g_gemm_kernel == 2 && large_lds_ok(lds)) {
-        dim3 lg((unsigned)((N + LBN - 1) / LBN), (unsigned)((M + LBM - 1) / LBM));
-        hipLaunchKernelGGL(gemm_bf16_nt_large_kernel<true>, lg, dim3(256), lds, as_stream(stream),
-                           M, N, K, (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
-        HX_LAUNCH_CHECK();
-        return HX_OK;
-    }
     const int64_t tiles128 = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    if (vec && K % 8 == 0 && K >= 8 && g_gemm_kernel != 1 && g_gemm_kernel != 2 && g_gemm_kernel != 4 &&
+    if (vec && K % 8 == 0 && K >= 8 && g_gemm_kernel != 1 && g_gemm_kernel != 4 &&
         (g_gemm_kernel == 3 || tiles128 < 128) && (M + 31) / 32 <= 65535) {
         // 64-wide tiles where they still give the GPU 256 blocks (decode in_proj), else 32-wide;
         // SP covers a wave's whole share of K where it can (one round of loads)
@@ -1242,7 +1070,8 @@ extern "C" int hx_gemm_bf16_splitk(int64_t M, int64_t N, int64_t K, const void* 
 
 extern "C" int hx_set_gemm_kernel(int k) {
     using namespace hx;
-    HX_REQUIRE(k >= 0 && k <= 6, HX_ERR_INVALID_INPUT, "hx_set_gemm_kernel: %d (0 auto, 1..6)", k);
+    HX_REQUIRE(k >= 0 && k <= 6 && k != 2, HX_ERR_INVALID_INPUT,
+               "hx_set_gemm_kernel: %d (0 auto, 1, 3, 4, 5, 6)", k);
     g_gemm_kernel = k;
     return HX_OK;
 }

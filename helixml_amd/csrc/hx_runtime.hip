@@ -5,6 +5,8 @@
 #include <cstring>
 
 #include "hx_common.h"
+#include "hx_once.h"
+#include <tuple>
 
 namespace hx {
 
@@ -21,6 +23,32 @@ int set_error(int code, const char* fmt, ...) {
 }
 
 void clear_error() { g_last_error[0] = 0; }
+
+bool grant_dynamic_lds(const void* fn, size_t dyn_bytes, size_t static_bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    static OnceMap<std::tuple<const void*, int, size_t>, bool> memo;
+    return memo.get(std::make_tuple(fn, dev, dyn_bytes), [&] {
+        int v = 0;
+        const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+                        (size_t)v >= dyn_bytes + static_bytes &&
+                        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn_bytes) ==
+                            hipSuccess;
+        (void)hipGetLastError();  // a refusal is an answer, not a pending error
+        return ok;
+    });
+}
+
+int device_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    static OnceMap<int, int> memo;
+    return memo.get(dev, [&] {
+        int v = 0;
+        return (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v
+                                                                                                              : 256;
+    });
+}
 
 }  // namespace hx
 

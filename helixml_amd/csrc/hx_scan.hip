@@ -1217,10 +1217,11 @@ __global__ __launch_bounds__(256) void scan_ws_kernel(
 //   * waves 0..2 and 4..6 are state waves: wave w < 3 holds states 0..7 of channel group w,
 //     wave w > 3 states 8..15 of group w - 4 (lane (r, c): channel c, states 8h + 2r, 8h + 2r + 1;
 //     B/C of step t0 + j in lane j of row r). Each reduce-scatters its 8 states' readouts
-//     across rows; the lower half hands its partials to the upper half through LDS, which adds
-//     them in the next phase (after the chunk barrier), then D*u, the gate and the stores;
-//   * waves 3 and 7 are element waves, each preparing half of every chunk's steps for all 48
-//     channels (softplus(delta + bias), dt*u, u, SiLU(z)).
+//     across rows and publishes the per-step partial sums of its half in LDS (s_y);
+//   * waves 3 and 7 are element waves, each owning half of every chunk's steps for all 48
+//     channels: they prepare softplus(delta + bias), dt*u, u and SiLU(z) two chunks ahead of the
+//     scan, and one phase after a chunk is scanned (after the chunk barrier) they finish it: the
+//     two halves' partial sums, D*u, the gate and the stores.
 // Waves of a block are placed on SIMDs round-robin, so waves w and w + 4 share a SIMD: SIMDs
 // 0..2 each run a lower and an upper state wave, SIMD 3 the two element waves. The hand-over
 // buffers hold each channel's 16 steps in the order 4 (s % 4) + s / 4 for all four operands.
@@ -1784,22 +1785,7 @@ size_t ws_dyn_lds(int NR, bool has_z, size_t es, size_t stat) {
     const size_t need = 84 * 1024 - stat;
     return ring > need ? ring : need;
 }
-bool ws_lds_ok(const void* fn, size_t bytes, size_t stat) {
-    struct Entry { const void* fn; int dev; int ok; };
-    static Entry cache[64];
-    static int n = 0;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    for (int i = 0; i < n; ++i)
-        if (cache[i].fn == fn && cache[i].dev == dev) return cache[i].ok != 0;
-    int v = 0;
-    const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
-                    (size_t)v >= bytes + stat &&
-                    hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
-    (void)hipGetLastError();
-    if (n < 64) cache[n++] = Entry{fn, dev, ok ? 1 : 0};
-    return ok;
-}
+bool ws_lds_ok(const void* fn, size_t bytes, size_t stat) { return grant_dynamic_lds(fn, bytes, stat); }
 
 template <typename T, int NR, bool HAS_Z, bool SP, bool SPLIT>
 int launch_ws(const ScanArgs& a) {
@@ -1857,18 +1843,6 @@ int dispatch_generic(const ScanArgs& a) {
     return launch_generic<T, 64>(a);
 }
 
-// Compute units of the current device (cached per device; 256 on an MI355X).
-int device_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int v = 0;
-        cached[dev] = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-                          ? v : 256;
-    }
-    return cached[dev];
-}
 
 // Whether the automatic choice takes the warp-specialised kernel over scan_wave3_kernel. Both
 // are bound by the state waves' issue rate. wave3 runs one wave per SIMD per 16 channels; the

@@ -2,6 +2,8 @@
 // (crates/hal/src/operations.rs:88-231) for one ROCm device over the C ABI. Host code only.
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
+#include <initializer_list>
 #include <functional>
 
 #include "helix/helix.hpp"
@@ -107,6 +109,7 @@ RocmBackend::RocmBackend(int device) : device_(device) {
 RocmBackend::~RocmBackend() {
     (void)hx_sync();
     for (auto& kv : live_) (void)hx_free(kv.second);
+    if (scan_ws_) (void)hx_free(scan_ws_);
 }
 
 std::string RocmBackend::device_id() const { return "rocm:" + std::to_string(device_); }
@@ -184,26 +187,191 @@ size_t elem_bytes(DataType t) {
 size_t elements(const MemoryHandle& h) {
     if (!h.shape.empty()) {
         size_t n = 1;
-        for (size_t d : h.shape) n *= d;
+        for (size_t d : h.shape) {
+            if (d != 0 && n > SIZE_MAX / d) invalid_input("handle shape overflows size_t");
+            n *= d;
+        }
         return n;
     }
     return h.size / elem_bytes(h.dtype);
+}
+size_t mul_checked(std::initializer_list<size_t> f) {
+    size_t n = 1;
+    for (size_t v : f) {
+        if (v != 0 && n > SIZE_MAX / v) invalid_input("operation sizes overflow size_t");
+        n *= v;
+    }
+    return n;
 }
 void need_f32(const MemoryHandle& h, const char* op) {
     if (h.dtype != DataType::F32)
         throw TensorError(ErrorKind::DTypeMismatch,
                           std::string("DType mismatch: expected \"F32\", got another type for ") + op);
 }
+void need_dtype(const MemoryHandle& h, DataType want, const char* op, const char* what) {
+    if (h.dtype != want)
+        throw TensorError(ErrorKind::DTypeMismatch, std::string("DType mismatch: expected \"") +
+                                                        (want == DataType::BF16 ? "BF16" : "F32") +
+                                                        "\", got another type for " + op + " " + what);
+}
+// A handle the operation reads or writes `bytes` of: it must have a device address and hold them.
+void need_bytes(const MemoryHandle& h, size_t bytes, const char* op, const char* what) {
+    if (h.address == 0) invalid_input(std::string(op) + ": " + what + " has no device address");
+    if (h.size < bytes)
+        invalid_input(std::string(op) + ": " + what + " holds " + std::to_string(h.size) +
+                      " bytes, the operation touches " + std::to_string(bytes));
+}
+// Whether optional input i is given (present with a device address).
+bool given(const Operation& op, size_t i) { return i < op.inputs.size() && op.inputs[i].address != 0; }
+int64_t size_param(const Operation& op, const char* k, double dflt, bool required) {
+    auto it = op.params.find(k);
+    double v = dflt;
+    if (it == op.params.end()) {
+        if (required) invalid_input(std::string("missing parameter ") + k);
+    } else {
+        v = it->second;
+    }
+    if (!(v >= 0.0) || v != std::floor(v) || v > 9.0e15)
+        invalid_input(std::string("parameter ") + k + " must be a non-negative integer");
+    return (int64_t)v;
+}
+void need_inputs(const Operation& op, size_t n) {
+    if (op.inputs.size() < n)
+        invalid_input(std::string(operation_name(op.op_type)) + " requires " + std::to_string(n) +
+                      " input" + (n > 1 ? "s" : ""));
+}
 }  // namespace
 
-MemoryHandle RocmBackend::execute_op(const Operation& op) {
-    auto param = [&](const char* k, double dflt, bool required) {
-        auto it = op.params.find(k);
-        if (it == op.params.end()) {
-            if (required) invalid_input(std::string("missing parameter ") + k);
-            return dflt;
+void validate_operation(const Operation& op) {
+    const OperationType t = op.op_type;
+    const char* name = operation_name(t);
+    switch (t) {
+        case OperationType::Add: case OperationType::Sub: case OperationType::Mul:
+        case OperationType::Div: {
+            need_inputs(op, 2);
+            need_f32(op.inputs[0], "binary op");
+            need_f32(op.inputs[1], "binary op");
+            const size_t n = elements(op.inputs[0]);
+            if (elements(op.inputs[1]) != n) shape_mismatch({n}, {elements(op.inputs[1])});
+            need_bytes(op.inputs[0], n * 4, name, "input 0");
+            need_bytes(op.inputs[1], n * 4, name, "input 1");
+            return;
         }
-        return it->second;
+        case OperationType::Sqrt: case OperationType::Abs: case OperationType::Sin:
+        case OperationType::Cos: case OperationType::Exp: case OperationType::Log:
+        case OperationType::Sigmoid: case OperationType::SiLU:
+            need_inputs(op, 1);
+            need_f32(op.inputs[0], "unary op");
+            need_bytes(op.inputs[0], elements(op.inputs[0]) * 4, name, "input 0");
+            return;
+        case OperationType::Mean: {
+            need_inputs(op, 1);
+            need_f32(op.inputs[0], "Mean");
+            const size_t n = elements(op.inputs[0]);
+            if (n == 0) invalid_input("Mean of an empty buffer");
+            need_bytes(op.inputs[0], n * 4, name, "input 0");
+            return;
+        }
+        case OperationType::Transpose: {
+            need_inputs(op, 1);
+            need_f32(op.inputs[0], "Transpose");
+            const auto& sh = op.inputs[0].shape;
+            if (sh.size() != 2) unsupported("Transpose needs a 2-D input shape");
+            need_bytes(op.inputs[0], mul_checked({sh[0], sh[1], 4}), name, "input 0");
+            return;
+        }
+        case OperationType::MatMul: {
+            need_inputs(op, 2);
+            need_f32(op.inputs[0], "MatMul");
+            need_f32(op.inputs[1], "MatMul");
+            const auto& a = op.inputs[0].shape;
+            const auto& b = op.inputs[1].shape;
+            if (a.size() != 2 || b.size() != 2) unsupported("MatMul needs 2-D input shapes");
+            if (a[1] != b[0]) shape_mismatch({a[1]}, {b[0]});
+            need_bytes(op.inputs[0], mul_checked({a[0], a[1], 4}), name, "input 0");
+            need_bytes(op.inputs[1], mul_checked({b[0], b[1], 4}), name, "input 1");
+            return;
+        }
+        case OperationType::SSMForward: {
+            // inputs u, delta, A, B, C[, D, z, dt_bias]; u, delta, B, C, z in u's storage type
+            if (op.inputs.size() < 5) invalid_input("SSMForward takes u, delta, A, B, C[, D, z, dt_bias]");
+            const size_t bt = (size_t)size_param(op, "batch", 0, true), L = (size_t)size_param(op, "seqlen", 0, true);
+            const size_t dim = (size_t)size_param(op, "dim", 0, true), N = (size_t)size_param(op, "dstate", 16, false);
+            (void)size_param(op, "softplus", 1, false);
+            const DataType st = op.inputs[0].dtype;
+            if (st != DataType::F32 && st != DataType::BF16)
+                throw TensorError(ErrorKind::DTypeMismatch,
+                                  "DType mismatch: expected \"F32\" or \"BF16\", got another type for SSMForward u");
+            const size_t es = st == DataType::BF16 ? 2 : 4;
+            const size_t seq = mul_checked({bt, L, dim, es}), bc = mul_checked({bt, L, N, es});
+            need_bytes(op.inputs[0], seq, name, "u");
+            need_dtype(op.inputs[1], st, name, "delta");
+            need_bytes(op.inputs[1], seq, name, "delta");
+            need_dtype(op.inputs[2], DataType::F32, name, "A");
+            need_bytes(op.inputs[2], mul_checked({dim, N, 4}), name, "A");
+            need_dtype(op.inputs[3], st, name, "B");
+            need_bytes(op.inputs[3], bc, name, "B");
+            need_dtype(op.inputs[4], st, name, "C");
+            need_bytes(op.inputs[4], bc, name, "C");
+            if (given(op, 5)) { need_dtype(op.inputs[5], DataType::F32, name, "D"); need_bytes(op.inputs[5], dim * 4, name, "D"); }
+            if (given(op, 6)) { need_dtype(op.inputs[6], st, name, "z"); need_bytes(op.inputs[6], seq, name, "z"); }
+            if (given(op, 7)) { need_dtype(op.inputs[7], DataType::F32, name, "dt_bias"); need_bytes(op.inputs[7], dim * 4, name, "dt_bias"); }
+            return;
+        }
+        case OperationType::StateUpdate: {
+            // inputs state, u, delta, A, B, C[, D, z, dt_bias]; u, delta, B, C, z in u's storage type
+            if (op.inputs.size() < 6) invalid_input("StateUpdate takes state, u, delta, A, B, C[, D, z, dt_bias]");
+            const size_t bt = (size_t)size_param(op, "batch", 0, true), dim = (size_t)size_param(op, "dim", 0, true);
+            const size_t N = (size_t)size_param(op, "dstate", 16, false);
+            (void)size_param(op, "softplus", 1, false);
+            const DataType st = op.inputs[1].dtype;
+            if (st != DataType::F32 && st != DataType::BF16)
+                throw TensorError(ErrorKind::DTypeMismatch,
+                                  "DType mismatch: expected \"F32\" or \"BF16\", got another type for StateUpdate u");
+            const size_t es = st == DataType::BF16 ? 2 : 4;
+            const size_t row = mul_checked({bt, dim, es}), bc = mul_checked({bt, N, es});
+            need_dtype(op.inputs[0], DataType::F32, name, "state");
+            need_bytes(op.inputs[0], mul_checked({bt, dim, N, 4}), name, "state");
+            need_bytes(op.inputs[1], row, name, "u");
+            need_dtype(op.inputs[2], st, name, "delta");
+            need_bytes(op.inputs[2], row, name, "delta");
+            need_dtype(op.inputs[3], DataType::F32, name, "A");
+            need_bytes(op.inputs[3], mul_checked({dim, N, 4}), name, "A");
+            need_dtype(op.inputs[4], st, name, "B");
+            need_bytes(op.inputs[4], bc, name, "B");
+            need_dtype(op.inputs[5], st, name, "C");
+            need_bytes(op.inputs[5], bc, name, "C");
+            if (given(op, 6)) { need_dtype(op.inputs[6], DataType::F32, name, "D"); need_bytes(op.inputs[6], dim * 4, name, "D"); }
+            if (given(op, 7)) { need_dtype(op.inputs[7], st, name, "z"); need_bytes(op.inputs[7], row, name, "z"); }
+            if (given(op, 8)) { need_dtype(op.inputs[8], DataType::F32, name, "dt_bias"); need_bytes(op.inputs[8], dim * 4, name, "dt_bias"); }
+            return;
+        }
+        default:
+            return;  // execute_op reports the operation as unsupported
+    }
+}
+
+void* RocmBackend::scan_workspace(size_t bytes) {
+    if (bytes == 0) return nullptr;
+    if (bytes > scan_ws_bytes_) {
+        if (scan_ws_) {
+            check(hx_sync(), "hx_sync");  // work queued on the old buffer finishes first
+            check(hx_free(scan_ws_), "hx_free");
+            scan_ws_ = nullptr;
+            scan_ws_bytes_ = 0;
+        }
+        check(hx_malloc(&scan_ws_, bytes), "hx_malloc");
+        scan_ws_bytes_ = bytes;
+    }
+    return scan_ws_;
+}
+
+MemoryHandle RocmBackend::execute_op(const Operation& op) {
+    // every input is checked against what the launch will touch before anything is launched
+    validate_operation(op);
+    auto param = [&](const char* k, double dflt) {
+        auto it = op.params.find(k);
+        return it == op.params.end() ? dflt : it->second;
     };
     auto ptr = [&](size_t i) -> void* {
         return i < op.inputs.size() && op.inputs[i].address ? (void*)op.inputs[i].address : nullptr;
@@ -215,20 +383,11 @@ MemoryHandle RocmBackend::execute_op(const Operation& op) {
         }
         return allocate(bytes, dt);
     };
-    auto need_inputs = [&](size_t n) {
-        if (op.inputs.size() < n)
-            invalid_input(std::string(operation_name(op.op_type)) + " requires " + std::to_string(n) +
-                          " input" + (n > 1 ? "s" : ""));
-    };
     const OperationType t = op.op_type;
     switch (t) {
         case OperationType::Add: case OperationType::Sub: case OperationType::Mul:
         case OperationType::Div: {
-            need_inputs(2);
-            need_f32(op.inputs[0], "binary op");
-            need_f32(op.inputs[1], "binary op");
             const size_t n = elements(op.inputs[0]);
-            if (elements(op.inputs[1]) != n) shape_mismatch({n}, {elements(op.inputs[1])});
             MemoryHandle o = out_for(n * 4, DataType::F32);
             o.shape = op.inputs[0].shape;
             const int code = t == OperationType::Add ? HX_ADD : t == OperationType::Sub ? HX_SUB
@@ -241,8 +400,6 @@ MemoryHandle RocmBackend::execute_op(const Operation& op) {
         case OperationType::Sqrt: case OperationType::Abs: case OperationType::Sin:
         case OperationType::Cos: case OperationType::Exp: case OperationType::Log:
         case OperationType::Sigmoid: case OperationType::SiLU: {
-            need_inputs(1);
-            need_f32(op.inputs[0], "unary op");
             const size_t n = elements(op.inputs[0]);
             MemoryHandle o = out_for(n * 4, DataType::F32);
             o.shape = op.inputs[0].shape;
@@ -257,10 +414,7 @@ MemoryHandle RocmBackend::execute_op(const Operation& op) {
         case OperationType::Mean: {
             // all elements -> one value (the reference backends' Mean, e.g.
             // backend-cpu/src/cpu_backend.rs:703-734)
-            need_inputs(1);
-            need_f32(op.inputs[0], "Mean");
             const size_t n = elements(op.inputs[0]);
-            if (n == 0) invalid_input("Mean of an empty buffer");
             MemoryHandle o = out_for(4, DataType::F32);
             o.shape = {1};
             check(hx_mean_axis_f32(1, (int64_t)n, 1, 1, (const float*)ptr(0), (float*)o.address, nullptr),
@@ -268,10 +422,7 @@ MemoryHandle RocmBackend::execute_op(const Operation& op) {
             return o;
         }
         case OperationType::Transpose: {
-            need_inputs(1);
-            need_f32(op.inputs[0], "Transpose");
             const auto& s = op.inputs[0].shape;
-            if (s.size() != 2) unsupported("Transpose needs a 2-D input shape");
             MemoryHandle o = out_for(s[0] * s[1] * 4, DataType::F32);
             o.shape = {s[1], s[0]};
             const int64_t shp[2] = {(int64_t)s[1], (int64_t)s[0]};
@@ -281,11 +432,8 @@ MemoryHandle RocmBackend::execute_op(const Operation& op) {
             return o;
         }
         case OperationType::MatMul: {
-            need_inputs(2);
             const auto& a = op.inputs[0].shape;
             const auto& b = op.inputs[1].shape;
-            if (a.size() != 2 || b.size() != 2) unsupported("MatMul needs 2-D input shapes");
-            if (a[1] != b[0]) shape_mismatch({a[1]}, {b[0]});
             MemoryHandle o = out_for(a[0] * b[1] * 4, DataType::F32);
             o.shape = {a[0], b[1]};
             check(hx_matmul_f32((int64_t)a[0], (int64_t)a[1], (int64_t)b[1], (const float*)ptr(0),
@@ -294,25 +442,27 @@ MemoryHandle RocmBackend::execute_op(const Operation& op) {
             return o;
         }
         case OperationType::SSMForward: {
-            if (op.inputs.size() < 5) invalid_input("SSMForward takes u, delta, A, B, C[, D, z, dt_bias]");
-            const int64_t bt = (int64_t)param("batch", 0, true), L = (int64_t)param("seqlen", 0, true);
-            const int64_t dim = (int64_t)param("dim", 0, true), N = (int64_t)param("dstate", 16, false);
-            const int sp = (int)param("softplus", 1, false);
+            // the library's long-sequence path (time segments with a carry) through a workspace
+            // this backend keeps, as the fused scan of hal/src/device.rs:191 would run
+            const int64_t bt = (int64_t)param("batch", 0), L = (int64_t)param("seqlen", 0);
+            const int64_t dim = (int64_t)param("dim", 0), N = (int64_t)param("dstate", 16);
+            const int sp = (int)param("softplus", 1);
             const bool bf = op.inputs[0].dtype == DataType::BF16;
+            const int dt = bf ? HX_BF16 : HX_F32;
             MemoryHandle o = out_for((size_t)(bt * L * dim) * (bf ? 2 : 4), op.inputs[0].dtype);
             o.shape = {(size_t)bt, (size_t)L, (size_t)dim};
-            check(hx_selective_scan_fwd(bt, L, dim, N, bf ? HX_BF16 : HX_F32, sp, ptr(0), ptr(1),
-                                        (const float*)ptr(2), ptr(3), ptr(4), (const float*)ptr(5), ptr(6),
-                                        (const float*)ptr(7), (void*)o.address, nullptr, nullptr, nullptr),
-                  "hx_selective_scan_fwd");
+            const size_t need = hx_selective_scan_workspace_size(bt, L, dim, N, dt);
+            void* ws = scan_workspace(need);
+            check(hx_selective_scan_fwd_ws(bt, L, dim, N, dt, sp, ptr(0), ptr(1), (const float*)ptr(2), ptr(3),
+                                           ptr(4), (const float*)ptr(5), ptr(6), (const float*)ptr(7),
+                                           (void*)o.address, nullptr, nullptr, ws, need, nullptr),
+                  "hx_selective_scan_fwd_ws");
             return o;
         }
         case OperationType::StateUpdate: {
-            if (op.inputs.size() < 6)
-                invalid_input("StateUpdate takes state, u, delta, A, B, C[, D, z, dt_bias]");
-            const int64_t bt = (int64_t)param("batch", 0, true), dim = (int64_t)param("dim", 0, true);
-            const int64_t N = (int64_t)param("dstate", 16, false);
-            const int sp = (int)param("softplus", 1, false);
+            const int64_t bt = (int64_t)param("batch", 0), dim = (int64_t)param("dim", 0);
+            const int64_t N = (int64_t)param("dstate", 16);
+            const int sp = (int)param("softplus", 1);
             const bool bf = op.inputs[1].dtype == DataType::BF16;
             MemoryHandle o = out_for((size_t)(bt * dim) * (bf ? 2 : 4), op.inputs[1].dtype);
             o.shape = {(size_t)bt, (size_t)dim};

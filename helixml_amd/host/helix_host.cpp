@@ -277,6 +277,7 @@ void S4Block::restore(const std::vector<HipTensor>& ck) {
                                                             std::to_string(ck.size()));
     A_real = ck[0].clone();
     A_imag = ck[1].clone();
+    parameters_changed();  // a new buffer may reuse a freed one's address
     B = ck[2].clone();
     C = ck[3].clone();
     D = ck[4].clone();
@@ -356,13 +357,19 @@ HipTensor selective_scan(const HipTensor& u, const HipTensor& delta, const HipTe
     if (C.shape() != Shape({bt, L, N})) shape_mismatch({bt, L, N}, C.shape().as_slice());
     HipTensor out(u.shape(), u.storage(), 0);
     if (last_state) *last_state = HipTensor(Shape({bt, dim, N}), Storage::F32, 0);
-    check(hx_selective_scan_fwd((int64_t)bt, (int64_t)L, (int64_t)dim, (int64_t)N,
-                                u.storage() == Storage::BF16 ? HX_BF16 : HX_F32, softplus ? 1 : 0,
-                                u.data(), delta.data(), (const float*)A.data(), B.data(), C.data(),
-                                D ? (const float*)D->data() : nullptr, z ? z->data() : nullptr,
-                                dt_bias ? (const float*)dt_bias->data() : nullptr, out.data(), nullptr,
-                                last_state ? (float*)last_state->data() : nullptr, nullptr),
-          "hx_selective_scan_fwd");
+    const int dt = u.storage() == Storage::BF16 ? HX_BF16 : HX_F32;
+    // the long-sequence path (time segments with a carry) needs scratch: kept per thread and
+    // grown on demand (this thread's calls are ordered on the default stream, so they share it)
+    thread_local HipTensor ws;
+    const size_t need = hx_selective_scan_workspace_size((int64_t)bt, (int64_t)L, (int64_t)dim, (int64_t)N, dt);
+    if (need && (!ws.defined() || ws.nbytes() < need)) ws = HipTensor(Shape({(need + 3) / 4}), Storage::F32, 0);
+    check(hx_selective_scan_fwd_ws((int64_t)bt, (int64_t)L, (int64_t)dim, (int64_t)N, dt, softplus ? 1 : 0,
+                                   u.data(), delta.data(), (const float*)A.data(), B.data(), C.data(),
+                                   D ? (const float*)D->data() : nullptr, z ? z->data() : nullptr,
+                                   dt_bias ? (const float*)dt_bias->data() : nullptr, out.data(), nullptr,
+                                   last_state ? (float*)last_state->data() : nullptr,
+                                   need ? ws.data() : nullptr, need ? ws.nbytes() : 0, nullptr),
+          "hx_selective_scan_fwd_ws");
     return out;
 }
 

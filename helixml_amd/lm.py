@@ -21,11 +21,12 @@ from typing import Dict, List, Optional
 import torch
 
 from . import _ffi
-from .ssm import _ptr, _stream
+from .ssm import _ptr, _stream, keep_for_stream, on_launch_stream
 
 _F32, _BF16 = _ffi.HX_F32, _ffi.HX_BF16
 
 
+@on_launch_stream
 def embedding(tokens, table, out=None, stream=None):
     """out[t] = table[tokens[t]] (hx_embedding_fwd); tokens int32 of any shape (made contiguous)."""
     if tokens.dtype != torch.int32:
@@ -39,6 +40,7 @@ def embedding(tokens, table, out=None, stream=None):
     return out
 
 
+@on_launch_stream
 def rmsnorm(x, weight, eps=1e-5, out_dtype=torch.float32, out=None, stream=None):
     """nn::RMSNorm::forward (crates/nn/src/lib.rs:258-285) over the last dim (hx_rmsnorm_fwd)."""
     dim = x.shape[-1]
@@ -51,6 +53,7 @@ def rmsnorm(x, weight, eps=1e-5, out_dtype=torch.float32, out=None, stream=None)
     return out
 
 
+@on_launch_stream
 def conv1d_step(x, weight, bias, state, out=None, stream=None):
     """One recurrent step of the causal conv (hx_conv1d_step); x [batch, dim] (rows may be
     strided), state [batch, width-1, dim] fp32 advanced in place."""
@@ -131,12 +134,14 @@ class ByteLM:
         return logits
 
     # ------------------------------------------------------------------ forward
+    @on_launch_stream
     def prefill(self, tokens, state=None, stream=None):
         """tokens int32 [batch, seqlen] -> (logits fp32 [batch, seqlen, vocab], decode state).
         ``state`` (from new_state) receives each layer's final scan state and conv window."""
         bt, L = tokens.shape
         x = embedding(tokens, self.embed, stream=stream)
         ws = self._workspace(bt, L)
+        keep_for_stream(ws, stream)
         if state is None:
             state = self.new_state(bt)
         s = _stream(stream)
@@ -147,6 +152,7 @@ class ByteLM:
                       ws.numel(), s)
         return self._head(x, stream), state
 
+    @on_launch_stream
     def decode_step(self, tokens, state, stream=None, workspace=None):
         """tokens int32 [batch] -> logits fp32 [batch, vocab]; advances ``state`` in place.
         ``workspace`` (uint8 device tensor of at least hx_mamba_layer_workspace_size(batch, 1,
@@ -154,6 +160,8 @@ class ByteLM:
         bt = tokens.shape[0]
         x = embedding(tokens, self.embed, stream=stream)
         ws = self._workspace(bt, 1) if workspace is None else workspace
+        if workspace is None:
+            keep_for_stream(ws, stream)
         s = _stream(stream)
         for p, (ssm_st, conv_st) in zip(self.layers, state):
             _ffi.call("hx_mamba_layer_decode", bt, self.d_model, self.d_inner, self.d_state,

@@ -11,6 +11,7 @@ CpuTensor validates before computing (backend-cpu/src/lib.rs:570-576, 648-656).
 """
 from __future__ import annotations
 
+import functools
 from typing import Optional
 
 import numpy as np
@@ -33,6 +34,36 @@ def _stream(stream) -> int:
     return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
 
 
+def _torch_stream(stream):
+    """The torch stream a launch goes to: the current stream for None, a torch stream as given,
+    anything else (a raw hipStream_t handle) wrapped as an external stream."""
+    if stream is None:
+        return torch.cuda.current_stream()
+    if isinstance(stream, torch.cuda.Stream):
+        return stream
+    return torch.cuda.ExternalStream(int(getattr(stream, "cuda_stream", stream)))
+
+
+def on_launch_stream(fn):
+    """Runs a wrapper with its launch stream current, so every temporary it allocates (outputs,
+    workspaces) belongs to the stream its kernels run on: torch's caching allocator then cannot
+    hand that memory to another allocation while those kernels may still use it."""
+    @functools.wraps(fn)
+    def run(*args, stream=None, **kwargs):
+        ts = _torch_stream(stream)
+        with torch.cuda.stream(ts):
+            return fn(*args, stream=ts, **kwargs)
+    run.on_launch_stream = True
+    return run
+
+
+def keep_for_stream(t: Optional[torch.Tensor], stream) -> None:
+    """Marks a persistent buffer (a workspace kept between calls) as used on ``stream``, so that
+    replacing it later cannot recycle its memory while work queued there still reads it."""
+    if t is not None and not torch.cuda.is_current_stream_capturing():
+        t.record_stream(stream)
+
+
 def _need(t: Optional[torch.Tensor], name: str, shape, dtype) -> None:
     if t is None:
         return
@@ -51,6 +82,7 @@ def selective_scan_workspace_size(batch, seqlen, dim, dstate, dtype=torch.float3
     return int(_ffi.lib().hx_selective_scan_workspace_size(batch, seqlen, dim, dstate, _STORAGE[dtype]))
 
 
+@on_launch_stream
 def selective_scan_fwd(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_softplus=True,
                        init_state=None, return_last_state=False, out=None, workspace=None,
                        stream=None):
@@ -91,6 +123,7 @@ def selective_scan_fwd(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_so
     return (out, last) if return_last_state else out
 
 
+@on_launch_stream
 def selective_state_update(state, u, delta, A, B, C, D=None, z=None, dt_bias=None,
                            delta_softplus=True, out=None, stream=None):
     """One decode step (hx_selective_state_update); updates ``state`` [batch, dim, dstate] in place.
@@ -129,6 +162,7 @@ def s4_discretize(a_real, a_imag, dt=0.1, device=None):
     return torch.from_numpy(a).to(device if device is not None else a_real.device)
 
 
+@on_launch_stream
 def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, parallel=False, a=None,
                workspace=None, stream=None):
     """Reference-mode S4Block::forward_ssm (crates/nn/src/ssm.rs:138-186) on x [d_model, L];
@@ -160,6 +194,7 @@ def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, parallel=False, a=
     return y
 
 
+@on_launch_stream
 def s4d_complex_fwd(x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D=None, stream=None):
     """S4D diagonal complex recurrence (hx_s4d_complex_fwd); x, y: [batch, L, dim]."""
     bt, L, dim = x.shape
@@ -180,6 +215,7 @@ def s4d_complex_fwd(x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D=None, stream=No
     return y
 
 
+@on_launch_stream
 def linear(X, W, bias=None, act=0, stream=None):
     """nn::Linear::forward (crates/nn/src/lib.rs:120-134); W is [out, in]."""
     R, IN = X.shape
@@ -197,6 +233,7 @@ def linear(X, W, bias=None, act=0, stream=None):
     return Y
 
 
+@on_launch_stream
 def matmul(A, B, stream=None):
     """CpuTensor::matmul 2-D x 2-D (crates/backend-cpu/src/lib.rs:644-678)."""
     M, K = A.shape
@@ -211,6 +248,7 @@ def matmul(A, B, stream=None):
     return Y
 
 
+@on_launch_stream
 def gemm_bf16(X, W, bias=None, act=0, out_dtype=torch.bfloat16, splits=None, stream=None,
               k_splits=None):
     """Matrix-core GEMM Y = X . W^T (+ bias)(, SiLU) (hx_gemm_bf16). X [M, K], W [N, K] bf16
@@ -264,6 +302,7 @@ def set_s4d_segments(n: int) -> None:
     _ffi.call("hx_set_s4d_segments", int(n))
 
 
+@on_launch_stream
 def conv1d_silu(x, weight, bias=None, out=None, stream=None):
     """Causal depthwise conv1d + bias + SiLU (hx_conv1d_silu). x [batch, L, dim] (rows may be
     strided, e.g. the x half of in_proj's output), weight [dim, width] fp32, bias [dim] fp32."""
@@ -286,6 +325,7 @@ def mamba_block_workspace_size(batch, seqlen, d_inner, dt_rank, dstate) -> int:
     return int(_ffi.lib().hx_mamba_block_workspace_size(batch, seqlen, d_inner, dt_rank, dstate))
 
 
+@on_launch_stream
 def mamba_block_fwd(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, workspace=None,
                     out=None, stream=None):
     """Full Mamba block forward (hx_mamba_block_fwd), bf16 storage. x [batch, L, d_model];
@@ -359,11 +399,15 @@ class MambaBlock:
         return dict(w_in=self.w_in, conv_w=self.conv_w, conv_b=self.conv_b, w_x=self.w_x,
                     w_dt=self.w_dt, dt_bias=self.dt_bias, A=self.A, D=self.D, w_out=self.w_out)
 
+    @on_launch_stream
     def forward(self, x, out=None, stream=None):
+        """Calls that share this block's workspace must be ordered on one stream (it holds
+        intermediates only during a call)."""
         bt, L, _ = x.shape
         need = mamba_block_workspace_size(bt, L, self.d_inner, self.dt_rank, self.d_state)
         if self._ws is None or self._ws.numel() < need:
             self._ws = torch.empty(need, device=x.device, dtype=torch.uint8)
+        keep_for_stream(self._ws, stream)
         return mamba_block_fwd(x, workspace=self._ws, out=out, stream=stream, **self.parameters())
 
     __call__ = forward

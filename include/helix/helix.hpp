@@ -242,8 +242,14 @@ public:
     S4Block(size_t d_model, size_t d_state, Rng& rng, int device = 0);
     // forward_ssm (ssm.rs:138-186): x [d_model, L] -> y with the reference's memory [L, d_model]
     // and shape field [d_model, L]. parallel = the time-parallel form (equal to rounding).
+    // The block keeps discretize(dt)'s decay, computed on the host from A_real / A_imag, for the
+    // buffers it was computed from, and a device workspace: forwards on one block must not run
+    // concurrently from several threads, and after writing into A_real / A_imag in place (their
+    // data() pointers) call parameters_changed(); assigning new tensors or restore() needs nothing.
     HipTensor forward_ssm(const HipTensor& x, const HipTensor* gate = nullptr,
                           bool parallel = false) const;
+    // Drops the kept decay: the next forward_ssm discretizes A_real / A_imag again.
+    void parameters_changed() { a_disc_ = HipTensor(); a_src_[0] = a_src_[1] = nullptr; }
     // Module::forward (ssm.rs:269-273) = forward_conv (ssm.rs:189-229) with compute_conv_kernel
     // (ssm.rs:232-251), written as the reference writes them over HipTensor ops, so every shape
     // gives the reference's result or error: input [batch, seq_len] (2-D slices), kernel
@@ -264,7 +270,7 @@ public:
 private:
     size_t d_model_, d_state_;
     // discretize(dt)'s decay (hx_s4_discretize, host libm) for the A_real / A_imag buffers it was
-    // computed from (parameters are immutable buffers, so their addresses identify them)
+    // computed from (identified by their addresses; parameters_changed() and restore() drop it)
     mutable HipTensor a_disc_;
     mutable const void* a_src_[2] = {nullptr, nullptr};
     mutable HipTensor workspace_;
@@ -506,11 +512,27 @@ public:
     void synchronize() override;
 
 private:
+    // device scratch of the scan's long-sequence path, kept between SSMForward operations and
+    // grown on demand (operations of one backend run in order on the default stream)
+    void* scan_workspace(size_t bytes);
     int device_;
     DeviceCapabilities caps_;
     uint64_t next_id_ = 1;
     std::map<uint64_t, void*> live_;
     std::map<uint64_t, MemoryHandle> pending_;  // execute_async outputs by handle id
+    void* scan_ws_ = nullptr;
+    size_t scan_ws_bytes_ = 0;
 };
+
+// Host-side check of an operation's inputs against what RocmBackend::execute_op would touch:
+// every input handle that is read must have a device address and hold the bytes the operation
+// reads (element counts from its shape, else its size), dtypes must be what the kernels take
+// (F32 for the elementwise ops, Mean, Transpose and MatMul; for SSMForward / StateUpdate the
+// storage type of u, F32 or BF16, shared by delta, B, C and z, with A, D, dt_bias and the state
+// F32), and size parameters must be non-negative integers. Throws the reference's TensorError
+// variants (InvalidInput, DTypeMismatch, ShapeMismatch, UnsupportedOperation); launches
+// nothing. execute_op calls it first. The reference's CPU backend clamps to the smallest
+// handle instead (backend-cpu/src/cpu_backend.rs); a device backend cannot read past a buffer.
+void validate_operation(const Operation& op);
 
 }  // namespace helix

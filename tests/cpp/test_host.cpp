@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "helix/helix.hpp"
+#include "helix_hip.h"
 
 extern "C" {
 void oracle_matmul(int64_t M, int64_t K, int64_t N, const float* A, const float* B, float* Y);
@@ -214,6 +215,84 @@ TEST_CPU(compute_graph_build_sort_and_cycle) {
     CHECK(msg.find("Circular dependency detected") != std::string::npos);
 }
 
+TEST_CPU(validate_operation_rejects_handles_the_launch_would_overrun) {
+    // RocmBackend::execute_op checks every input against what its launch touches before anything
+    // runs; the addresses below are never dereferenced
+    auto h = [](size_t bytes, std::vector<size_t> shape, DataType dt = DataType::F32) {
+        MemoryHandle m;
+        m.address = 0x10000;
+        m.size = bytes;
+        m.shape = std::move(shape);
+        m.dtype = dt;
+        return m;
+    };
+    std::string msg;
+    Operation add(OperationType::Add);
+    add.inputs = {h(24, {2, 3}), h(20, {2, 3})};  // second holds 5 floats, shape says 6
+    CHECK(throws_kind([&] { validate_operation(add); }, ErrorKind::InvalidInput, &msg));
+    CHECK(msg.find("input 1 holds 20 bytes") != std::string::npos);
+    add.inputs[1] = h(24, {2, 3});
+    validate_operation(add);  // well-formed: no throw
+    add.inputs[1].address = 0;
+    CHECK(throws_kind([&] { validate_operation(add); }, ErrorKind::InvalidInput));
+    Operation mm(OperationType::MatMul);
+    mm.inputs = {h(2 * 3 * 2, {2, 3}, DataType::BF16), h(3 * 4 * 4, {3, 4})};  // bf16 read as f32
+    CHECK(throws_kind([&] { validate_operation(mm); }, ErrorKind::DTypeMismatch));
+    mm.inputs[0] = h(2 * 3 * 4, {2, 3});
+    mm.inputs[1] = h(3 * 4 * 4 - 4, {3, 4});
+    CHECK(throws_kind([&] { validate_operation(mm); }, ErrorKind::InvalidInput));
+    Operation tr(OperationType::Transpose);
+    tr.inputs = {h(16, {3, 2})};
+    CHECK(throws_kind([&] { validate_operation(tr); }, ErrorKind::InvalidInput));
+    // SSMForward: u, delta, A, B, C[, D, z, dt_bias]
+    const size_t bt = 2, L = 5, dim = 8, N = 16;
+    auto ssm = [&](DataType st) {
+        const size_t es = st == DataType::BF16 ? 2 : 4;
+        Operation op(OperationType::SSMForward);
+        op.inputs = {h(bt * L * dim * es, {}, st), h(bt * L * dim * es, {}, st), h(dim * N * 4, {}),
+                     h(bt * L * N * es, {}, st), h(bt * L * N * es, {}, st), h(dim * 4, {}),
+                     h(bt * L * dim * es, {}, st), h(dim * 4, {})};
+        op.params = {{"batch", (double)bt}, {"seqlen", (double)L}, {"dim", (double)dim}, {"dstate", (double)N}};
+        return op;
+    };
+    validate_operation(ssm(DataType::F32));
+    validate_operation(ssm(DataType::BF16));
+    auto bad = ssm(DataType::F32);
+    bad.inputs[3].dtype = DataType::BF16;  // B not in u's storage type
+    CHECK(throws_kind([&] { validate_operation(bad); }, ErrorKind::DTypeMismatch, &msg));
+    CHECK(msg.find("SSMForward B") != std::string::npos);
+    bad = ssm(DataType::BF16);
+    bad.inputs[2].dtype = DataType::BF16;  // A must be F32
+    CHECK(throws_kind([&] { validate_operation(bad); }, ErrorKind::DTypeMismatch));
+    bad = ssm(DataType::F32);
+    bad.inputs[6].size -= 4;  // z one element short
+    CHECK(throws_kind([&] { validate_operation(bad); }, ErrorKind::InvalidInput, &msg));
+    CHECK(msg.find("SSMForward: z holds") != std::string::npos);
+    bad = ssm(DataType::F32);
+    bad.params["seqlen"] = 6;  // more steps than the buffers hold
+    CHECK(throws_kind([&] { validate_operation(bad); }, ErrorKind::InvalidInput));
+    bad = ssm(DataType::F32);
+    bad.params["dim"] = -1;
+    CHECK(throws_kind([&] { validate_operation(bad); }, ErrorKind::InvalidInput));
+    bad = ssm(DataType::F32);
+    bad.inputs[0].dtype = DataType::F16;
+    CHECK(throws_kind([&] { validate_operation(bad); }, ErrorKind::DTypeMismatch));
+    bad = ssm(DataType::F32);
+    bad.inputs[6].address = 0;  // an absent optional operand (z) is allowed
+    validate_operation(bad);
+    // StateUpdate: state, u, delta, A, B, C[, D, z, dt_bias]
+    Operation su(OperationType::StateUpdate);
+    su.inputs = {h(bt * dim * N * 4 - 4, {}), h(bt * dim * 4, {}), h(bt * dim * 4, {}), h(dim * N * 4, {}),
+                 h(bt * N * 4, {}), h(bt * N * 4, {})};
+    su.params = {{"batch", (double)bt}, {"dim", (double)dim}};
+    CHECK(throws_kind([&] { validate_operation(su); }, ErrorKind::InvalidInput, &msg));
+    CHECK(msg.find("state holds") != std::string::npos);
+    su.inputs[0].size += 4;
+    validate_operation(su);
+    su.inputs[5].dtype = DataType::BF16;
+    CHECK(throws_kind([&] { validate_operation(su); }, ErrorKind::DTypeMismatch));
+}
+
 // ============================================================================ device tests
 TEST_GPU(reference_kat_matmul_ones) {
     // backend-cpu/src/lib.rs:1747-1758: ones[2,3] . ones[3,4] == 3
@@ -383,6 +462,67 @@ TEST_GPU(selective_scan_and_backend_ssm_forward) {
     std::vector<float> mh(12 * 9);
     be.copy_to_host(mh.data(), mo, mh.size() * 4);
     CHECK(bits_equal(mh, a.matmul(b).to_host()));
+}
+
+TEST_GPU(long_sequence_scan_on_every_surface) {
+    // 1 x 16384 x 512: 8 (batch, 64-channel) tiles cannot fill the GPU, so the library cuts the
+    // sequence into time segments with a carry (a workspace is needed). helix::selective_scan and
+    // the HAL's SSMForward take that path and give the C ABI's hx_selective_scan_fwd_ws result
+    // bit for bit (the call the Python layer makes), within 1e-4 of the sequential oracle.
+    const size_t bt = 1, L = 16384, dim = 512, N = 16;
+    const size_t need = hx_selective_scan_workspace_size(bt, L, dim, N, HX_F32);
+    CHECK(need > 0);
+    auto u = randn(bt * L * dim, 60), dl = randn(bt * L * dim, 61), Bv = randn(bt * L * N, 62),
+         Cv = randn(bt * L * N, 63), Dv = randn(dim, 64), zv = randn(bt * L * dim, 65);
+    for (auto& v : dl) v = v * 0.5f - 4.0f;
+    std::vector<float> Av(dim * N);
+    for (size_t d = 0; d < dim; ++d)
+        for (size_t n = 0; n < N; ++n) Av[d * N + n] = -(float)(n + 1);
+    auto tu = HipTensor::from_host(u, Shape({bt, L, dim})), td = HipTensor::from_host(dl, Shape({bt, L, dim}));
+    auto tA = HipTensor::from_host(Av, Shape({dim, N})), tB = HipTensor::from_host(Bv, Shape({bt, L, N}));
+    auto tC = HipTensor::from_host(Cv, Shape({bt, L, N})), tD = HipTensor::from_host(Dv, Shape({dim}));
+    auto tz = HipTensor::from_host(zv, Shape({bt, L, dim}));
+    // the C ABI's segmented path
+    HipTensor ws(Shape({(need + 3) / 4}), Storage::F32, 0), yc(Shape({bt, L, dim}), Storage::F32, 0);
+    CHECK(hx_selective_scan_fwd_ws(bt, L, dim, N, HX_F32, 1, tu.data(), td.data(), (const float*)tA.data(),
+                                   tB.data(), tC.data(), (const float*)tD.data(), tz.data(), nullptr, yc.data(),
+                                   nullptr, nullptr, ws.data(), ws.nbytes(), nullptr) == HX_OK);
+    const auto ych = yc.to_host();
+    // the C++ host layer
+    const auto yh = selective_scan(tu, td, tA, tB, tC, &tD, &tz, nullptr, true).to_host();
+    CHECK(bits_equal(yh, ych));
+    // the HAL
+    RocmBackend be(0);
+    auto handle = [&](const HipTensor& t) {
+        MemoryHandle m;
+        m.address = (uintptr_t)t.data();
+        m.size = t.nbytes();
+        return m;
+    };
+    Operation op(OperationType::SSMForward);
+    op.inputs = {handle(tu), handle(td), handle(tA), handle(tB), handle(tC), handle(tD), handle(tz)};
+    op.params = {{"batch", (double)bt}, {"seqlen", (double)L}, {"dim", (double)dim}, {"dstate", (double)N}};
+    MemoryHandle out = be.execute_op(op);
+    std::vector<float> yb(bt * L * dim);
+    be.copy_to_host(yb.data(), out, yb.size() * 4);
+    be.deallocate(out);
+    CHECK(bits_equal(yb, ych));
+    // and a second, shorter call reuses the backend's workspace
+    Operation op2 = op;
+    op2.params["seqlen"] = 8192.0;
+    MemoryHandle out2 = be.execute_op(op2);
+    std::vector<float> yb2(bt * 8192 * dim);
+    be.copy_to_host(yb2.data(), out2, yb2.size() * 4);
+    be.deallocate(out2);
+    std::vector<float> r(bt * L * dim);
+    oracle_selective_scan(bt, L, dim, N, 1, u.data(), dl.data(), Av.data(), Bv.data(), Cv.data(), Dv.data(),
+                          zv.data(), nullptr, r.data(), nullptr, nullptr);
+    const double e = rel_err(yh, r);
+    std::printf("  1x16384x512 segmented scan: max rel err %.3e vs oracle\n", e);
+    CHECK(e < 1e-4);
+    // the first 8192 steps of a sequence do not depend on what follows
+    std::vector<float> r2(r.begin(), r.begin() + bt * 8192 * dim);
+    CHECK(rel_err(yb2, r2) < 1e-4);
 }
 
 TEST_GPU(fused_mamba_block_runs_and_regrows_workspace) {

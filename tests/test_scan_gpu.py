@@ -293,13 +293,15 @@ def test_baseline_config4_scan_full_size(dev, variant):
     assert err <= TOL_F32
 
 
-def test_warp_specialised_partial_group_large_offsets(dev):
-    """dim % 48 != 0 with a batch row past 2^31 bytes (1 x 30000 x 20000 fp32, 2.4 GB per
-    operand): the lanes of the last block's channels past dim must not write anywhere. Their
-    32-bit store offsets start past the row's end; advancing them by whole chunks used to wrap
-    below it and overwrite channel 18176 (2^32 mod the row size) at early steps. Channels are
-    independent, so the oracle runs on the touched channels only, over the whole sequence."""
-    ssm.set_scan_variant(44)
+@pytest.mark.parametrize("variant", [0, 44, 46])
+def test_warp_specialised_partial_group_large_offsets(dev, variant):
+    """dim % 48 != 0 with a batch row past 2^31 bytes (1 x 30000 x 20000 fp32,
+    2.4 GB per operand): the lanes of the last block's channels past dim must not write anywhere.
+    Their 32-bit store offsets start past the row's end; advancing them by whole chunks used to
+    wrap below it and overwrite channel 18176 (2^32 mod the row size) at early steps. Channels are
+    independent, so the oracle runs on the touched channels only, over the whole sequence. Run
+    for every warp-specialised kernel and the automatic choice."""
+    ssm.set_scan_variant(variant)
     bt, L, dim, N = 1, 30000, 20000, 16
     g = torch.Generator(device=dev).manual_seed(0x5753)
     u = torch.randn((bt, L, dim), generator=g, device=dev)
@@ -309,7 +311,7 @@ def test_warp_specialised_partial_group_large_offsets(dev):
     C = torch.randn((bt, L, N), generator=g, device=dev)
     A = -torch.arange(1, N + 1, device=dev, dtype=torch.float32).repeat(dim, 1).contiguous()
     D = torch.randn((dim,), generator=g, device=dev)
-    print("case 1x30000x20000 fp32 variant 44", flush=True)
+    print(f"case 1x30000x20000 fp32 variant {variant}", flush=True)
     out = ssm.selective_scan_fwd(u, delta, A, B, C, D, z)
     torch.cuda.synchronize()
     chans = [0, 18176, dim - 32, dim - 1]
