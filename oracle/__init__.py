@@ -89,6 +89,7 @@ def lib() -> ctypes.CDLL:
             "oracle_selective_state_update": [_i64, _i64, _i64, _int] + [_p] * 10,
             "oracle_s4d_complex": [_i64, _i64, _i64, _i64] + [_p] * 10,
             "oracle_selective_scan_omp": [_i64, _i64, _i64, _i64, _int] + [_p] * 9 + [_int],
+            "oracle_s4_ref_fwd_omp": [_i64, _i64, _i64, _f] + [_p] * 10 + [_int],
             "oracle_max_threads": [],
             "oracle_conv1d_silu": [_i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
             "oracle_r_s4_forward_ssm": [_i64, _i64, _i64, _f] + [_p] * 9,
@@ -172,6 +173,21 @@ def s4_ref_fwd(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, f64=False):
     fn = lib().oracle_s4_ref_fwd_f64 if f64 else lib().oracle_s4_ref_fwd
     fn(M, N, L, dt, _ptr(x), _ptr(a_real), _ptr(a_imag), _ptr(B), _ptr(C), _ptr(D), _ptr(gate),
        _ptr(y), _ptr(work))
+    return y
+
+
+def s4_ref_fwd_omp(x, a_real, a_imag, B, C, D, gate=None, dt=0.1, threads=0):
+    """s4_ref_fwd's values bit for bit, with the projection and readout spread over threads
+    (hx_oracle_omp.c; N <= 256)."""
+    x, a_real, a_imag, B, C, D, gate = map(_f32, (x, a_real, a_imag, B, C, D, gate))
+    M, L = x.shape
+    N = a_real.shape[0]
+    assert N <= 256
+    y = np.empty((L, M), np.float32)
+    U = np.empty((L, N), np.float32)
+    H = np.empty((L, N), np.float32)
+    lib().oracle_s4_ref_fwd_omp(M, N, L, dt, _ptr(x), _ptr(a_real), _ptr(a_imag), _ptr(B), _ptr(C),
+                                _ptr(D), _ptr(gate), _ptr(y), _ptr(U), _ptr(H), int(threads))
     return y
 
 
@@ -456,12 +472,15 @@ def numpy_conv1d_silu(x, w, bias=None):
     return y / (1.0 + np.exp(-y))
 
 
-def numpy_mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, dt_rank):
-    """float64 block with the same bf16 storage rounding points as ``mamba_block``."""
+def numpy_mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, dt_rank,
+                      round_out=True, return_state=False):
+    """float64 block with the same bf16 storage rounding points as ``mamba_block`` (and its
+    ``round_out`` / ``return_state`` options)."""
     r = lambda a: bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
     Bt, L, dm = x.shape
     di = w_dt.shape[0]
     N = A.shape[1]
+    K = np.asarray(conv_w).shape[1]
     xz = r(x).reshape(-1, dm) @ r(w_in).T
     xp, z = r(xz[:, :di]).reshape(Bt, L, di), r(xz[:, di:]).reshape(Bt, L, di)
     xc = r(numpy_conv1d_silu(xp, conv_w, conv_b))
@@ -470,8 +489,74 @@ def numpy_mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, 
     Bm = r(dbc[:, dt_rank:dt_rank + N]).reshape(Bt, L, N)
     Cm = r(dbc[:, dt_rank + N:]).reshape(Bt, L, N)
     dt = r(dtlo @ r(w_dt).T).reshape(Bt, L, di)
-    y, _ = numpy_selective_scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True)
-    return r(r(y).reshape(-1, di) @ r(w_out).T).reshape(Bt, L, dm)
+    y, last = numpy_selective_scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True)
+    out = r(y).reshape(-1, di) @ r(w_out).T
+    out = (r(out) if round_out else out).reshape(Bt, L, dm)
+    if not return_state:
+        return out
+    conv = np.zeros((Bt, max(K - 1, 1), di))
+    for j in range(K - 1):
+        t = L - (K - 1) + j
+        if t >= 0:
+            conv[:, j, :] = xp[:, t, :]
+    return out, last, conv
+
+
+def numpy_rmsnorm(X, w, eps):
+    """float64 RMSNorm (crates/nn/src/lib.rs:258-285): x / sqrt(mean(x^2) + eps) * w per row."""
+    X = np.asarray(X, np.float64)
+    return X / np.sqrt((X * X).mean(axis=-1, keepdims=True) + eps) * np.asarray(w, np.float64)
+
+
+def numpy_lm_head(x, params, eps):
+    r = lambda a: bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
+    shp = x.shape
+    xn = r(numpy_rmsnorm(np.asarray(x, np.float64).reshape(-1, shp[-1]), params["norm_f"], eps))
+    return (xn @ r(params["w_head"]).T).reshape(*shp[:-1], -1)
+
+
+def numpy_lm_prefill(tokens, params, dt_rank, eps=1e-5):
+    """float64 twin of ``lm_prefill`` with the same bf16 storage rounding points: the exact value
+    of what the f32 restatement computes, for bounding its own rounding."""
+    r = lambda a: bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
+    x = np.asarray(params["embed"], np.float64)[np.asarray(tokens)]
+    Bt, L, dm = x.shape
+    states = []
+    for p in params["layers"]:
+        xn = r(numpy_rmsnorm(x.reshape(-1, dm), p["norm_w"], eps)).reshape(Bt, L, dm)
+        blk = {k: p[k] for k in ("w_in", "conv_w", "conv_b", "w_x", "w_dt", "dt_bias", "A", "D", "w_out")}
+        out, last, conv = numpy_mamba_block(xn, **blk, dt_rank=dt_rank, round_out=False, return_state=True)
+        x = x + out
+        states.append((last, conv))
+    return numpy_lm_head(x, params, eps), states
+
+
+def numpy_lm_decode_step(tokens, params, states, dt_rank, eps=1e-5):
+    """float64 twin of ``lm_decode_step`` (same bf16 storage rounding points)."""
+    r = lambda a: bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
+    x = np.asarray(params["embed"], np.float64)[np.asarray(tokens)]
+    new = []
+    for p, (ssm_st, conv_st) in zip(params["layers"], states):
+        di = p["w_dt"].shape[0]
+        N = np.asarray(p["A"]).shape[1]
+        w = np.asarray(p["conv_w"], np.float64)
+        K = w.shape[1]
+        xn = r(numpy_rmsnorm(x, p["norm_w"], eps))
+        xz = xn @ r(p["w_in"]).T
+        xp, z = r(xz[:, :di]), r(xz[:, di:])
+        win = np.concatenate([np.asarray(conv_st, np.float64)[:, :K - 1, :], xp[:, None, :]], axis=1)
+        acc = np.asarray(p["conv_b"], np.float64)[None, :] + np.einsum("dj,bjd->bd", w, win)
+        xc = r(acc / (1.0 + np.exp(-acc)))
+        conv_st = win[:, 1:, :] if K > 1 else np.asarray(conv_st, np.float64)
+        dbc = xc @ r(p["w_x"]).T
+        dtlo = r(dbc[:, :dt_rank])
+        Bv, Cv = r(dbc[:, dt_rank:dt_rank + N]), r(dbc[:, dt_rank + N:])
+        dt = r(dtlo @ r(p["w_dt"]).T)
+        y, ssm_st = numpy_selective_scan(xc[:, None], dt[:, None], p["A"], Bv[:, None], Cv[:, None], p["D"],
+                                         z[:, None], p["dt_bias"], True, init_state=ssm_st)
+        x = x + r(y[:, 0]) @ r(p["w_out"]).T
+        new.append((ssm_st, conv_st))
+    return numpy_lm_head(x, params, eps), new
 
 
 # ------------------------------------------------------------------ tensor primitives

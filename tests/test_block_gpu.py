@@ -2,9 +2,11 @@
 (oracle.conv1d_silu, oracle.mamba_block: f32 arithmetic with bf16 rounding at the same storage
 points as the device path). The conv is elementwise-checked (rel_err 1e-4 fp32). The block ends in
 a GEMM whose outputs cancel, and a one-ulp flip of any bf16 intermediate propagates, so elementwise
-relative error is unbounded even between two correct CPU restatements; its bar is normwise
+relative error is large even between two correct CPU restatements. The block is held normwise
 (max|g - r| / max|r|): <= 2e-2 against the fp32 reference with no storage rounding (the
-bf16-storage tolerance) and <= 1e-2 against the oracle that rounds the same intermediates.
+bf16-storage tolerance) and <= 1e-2 against the oracle that rounds the same intermediates; and
+elementwise against the float64 twin of that oracle, to twice the f32 oracle's own elementwise
+distance from it (see check_block).
 At the BASELINE config-3 size the oracle checks causal prefixes of the first and
 last sequences (the block is causal in time and independent across the batch), and the device
 output's prefix must equal a device run on that prefix alone, bit for bit."""
@@ -79,15 +81,22 @@ def test_mamba_block_vs_oracle(dev, bt, L, dm, di, r):
 
 
 def check_block(g, p, r, what=""):
+    """Normwise: <= 1e-2 against the same-rounding f32 oracle, <= 2e-2 against the fp32 oracle
+    with no storage rounding. Elementwise (north_star's metric, floor 1e-3 max|ref|) against the
+    float64 twin with the same rounding points: within twice the f32 oracle's own elementwise
+    distance from that twin, or twice the bf16 bar where that is larger. The f32 oracle's distance
+    is what a correct f32 evaluation of these rounding points carries (one-ulp bf16 flips of
+    intermediates that cancel in the output GEMM), measured on the same inputs."""
     ref = oracle.mamba_block(**p, dt_rank=r)
+    ref64 = oracle.numpy_mamba_block(**p, dt_rank=r)
     e_same = norm_err(g, ref)
     e_fp32 = norm_err(g, oracle.mamba_block(**p, dt_rank=r, bf16=False))
-    # the elementwise figure (relative error with a floor of 1e-3 x max|ref|), reported beside the
-    # normwise bar the test holds
+    e_el, own_el = rel_err(g, ref64), rel_err(ref, ref64)
     print(f"block{what}: normwise {e_same:.3e} (bf16-storage oracle), {e_fp32:.3e} (fp32 oracle); "
-          f"elementwise {rel_err(g, ref):.3e}", flush=True)
+          f"elementwise vs float64 twin {e_el:.3e} (f32 oracle's own {own_el:.3e})", flush=True)
     assert e_same <= 1e-2, f"{what} vs bf16-storage oracle: {e_same}"
     assert e_fp32 <= TOL_BF16, f"{what} vs fp32 oracle: {e_fp32}"
+    assert e_el <= 2 * max(TOL_BF16, own_el), f"{what} elementwise vs float64 twin: {e_el} (own {own_el})"
 
 
 def test_mamba_block_class_matches_functional(dev):

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.util import rel_err
+from tests.util import norm_err, rel_err
 
 F = np.float32
 
@@ -403,6 +403,53 @@ def test_mamba_block_vs_numpy_f64():
     # both round the same storage points to bf16; a one-ulp bf16 flip of an intermediate is the
     # largest legitimate difference
     assert rel_err(y, r) < 2e-2
+
+
+def test_mamba_block_f64_state_and_unrounded_output():
+    """The float64 twin's layer options: its decode hand-off equals the f32 restatement's conv
+    window exactly (both hold bf16 values) and its scan state to rounding; round_out=False skips
+    only the final rounding."""
+    from tests.util import block_inputs
+    p = block_inputs(2, 24, 16, 32, 16, 8, 4, seed=35)
+    y, last, conv = oracle.mamba_block(**p, dt_rank=8, round_out=False, return_state=True)
+    y64, last64, conv64 = oracle.numpy_mamba_block(**p, dt_rank=8, round_out=False, return_state=True)
+    assert np.array_equal(conv64, conv)
+    assert rel_err(last64, last) < 1e-2
+    assert norm_err(y64, y) < 1e-2
+    assert np.array_equal(oracle.bf16_round(y64.astype(np.float32)),
+                          oracle.bf16_round(oracle.numpy_mamba_block(**p, dt_rank=8).astype(np.float32)))
+
+
+def test_lm_f64_twin_matches_f32_oracle_and_catches_a_dropped_norm():
+    """The float64 twins of the byte LM (prefill, decode) agree with the pinned f32 restatement
+    to the bf16 storage bar (they share every rounding point); a twin that skips a layer's
+    RMSNorm weight does not."""
+    from tests.util import lm_params
+    P = lm_params(2, 32, 64, 16, 8, 4, 256, seed=45)
+    tok = np.random.default_rng(46).integers(0, 256, (3, 12))
+    lg, st = oracle.lm_prefill(tok[:, :11], P, 8)
+    lg64, st64 = oracle.numpy_lm_prefill(tok[:, :11], P, 8)
+    assert norm_err(lg64, lg) < 1e-2
+    for (a, b), (c, d) in zip(st, st64):
+        assert np.array_equal(b, d) and rel_err(c, a) < 1e-2
+    dl, _ = oracle.lm_decode_step(tok[:, 11], P, st, 8)
+    dl64, _ = oracle.numpy_lm_decode_step(tok[:, 11], P, st64, 8)
+    assert norm_err(dl64, dl) < 1e-2
+    full64, _ = oracle.numpy_lm_prefill(tok, P, 8)
+    assert norm_err(dl64, full64[:, 11]) < 1e-2
+    bad = dict(P, layers=[dict(P["layers"][0], norm_w=np.ones_like(P["layers"][0]["norm_w"])),
+                          P["layers"][1]])
+    lgb, _ = oracle.numpy_lm_prefill(tok[:, :11], bad, 8)
+    assert norm_err(lgb, lg) > 5e-2
+
+
+def test_s4_ref_omp_is_bit_identical_to_the_serial_restatement():
+    M, N, L = 96, 16, 1500
+    p = s4_params(M, N, 24)
+    x = np.random.default_rng(25).standard_normal((M, L)).astype(F)
+    gate = np.random.default_rng(26).standard_normal(M).astype(F)
+    assert np.array_equal(oracle.s4_ref_fwd_omp(x, **p, gate=gate, threads=4), oracle.s4_ref_fwd(x, **p, gate=gate))
+    assert np.array_equal(oracle.s4_ref_fwd_omp(x, **p, threads=3), oracle.s4_ref_fwd(x, **p))
 
 
 def test_s4_ref_f64_matches_numpy_and_f32():

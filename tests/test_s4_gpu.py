@@ -165,8 +165,23 @@ def test_s4_ref_parallel_config4_full_size(dev):
     g = g.cpu().numpy()
     err64 = rel_err(g, oracle.s4_ref_fwd(**p, f64=True))
     assert err64 <= TOL_F32, err64
-    nerr = norm_err(g, oracle.s4_ref_fwd(**p))
+    nerr = norm_err(g, oracle.s4_ref_fwd_omp(**p))
     assert nerr <= 1e-6, nerr
+
+
+def test_s4_ref_exact_config4_full_size(dev):
+    """BASELINE config 4, S4 reference mode as the bench's exact leg times it (hx_s4_ref_fwd):
+    d_model 2048, N 16, L 65536, A_real = -0.5, A_imag = pi*n, over the whole sequence, bit for
+    bit against the f32 restatement (its OpenMP form, bit-identical to the sequential one:
+    tests/test_oracle.py)."""
+    M, N, L = 2048, 16, 65536
+    p = s4_inputs(M, N, L, seed=405, a_real=np.full(N, -0.5), a_imag=np.pi * np.arange(N))
+    print("case s4 exact 2048x16x65536", flush=True)
+    g = ssm.s4_ref_fwd(**{k: dv(v, dev) for k, v in p.items()})
+    torch.cuda.synchronize()
+    g = g.cpu().numpy()
+    r = oracle.s4_ref_fwd_omp(**p)
+    assert np.array_equal(g, r), f"max abs diff {np.abs(g - r).max()}"
 
 
 # ------------------------------------------------------------------ S4D complex, wave path
@@ -234,17 +249,17 @@ def test_s4d_wave_path_equals_thread_path(dev):
 
 def test_s4d_config4_full_size(dev):
     """BASELINE config 4, S4D complex: batch 1, L 65536, d 2048, N 16 (A = -0.5 + i*pi*n).
-    Channels are independent, so the oracle checks the first and last 16 channels over the
-    whole sequence (every segment boundary and carry), and the whole output is finite."""
+    Channels are independent, so the oracle checks the first and last 16 channels and every
+    8th channel (256 more, spread over every block and wave of the grid) over the whole sequence
+    (every segment boundary and carry), and the whole output is finite."""
     bt, L, dim = 1, 65536, 2048
     x, p = s4d_inputs(bt, L, dim, 16, seed=4)
     g = ssm.s4d_complex_fwd(dv(x, dev), **{k: dv(v, dev) for k, v in p.items()})
     torch.cuda.synchronize()
     assert torch.isfinite(g).all()
     gh = g.cpu().numpy()
-    for lo in (0, dim - 16):
-        sl = slice(lo, lo + 16)
-        ps = {k: (v[sl] if v.ndim >= 1 else v) for k, v in p.items()}
+    for sl in (slice(0, 16), slice(dim - 16, dim), slice(3, dim, 8)):
+        ps = {k: (np.ascontiguousarray(v[sl]) if v.ndim >= 1 else v) for k, v in p.items()}
         r = oracle.s4d_complex(np.ascontiguousarray(x[:, :, sl]), **ps)
         err = rel_err(gh[:, :, sl], r)
-        assert err <= TOL_F32, (lo, err)
+        assert err <= TOL_F32, (sl, err)
