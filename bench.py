@@ -150,6 +150,43 @@ def cpu_baseline_scan(x_dev, sample_batches):
                 omp=dict(value=toks / (t3 - t2), threads=threads, seconds=round(t3 - t2, 3))), out1
 
 
+def fit_time(run, sizes, warm=True):
+    """Times run(n) once at each sample size n and fits T(n) = a + b*n through the points (the
+    fixed part a: weight transposes and allocations that do not grow with n; one point or a
+    non-increasing pair: T = b*n). warm: one untimed call at the smallest size first (it starts the
+    OpenMP pool and faults in the pages). Returns (a, b, [[n, seconds], ...])."""
+    if warm:
+        run(sizes[0])
+    pts = []
+    for n in sizes:
+        t0 = time.perf_counter()
+        run(n)
+        pts.append([n, time.perf_counter() - t0])
+    if len(pts) >= 2 and pts[-1][1] > pts[0][1]:
+        (n0, t0), (n1, t1) = pts[0], pts[-1]
+        b = (t1 - t0) / (n1 - n0)
+        a = max(t0 - b * n0, 0.0)
+    else:
+        a, b = 0.0, pts[-1][1] / pts[-1][0]
+    return a, b, pts
+
+
+def cpu_leg(run, sizes, full, units_full, unit, cores, sample, warm=True, **extra):
+    """A CPU baseline leg: run(n) at the sample sizes, extrapolated linearly to `full` (the size
+    of the GPU step, in the same units as the sizes); value = units_full / T(full)."""
+    a, b, pts = fit_time(run, sizes, warm)
+    t_full = a + b * full
+    return dict(value=units_full / t_full, unit=unit, cores=cores, kind="port", sample=sample,
+                extrapolated={"model": "T(n) = a + b*n, linear in n", "n_full": full,
+                              "a_s": a, "b_s_per_n": b, "samples_n_s": pts, "t_full_s": t_full},
+                host=host_info(), **extra)
+
+
+def norm_err(g, r):
+    g, r = np.asarray(g, np.float64), np.asarray(r, np.float64)
+    return float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30))
+
+
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 
 
@@ -216,6 +253,37 @@ def bench_block(args, dev):
     breakdown["conv1d_silu"]["hbm_gbs"] = 2 * M * di * 2 / (breakdown["conv1d_silu"]["ms"] * 1e-3) / 1e9
     total_flops = sum(flops.values())
     gemm_ms = sum(breakdown[n]["ms"] for n in flops)
+    cpu = None
+    if not args.no_cpu:
+        # (O): the block over OpenMP (blocked products, 16-channel scan tasks), f32 throughout,
+        # on batch row 0 of input set 0 at two prefix lengths; (R): the reference's Linear
+        # execution shape (transpose copy, ijk matmul, broadcast add, one thread) for the four
+        # projections, the sequential C conv and scan beside it, at two short prefixes. Both are
+        # extrapolated linearly in tokens to the step's 4 x 4096 (the block is causal and its
+        # cost per token does not depend on the position).
+        import oracle  # test/bench infrastructure only
+        th = oracle.max_threads()
+        hp = {k: v.float().cpu().numpy() for k, v in prm.items()}
+        x0 = xs[0][:1].float().cpu().numpy()
+        got = {}
+
+        def run_o(n):
+            got["y"] = oracle.mamba_block(x0[:, :n], **hp, dt_rank=r, bf16=False, impl="omp", threads=th)
+
+        def run_r(n):
+            oracle.mamba_block(x0[:, :n], **hp, dt_rank=r, bf16=False, impl="ref")
+
+        no, nr = (1024, 2048), (16, 48)
+        cpu = cpu_leg(run_o, no, M, M, "tokens/s", th,
+                      f"OpenMP block (oracle/hx_oracle_omp.c, f32) on batch row 0 of input set 0, "
+                      f"prefixes of {no[0]} and {no[1]} tokens", kind_note="(O) optimised, all host cores")
+        # the GPU's bf16-storage output against the f32 CPU block on the same tokens
+        cpu["gpu_vs_cpu_normwise_err"] = norm_err(outs[0][0, :no[-1]].float().cpu().numpy(), got["y"][0])
+        cpu["reference_shape"] = cpu_leg(
+            run_r, nr, M, M, "tokens/s", 1,
+            f"the block with the reference's Linear execution shape (oracle/hx_oracle_ref.c), one "
+            f"thread, on batch row 0 of input set 0, prefixes of {nr[0]} and {nr[1]} tokens",
+            warm=False, kind_note="(R) reference-faithful, 1 core, linearly extrapolated")
     rec = {
         "metric": "Mamba block fwd tokens/s (config 3), 1 GPU",
         "value": M * 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -232,7 +300,7 @@ def bench_block(args, dev):
                      "traffic": None, "algorithmic_flops": total_flops, "kernel_ms": gemm_ms},
         "breakdown": breakdown,
         "timing": timing,
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(rec))
 
@@ -276,7 +344,7 @@ def bench_s4(args, dev):
                    D=torch.randn((M,), generator=gen, device=dev))
 
         def step(i):
-            ssm.s4d_complex_fwd(xs[i], **prm)
+            return ssm.s4d_complex_fwd(xs[i], **prm)
 
         workload = "S4D diagonal complex recurrence (batch 1, L 65536, d 2048, N 16, A = -0.5 + i*pi*n)"
     ms = time_steps(step, 2, args.steps, args.warmup)
@@ -295,11 +363,40 @@ def bench_s4(args, dev):
         yr = oracle.r_s4_forward_ssm(xh, hp["a_real"], hp["a_imag"], hp["B"], hp["C"], hp["D"])
         t1 = time.perf_counter()
         ref = oracle.s4_ref_fwd(xh, hp["a_real"], hp["a_imag"], hp["B"], hp["C"], hp["D"])
+        th = oracle.max_threads()
+        oracle.s4_ref_fwd_omp(xh[:, :256], hp["a_real"], hp["a_imag"], hp["B"], hp["C"], hp["D"], threads=th)
+        t2 = time.perf_counter()
+        yo = oracle.s4_ref_fwd_omp(xh, hp["a_real"], hp["a_imag"], hp["B"], hp["C"], hp["D"], threads=th)
+        t3 = time.perf_counter()
         cpu = dict(value=ls / (t1 - t0), unit="tokens/s", cores=1, kind="port",
                    sample=f"first {ls} of {L} steps of input set 0 (d_model {M}, N {N}): "
                           f"S4Block::forward_ssm restated op by op with the reference's per-op "
                           f"allocation (oracle/hx_oracle_ref.c), {t1 - t0:.2f} s",
-                   host=host_info(), bit_identical_to_oracle=bool(np.array_equal(yr, ref)))
+                   kind_note="(R) reference-faithful, 1 core",
+                   host=host_info(), bit_identical_to_oracle=bool(np.array_equal(yr, ref)),
+                   omp=dict(value=ls / (t3 - t2), unit="tokens/s", cores=th, seconds=round(t3 - t2, 3),
+                            kind_note="(O) projection and readout over OpenMP (oracle/hx_oracle_omp.c), "
+                                      "same sample",
+                            bit_identical_to_oracle=bool(np.array_equal(yo, ref))))
+    if not args.no_cpu and args.workload == "c4s4d":
+        # (O): the S4D recurrence in f32 over OpenMP (16-channel tasks) on the first 256 and 512
+        # channels of input set 0, full length; the cost is linear in channels
+        import oracle  # test/bench infrastructure only
+        th = oracle.max_threads()
+        hp = {k: v.cpu().numpy() for k, v in prm.items()}
+        got = {}
+        host = {n: (xs[0][:, :, :n].contiguous().cpu().numpy(),
+                    {k: np.ascontiguousarray(v[:n]) for k, v in hp.items()}) for n in (256, 512)}
+
+        def run_o(n):
+            got["y"] = oracle.s4d_complex_omp(host[n][0], **host[n][1], threads=th)
+
+        y_gpu = step(0)
+        torch.cuda.synchronize()
+        cpu = cpu_leg(run_o, (256, 512), M, L, "tokens/s", th,
+                      f"S4D f32 recurrence over OpenMP (oracle/hx_oracle_omp.c) on channels 0..255 and "
+                      f"0..511 of input set 0, all {L} steps", kind_note="(O) optimised, all host cores")
+        cpu["gpu_vs_cpu_normwise_err"] = norm_err(y_gpu[:, :, :512].cpu().numpy(), got["y"])
     print(json.dumps({
         "metric": "S4 recurrence tokens/s (config 4), 1 GPU", "value": L * 1e3 / ms, "unit": "tokens/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
@@ -361,10 +458,20 @@ def bench_c1(args, dev):
             oracle.r_mamba_mlp(X, Wg, bg, Wo, bo)
             oracle.r_s4_forward_ssm(xs, ar, ai, B, C, D)
         t1 = time.perf_counter()
+        th = oracle.max_threads()
+        oracle.linear_omp(oracle.linear_omp(X, Wg, bg, 1, th), Wo, bo, 0, th)
+        t2 = time.perf_counter()
+        for _ in range(reps):
+            oracle.linear_omp(oracle.linear_omp(X, Wg, bg, 1, th), Wo, bo, 0, th)
+            oracle.s4_ref_fwd_omp(xs, ar, ai, B, C, D, threads=th)
+        t3 = time.perf_counter()
         cpu = dict(value=R * reps / (t1 - t0), unit="tokens/s", cores=1, kind="port",
                    sample=f"{reps} repetitions of both config-1 forwards in the reference's "
                           f"execution shape (oracle/hx_oracle_ref.c), {t1 - t0:.2f} s",
-                   host=host_info())
+                   kind_note="(R) reference-faithful, 1 core", host=host_info(),
+                   omp=dict(value=R * reps / (t3 - t2), unit="tokens/s", cores=th, seconds=round(t3 - t2, 3),
+                            kind_note="(O) the same forwards over OpenMP (oracle/hx_oracle_omp.c), "
+                                      f"{reps} repetitions"))
     print(json.dumps({
         "metric": "config-1 forwards (exported MambaBlock MLP [100, 64] + S4Block::forward_ssm "
                   "[64, 100]) tokens/s, 1 GPU",
@@ -402,10 +509,41 @@ def bench_lm(args, dev):
             + 2 * tokens * m.vocab * d
         workload = "byte LM prefill, 12 x (RMSNorm + Mamba) d_model 512, batch 16 x L 8192"
         extra = {"tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_flops": flops}
+        extra["timing"] = dict(LAST_TIMING)
+        if not args.no_cpu:
+            # (O): the LM over OpenMP (f32 throughout) on sequence 0 of token set 0 at two
+            # prefix lengths; (R): the reference's Linear execution shape, one thread, at two
+            # short prefixes; both extrapolated linearly in tokens to the step's 16 x 8192
+            import oracle  # test/bench infrastructure only
+            th = oracle.max_threads()
+            P = m.host_params()
+            t0 = toks[0][:1].cpu().numpy()
+            got = {}
+
+            def run_o(n):
+                got["lg"] = oracle.lm_prefill(t0[:, :n], P, m.dt_rank, m.eps, bf16=False, impl="omp",
+                                              threads=th)[0]
+
+            def run_r(n):
+                oracle.lm_prefill(t0[:, :n], P, m.dt_rank, m.eps, bf16=False, impl="ref")
+
+            no, nr = (1024, 2048), (16, 48)
+            cpu = cpu_leg(run_o, no, tokens, tokens, "tokens/s", th,
+                          f"OpenMP LM (oracle/hx_oracle_omp.c, f32) on sequence 0 of token set 0, "
+                          f"prefixes of {no[0]} and {no[1]} tokens", kind_note="(O) optimised, all host cores")
+            g, _ = m.prefill(toks[0][:1, :no[-1]].contiguous())
+            cpu["gpu_vs_cpu_normwise_err"] = norm_err(g.cpu().numpy(), got["lg"])
+            cpu["reference_shape"] = cpu_leg(
+                run_r, nr, tokens, tokens, "tokens/s", 1,
+                f"the LM with the reference's Linear execution shape (oracle/hx_oracle_ref.c), one "
+                f"thread, on sequence 0 of token set 0, prefixes of {nr[0]} and {nr[1]} tokens",
+                warm=False, kind_note="(R) reference-faithful, 1 core, linearly extrapolated")
+            extra["cpu_baseline"] = cpu
     else:
         bt = 256
         pre = torch.randint(0, 256, (bt, 64), generator=gen, device=dev, dtype=torch.int32)
         _, state = m.prefill(pre)
+        saved = [(a.clone(), c.clone()) for a, c in state]  # the state the timed steps start from
         toks = [torch.randint(0, 256, (bt,), generator=gen, device=dev, dtype=torch.int32)
                 for _ in range(4)]
         graph_step = m.decode_graph(state)  # the step captured as a HIP graph
@@ -417,8 +555,27 @@ def bench_lm(args, dev):
         ms = time_steps(step, 4, steps, args.warmup)
         tokens = bt
         workload = "byte LM recurrent decode step (HIP graph), 12 layers d_model 512, batch 256"
-        extra = {}
-    extra["timing"] = dict(LAST_TIMING)
+        extra = {"timing": dict(LAST_TIMING)}
+        if not args.no_cpu:
+            # (O): one decode step of all 256 sequences over OpenMP (f32 throughout) from the
+            # state the timed steps start from (the 64-token prefill's, copied to the host)
+            import oracle  # test/bench infrastructure only
+            th = oracle.max_threads()
+            P = m.host_params()
+            st_h = [(a.cpu().numpy(), c.cpu().numpy()) for a, c in saved]
+            t0 = toks[0].cpu().numpy()
+            got = {}
+
+            def run_o(n):
+                got["lg"] = oracle.lm_decode_step(t0[:n], P, [(a[:n], c[:n]) for a, c in st_h], m.dt_rank,
+                                                  m.eps, bf16=False, impl="omp", threads=th)[0]
+
+            cpu = cpu_leg(run_o, (bt,), bt, bt, "tokens/s", th,
+                          f"one OpenMP decode step (oracle/hx_oracle_omp.c, f32) of all {bt} sequences "
+                          f"from the timed steps' starting state", kind_note="(O) optimised, all host cores")
+            g = m.decode_step(toks[0], [(a.clone(), c.clone()) for a, c in saved])
+            cpu["gpu_vs_cpu_normwise_err"] = norm_err(g.cpu().numpy(), got["lg"])
+            extra["cpu_baseline"] = cpu
     rec = {
         "metric": ("byte LM prefill tokens/s (config 5), 1 GPU" if args.workload == "c5"
                    else "byte LM decode tokens/s (config 5, one step at batch 256), 1 GPU"),
@@ -506,6 +663,30 @@ def main():
 
     cpu = None
     parity = None
+    if not args.no_cpu and args.workload == "c4":
+        # (O): the OpenMP scan (16-channel tasks, oracle/hx_oracle_omp.c) on the first 256 and 512
+        # channels of input set 0 over the full 65536 steps; the cost is linear in channels
+        import oracle  # test/bench infrastructure only
+        th = oracle.max_threads()
+        step(0)
+        torch.cuda.synchronize()
+        got, x = {}, sets[0]
+        host = {n: {k: v.contiguous().cpu().numpy() for k, v in
+                    dict(u=x["u"][:, :, :n], delta=x["delta"][:, :, :n], z=x["z"][:, :, :n],
+                         A=x["A"][:n], D=x["D"][:n], B=x["B"], C=x["C"]).items()}
+                for n in (256, 512)}
+
+        def run_o(n):
+            got["y"] = oracle.selective_scan_omp(**host[n], threads=th)
+
+        cpu = cpu_leg(run_o, (256, 512), dim, tokens, "tokens/s", th,
+                      f"OpenMP scan on channels 0..255 and 0..511 of input set 0, all {L} steps",
+                      kind_note="(O) optimised, all host cores",
+                      note="no reference implementation of the selective scan exists "
+                           "(crates/nn/src/ssm.rs:474-483 delegates to the S4 recurrence): the "
+                           "port restates the textbook scan with the reference's discretisation")
+        g = outs[0][:, :, :512].float().cpu().numpy()
+        cpu["gpu_vs_cpu_normwise_err"] = norm_err(g, got["y"])
     if not args.no_cpu and args.workload in ("c2", "c2bf16"):
         step(0)
         torch.cuda.synchronize()
@@ -515,6 +696,19 @@ def main():
         r = ref.astype(np.float64)
         floor = 1e-3 * np.abs(r).max()
         parity = float((np.abs(g - r) / np.maximum(np.abs(r), floor)).max())
+
+    copy_ceiling = None
+    if args.workload in ("c2", "c2bf16"):
+        # the measured HBM ceiling beside the 8 TB/s spec: a plain device copy (read + write) of
+        # two 512 MiB buffers in rotation, timed the same way
+        n = 512 * 2**20 // 4
+        src = [torch.randn(n, device=dev) for _ in range(2)]
+        dst = [torch.empty_like(v) for v in src]
+        cms = time_steps(lambda i: dst[i].copy_(src[i]), 2, 20, 5, settle_s=0.05)
+        cgbs = 2 * n * 4 / (cms * 1e-3) / 1e9
+        copy_ceiling = {"gbs": cgbs, "frac_of_8TBs": cgbs / PEAK_HBM_GBS, "bytes_per_step": 2 * n * 4,
+                        "scan_frac_of_copy": achieved / cgbs}
+        del src, dst
 
     traffic = None
     issue = None
@@ -564,6 +758,7 @@ def main():
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "algorithmic_bytes": nbytes, "kernel_ms": ms},
         "issue_roofline": issue,
+        "copy_ceiling": copy_ceiling,
         "timing": timing,
         "cpu_baseline": cpu,
         "parity_max_rel_err": parity,

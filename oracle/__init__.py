@@ -88,7 +88,13 @@ def lib() -> ctypes.CDLL:
             "oracle_selective_scan_f64": [_i64, _i64, _i64, _i64, _int] + [_p] * 11,
             "oracle_selective_state_update": [_i64, _i64, _i64, _int] + [_p] * 10,
             "oracle_s4d_complex": [_i64, _i64, _i64, _i64] + [_p] * 10,
-            "oracle_selective_scan_omp": [_i64, _i64, _i64, _i64, _int] + [_p] * 9 + [_int],
+            "oracle_selective_scan_omp": [_i64, _i64, _i64, _i64, _int] + [_p] * 11 + [_int],
+            "oracle_selective_state_update_omp": [_i64, _i64, _i64, _int] + [_p] * 10 + [_int],
+            "oracle_linear_omp": [_i64, _i64, _i64, _p, _p, _p, _int, _p, _p, _int],
+            "oracle_conv1d_silu_omp": [_i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _int],
+            "oracle_rmsnorm_omp": [_i64, _i64, _p, _p, _f, _p, _int],
+            "oracle_s4d_complex_omp": [_i64, _i64, _i64, _i64] + [_p] * 10 + [_int],
+            "oracle_r_linear": [_i64, _i64, _i64, _p, _p, _p, _p],
             "oracle_s4_ref_fwd_omp": [_i64, _i64, _i64, _f] + [_p] * 10 + [_int],
             "oracle_max_threads": [],
             "oracle_conv1d_silu": [_i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
@@ -234,15 +240,121 @@ def selective_state_update(state, u, delta, A, B, C, D=None, z=None, dt_bias=Non
     return out, state
 
 
-def selective_scan_omp(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_softplus=True, threads=0):
-    u, delta, A, B, C, D, z, dt_bias = map(_f32, (u, delta, A, B, C, D, z, dt_bias))
+def selective_scan_omp(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_softplus=True,
+                       init_state=None, return_last_state=False, threads=0):
+    """selective_scan's values bit for bit, (batch, 16-channel block) tasks over threads."""
+    u, delta, A, B, C, D, z, dt_bias, init_state = map(_f32, (u, delta, A, B, C, D, z, dt_bias, init_state))
     Bt, L, Dd = u.shape
     N = A.shape[1]
+    assert N <= 256
     out = np.empty((Bt, L, Dd), np.float32)
+    last = np.empty((Bt, Dd, N), np.float32) if return_last_state else None
     lib().oracle_selective_scan_omp(Bt, L, Dd, N, int(bool(delta_softplus)), _ptr(u), _ptr(delta),
                                     _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(dt_bias),
-                                    _ptr(out), int(threads))
-    return out
+                                    _ptr(out), _ptr(init_state), _ptr(last), int(threads))
+    return (out, last) if return_last_state else out
+
+
+def selective_state_update_omp(state, u, delta, A, B, C, D=None, z=None, dt_bias=None,
+                               delta_softplus=True, threads=0):
+    """selective_state_update over threads; returns (out [Bt, Dd], new_state [Bt, Dd, N])."""
+    state = np.array(state, dtype=np.float32, copy=True)
+    u, delta, A, B, C, D, z, dt_bias = map(_f32, (u, delta, A, B, C, D, z, dt_bias))
+    Bt, Dd = u.shape
+    N = A.shape[1]
+    assert N <= 256
+    out = np.empty((Bt, Dd), np.float32)
+    lib().oracle_selective_state_update_omp(Bt, Dd, N, int(bool(delta_softplus)), _ptr(state), _ptr(u),
+                                            _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z),
+                                            _ptr(dt_bias), _ptr(out), int(threads))
+    return out, state
+
+
+def linear_omp(X, W, bias=None, act=0, threads=0):
+    """linear's values bit for bit: a blocked product over a packed W^T (hx_oracle_omp.c)."""
+    X, W, bias = _f32(X), _f32(W), _f32(bias)
+    R, IN = X.shape
+    OUT = W.shape[0]
+    Y = np.empty((R, OUT), np.float32)
+    Wt = np.empty((IN, OUT), np.float32)
+    lib().oracle_linear_omp(R, IN, OUT, _ptr(X), _ptr(W), _ptr(bias), act, _ptr(Y), _ptr(Wt), int(threads))
+    return Y
+
+
+def r_linear(X, W, bias=None):
+    """Linear::forward in the reference's execution shape (transpose copy, ijk matmul, broadcast
+    bias add, hx_oracle_ref.c); linear's values bit for bit."""
+    X, W, bias = _f32(X), _f32(W), _f32(bias)
+    R, IN = X.shape
+    OUT = W.shape[0]
+    Y = np.empty((R, OUT), np.float32)
+    lib().oracle_r_linear(R, IN, OUT, _ptr(X), _ptr(W), _ptr(bias), _ptr(Y))
+    return Y
+
+
+def conv1d_silu_omp(x, w, bias=None, threads=0):
+    """conv1d_silu's values bit for bit, rows over threads."""
+    x = np.asarray(x, np.float32)
+    Bt, L, Dd = x.shape
+    xs = np.ascontiguousarray(x)
+    w, bias = _f32(w), _f32(bias)
+    y = np.empty((Bt, L, Dd), np.float32)
+    lib().oracle_conv1d_silu_omp(Bt, L, Dd, w.shape[1], _ptr(xs), Dd, _ptr(w), _ptr(bias), _ptr(y),
+                                 int(threads))
+    return y
+
+
+def rmsnorm_omp(X, w, eps, threads=0):
+    """rmsnorm's values bit for bit, rows over threads."""
+    X, w = _f32(X), _f32(w)
+    R, Dm = X.shape
+    Y = np.empty_like(X)
+    lib().oracle_rmsnorm_omp(R, Dm, _ptr(X), _ptr(w), eps, _ptr(Y), int(threads))
+    return Y
+
+
+def s4d_complex_omp(x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D=None, threads=0):
+    """s4d_complex in f32 arithmetic over threads (within rounding of the f64 checker)."""
+    x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D = map(_f32, (x, dt, a_re, a_im, B_re, B_im, C_re, C_im, D))
+    Bt, L, Dd = x.shape
+    N = a_re.shape[1]
+    assert N <= 256
+    y = np.empty((Bt, L, Dd), np.float32)
+    lib().oracle_s4d_complex_omp(Bt, L, Dd, N, _ptr(x), _ptr(dt), _ptr(a_re), _ptr(a_im), _ptr(B_re),
+                                 _ptr(B_im), _ptr(C_re), _ptr(C_im), _ptr(D), _ptr(y), int(threads))
+    return y
+
+
+class _Prims:
+    """The primitives a composition (mamba_block, the byte LM) runs on.
+    impl "seq": the sequential C restatement; "omp": hx_oracle_omp.c over `threads` threads (same
+    values); "ref": Linear in the reference's execution shape (hx_oracle_ref.c), the rest
+    sequential (the reference has no conv, scan or norm kernels of its own to time)."""
+
+    def __init__(self, impl="seq", threads=0):
+        assert impl in ("seq", "omp", "ref"), impl
+        self.impl, self.threads = impl, threads
+
+    def linear(self, X, W):
+        if self.impl == "omp":
+            return linear_omp(X, W, threads=self.threads)
+        return r_linear(X, W) if self.impl == "ref" else linear(X, W)
+
+    def conv1d_silu(self, x, w, b):
+        return conv1d_silu_omp(x, w, b, self.threads) if self.impl == "omp" else conv1d_silu(x, w, b)
+
+    def rmsnorm(self, X, w, eps):
+        return rmsnorm_omp(X, w, eps, self.threads) if self.impl == "omp" else rmsnorm(X, w, eps)
+
+    def scan(self, *a, **k):
+        if self.impl == "omp":
+            return selective_scan_omp(*a, **k, threads=self.threads)
+        return selective_scan(*a, **k)
+
+    def state_update(self, *a, **k):
+        if self.impl == "omp":
+            return selective_state_update_omp(*a, **k, threads=self.threads)
+        return selective_state_update(*a, **k)
 
 
 def r_s4_forward_ssm(x, a_real, a_imag, B, C, D, delta=None, lam=None, dt=0.1):
@@ -305,31 +417,34 @@ def bf16_round(a):
 
 
 def mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, dt_rank, bf16=True,
-                round_out=True, return_state=False):
+                round_out=True, return_state=False, impl="seq", threads=0):
     """Mamba block forward: x [Bt, L, d_model] -> [Bt, L, d_model].
     in_proj -> (x | z); SiLU(conv1d(x)); x_proj -> (dt_lo | B | C); dt = dt_lo . w_dt^T;
     selective_scan(softplus(dt + dt_bias)); out_proj. Every intermediate the GPU stores in bf16 is
     rounded to bf16 here too (``bf16=True``); arithmetic is f32. ``round_out=False`` leaves the
     out_proj result in f32 (the layer form, which adds it to an f32 residual stream).
     ``return_state``: also return the decode hand-off (scan last state [Bt, d_inner, N], conv
-    window [Bt, d_conv-1, d_inner] = the last d_conv-1 conv inputs)."""
+    window [Bt, d_conv-1, d_inner] = the last d_conv-1 conv inputs). ``impl``/``threads`` pick
+    the primitives (_Prims: sequential, OpenMP or the reference's Linear); the values do not
+    depend on them."""
+    ops = _Prims(impl, threads)
     rnd = bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
     Bt, L, dm = x.shape
     di = w_dt.shape[0]
     N = A.shape[1]
     K = conv_w.shape[1]
     X = rnd(x).reshape(Bt * L, dm)
-    xz = linear(X, rnd(w_in))
+    xz = ops.linear(X, rnd(w_in))
     xp = rnd(xz[:, :di]).reshape(Bt, L, di)
     z = rnd(xz[:, di:]).reshape(Bt, L, di)
-    xc = rnd(conv1d_silu(xp, conv_w, conv_b))
-    dbc = linear(xc.reshape(Bt * L, di), rnd(w_x))
+    xc = rnd(ops.conv1d_silu(xp, conv_w, conv_b))
+    dbc = ops.linear(xc.reshape(Bt * L, di), rnd(w_x))
     dtlo = rnd(dbc[:, :dt_rank])
     Bm = rnd(dbc[:, dt_rank:dt_rank + N]).reshape(Bt, L, N)
     Cm = rnd(dbc[:, dt_rank + N:]).reshape(Bt, L, N)
-    dt = rnd(linear(dtlo, rnd(w_dt))).reshape(Bt, L, di)
-    y, last = selective_scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True, return_last_state=True)
-    out = linear(rnd(y).reshape(Bt * L, di), rnd(w_out))
+    dt = rnd(ops.linear(dtlo, rnd(w_dt))).reshape(Bt, L, di)
+    y, last = ops.scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True, return_last_state=True)
+    out = ops.linear(rnd(y).reshape(Bt * L, di), rnd(w_out))
     out = (rnd(out) if round_out else out).reshape(Bt, L, dm)
     if not return_state:
         return out
@@ -358,54 +473,62 @@ def conv1d_step(x, w, bias, state):
     return xc, new_state
 
 
-def mamba_layer_decode(resid, p, state, dt_rank, eps):
+def mamba_layer_decode(resid, p, state, dt_rank, eps, bf16=True, impl="seq", threads=0):
     """One decode step of a pre-norm layer; resid [Bt, d_model] f32. Returns (resid, state)."""
-    rnd = bf16_round
+    ops = _Prims(impl, threads)
+    rnd = bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
     ssm_st, conv_st = state
     di = p["w_dt"].shape[0]
     N = p["A"].shape[1]
-    xn = rnd(rmsnorm(resid, p["norm_w"], eps))
-    xz = linear(xn, rnd(p["w_in"]))
+    xn = rnd(ops.rmsnorm(resid, p["norm_w"], eps))
+    xz = ops.linear(xn, rnd(p["w_in"]))
     xp, z = rnd(xz[:, :di]), rnd(xz[:, di:])
     xc, conv_st = conv1d_step(xp, p["conv_w"], p["conv_b"], conv_st)
     xc = rnd(xc)
-    dbc = linear(xc, rnd(p["w_x"]))
+    dbc = ops.linear(xc, rnd(p["w_x"]))
     dtlo = rnd(dbc[:, :dt_rank])
     Bv, Cv = rnd(dbc[:, dt_rank:dt_rank + N]), rnd(dbc[:, dt_rank + N:])
-    dt = rnd(linear(dtlo, rnd(p["w_dt"])))
-    y, ssm_st = selective_state_update(ssm_st, xc, dt, p["A"], Bv, Cv, p["D"], z, p["dt_bias"], True)
-    resid = (resid + linear(rnd(y), rnd(p["w_out"]))).astype(np.float32)
+    dt = rnd(ops.linear(dtlo, rnd(p["w_dt"])))
+    y, ssm_st = ops.state_update(ssm_st, xc, dt, p["A"], Bv, Cv, p["D"], z, p["dt_bias"], True)
+    resid = (resid + ops.linear(rnd(y), rnd(p["w_out"]))).astype(np.float32)
     return resid, (ssm_st, conv_st)
 
 
-def lm_head(x, params, eps):
+def lm_head(x, params, eps, bf16=True, impl="seq", threads=0):
+    ops = _Prims(impl, threads)
+    rnd = bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
     shp = x.shape
-    xn = bf16_round(rmsnorm(x.reshape(-1, shp[-1]), params["norm_f"], eps))
-    return linear(xn, bf16_round(params["w_head"])).reshape(*shp[:-1], -1)
+    xn = rnd(ops.rmsnorm(x.reshape(-1, shp[-1]), params["norm_f"], eps))
+    return ops.linear(xn, rnd(params["w_head"])).reshape(*shp[:-1], -1)
 
 
-def lm_prefill(tokens, params, dt_rank, eps=1e-5):
-    """Byte LM prefill: tokens [Bt, L] int -> (logits [Bt, L, vocab] f32, per-layer state)."""
+def lm_prefill(tokens, params, dt_rank, eps=1e-5, bf16=True, impl="seq", threads=0):
+    """Byte LM prefill: tokens [Bt, L] int -> (logits [Bt, L, vocab] f32, per-layer state).
+    bf16=False keeps every intermediate in f32 (the CPU timing legs); impl/threads as in
+    mamba_block."""
+    rnd = bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
+    ops = _Prims(impl, threads)
     x = np.asarray(params["embed"], np.float32)[np.asarray(tokens)]
     Bt, L, dm = x.shape
     states = []
     for p in params["layers"]:
-        xn = bf16_round(rmsnorm(x.reshape(-1, dm), p["norm_w"], eps)).reshape(Bt, L, dm)
+        xn = rnd(ops.rmsnorm(x.reshape(-1, dm), p["norm_w"], eps)).reshape(Bt, L, dm)
         blk = {k: p[k] for k in ("w_in", "conv_w", "conv_b", "w_x", "w_dt", "dt_bias", "A", "D", "w_out")}
-        out, last, conv = mamba_block(xn, **blk, dt_rank=dt_rank, round_out=False, return_state=True)
+        out, last, conv = mamba_block(xn, **blk, dt_rank=dt_rank, bf16=bf16, round_out=False,
+                                      return_state=True, impl=impl, threads=threads)
         x = (x + out).astype(np.float32)
         states.append((last, conv))
-    return lm_head(x, params, eps), states
+    return lm_head(x, params, eps, bf16, impl, threads), states
 
 
-def lm_decode_step(tokens, params, states, dt_rank, eps=1e-5):
+def lm_decode_step(tokens, params, states, dt_rank, eps=1e-5, bf16=True, impl="seq", threads=0):
     """One decode step: tokens [Bt] -> (logits [Bt, vocab], new per-layer states)."""
     x = np.asarray(params["embed"], np.float32)[np.asarray(tokens)]
     new = []
     for p, st in zip(params["layers"], states):
-        x, st = mamba_layer_decode(x, p, st, dt_rank, eps)
+        x, st = mamba_layer_decode(x, p, st, dt_rank, eps, bf16, impl, threads)
         new.append(st)
-    return lm_head(x, params, eps), new
+    return lm_head(x, params, eps, bf16, impl, threads), new
 
 
 # ------------------------------------------------------------------ independent float64 restatements

@@ -149,6 +149,15 @@ static float* r_linear(const float* X, const float* W, const float* bias, int64_
     return res;
 }
 
+/* Linear::forward in the reference's execution shape, exported for the block and LM timing
+ * legs: Y [R, OUT] = X . W^T (+ bias); same values as oracle_linear, bit for bit. */
+void oracle_r_linear(int64_t R, int64_t IN, int64_t OUT, const float* X, const float* W,
+                     const float* bias, float* Y) {
+    float* o = r_linear(X, W, bias, R, IN, OUT);
+    memcpy(Y, o, (size_t)(R * OUT) * sizeof(float));
+    free(o);
+}
+
 /* nn::MambaBlock::forward_mamba (lib.rs:888-906): Y = out_proj(silu(gate(X))). */
 void oracle_r_mamba_mlp(int64_t R, int64_t d_model, int64_t d_inner, const float* X,
                         const float* Wg, const float* bg, const float* Wo, const float* bo,

@@ -289,8 +289,71 @@ def test_scan_f32_f64_and_numpy_agree():
 
 
 def test_scan_omp_matches_serial():
+    # 33 channels: two full 16-channel tasks and a ragged one per batch row
     x = inputs(2, 64, 33, 16, 5)
     assert np.array_equal(oracle.selective_scan_omp(**x, threads=3), oracle.selective_scan(**x))
+    init = np.random.default_rng(6).standard_normal((2, 33, 16)).astype(F)
+    o, s = oracle.selective_scan_omp(**x, init_state=init, return_last_state=True, threads=4)
+    ro, rs = oracle.selective_scan(**x, init_state=init, return_last_state=True)
+    assert np.array_equal(o, ro) and np.array_equal(s, rs)
+    st = {k: (v[:, 0] if k in ("u", "delta", "z", "B", "C") else v) for k, v in x.items()}
+    so, ss = oracle.selective_state_update_omp(init, **st, threads=2)
+    ro, rs = oracle.selective_state_update(init, **st)
+    assert np.array_equal(so, ro) and np.array_equal(ss, rs)
+
+
+def test_omp_linear_conv_norm_are_bit_identical_to_the_serial_restatement():
+    """The blocked product (full 4x64 tiles and ragged edges, bias, silu), the row-parallel conv
+    and RMSNorm give the sequential functions' values exactly, as do the reference-shaped Linear
+    and the compositions built on each set of primitives."""
+    rng = np.random.default_rng(60)
+    for R, IN, OUT in ((8, 96, 128), (7, 33, 70), (1, 5, 3), (130, 64, 200)):
+        X = rng.standard_normal((R, IN)).astype(F)
+        W = rng.standard_normal((OUT, IN)).astype(F)
+        b = rng.standard_normal(OUT).astype(F)
+        for bias, act in ((None, 0), (b, 0), (b, 1)):
+            want = oracle.linear(X, W, bias, act)
+            assert np.array_equal(oracle.linear_omp(X, W, bias, act, threads=3), want), (R, IN, OUT, act)
+        assert np.array_equal(oracle.r_linear(X, W, b), oracle.linear(X, W, b))
+    x = rng.standard_normal((3, 20, 37)).astype(F)
+    w = rng.standard_normal((37, 4)).astype(F)
+    cb = rng.standard_normal(37).astype(F)
+    assert np.array_equal(oracle.conv1d_silu_omp(x, w, cb, threads=3), oracle.conv1d_silu(x, w, cb))
+    X = rng.standard_normal((9, 40)).astype(F)
+    g = rng.standard_normal(40).astype(F)
+    assert np.array_equal(oracle.rmsnorm_omp(X, g, 1e-5, threads=2), oracle.rmsnorm(X, g, 1e-5))
+    from tests.util import block_inputs, lm_params
+    p = block_inputs(2, 24, 16, 32, 16, 8, 4, seed=61)
+    want = oracle.mamba_block(**p, dt_rank=8, bf16=False)
+    assert np.array_equal(oracle.mamba_block(**p, dt_rank=8, bf16=False, impl="omp", threads=3), want)
+    assert np.array_equal(oracle.mamba_block(**p, dt_rank=8, bf16=False, impl="ref"), want)
+    P = lm_params(2, 32, 64, 16, 8, 4, 256, seed=62)
+    tok = np.random.default_rng(63).integers(0, 256, (3, 10))
+    lg, st = oracle.lm_prefill(tok[:, :9], P, 8, bf16=False)
+    lo, so = oracle.lm_prefill(tok[:, :9], P, 8, bf16=False, impl="omp", threads=3)
+    assert np.array_equal(lo, lg)
+    dl, _ = oracle.lm_decode_step(tok[:, 9], P, st, 8, bf16=False)
+    do, _ = oracle.lm_decode_step(tok[:, 9], P, so, 8, bf16=False, impl="omp", threads=2)
+    assert np.array_equal(do, dl)
+
+
+def test_s4d_complex_omp_f32_within_rounding_of_the_f64_checker():
+    rng = np.random.default_rng(64)
+    Bt, L, Dd, N = 2, 700, 37, 16
+    x = rng.standard_normal((Bt, L, Dd)).astype(F)
+    prm = dict(dt=np.full(Dd, 0.1, F), a_re=np.full((Dd, N), -0.5, F),
+               a_im=np.tile(np.pi * np.arange(N, dtype=F), (Dd, 1)),
+               B_re=(rng.standard_normal((Dd, N)) * 0.1).astype(F),
+               B_im=(rng.standard_normal((Dd, N)) * 0.1).astype(F),
+               C_re=(rng.standard_normal((Dd, N)) * 0.1).astype(F),
+               C_im=(rng.standard_normal((Dd, N)) * 0.1).astype(F),
+               D=rng.standard_normal(Dd).astype(F))
+    ref = oracle.s4d_complex(x, **prm)
+    got = oracle.s4d_complex_omp(x, **prm, threads=3)
+    assert got.dtype == np.float32 and norm_err(got, ref) < 1e-5
+    # a dropped imaginary coupling is far outside that bar
+    bad = oracle.s4d_complex_omp(x, **dict(prm, C_im=np.zeros_like(prm["C_im"])), threads=3)
+    assert norm_err(bad, ref) > 1e-2
 
 
 def test_scan_softplus_threshold():
