@@ -2,6 +2,7 @@
 // Host code only (no kernels): shapes are checked here with the reference's error variants,
 // then every computation is one or more hx_* calls.
 #include "helix/helix.hpp"
+#include "ndlayout.hpp"
 
 #include <cmath>
 #include <cstring>
@@ -165,14 +166,36 @@ HipTensor HipTensor::to_storage(Storage st) const {
 HipTensor HipTensor::reshape(Shape s) const {
     if (s.numel() != numel()) shape_mismatch({numel()}, {s.numel()});
     HipTensor t = *this;
+    // lib.rs:94-113: to_shape(..).to_owned() keeps the strides a copy-free view has, else row-major
+    std::vector<int64_t> st = ndlayout::reshaped(shape_.as_slice(), ref_strides(), s.as_slice());
     t.shape_ = std::move(s);
+    t.strides_.clear();
+    t.set_ref_strides(std::move(st));
     return t;
 }
 
 HipTensor HipTensor::clone() const {
     HipTensor t(shape_, storage_, device_);
     if (numel()) check(hx_memcpy_d2d(t.data(), data(), nbytes(), nullptr), "hx_memcpy_d2d");
+    t.strides_ = strides_;  // an ndarray clone keeps its strides
     return t;
+}
+
+std::vector<int64_t> HipTensor::ref_strides() const {
+    return strides_.empty() ? ndlayout::c_strides(shape_.as_slice()) : strides_;
+}
+
+void HipTensor::set_ref_strides(std::vector<int64_t> strides) {
+    if (strides.size() != shape_.ndim())
+        throw TensorError(ErrorKind::InvalidInput, "strides of rank " + std::to_string(strides.size()) +
+                                                       " for a tensor of rank " +
+                                                       std::to_string(shape_.ndim()));
+    if (strides == ndlayout::c_strides(shape_.as_slice())) strides.clear();
+    strides_ = std::move(strides);
+}
+
+bool HipTensor::is_contiguous() const {
+    return strides_.empty() || ndlayout::is_standard_layout(shape_.as_slice(), strides_);
 }
 
 // ----------------------------------------------------------------------------- nn

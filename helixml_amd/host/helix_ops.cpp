@@ -10,6 +10,7 @@
 #include "helix/helix.hpp"
 #include "helix_detail.h"
 #include "helix_hip.h"
+#include "ndlayout.hpp"
 
 namespace helix {
 
@@ -23,6 +24,14 @@ namespace {
 void need_f32(const HipTensor& t) {
     if (t.storage() != Storage::F32)
         throw TensorError(ErrorKind::DTypeMismatch, "DType mismatch: expected \"F32 storage\", got \"BF16\"");
+}
+
+// cat, stack and broadcast_to read `data.as_slice().unwrap()`, which panics unless the array is
+// in standard layout (e.g. after a transpose of two axes longer than 1)
+void need_standard_layout(const HipTensor& t, const char* op) {
+    if (!t.is_contiguous())
+        unsupported(std::string(op) + " of a tensor that is not in standard layout (the reference's "
+                    "as_slice().unwrap() panics)");
 }
 
 std::vector<int64_t> row_major_strides(const std::vector<size_t>& dims) {
@@ -51,6 +60,8 @@ HipTensor binary(const HipTensor& a, const HipTensor& b, int op) {
     check(hx_binary_f32(op, (int64_t)a.numel(), (const float*)a.data(), (const float*)b.data(),
                         (float*)y.data(), nullptr),
           "hx_binary_f32");
+    // &a + &b collects by the Zip's layout preference (C or F order)
+    y.set_ref_strides(ndlayout::collect(a.shape().as_slice(), {a.ref_strides(), b.ref_strides()}));
     return y;
 }
 
@@ -59,6 +70,7 @@ HipTensor unary(const HipTensor& x, int op, float s = 0.0f) {
     HipTensor y(x.shape(), Storage::F32, 0);
     check(hx_unary_f32(op, (int64_t)x.numel(), (const float*)x.data(), s, (float*)y.data(), nullptr),
           "hx_unary_f32");
+    y.set_ref_strides(x.ref_strides());  // mapv / map_inplace keep the strides
     return y;
 }
 
@@ -150,11 +162,26 @@ HipTensor HipTensor::mean(const std::vector<size_t>* dims, bool /*keepdim*/) con
         nd.erase(nd.begin() + (long)ax);
         HipTensor y(Shape(nd), Storage::F32, device_);
         // ndarray sums a lane with its unrolled fold when the axis is the array's minimum-stride
-        // axis, i.e. the last one of a row-major array
-        const int lane = ax + 1 == d.size() ? 1 : 0;
-        check(hx_mean_axis_f32((int64_t)outer, (int64_t)d[ax], (int64_t)inner, lane,
-                               (const float*)cur.data(), (float*)y.data(), nullptr),
-              "hx_mean_axis_f32");
+        // axis with contiguous lanes (the last axis of a row-major array), else in axis order
+        const std::vector<int64_t> cs = cur.ref_strides();
+        const int lane = ndlayout::sums_with_lane_fold(d, cs, ax) ? 1 : 0;
+        if (lane && inner > 1) {
+            // the reference's lanes are contiguous along an axis that is not last on the device:
+            // bring that axis last ([outer, inner, len]) and fold the rows
+            const size_t len = d[ax];
+            HipTensor tmp(Shape({outer, inner, len}), Storage::F32, device_);
+            strided_copy({outer, inner, len}, (const float*)cur.data(),
+                         {(int64_t)(len * inner), 1, (int64_t)inner}, (float*)tmp.data(),
+                         row_major_strides({outer, inner, len}));
+            check(hx_mean_axis_f32((int64_t)(outer * inner), (int64_t)len, 1, 1,
+                                   (const float*)tmp.data(), (float*)y.data(), nullptr),
+                  "hx_mean_axis_f32");
+        } else {
+            check(hx_mean_axis_f32((int64_t)outer, (int64_t)d[ax], (int64_t)inner, lane,
+                                   (const float*)cur.data(), (float*)y.data(), nullptr),
+                  "hx_mean_axis_f32");
+        }
+        y.set_ref_strides(ndlayout::mean_axis_result(d, cs, ax));
         cur = y;
     }
     return order.empty() ? clone() : cur;
@@ -168,6 +195,7 @@ HipTensor HipTensor::broadcast_to(const Shape& target) const {
     const size_t sn = s.size(), tn = t.size();
     if (sn > tn) shape_mismatch({tn}, {sn});  // lib.rs:1356-1361
     if (shape_ == target) return clone();      // lib.rs:1364-1366
+    need_standard_layout(*this, "broadcast_to");
     std::vector<size_t> padded(tn - sn, 1);
     padded.insert(padded.end(), s.begin(), s.end());
     for (size_t j = 0; j < tn; ++j)  // lib.rs:1373-1380
@@ -208,6 +236,7 @@ HipTensor HipTensor::transpose(size_t d0, size_t d1) const {
     std::swap(src[d0], src[d1]);
     HipTensor y(Shape(nd), Storage::F32, device_);
     if (y.numel()) strided_copy(nd, (const float*)data(), src, (float*)y.data(), row_major_strides(nd));
+    y.set_ref_strides(ndlayout::transposed(ref_strides(), d0, d1));  // permuted_axes + to_owned
     return y;
 }
 
@@ -224,6 +253,7 @@ HipTensor HipTensor::slice(const std::vector<size_t>& start, const std::vector<s
     HipTensor y(Shape(nd), Storage::F32, device_);
     const float* base = (const float*)data() + start[0] * s[1] + start[1];
     strided_copy(nd, base, {(int64_t)s[1], 1}, (float*)y.data(), row_major_strides(nd));
+    y.set_ref_strides(ndlayout::owned(nd, ref_strides()));  // to_owned of the sliced view
     return y;
 }
 
@@ -243,6 +273,7 @@ HipTensor HipTensor::cat(const std::vector<HipTensor>& ts, size_t dim) {
     size_t total = 0;
     for (const HipTensor& t : ts) {
         need_f32(t);
+        need_standard_layout(t, "cat");  // lib.rs:233
         total += t.numel();
     }
     HipTensor y(Shape({total}), Storage::F32, ts[0].device_);
@@ -272,6 +303,7 @@ HipTensor HipTensor::stack(const std::vector<HipTensor>& ts, size_t dim) {
         // carries it)
         for (size_t k = 0; k < ts.size(); ++k) {
             need_f32(ts[k]);
+            need_standard_layout(ts[k], "stack");  // lib.rs:284, 301, 318
             if (each)
                 check(hx_memcpy_d2d((float*)y.data() + k * each, ts[k].data(), each * 4, nullptr),
                       "hx_memcpy_d2d");
@@ -286,6 +318,7 @@ HipTensor HipTensor::stack(const std::vector<HipTensor>& ts, size_t dim) {
     for (size_t i = dim; i < nd; ++i) inner *= f.dim(i);
     for (size_t k = 0; k < ts.size(); ++k) {
         need_f32(ts[k]);
+        need_standard_layout(ts[k], "stack");  // lib.rs:413
         if (!each) continue;
         strided_copy({outer, inner}, (const float*)ts[k].data(), {(int64_t)inner, 1},
                      (float*)y.data() + k * inner, {(int64_t)(ts.size() * inner), 1});

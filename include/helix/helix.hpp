@@ -111,7 +111,9 @@ private:
 };
 
 // A device tensor: the HipTensor a crates/backend-hip would define. Owns device memory
-// (hx_malloc/hx_free), row-major contiguous.
+// (hx_malloc/hx_free); the data are row-major contiguous. Beside them it records the strides the
+// reference's ndarray array would have (helixml_amd/host/ndlayout.hpp): a transpose keeps permuted
+// strides there, and mean's summation order and cat/stack/broadcast_to's failures follow them.
 class HipTensor {
 public:
     HipTensor() = default;
@@ -179,8 +181,15 @@ public:
     // and `dim` only places the count in the shape field; 0-D and >= 4-D inputs are placed by
     // the generic stack (lib.rs:390-467)
     static HipTensor stack(const std::vector<HipTensor>& ts, size_t dim);
-    HipTensor contiguous() const { return clone(); }  // device tensors are always row-major
-    bool is_contiguous() const { return true; }
+    // lib.rs:84-91: to_owned() keeps the array's memory order, so the copy keeps its strides
+    HipTensor contiguous() const { return clone(); }
+    // lib.rs:80-82: the reference array's standard (row-major) layout
+    bool is_contiguous() const;
+    // The reference array's strides, in elements (row-major unless set).
+    std::vector<int64_t> ref_strides() const;
+    // Metadata only: records the strides the reference's array has after the operation that made
+    // this tensor (row-major strides clear the record).
+    void set_ref_strides(std::vector<int64_t> strides);
 
 private:
     struct Buffer {
@@ -194,6 +203,7 @@ private:
     Shape shape_;
     Storage storage_ = Storage::F32;
     int device_ = 0;
+    std::vector<int64_t> strides_;  // the reference array's strides; empty = row-major
 };
 
 // ----------------------------------------------------------------------------- nn

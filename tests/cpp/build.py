@@ -15,7 +15,7 @@ EXE = HERE / "helix_host_tests"
 def build() -> Path:
     lib_dir = ROOT / "helixml_amd"
     ora_dir = ROOT / "oracle"
-    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", f"-I{ROOT / 'include'}",
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", f"-I{ROOT / 'include'}", f"-I{ROOT / 'helixml_amd' / 'host'}",
            str(HERE / "test_host.cpp"), "-o", str(EXE),
            f"-L{lib_dir}", "-lhelix_hip", f"-L{ora_dir}", "-l:liboracle.so",
            f"-Wl,-rpath,{lib_dir}", f"-Wl,-rpath,{ora_dir}",

@@ -18,6 +18,7 @@
 
 #include "helix/helix.hpp"
 #include "helix_hip.h"
+#include "ndlayout.hpp"
 
 extern "C" {
 void oracle_matmul(int64_t M, int64_t K, int64_t N, const float* A, const float* B, float* Y);
@@ -213,6 +214,52 @@ TEST_CPU(compute_graph_build_sort_and_cycle) {
     std::string msg;
     CHECK(throws_kind([&] { (void)g.topological_sort(); }, ErrorKind::InvalidInput, &msg));
     CHECK(msg.find("Circular dependency detected") != std::string::npos);
+}
+
+// ndarray 0.15's layout rules as the mirror restates them, on hand-derived cases
+TEST_CPU(ndarray_layout_rules) {
+    namespace L = helix::ndlayout;
+    using S = L::Strides;
+    // row-major [2, 3]: the last axis is the minimum-stride axis and folds its lanes
+    CHECK((L::c_strides({2, 3}) == S{3, 1}) && (L::f_strides({2, 3}) == S{1, 2}));
+    CHECK(L::min_stride_axis({2, 3}, {3, 1}) == 1);
+    CHECK(L::sums_with_lane_fold({2, 3}, {3, 1}, 1) && !L::sums_with_lane_fold({2, 3}, {3, 1}, 0));
+    // transpose of row-major [3, 2] -> [2, 3] with strides (1, 2): F order, contiguous in memory
+    // order, not standard; axis 0 now folds its lanes and axis 1 sums in order
+    const S t = L::transposed({2, 1}, 0, 1);
+    CHECK((t == S{1, 2}));
+    CHECK(L::is_contiguous({2, 3}, t) && !L::is_standard_layout({2, 3}, t));
+    CHECK(L::array_layout({2, 3}, t) == (L::kFOrder | L::kFPrefer));
+    CHECK(L::min_stride_axis({2, 3}, t) == 0);
+    CHECK(L::sums_with_lane_fold({2, 3}, t, 0) && !L::sums_with_lane_fold({2, 3}, t, 1));
+    // a length-1 axis carries any stride: [3, 1] -> [1, 3] stays standard
+    CHECK(L::is_standard_layout({1, 3}, L::transposed({1, 1}, 0, 1)));
+    // ties in |stride| go to the later axis
+    CHECK(L::min_stride_axis({3, 1}, {1, 1}) == 1 && L::min_stride_axis({3, 1}, {1, 3}) == 0);
+    // binary ops collect F only when the Zip prefers F: F + F -> F, F + C -> C (tendencies cancel)
+    CHECK((L::collect({2, 3}, {t, t}) == S{1, 2}));
+    CHECK((L::collect({2, 3}, {t, {3, 1}}) == S{3, 1}));
+    // 3-D: full reversal is F; swapping the outer two axes of [2, 3, 4] leaves only a C
+    // preference (last stride 1), and F + that prefers F (tendency -2 + 1)
+    const S f3 = L::transposed({12, 4, 1}, 0, 2);  // [4, 3, 2]
+    CHECK((f3 == S{1, 4, 12}) && L::array_layout({4, 3, 2}, f3) == (L::kFOrder | L::kFPrefer));
+    const S p3 = L::transposed({12, 4, 1}, 0, 1);  // [3, 2, 4] strides (4, 12, 1)
+    CHECK(L::array_layout({3, 2, 4}, p3) == L::kCPrefer);
+    CHECK((L::collect({3, 2, 4}, {p3, p3}) == L::c_strides({3, 2, 4})));
+    CHECK((L::collect({3, 2, 4}, {L::f_strides({3, 2, 4}), p3}) == L::f_strides({3, 2, 4})));
+    // mean_axis over the minimum-stride axis collects the remaining view: (4, 12) -> row-major
+    CHECK((L::mean_axis_result({4, 3, 2}, f3, 0) == S{2, 1}));
+    CHECK((L::mean_axis_result({2, 3}, t, 1) == S{1}));
+    // reshape: the same shape keeps F; [2, 3] F -> [6] needs a copy (row-major); C [2, 3] ->
+    // [3, 2] is a view; F [4, 6] -> [4, 2, 3] splits the outer axis as a view (1, 12, 4)
+    CHECK((L::reshaped({2, 3}, t, {2, 3}) == S{1, 2}));
+    CHECK((L::reshaped({2, 3}, t, {6}) == S{1}));
+    CHECK((L::reshaped({2, 3}, {3, 1}, {3, 2}) == S{2, 1}));
+    CHECK((L::reshaped({4, 6}, {1, 4}, {4, 2, 3}) == S{1, 12, 4}));
+    CHECK(L::is_contiguous({4, 2, 3}, {1, 12, 4}));
+    // to_owned of a sliced view keeps its strides only when it is contiguous in memory order
+    CHECK((L::owned({4, 2}, {1, 4}) == S{1, 4}));     // full columns of an F [4, n] array
+    CHECK((L::owned({3, 2}, {1, 4}) == S{2, 1}));     // partial columns: a row-major copy
 }
 
 TEST_CPU(validate_operation_rejects_handles_the_launch_would_overrun) {
@@ -623,6 +670,55 @@ TEST_GPU(hiptensor_shape_ops_and_mean) {
     CHECK(bits_equal(x.mean(&first).to_host(), r1));
     const std::vector<size_t> bad = {2};
     CHECK(throws_kind([&] { (void)x.mean(&bad); }, ErrorKind::InvalidDimension));
+}
+
+// A transposed tensor keeps the reference array's permuted strides: mean sums its axes in the
+// order ndarray uses for that layout, cat/stack/broadcast_to fail where the reference's
+// as_slice().unwrap() panics, and the operations that keep or drop the order do so.
+TEST_GPU(transposed_tensor_follows_the_reference_layout) {
+    const size_t R = 13, C = 11;  // both >= 9: the lane fold and the in-order sum differ
+    auto xv = randn(R * C, 81);
+    auto x = HipTensor::from_host(xv, Shape({R, C}));
+    std::vector<float> rows_fold(R), rows_seq(R), cols_fold(C), cols_seq(C);
+    oracle_mean_axis(R, C, 1, 1, xv.data(), rows_fold.data());  // each row of x, lane fold
+    oracle_mean_axis(R, C, 1, 0, xv.data(), rows_seq.data());   // each row of x, in order
+    oracle_mean_axis(1, R, C, 0, xv.data(), cols_seq.data());   // each column of x, in order
+    {
+        std::vector<float> xt(R * C);  // each column of x by the lane fold (x^T row-major)
+        for (size_t r = 0; r < R; ++r)
+            for (size_t c = 0; c < C; ++c) xt[c * R + r] = xv[r * C + c];
+        oracle_mean_axis(C, R, 1, 1, xt.data(), cols_fold.data());
+    }
+    CHECK(!bits_equal(rows_fold, rows_seq) && !bits_equal(cols_fold, cols_seq));
+    auto xT = x.transpose(0, 1);  // [C, R], strides (1, C) in the reference
+    CHECK(x.is_contiguous() && !xT.is_contiguous());
+    const std::vector<size_t> last = {1}, first = {0};
+    // over xT's last axis (x's columns): not the minimum-stride axis -> in order
+    CHECK(bits_equal(xT.mean(&last).to_host(), cols_seq));
+    // over xT's axis 0 (x's rows): the minimum-stride axis with contiguous lanes -> lane fold
+    CHECK(bits_equal(xT.mean(&first).to_host(), rows_fold));
+    // both axes, last first: in-order column means, then a 1-D lane fold
+    std::vector<float> all(1);
+    oracle_mean_axis(1, C, 1, 1, cols_seq.data(), all.data());
+    CHECK(bits_equal(xT.mean().to_host(), all));
+    // elementwise maps keep the order, F + F stays F, F + C collects row-major
+    CHECK(!xT.exp().is_contiguous() && !xT.mul(xT).is_contiguous());
+    auto mixed = xT.add(HipTensor::ones(Shape({C, R})));
+    CHECK(mixed.is_contiguous());
+    std::vector<float> mv = mixed.to_host(), mixed_rows(C);
+    oracle_mean_axis(C, R, 1, 1, mv.data(), mixed_rows.data());
+    CHECK(bits_equal(mixed.mean(&last).to_host(), mixed_rows));
+    // contiguous() is to_owned(): it keeps the order; a reshape that needs a copy drops it
+    CHECK(!xT.contiguous().is_contiguous());
+    CHECK(!xT.reshape(Shape({C, R})).is_contiguous() && xT.reshape(Shape({C * R})).is_contiguous());
+    // a slice of whole columns stays F; one of part of them is a row-major copy
+    CHECK(!xT.slice({0, 0}, {C, 2}).is_contiguous() && xT.slice({0, 0}, {3, 2}).is_contiguous());
+    // as_slice().unwrap() panics in the reference: stack, broadcast_to
+    CHECK(throws_kind([&] { (void)HipTensor::stack({xT, xT}, 0); }, ErrorKind::UnsupportedOperation));
+    CHECK(throws_kind([&] { (void)xT.broadcast_to(Shape({2, C, R})); }, ErrorKind::UnsupportedOperation));
+    CHECK((xT.broadcast_to(Shape({C, R})).shape() == Shape({C, R})));  // same shape: a clone
+    // a transpose of a length-1 axis stays standard
+    CHECK(HipTensor::ones(Shape({1, 5})).transpose(0, 1).is_contiguous());
 }
 
 TEST_GPU(matmul_vector_forms_and_rank_errors) {
