@@ -232,10 +232,8 @@ def bench_block(args, dev):
     stages = {
         "in_proj": lambda i: ssm.gemm_bf16(x2, prm["w_in"], splits=(di,)),
         "conv1d_silu": lambda i: ssm.conv1d_silu(xz[0].view(bt, L, di), prm["conv_w"], prm["conv_b"], out=xc),
-        # the block splits x_proj's K four ways for a narrow, long product (hx_block.hip)
-        "x_proj": lambda i: ssm.gemm_bf16(xc.view(M, di), prm["w_x"], splits=(r, r + N),
-                                          k_splits=4 if (di >= 2048 and di % 256 == 0 and r + 2 * N <= 256
-                                                         and 8 * (r + 2 * N) <= di) else None),
+        # narrow and long: the automatic choice is the 64-row narrow kernel, as in the block
+        "x_proj": lambda i: ssm.gemm_bf16(xc.view(M, di), prm["w_x"], splits=(r, r + N)),
         "dt_proj": lambda i: ssm.gemm_bf16(dbc[0], prm["w_dt"]),
         "scan": lambda i: ssm.selective_scan_fwd(xc, dt.view(bt, L, di), prm["A"], Bm, Cm, prm["D"],
                                                  xz[1].view(bt, L, di), prm["dt_bias"], out=y),

@@ -564,11 +564,13 @@ int block_core(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner, 
                              w.conv_b, b.xconv, stream)))
         return rc;
     // x_proj: [M, d_inner] x [dt_rank + 2N, d_inner]^T -> dt_lo | B | C. Narrow and long (config 3:
-    // N 160, K 4096, 64 tiles of 256 x 256): K is split four ways and the fp32 partials go to the
-    // in_proj x region, which the conv has consumed by now. The choice depends on the weight shape
-    // only, so every batch size and sequence length gets the same arithmetic per token.
+    // N 160, K 4096): hx_gemm_bf16's narrow kernel streams xconv once with every column in the
+    // block. Where that kernel does not apply, a long K is split four ways with the fp32 partials
+    // in the in_proj x region, which the conv has consumed by now. Either choice depends on the
+    // weight shape only, so every batch size and sequence length gets the same arithmetic per token.
     const int64_t nx = dt_rank + 2 * dstate;
-    const int splits = (d_inner >= 2048 && d_inner % 256 == 0 && nx <= 256 && 4 * nx * 2 <= d_inner) ? 4 : 1;
+    const int splits = (!hx::gemm_narrow_auto(nx, d_inner) && d_inner >= 2048 && d_inner % 256 == 0 &&
+                        nx <= 256 && 4 * nx * 2 <= d_inner) ? 4 : 1;
     rc = splits > 1 ? hx_gemm_bf16_splitk(M, nx, d_inner, b.xconv, d_inner, w.w_x, d_inner, nullptr, 0,
                                           HX_BF16, b.dtlo, dt_rank, dt_rank, b.B, dstate, dt_rank + dstate,
                                           b.C, dstate, splits, b.xpart, (size_t)M * d_inner * 2, stream)

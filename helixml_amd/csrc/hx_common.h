@@ -29,6 +29,10 @@ int scan_scratch_setup(void** out);
 bool grant_dynamic_lds(const void* fn, size_t dyn_bytes, size_t static_bytes);
 // Compute units of the current device (stored per device; 256 if the query fails). Thread-safe.
 int device_cus();
+// Whether hx_gemm_bf16's automatic choice takes the narrow kernel (64-row tiles holding every
+// column: N <= 192, K >= 1024, K % 64 == 0). It depends on the weight shape only, so every M
+// gets the same arithmetic per row.
+bool gemm_narrow_auto(int64_t N, int64_t K);
 
 #define HX_HIP_CHECK(expr)                                                                   \
     do {                                                                                     \

@@ -652,6 +652,127 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_dlds_kernel(int64_t M, int64
 }
 
 
+// ----------------------------------------------------------------------------- narrow N
+// Products with few output columns and a long K (the block's x_proj: N = dt_rank + 2 dstate, 160
+// at config 3 and 64 at config 5, K = d_inner), which stream X from HBM once: a block owns 64 rows
+// and every column, so the grid is M / 64 blocks and no K split is needed. Block tile 64 x NB
+// (NB = 64 CB, N <= NB): 4 waves in 2 x 2, each 32 rows x 32 CB columns (CB
+// v_mfma_f32_32x32x16_bf16 per 16-wide K step, K ascending as in the other kernels, so each
+// output is the same sum). K tiles of 64 move straight into a 3-stage LDS ring with
+// global_load_lds_dwordx4 (A rows 0..63, then W rows 0..NB-1, 128-byte rows with the 16-byte
+// chunks XOR-swizzled by row); the loads of tile kt+2 are issued while tile kt is multiplied.
+// W (at most NB x K) is read by every block and stays in L2. Requires K % 64 == 0 and 16-byte
+// aligned rows; rows past M or N are clamped (their outputs are discarded).
+constexpr int NBM = 64, NST3 = 3;
+
+template <int CB>
+constexpr int narrow_stage_bytes() { return (NBM + 64 * CB) * 128; }
+
+template <int CB>
+__global__ __launch_bounds__(256) void gemm_bf16_nt_narrow_kernel(int64_t M, int64_t N, int64_t K,
+                                                                  const uint16_t* __restrict__ X,
+                                                                  int64_t ldx,
+                                                                  const uint16_t* __restrict__ W,
+                                                                  int64_t ldw,
+                                                                  const float* __restrict__ bias,
+                                                                  GemmOut o) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    char* sbase = reinterpret_cast<char*>(smem);
+    constexpr int SB = narrow_stage_bytes<CB>();
+    constexpr int QW = (NBM + 64 * CB) / 8 / 4;  // 1-KiB load regions per wave per tile
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int64_t m0 = (int64_t)blockIdx.x * NBM;
+
+    // region q = QW * wave + j of a stage: rows 8q .. 8q + 7 (0..63 = A, then W); lane L fills
+    // row 8q + L / 8, slot L % 8 with K-chunk (L % 8) ^ (row & 7)
+    const uint16_t* src[QW];
+#pragma unroll
+    for (int j = 0; j < QW; ++j) {
+        const int q = wave * QW + j;
+        const int row = q * 8 + (lane >> 3);
+        const int chunk = (lane & 7) ^ (row & 7);
+        if (row < NBM) {
+            const int64_t gr = m0 + row < M ? m0 + row : M - 1;
+            src[j] = X + gr * ldx + chunk * 8;
+        } else {
+            const int64_t gr = row - NBM < N ? row - NBM : N - 1;
+            src[j] = W + gr * ldw + chunk * 8;
+        }
+    }
+    auto issue = [&](int64_t kt) __attribute__((always_inline)) {
+        char* stage = sbase + (int)(kt % NST3) * SB;
+#pragma unroll
+        for (int j = 0; j < QW; ++j)
+            __builtin_amdgcn_global_load_lds((gvoid_t*)(src[j] + kt * 64),
+                                             (lvoid_t*)(stage + (wave * QW + j) * 1024), 16, 0, 0);
+    };
+
+    f32x16 acc[CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+
+    const int fr = lane & 31;
+    const int fc = lane >> 5;
+    const int64_t nk = K / 64;
+    issue(0);
+    if (nk > 1) issue(1);
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        // this wave's loads of tile kt are done when at most the QW of tile kt+1 remain; wait and
+        // barrier in one statement so the compiler adds no wait for tile kt+1's loads
+        if (kt + 1 < nk) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(QW) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kt + 2 < nk) issue(kt + 2);  // stage (kt+2)%3 was last read in iteration kt-1
+        const char* stage = sbase + (int)(kt % NST3) * SB;
+        const char* aw = stage + (wm * 32 + fr) * 128;
+        const char* bw = stage + (NBM + wn * 32 * CB + fr) * 128;
+        auto load = [&](int s, bf16x8& af, bf16x8* bf) __attribute__((always_inline)) {
+            const int off = ((2 * s + fc) ^ (fr & 7)) << 4;
+            af = *reinterpret_cast<const bf16x8*>(aw + off);
+#pragma unroll
+            for (int j = 0; j < CB; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(bw + j * 32 * 128 + off);
+        };
+        bf16x8 fa[2], fb[2][CB];
+        load(0, fa[0], fb[0]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (s + 1 < 4) load(s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < CB; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s & 1], fb[s & 1][j], acc[j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();  // the epilogue reuses stage memory
+
+    // 32 x 64 slabs staged per wave (two column blocks at a time); the wave's columns end at
+    // n_end, past which a slab's second half (odd CB) holds no result
+    float* st = reinterpret_cast<float*>(smem) + wave * (32 * 68);
+    const int64_t c0 = (int64_t)wn * 32 * CB;
+    const int64_t n_end = c0 + 32 * CB < N ? c0 + 32 * CB : N;
+#pragma unroll
+    for (int g = 0; g < (CB + 1) / 2; ++g) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            if (2 * g + jj >= CB) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                st[row * 68 + jj * 32 + (lane & 31)] = acc[2 * g + jj][r];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        store_tile_rows(o, bias, st, M, n_end, m0 + wm * 32, c0 + 64 * g, lane);
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 // ----------------------------------------------------------------------------- 256 x 256
 // Direct-to-LDS kernel with a 256 x 256 block tile: 4 waves in 2 x 2, each a 128 x 128 tile
 // (4 x 4 v_mfma_f32_32x32x16_bf16 per 16-wide K step, 256 fp32 accumulators per lane, kept in
@@ -926,7 +1047,38 @@ int launch_d256(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, con
 }
 
 bool dlds_ok(size_t bytes) { return hx::grant_dynamic_lds((const void*)hx::gemm_bf16_nt_dlds_kernel, bytes, 0); }
+
+template <int CB>
+int launch_narrow_cb(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* W,
+                     int64_t ldw, const float* bias, const hx::GemmOut& o, void* stream) {
+    using namespace hx;
+    const size_t bytes = (size_t)NST3 * narrow_stage_bytes<CB>();
+    HX_REQUIRE(grant_dynamic_lds((const void*)gemm_bf16_nt_narrow_kernel<CB>, bytes, 0), HX_ERR_UNSUPPORTED,
+               "gemm_bf16: the device does not grant %zu bytes of LDS", bytes);
+    HX_REQUIRE((M + NBM - 1) / NBM <= 0x7fffffff, HX_ERR_UNSUPPORTED, "gemm_bf16: M=%lld too large",
+               (long long)M);
+    hipLaunchKernelGGL((gemm_bf16_nt_narrow_kernel<CB>), dim3((unsigned)((M + NBM - 1) / NBM)), dim3(256),
+                       bytes, as_stream(stream), M, N, K, (const uint16_t*)X, ldx, (const uint16_t*)W, ldw,
+                       bias, o);
+    HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+// The narrow kernel for 1 <= N <= 256 (block tile 64 x 64 ceil(N / 64)).
+int launch_narrow(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* W,
+                  int64_t ldw, const float* bias, const hx::GemmOut& o, void* stream) {
+    switch ((N + 63) / 64) {
+        case 1: return launch_narrow_cb<1>(M, N, K, X, ldx, W, ldw, bias, o, stream);
+        case 2: return launch_narrow_cb<2>(M, N, K, X, ldx, W, ldw, bias, o, stream);
+        case 3: return launch_narrow_cb<3>(M, N, K, X, ldx, W, ldw, bias, o, stream);
+        default: return launch_narrow_cb<4>(M, N, K, X, ldx, W, ldw, bias, o, stream);
+    }
+}
 }  // namespace
+
+namespace hx {
+bool gemm_narrow_auto(int64_t N, int64_t K) { return N >= 1 && N <= 192 && K >= 1024 && K % 64 == 0; }
+}  // namespace hx
 
 extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
                             const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
@@ -950,6 +1102,11 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     HX_REQUIRE((N + BN - 1) / BN <= 0x7fffffff && (M + BM - 1) / BM <= 65535, HX_ERR_UNSUPPORTED,
                "gemm_bf16: M=%lld too large for the grid", (long long)M);
     GemmOut o{{Y0, Y1, Y2}, {ld0, ld1, ld2}, split1, split2, out_dtype == HX_BF16, act};
+    // narrow N, long K (x_proj): one pass over X with every column in the block, chosen by the
+    // weight shape alone (measured on MI355X: config 3 x_proj N 160 K 4096, config 5 N 64 K 1024)
+    if (vec && K % 64 == 0 && N <= 256 &&
+        (g_gemm_kernel == 7 || (g_gemm_kernel == 0 && gemm_narrow_auto(N, K))))
+        return launch_narrow(M, N, K, X, ldx, W, ldw, bias, o, stream);
     // auto: the 256 x 256 kernel wherever it fills the GPU with tiles at least 256 columns wide
     // (measured on MI355X ahead of every other kernel here for the block's in_proj, out_proj,
     // dt_proj and the LM head: 1.5-2.3x the 128 x 128 kernel; behind it for the narrow x_proj);
@@ -1070,8 +1227,8 @@ extern "C" int hx_gemm_bf16_splitk(int64_t M, int64_t N, int64_t K, const void* 
 
 extern "C" int hx_set_gemm_kernel(int k) {
     using namespace hx;
-    HX_REQUIRE(k >= 0 && k <= 6 && k != 2, HX_ERR_INVALID_INPUT,
-               "hx_set_gemm_kernel: %d (0 auto, 1, 3, 4, 5, 6)", k);
+    HX_REQUIRE(k >= 0 && k <= 7 && k != 2, HX_ERR_INVALID_INPUT,
+               "hx_set_gemm_kernel: %d (0 auto, 1, 3, 4, 5, 6, 7)", k);
     g_gemm_kernel = k;
     return HX_OK;
 }

@@ -68,14 +68,14 @@ def gemm_kernel(dev, request):
     ssm.set_gemm_kernel(0)
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6, 7], indirect=True)
 @pytest.mark.parametrize("M,N,K", [(512, 256, 512), (300, 200, 136), (257, 129, 64), (1024, 2048, 1024),
                                    (100, 72, 1000), (256, 64, 1024), (33, 40, 24), (300, 260, 192),
                                    (600, 136, 128)])
 @pytest.mark.parametrize("act", [0, 1])
 def test_gemm_tile_kernels_fp32_out(dev, gemm_kernel, M, N, K, act):
     """Each tile kernel (128 x 128 x 32, the small-M kernel's 32 x 32 / 32 x 64 tiles with K split
-    over 4 waves, 256 x 128 x 64 direct-to-LDS, 256 x 256)
+    over 4 waves, 256 x 128 x 64 direct-to-LDS, 256 x 256, the narrow 64-row kernel for N <= 256)
     on aligned and ragged shapes; the direct-to-LDS kernels take the shapes with K % 64 (or 32)
     == 0 (1, 2, 3 and more K tiles) and fall back on the others."""
     g = torch.Generator().manual_seed(M + N + K)
@@ -88,7 +88,7 @@ def test_gemm_tile_kernels_fp32_out(dev, gemm_kernel, M, N, K, act):
     assert err <= 1e-5, err
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6, 7], indirect=True)
 @pytest.mark.parametrize("splits", [(128, 144), (100, 133), (8, 16)])
 def test_gemm_tile_kernels_splits_bf16(dev, gemm_kernel, splits):
     """Column splits on vector boundaries and straddling them (100, 133 are not multiples of 8)."""
@@ -103,7 +103,7 @@ def test_gemm_tile_kernels_splits_bf16(dev, gemm_kernel, splits):
     assert err <= 2 ** -7, err  # within one bf16 ulp of the rounded reference
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6, 7], indirect=True)
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 def test_gemm_accumulate_into_output(dev, gemm_kernel, out_dtype):
     """act bit 1: Y += X . W^T (the residual add of a pre-norm layer)."""
@@ -195,3 +195,52 @@ def test_gemm_grouped_tile_order(dev, gemm_kernel, M, N, K):
     yh = y.cpu().numpy()
     assert not np.isnan(yh).any()
     assert norm_err(yh, ref(X, W)) <= 1e-5
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", [(2000, 160, 4096), (333, 64, 1024), (64, 192, 2048), (7, 1, 1024),
+                                   (130, 250, 1088)])
+def test_gemm_narrow_kernel(dev, out_dtype, M, N, K):
+    """The narrow kernel (64-row tiles holding every column, the x_proj shapes) on its own
+    (kernel 7) and as the automatic choice: the block's dt_lo | B | C splits, bias, accumulate,
+    ragged M and N; its fp32 sums are the 256 x 128 direct-to-LDS kernel's bit for bit (both add
+    the same 32 x 32 x 16 MFMA products with K ascending)."""
+    g = torch.Generator().manual_seed(M + N + K)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
+    b = torch.randn(N, generator=g).to(dev)
+    r = ref(X, W, b)
+    try:
+        ssm.set_gemm_kernel(7)
+        y7 = ssm.gemm_bf16(X, W, b, out_dtype=out_dtype)
+        s1, s2 = max(1, N // 5), max(1, N // 5) + (N > 2)
+        parts = ssm.gemm_bf16(X, W, b, splits=(s1, s2), out_dtype=out_dtype) if N > 2 else None
+        ssm.set_gemm_kernel(4)
+        y4 = ssm.gemm_bf16(X, W, b, out_dtype=torch.float32)
+        ssm.set_gemm_kernel(7)
+        y7f = ssm.gemm_bf16(X, W, b, out_dtype=torch.float32)
+    finally:
+        ssm.set_gemm_kernel(0)
+    y0 = ssm.gemm_bf16(X, W, b, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    if out_dtype == torch.float32:
+        assert norm_err(y7.cpu().numpy(), r) <= 1e-5
+    else:
+        assert rel_err(y7.float().cpu().numpy(), bf16_round(r)) <= 2 ** -7
+    if N <= 192 and K >= 1024:  # the automatic choice for this weight shape
+        assert torch.equal(y0, y7)
+    if K % 64 == 0:
+        assert torch.equal(y7f, y4), "narrow and direct-to-LDS sums differ"
+    if parts is not None:
+        got = torch.cat([p.float() for p in parts], 1)
+        assert torch.equal(got, y7.float())
+    # accumulate into the output (act bit 1)
+    from helixml_amd import _ffi
+    Y0 = torch.randn(M, N, generator=g).to(dev).to(out_dtype)
+    Y = Y0.clone()
+    od = _ffi.HX_F32 if out_dtype == torch.float32 else _ffi.HX_BF16
+    _ffi.call("hx_gemm_bf16", M, N, K, X.data_ptr(), K, W.data_ptr(), K, None, 2, od,
+              Y.data_ptr(), N, N, None, 0, N, None, 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    err = norm_err(Y.float().cpu().numpy(), Y0.float().cpu().numpy() + ref(X, W))
+    assert err <= (1e-5 if out_dtype == torch.float32 else 2 ** -8), err
