@@ -8,7 +8,7 @@ cannot serve a step from the previous one. A "step" is one hx_selective_scan_fwd
 batch. Prints ONE JSON line.
 
   python bench.py [--steps K] [--warmup W]
-                  [--workload c1|c2|c2bf16|c3|c4|c4s4|c4s4exact|c4s4d|c5|c5dec|copy] [--no-cpu]
+                  [--workload c1|c2|c2bf16|c3|c4|c4s4|c4s4exact|c4s4d|c5|c5dec|copy|gemm] [--no-cpu]
 
 Timing: an untimed clock-settle phase (the step back to back for SETTLE_S seconds) and W untimed
 warmup steps, then exactly K timed steps with a HIP event between consecutive steps; ms_per_step
@@ -25,6 +25,7 @@ c3 = BASELINE config 3, the full Mamba block (in_proj, conv1d+SiLU, x_proj, dt_p
 out_proj) at batch 4 x L 4096 x d_model 2048, bf16 storage; reported separately from the metric.
 c4s4 / c4s4exact / c4s4d = BASELINE config 4's S4 recurrence (d 2048, N 16, L 65536): reference
 mode time-parallel, reference mode bit-exact, and the S4D diagonal complex form.
+gemm = the block's and the LM's projection shapes, here and through the vendor library.
 c5 / c5dec = BASELINE config 5's byte LM (12 x (RMSNorm + Mamba), d_model 512): prefill of
 16 x 8192 tokens, and one recurrent decode step at batch 256 (after a 64-token prefill).
 """
@@ -587,6 +588,45 @@ def bench_lm(args, dev):
     print(json.dumps(rec))
 
 
+def bench_gemm(args, dev):
+    """The block's and the LM's projection shapes through hx_gemm_bf16 (automatic kernel choice)
+    and through the vendor library (torch.nn.functional.linear, hipBLASLt) in the same process on
+    the same random bf16 operands (X ~ N(0, 1), W ~ N(0, 1/K)); best of three rounds of 10 calls
+    each, rounds interleaved. One JSON line per shape."""
+    shapes = {"config3 in_proj": (16384, 2048, 8192), "config3 out_proj": (16384, 4096, 2048),
+              "config3 x_proj": (16384, 4096, 160), "config3 dt_proj": (16384, 128, 4096),
+              "config5 in_proj": (131072, 512, 2048), "config5 x_proj": (131072, 1024, 64),
+              "config5 dt_proj": (131072, 32, 1024), "config5 head": (131072, 512, 256)}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+
+    def timed(fn, n=10):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for _ in range(n):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / n * 1e3
+
+    for name, (M, K, N) in shapes.items():
+        x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+        w = (torch.randn(N, K, device=dev, generator=gen) / K ** 0.5).to(torch.bfloat16)
+        here, vendor = [], []
+        for _ in range(3):
+            here.append(timed(lambda: ssm.gemm_bf16(x, w)))
+            vendor.append(timed(lambda: torch.nn.functional.linear(x, w)))
+        print(json.dumps({"metric": "bf16 GEMM time, here vs vendor library", "shape": name, "M": M,
+                          "K": K, "N": N, "here_us": min(here), "vendor_us": min(vendor),
+                          "here_rounds_us": here, "vendor_rounds_us": vendor,
+                          "here_tflops": 2 * M * N * K / min(here) / 1e6,
+                          "higher_is_better": False}))
+        del x, w
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -594,7 +634,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c2bf16", "c4", "c3", "c4s4", "c4s4exact", "c4s4d", "c5",
-                             "c5dec", "copy"],
+                             "c5dec", "copy", "gemm"],
                     help="copy = plain device copy of 512 MiB (HBM ceiling and counter calibration)")
     ap.add_argument("--variant", type=int, default=0, help="scan kernel variant (hx_set_scan_variant)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -614,6 +654,9 @@ def main():
 
     if args.workload == "c1":
         bench_c1(args, dev)
+        return
+    if args.workload == "gemm":
+        bench_gemm(args, dev)
         return
     if args.workload == "copy":
         n = 512 * 2**20 // 4
