@@ -1104,7 +1104,9 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     GemmOut o{{Y0, Y1, Y2}, {ld0, ld1, ld2}, split1, split2, out_dtype == HX_BF16, act};
     // narrow N, long K (x_proj): one pass over X with every column in the block, chosen by the
     // weight shape alone (measured on MI355X: config 3 x_proj N 160 K 4096, config 5 N 64 K 1024)
-    if (vec && K % 64 == 0 && N <= 256 &&
+    // the tile kernels below load whole K tiles unguarded: K == 0 (Y = bias) takes the guarded
+    // 128 x 128 kernel
+    if (vec && K > 0 && K % 64 == 0 && N <= 256 &&
         (g_gemm_kernel == 7 || (g_gemm_kernel == 0 && gemm_narrow_auto(N, K))))
         return launch_narrow(M, N, K, X, ldx, W, ldw, bias, o, stream);
     // auto: the 256 x 256 kernel wherever it fills the GPU with tiles at least 256 columns wide
@@ -1113,9 +1115,9 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     // the 32-wide K tile where K is not a multiple of 64 (config 5 dt_proj, K = 32)
     const bool d256_auto = g_gemm_kernel == 0 && N >= 256 && M >= 256 &&
                            ((M + XBM - 1) / XBM) * ((N + XBN - 1) / XBN) >= 256;
-    if (vec && K % 64 == 0 && (g_gemm_kernel == 5 || d256_auto) && d256_ok<64, 2>())
+    if (vec && K > 0 && K % 64 == 0 && (g_gemm_kernel == 5 || d256_auto) && d256_ok<64, 2>())
         return launch_d256<64, 2>(M, N, K, X, ldx, W, ldw, bias, o, stream);
-    if (vec && K % 32 == 0 && (g_gemm_kernel == 6 || (d256_auto && K % 64 != 0)) && d256_ok<32, 4>())
+    if (vec && K > 0 && K % 32 == 0 && (g_gemm_kernel == 6 || (d256_auto && K % 64 != 0)) && d256_ok<32, 4>())
         return launch_d256<32, 4>(M, N, K, X, ldx, W, ldw, bias, o, stream);
     const size_t dlds = (size_t)DSTAGES * DSTAGE_BYTES;
     // auto: the direct-to-LDS kernel for long K (measured ahead of the 128 x 128 kernel from
@@ -1124,7 +1126,7 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     // epilogue). Its per-element arithmetic is the 256 x 256 kernel's (K ascending in 16-wide
     // MFMA steps), so a short batch that lands here matches a long one that takes that kernel.
     const int64_t tiles_dlds = ((M + LBM - 1) / LBM) * ((N + LBN - 1) / LBN);
-    if (vec && K % LBK == 0 &&
+    if (vec && K > 0 && K % LBK == 0 &&
         (g_gemm_kernel == 4 ||
          (g_gemm_kernel == 0 && (K >= 2048 || (K >= 1024 && N <= 128 && tiles_dlds >= 128)))) &&
         dlds_ok(dlds)) {
@@ -1193,8 +1195,8 @@ extern "C" int hx_gemm_bf16_splitk(int64_t M, int64_t N, int64_t K, const void* 
     HX_REQUIRE(X && W && Y0, HX_ERR_INVALID_INPUT, "gemm_bf16_splitk: X, W and Y0 must be non-NULL");
     HX_REQUIRE(ldx >= K && ldw >= K && ld0 >= 0, HX_ERR_INVALID_DIMENSION,
                "gemm_bf16_splitk: leading dimensions smaller than K");
-    HX_REQUIRE(K % ((int64_t)splits * 64) == 0, HX_ERR_UNSUPPORTED,
-               "gemm_bf16_splitk: K %lld is not a multiple of 64 * splits", (long long)K);
+    HX_REQUIRE(K > 0 && K % ((int64_t)splits * 64) == 0, HX_ERR_UNSUPPORTED,
+               "gemm_bf16_splitk: K %lld is not a positive multiple of 64 * splits", (long long)K);
     HX_REQUIRE(ldx % 8 == 0 && ldw % 8 == 0 && aligned(X, 16) && aligned(W, 16), HX_ERR_UNSUPPORTED,
                "gemm_bf16_splitk: rows of X and W must be 16-byte aligned");
     HX_REQUIRE(workspace && aligned(workspace, 16) &&

@@ -244,3 +244,24 @@ def test_gemm_narrow_kernel(dev, out_dtype, M, N, K):
     torch.cuda.synchronize()
     err = norm_err(Y.float().cpu().numpy(), Y0.float().cpu().numpy() + ref(X, W))
     assert err <= (1e-5 if out_dtype == torch.float32 else 2 ** -8), err
+
+
+@pytest.mark.parametrize("gemm_kernel", [0, 4, 5, 6, 7], indirect=True)
+def test_gemm_empty_k_is_bias(dev, gemm_kernel):
+    """K == 0 gives Y = bias (zeros without one) on every kernel choice: the tile kernels, which
+    load whole K tiles, hand it to the guarded 128 x 128 kernel; split-K rejects it."""
+    from helixml_amd import _ffi
+    M, N = 300, 200
+    X = torch.zeros(M, 8, device=dev, dtype=torch.bfloat16)  # 16-byte rows: the vector paths' layout
+    W = torch.zeros(N, 8, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(N, device=dev)
+    Y = torch.full((M, N), 7.0, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    _ffi.call("hx_gemm_bf16", M, N, 0, X.data_ptr(), 8, W.data_ptr(), 8, b.data_ptr(), 0, _ffi.HX_F32,
+              Y.data_ptr(), N, N, None, 0, N, None, 0, s)
+    torch.cuda.synchronize()
+    assert torch.equal(Y, b.expand(M, N))
+    ws = torch.empty(2 * M * N, device=dev)
+    with pytest.raises(UnsupportedOperation):
+        _ffi.call("hx_gemm_bf16_splitk", M, N, 0, X.data_ptr(), 8, W.data_ptr(), 8, None, 0, _ffi.HX_F32,
+                  Y.data_ptr(), N, N, None, 0, N, None, 0, 2, ws.data_ptr(), ws.numel() * 4, s)
