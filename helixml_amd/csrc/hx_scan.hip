@@ -482,8 +482,10 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
     }
     const float Dd = Dv ? Dv[dc] : 0.0f;
     const float bias = dt_bias ? dt_bias[dc] : 0.0f;
-    // END_ONLY: decay from the segment's end back to the step reached, per state
+    // END_ONLY: decay from the segment's end back to the step reached, per state, and the sum of
+    // dt over those steps (the decay is exp(A * S))
     float Q[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    float S = 0.0f;
 
     float4 ru[PF], rd[PF], rz[PF], rb[PF], rc[PF];
     auto fetch = [&](int k) __attribute__((always_inline)) {
@@ -555,29 +557,20 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
         const float ck[4] = {C4.x, C4.y, C4.z, C4.w};
         float P[16];
         if constexpr (END_ONLY) {
-            // steps 15..0: h += Q * B*dt*u, then Q *= exp(dt*A); h is the end state from a zero
-            // state at the step reached, Q the decay from there to the end
-            StepLoop<4>::run([&](auto gc) {
-                constexpr int g = decltype(gc)::value;
-                float ab[4][4];
+            // steps 15..0: h += exp(A * S) * B*dt*u, then S += dt; h is the end state from a zero
+            // state at the step reached, S the sum of dt from there to the end. The decay to the
+            // end is formed from S (one exponential per state-step) rather than as a running
+            // product of the per-step decays (an exponential and a multiply).
+            StepLoop<16>::run([&](auto ec) {
+                constexpr int s = 15 - decltype(ec)::value;
+                const float dus = gdu[s & 3][s >> 2];
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int s = 15 - (4 * g + e);
-                        ab[e][k] = fast_exp2(gdl[s & 3][s >> 2] * A2[k]);
-                    }
-                StepLoop<4>::run([&](auto ec) {
-                    constexpr int e = decltype(ec)::value;
-                    constexpr int s = 15 - (4 * g + e);
-                    const float dus = gdu[s & 3][s >> 2];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        h[k] = fmaf(Q[k], dpp<kDppBcast<s>>(bk[k]) * dus, h[k]);
-                        Q[k] *= ab[e][k];
-                    }
-                });
+                for (int k = 0; k < 4; ++k)
+                    h[k] = fmaf(fast_exp2(A2[k] * S), dpp<kDppBcast<s>>(bk[k]) * dus, h[k]);
+                S += gdl[s & 3][s >> 2];
             });
+#pragma unroll
+            for (int k = 0; k < 4; ++k) Q[k] = fast_exp2(A2[k] * S);
         } else {
         StepLoop<4>::run([&](auto gc) {
             constexpr int g = decltype(gc)::value;
