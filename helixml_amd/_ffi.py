@@ -106,6 +106,7 @@ SIGNATURES = {
     "hx_gemm_bf16_splitk": [_i64, _i64, _i64, _p, _i64, _p, _i64, _p, _int, _int,
                             _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _int, _p, _sz, _p],
     "hx_conv1d_silu": [_i64, _i64, _i64, _i64, _int, _p, _i64, _p, _p, _p, _p],
+    "hx_selective_scan_dtproj_fwd": [_i64, _i64, _i64, _i64] + [_p] * 12,
     "hx_mamba_block_workspace_size": [_i64, _i64, _i64, _i64, _i64],
     "hx_mamba_block_fwd": [_i64] * 7 + [_p] * 12 + [_sz, _p],
     "hx_embedding_fwd": [_i64, _i64, _i64, _p, _p, _p, _p],

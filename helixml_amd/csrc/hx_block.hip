@@ -578,13 +578,23 @@ int block_core(int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner, 
                                    b.dtlo, dt_rank, dt_rank, b.B, dstate, dt_rank + dstate, b.C, dstate,
                                    stream);
     if (rc) return rc;
-    // dt_proj: [M, dt_rank] x [d_inner, dt_rank]^T -> dt (dt_bias is added inside the scan)
-    if ((rc = hx_gemm_bf16(M, d_inner, dt_rank, b.dtlo, dt_rank, w.w_dt, dt_rank, nullptr, 0,
-                           HX_BF16, b.dt, d_inner, d_inner, nullptr, 0, d_inner, nullptr, 0, stream)))
-        return rc;
-    if ((rc = hx_selective_scan_fwd(batch, seqlen, d_inner, dstate, HX_BF16, 1, b.xconv, b.dt, w.A,
-                                    b.B, b.C, w.D, b.z, w.dt_bias, b.y, nullptr, last_state, stream)))
-        return rc;
+    if (hx::scan_variant_is_auto() && hx::scan_dtproj_ok(batch, seqlen, d_inner, dt_rank)) {
+        // dt_proj inside the scan: each 16-step chunk's dt tile is dt_lo . w_dt^T on the matrix
+        // core, rounded to bf16 as the separate product stores it (dt_bias is added after)
+        rc = hx::scan_fwd_dtproj(batch, seqlen, d_inner, (const uint16_t*)b.xconv, (const uint16_t*)b.dtlo,
+                                 dt_rank, (const uint16_t*)w.w_dt, w.A, (const uint16_t*)b.B,
+                                 (const uint16_t*)b.C, w.D, (const uint16_t*)b.z, w.dt_bias,
+                                 (uint16_t*)b.y, last_state, hx::as_stream(stream));
+        if (rc) return rc;
+    } else {
+        // dt_proj: [M, dt_rank] x [d_inner, dt_rank]^T -> dt (dt_bias is added inside the scan)
+        if ((rc = hx_gemm_bf16(M, d_inner, dt_rank, b.dtlo, dt_rank, w.w_dt, dt_rank, nullptr, 0,
+                               HX_BF16, b.dt, d_inner, d_inner, nullptr, 0, d_inner, nullptr, 0, stream)))
+            return rc;
+        if ((rc = hx_selective_scan_fwd(batch, seqlen, d_inner, dstate, HX_BF16, 1, b.xconv, b.dt, w.A,
+                                        b.B, b.C, w.D, b.z, w.dt_bias, b.y, nullptr, last_state, stream)))
+            return rc;
+    }
     // out_proj: [M, d_inner] x [d_model, d_inner]^T -> out (+= out when accumulating)
     return hx_gemm_bf16(M, d_model, d_inner, b.y, d_inner, w.w_out, d_inner, nullptr,
                         accumulate ? 2 : 0, out_dtype, out, d_model, d_model, nullptr, 0, d_model,

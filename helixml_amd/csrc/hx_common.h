@@ -34,6 +34,21 @@ int device_cus();
 // gets the same arithmetic per row.
 bool gemm_narrow_auto(int64_t N, int64_t K);
 
+// The Mamba block's dt_proj and selective scan in one launch (bf16 storage, dstate 16, softplus,
+// z gate, zero initial state): delta = bf16(dt_lo . w_dt^T) is formed per 16-step chunk on the
+// matrix core inside the wave kernel instead of being read from memory. dt_lo [batch, seqlen,
+// rank], w_dt [dim, rank] bf16; the other operands as hx_selective_scan_fwd's. scan_dtproj_ok
+// tells whether the sizes fit (rank 32, 64, 96 or 128; seqlen * dim < 2^31); it depends on the
+// weight shape and the sizes only, not on the data.
+bool scan_dtproj_ok(int64_t batch, int64_t seqlen, int64_t dim, int64_t rank);
+// Whether the calling thread's scan variant (hx_set_scan_variant) is the automatic choice; a
+// forced variant also makes the block run its dt projection and scan as separate steps.
+bool scan_variant_is_auto();
+int scan_fwd_dtproj(int64_t batch, int64_t seqlen, int64_t dim, const uint16_t* u, const uint16_t* dtlo,
+                    int64_t rank, const uint16_t* w_dt, const float* A, const uint16_t* B,
+                    const uint16_t* C, const float* D, const uint16_t* z, const float* dt_bias,
+                    uint16_t* out, float* last_state, hipStream_t stream);
+
 #define HX_HIP_CHECK(expr)                                                                   \
     do {                                                                                     \
         hipError_t hx_e_ = (expr);                                                           \

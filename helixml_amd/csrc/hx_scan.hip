@@ -211,6 +211,11 @@ struct WaveSeg {
     const float* seg_init;  // [nseg][B][D][16] entry states (full mode, nseg > 1)
     float* seg_hend;        // [nseg][B][D][16] end state from zero (END_ONLY)
     float* seg_decay;       // [nseg][B][D][16] decay over the segment (END_ONLY; 0 = dropped)
+    // fused dt projection (scan_wave3_kernel with DTP, bf16 storage): delta = bf16(dt_lo . w_dt^T)
+    // formed in the kernel, dt_lo [B][L][rank], w_dt [D][rank], rank a multiple of 32 up to 128
+    const uint16_t* dtlo = nullptr;
+    const uint16_t* wdt = nullptr;
+    int rank = 0;
 };
 
 template <typename T, int PF, bool HAS_Z, bool SOFTPLUS, bool END_ONLY>
@@ -417,7 +422,14 @@ __global__ __launch_bounds__(256) void scan_wave_kernel(
 //     wave's staging writes and reads).
 // WPB waves per block (64 * WPB threads). Requires L * Dm < 2^31 (32-bit offsets within a
 // batch row).
-template <typename T, int PF, bool HAS_Z, bool SOFTPLUS, bool END_ONLY, int WPB>
+// DTPK > 0 (bf16 storage): the block's dt_proj fused in, rank = 32 DTPK. delta is not read; each
+// chunk's dt tile [16 steps x 16 channels] = dt_lo [16 x rank] . w_dt[16 channels x rank]^T is
+// formed on the matrix core (DTPK v_mfma_f32_16x16x32_bf16, fp32 sums), rounded to bf16 as the
+// unfused path stores dt, and staged in the delta slot, so the rest of the kernel is unchanged.
+// Lane (r, c) holds w_dt's row for channel c and dt_lo's row for step c of the chunk (8 K values
+// per 16-lane group), and receives dt of steps 4r..4r+3 of channel c. The rank is a template
+// argument so that every load is unconditional (the wait counts stay exact).
+template <typename T, int PF, bool HAS_Z, bool SOFTPLUS, bool END_ONLY, int WPB, int DTPK = 0>
 __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
     int64_t L, int64_t Dm, int ntiles, int64_t Bt,
     const T* __restrict__ u, const T* __restrict__ delta, const float* __restrict__ A,
@@ -487,11 +499,41 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
     float Q[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     float S = 0.0f;
 
+    // fused dt projection: w_dt fragments of this lane's channel, and dt_lo row offsets (32-bit
+    // inside the batch row) that advance with the chunks like the tile offsets
+    constexpr bool DTP = DTPK > 0;
+    constexpr int NKB = DTP ? DTPK : 1;
+    static_assert(!(DTP && END_ONLY), "the fused dt projection has no end-state pass");
+    typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+    typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+    bf16x8_t wdtf[NKB];
+    bf16x8_t rdl[PF][NKB];
+    const uint16_t* dlb = nullptr;
+    uint32_t dl_next = 0, dl_first = 0, dl_last = 0, dl_step = 0;
+    if constexpr (DTP) {
+        const uint32_t R = 32 * DTPK;
+        const int kq = 8 * (lane >> 4);
+        const uint16_t* wr = sg.wdt + dc * R + kq;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) wdtf[kb] = *reinterpret_cast<const bf16x8_t*>(wr + 32 * kb);
+        dlb = sg.dtlo + b * L * R;
+        dl_first = (uint32_t)(tbeg + c) * R + kq;
+        dl_last = (uint32_t)(tend - 1) * R + kq;
+        dl_next = (uint32_t)((END_ONLY ? tend - TCH : tbeg) + c) * R + kq;
+        dl_step = TCH * R;
+    }
+
     float4 ru[PF], rd[PF], rz[PF], rb[PF], rc[PF];
     auto fetch = [&](int k) __attribute__((always_inline)) {
         const uint32_t xo = x_next < x_last ? x_next : x_last;
         ru[k] = Vec4<T>::load(ub + xo);
-        rd[k] = Vec4<T>::load(db + xo);
+        if constexpr (DTP) {
+            const uint32_t o = dl_next < dl_last ? dl_next : dl_last;
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) rdl[k][kb] = *reinterpret_cast<const bf16x8_t*>(dlb + o + 32 * kb);
+        } else {
+            rd[k] = Vec4<T>::load(db + xo);
+        }
         rz[k] = USE_Z ? Vec4<T>::load(zb + xo) : make_float4(0, 0, 0, 0);
         const uint32_t bo = bc_next < bc_last ? bc_next : bc_last;
         rb[k] = Vec4<T>::load(Bb + bo);
@@ -499,14 +541,38 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
         if constexpr (END_ONLY) {  // backwards; past the segment's start the first chunk repeats
             x_next = x_next >= x_first + x_step ? x_next - x_step : x_first;
             bc_next = bc_next >= bc_first + bc_step ? bc_next - bc_step : bc_first;
+            if constexpr (DTP) dl_next = dl_next >= dl_first + dl_step ? dl_next - dl_step : dl_first;
         } else {
             x_next += x_step;
             bc_next += bc_step;
+            if constexpr (DTP) dl_next += dl_step;
+        }
+    };
+    // DTP: the dt tile of the chunk in slot k on the matrix core (lane (r, c) gets steps 4r..4r+3
+    // of channel c), and its staging, rounded to bf16, in the delta slot of LDS buffer buf
+    auto dt_tile = [&](int k) __attribute__((always_inline)) {
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (DTP) {
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rdl[k][kb], wdtf[kb], acc, 0, 0, 0);
+        }
+        return acc;
+    };
+    auto stage_dt = [&](const f32x4_t& acc, int buf) __attribute__((always_inline)) {
+        // round to bf16 with v_cvt_pk_bf16_f32 (round to nearest even, as Storage<uint16_t>::round
+        // for every non-NaN value) and widen back: branch-free
+        typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32v2_t;
+        typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16v2_t;
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+            const uint32_t pk = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32v2_t{acc[j], acc[j + 1]}, bf16v2_t));
+            s_in[w][buf][1][4 * r + j][c] = __uint_as_float(pk << 16);
+            s_in[w][buf][1][4 * r + j + 1][c] = __uint_as_float(pk & 0xffff0000u);
         }
     };
     auto stage_in = [&](int k, int buf) __attribute__((always_inline)) {
         *reinterpret_cast<float4*>(&s_in[w][buf][0][mrow][mcl]) = ru[k];
-        *reinterpret_cast<float4*>(&s_in[w][buf][1][mrow][mcl]) = rd[k];
+        if constexpr (!DTP) *reinterpret_cast<float4*>(&s_in[w][buf][1][mrow][mcl]) = rd[k];
         if (USE_Z) *reinterpret_cast<float4*>(&s_in[w][buf][2][mrow][mcl]) = rz[k];
     };
     auto store_out = [&](int64_t t0, int buf) __attribute__((always_inline)) {
@@ -613,6 +679,7 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
 #pragma unroll
     for (int k = 0; k < PF; ++k) fetch(k);
     stage_in(0, 0);
+    if constexpr (DTP) stage_dt(dt_tile(0), 0);
     float4 B4 = rb[0], C4 = rc[0];
     fetch(0);
     // END_ONLY: the segment's chunks from the last back to the first (all whole: segment lengths
@@ -657,6 +724,9 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
             constexpr int buf = k & 1;  // PF is even
             const int64_t t0 = tb0 + k * TCH;
             if (t0 >= tend) return;  // uniform
+            // DTP: the next chunk's dt tile starts on the matrix core here and is staged after
+            // this chunk's math, which hides its latency (its slot is refetched just below)
+            [[maybe_unused]] const f32x4_t dnext = dt_tile(kn);
             stage_in(kn, buf ^ 1);
             if (t0 > tbeg) store_out(t0 - TCH, END_ONLY ? 0 : buf ^ 1);
             const float4 Bn = rb[kn], Cn = rc[kn];
@@ -665,6 +735,7 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
                 compute(t0, buf, B4, C4, std::true_type{});
             else
                 compute(t0, buf, B4, C4, std::false_type{});
+            if constexpr (DTP) stage_dt(dnext, buf ^ 1);
             B4 = Bn;
             C4 = Cn;
             __builtin_amdgcn_wave_barrier();
@@ -1962,6 +2033,64 @@ int scan_entry(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, int d
 }
 }  // namespace
 }  // namespace hx
+
+namespace hx {
+bool scan_variant_is_auto() { return g_scan_variant == 0; }
+
+bool scan_dtproj_ok(int64_t batch, int64_t seqlen, int64_t dim, int64_t rank) {
+    return rank >= 32 && rank <= 128 && rank % 32 == 0 && dim % 4 == 0 && seqlen * dim < (1LL << 31) &&
+           batch >= 1 && batch <= 65535 && batch * ((dim + 63) / 64) <= 0x7fffffff;
+}
+
+int scan_fwd_dtproj(int64_t batch, int64_t seqlen, int64_t dim, const uint16_t* u, const uint16_t* dtlo,
+                    int64_t rank, const uint16_t* w_dt, const float* A, const uint16_t* B,
+                    const uint16_t* C, const float* D, const uint16_t* z, const float* dt_bias,
+                    uint16_t* out, float* last_state, hipStream_t stream) {
+    HX_REQUIRE(scan_dtproj_ok(batch, seqlen, dim, rank), HX_ERR_UNSUPPORTED,
+               "selective scan with dt_proj: sizes outside the fused path (batch %lld, seqlen %lld, "
+               "dim %lld, dt_rank %lld)", (long long)batch, (long long)seqlen, (long long)dim, (long long)rank);
+    HX_REQUIRE(u && dtlo && w_dt && A && B && C && z && out, HX_ERR_INVALID_INPUT,
+               "selective scan with dt_proj: a required pointer is NULL");
+    HX_REQUIRE(aligned(u, 16) && aligned(z, 16) && aligned(out, 16) && aligned(dtlo, 16) && aligned(w_dt, 16) &&
+                   aligned(B, 32) && aligned(C, 32) && (!D || aligned(D, 16)) && (!dt_bias || aligned(dt_bias, 16)),
+               HX_ERR_UNSUPPORTED, "selective scan with dt_proj: operands not 16-byte aligned");
+    if (seqlen == 0)  // no steps: the final state is the zero initial state
+        return last_state ? hx_fill_f32(batch * dim * 16, 0.0f, last_state, stream) : (int)HX_OK;
+    constexpr int WPB = 4;
+    const int64_t ntiles = (dim + 16 * WPB - 1) / (16 * WPB);
+    WaveSeg sg{seqlen, 1, nullptr, nullptr, nullptr};
+    sg.dtlo = dtlo;
+    sg.wdt = w_dt;
+    sg.rank = (int)rank;
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)(ntiles * batch)), dim3(64 * WPB), 0, stream, seqlen, dim,
+                           (int)ntiles, batch, u, (const uint16_t*)nullptr, A, B, C, D, z, dt_bias, out,
+                           (const float*)nullptr, last_state, sg);
+        HX_LAUNCH_CHECK();
+        return (int)HX_OK;
+    };
+    switch (rank / 32) {
+        case 1: return go(scan_wave3_kernel<uint16_t, 2, true, true, false, WPB, 1>);
+        case 2: return go(scan_wave3_kernel<uint16_t, 2, true, true, false, WPB, 2>);
+        case 3: return go(scan_wave3_kernel<uint16_t, 2, true, true, false, WPB, 3>);
+        default: return go(scan_wave3_kernel<uint16_t, 2, true, true, false, WPB, 4>);
+    }
+}
+}  // namespace hx
+
+extern "C" int hx_selective_scan_dtproj_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dt_rank,
+                                            const void* u, const void* dt_lo, const void* w_dt,
+                                            const float* A, const void* B, const void* C, const float* D,
+                                            const void* z, const float* dt_bias, void* out,
+                                            float* last_state, void* stream) {
+    using namespace hx;
+    HX_REQUIRE(batch >= 0 && seqlen >= 0 && dim >= 0 && dt_rank >= 0, HX_ERR_INVALID_DIMENSION,
+               "selective scan with dt_proj: negative size");
+    if (batch == 0 || dim == 0) return HX_OK;
+    return scan_fwd_dtproj(batch, seqlen, dim, (const uint16_t*)u, (const uint16_t*)dt_lo, dt_rank,
+                           (const uint16_t*)w_dt, A, (const uint16_t*)B, (const uint16_t*)C, D,
+                           (const uint16_t*)z, dt_bias, (uint16_t*)out, last_state, as_stream(stream));
+}
 
 extern "C" int hx_selective_scan_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
                                      int dtype, int delta_softplus, const void* u,

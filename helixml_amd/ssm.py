@@ -124,6 +124,35 @@ def selective_scan_fwd(u, delta, A, B, C, D=None, z=None, dt_bias=None, delta_so
 
 
 @on_launch_stream
+def selective_scan_dtproj_fwd(u, dt_lo, w_dt, A, B, C, D, z, dt_bias, return_last_state=False,
+                              out=None, stream=None):
+    """The block's dt projection and selective scan in one launch (hx_selective_scan_dtproj_fwd):
+    dt = bf16(dt_lo . w_dt^T) formed per 16-step chunk on the matrix core, then the scan with
+    softplus(dt + dt_bias) and the SiLU(z) gate from a zero state. bf16 u, z, out [batch, L, dim],
+    dt_lo [batch, L, dt_rank], w_dt [dim, dt_rank], B, C [batch, L, 16]; A [dim, 16], D, dt_bias
+    [dim] fp32."""
+    bt, L, dim = u.shape
+    r = dt_lo.shape[-1]
+    bf = torch.bfloat16
+    _need(u, "u", (bt, L, dim), bf)
+    _need(dt_lo, "dt_lo", (bt, L, r), bf)
+    _need(w_dt, "w_dt", (dim, r), bf)
+    _need(A, "A", (dim, 16), torch.float32)
+    _need(B, "B", (bt, L, 16), bf)
+    _need(C, "C", (bt, L, 16), bf)
+    _need(D, "D", (dim,), torch.float32)
+    _need(z, "z", (bt, L, dim), bf)
+    _need(dt_bias, "dt_bias", (dim,), torch.float32)
+    if out is None:
+        out = torch.empty_like(u)
+    _need(out, "out", (bt, L, dim), bf)
+    last = torch.empty((bt, dim, 16), device=u.device, dtype=torch.float32) if return_last_state else None
+    _ffi.call("hx_selective_scan_dtproj_fwd", bt, L, dim, r, _ptr(u), _ptr(dt_lo), _ptr(w_dt), _ptr(A),
+              _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(out), _ptr(last), _stream(stream))
+    return (out, last) if return_last_state else out
+
+
+@on_launch_stream
 def selective_state_update(state, u, delta, A, B, C, D=None, z=None, dt_bias=None,
                            delta_softplus=True, out=None, stream=None):
     """One decode step (hx_selective_state_update); updates ``state`` [batch, dim, dstate] in place.

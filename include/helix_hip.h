@@ -242,6 +242,20 @@ int hx_conv1d_silu(int64_t batch, int64_t seqlen, int64_t dim, int64_t width, in
                    const void* x, int64_t ldx, const float* weight, const float* bias, void* y,
                    void* stream);
 
+/* The Mamba block's dt projection and selective scan in one launch (the steps
+ * dt = dt_lo . w_dt^T; y = selective_scan(u, dt, ...) of hx_mamba_block_fwd below): bf16 storage,
+ * dstate 16, softplus(dt + dt_bias), SiLU(z) gate, zero initial state. Each 16-step chunk's
+ * [16 steps x 16 channels] dt tile is formed on the matrix core from dt_lo [batch, seqlen, dt_rank]
+ * and w_dt [dim, dt_rank] (bf16, 16-byte aligned rows), rounded to bf16 as a stored dt would be,
+ * so no dt tensor is written or read. The other operands as hx_selective_scan_fwd's with
+ * dtype HX_BF16 (z required). dt_rank 32, 64, 96 or 128, seqlen * dim < 2^31, dim % 4 == 0;
+ * HX_ERR_UNSUPPORTED otherwise. No counterpart in the reference (its block never projects dt);
+ * a fusion of two of the block's steps. */
+int hx_selective_scan_dtproj_fwd(int64_t batch, int64_t seqlen, int64_t dim, int64_t dt_rank,
+                                 const void* u, const void* dt_lo, const void* w_dt, const float* A,
+                                 const void* B, const void* C, const float* D, const void* z,
+                                 const float* dt_bias, void* out, float* last_state, void* stream);
+
 /* Full Mamba block forward, bf16 storage / fp32 arithmetic:
  *   x|z = x . w_in^T; xc = SiLU(conv1d(x)); dt_lo|B|C = xc . w_x^T; dt = dt_lo . w_dt^T;
  *   y = selective_scan(xc, dt, A, B, C, D, z, dt_bias, softplus); out = y . w_out^T.
@@ -368,6 +382,8 @@ int hx_eye_f32(int64_t n, float* y, void* stream);
  * channels per block), 46 = its split-state form (6 state waves holding half of each channel's
  * states + 2 element waves; bf16 storage needs dim % 8 == 0; the automatic choice for fp32
  * wherever 44 would be, while bf16 keeps 44).
+ * A forced variant also makes the Mamba block and layer forwards run their dt projection and
+ * scan as two steps (with the forced scan kernel) instead of hx_selective_scan_dtproj_fwd.
  * A measurement knob with no reference counterpart; results agree within fp32 rounding for
  * every variant. */
 int hx_set_scan_variant(int variant);

@@ -596,9 +596,11 @@ def numpy_conv1d_silu(x, w, bias=None):
 
 
 def numpy_mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, dt_rank,
-                      round_out=True, return_state=False):
+                      round_out=True, return_state=False, return_terms=False):
     """float64 block with the same bf16 storage rounding points as ``mamba_block`` (and its
-    ``round_out`` / ``return_state`` options)."""
+    ``round_out`` / ``return_state`` options). ``return_terms``: also return |y| . |w_out|^T
+    [Bt, L, d_model], the sum of the magnitudes of the terms the output product adds (the scale
+    a componentwise error bound of that product is relative to)."""
     r = lambda a: bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
     Bt, L, dm = x.shape
     di = w_dt.shape[0]
@@ -615,6 +617,9 @@ def numpy_mamba_block(x, w_in, conv_w, conv_b, w_x, w_dt, dt_bias, A, D, w_out, 
     y, last = numpy_selective_scan(xc, dt, A, Bm, Cm, D, z, dt_bias, True)
     out = r(y).reshape(-1, di) @ r(w_out).T
     out = (r(out) if round_out else out).reshape(Bt, L, dm)
+    if return_terms:
+        terms = (np.abs(r(y)).reshape(-1, di) @ np.abs(r(w_out)).T).reshape(Bt, L, dm)
+        return (out, terms) if not return_state else (out, last, conv, terms)
     if not return_state:
         return out
     conv = np.zeros((Bt, max(K - 1, 1), di))
@@ -631,16 +636,23 @@ def numpy_rmsnorm(X, w, eps):
     return X / np.sqrt((X * X).mean(axis=-1, keepdims=True) + eps) * np.asarray(w, np.float64)
 
 
-def numpy_lm_head(x, params, eps):
+def numpy_lm_head(x, params, eps, return_terms=False):
+    """float64 head: logits = bf16(RMSNorm(x)) . w_head^T. ``return_terms``: also |xn| . |w_head|^T,
+    the sum of the magnitudes of the terms each logit adds (the scale of a componentwise bound)."""
     r = lambda a: bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
     shp = x.shape
     xn = r(numpy_rmsnorm(np.asarray(x, np.float64).reshape(-1, shp[-1]), params["norm_f"], eps))
-    return (xn @ r(params["w_head"]).T).reshape(*shp[:-1], -1)
+    w = r(params["w_head"])
+    logits = (xn @ w.T).reshape(*shp[:-1], -1)
+    if not return_terms:
+        return logits
+    return logits, (np.abs(xn) @ np.abs(w).T).reshape(*shp[:-1], -1)
 
 
-def numpy_lm_prefill(tokens, params, dt_rank, eps=1e-5):
+def numpy_lm_prefill(tokens, params, dt_rank, eps=1e-5, return_terms=False):
     """float64 twin of ``lm_prefill`` with the same bf16 storage rounding points: the exact value
-    of what the f32 restatement computes, for bounding its own rounding."""
+    of what the f32 restatement computes, for bounding its own rounding. ``return_terms``: also
+    the head's term magnitudes (numpy_lm_head)."""
     r = lambda a: bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
     x = np.asarray(params["embed"], np.float64)[np.asarray(tokens)]
     Bt, L, dm = x.shape
@@ -651,11 +663,15 @@ def numpy_lm_prefill(tokens, params, dt_rank, eps=1e-5):
         out, last, conv = numpy_mamba_block(xn, **blk, dt_rank=dt_rank, round_out=False, return_state=True)
         x = x + out
         states.append((last, conv))
+    if return_terms:
+        logits, terms = numpy_lm_head(x, params, eps, return_terms=True)
+        return logits, states, terms
     return numpy_lm_head(x, params, eps), states
 
 
-def numpy_lm_decode_step(tokens, params, states, dt_rank, eps=1e-5):
-    """float64 twin of ``lm_decode_step`` (same bf16 storage rounding points)."""
+def numpy_lm_decode_step(tokens, params, states, dt_rank, eps=1e-5, return_terms=False):
+    """float64 twin of ``lm_decode_step`` (same bf16 storage rounding points); ``return_terms`` as
+    numpy_lm_prefill's."""
     r = lambda a: bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
     x = np.asarray(params["embed"], np.float64)[np.asarray(tokens)]
     new = []
@@ -679,6 +695,9 @@ def numpy_lm_decode_step(tokens, params, states, dt_rank, eps=1e-5):
                                          z[:, None], p["dt_bias"], True, init_state=ssm_st)
         x = x + r(y[:, 0]) @ r(p["w_out"]).T
         new.append((ssm_st, conv_st))
+    if return_terms:
+        logits, terms = numpy_lm_head(x, params, eps, return_terms=True)
+        return logits, new, terms
     return numpy_lm_head(x, params, eps), new
 
 

@@ -695,3 +695,24 @@ def test_reference_execution_shape_restatement_is_bit_identical():
     bg = rng.standard_normal(128).astype(F) * np.float32(0.1)
     bo = rng.standard_normal(64).astype(F) * np.float32(0.1)
     assert np.array_equal(oracle.r_mamba_mlp(X, Wg, bg, Wo, bo), oracle.mamba_mlp(X, Wg, bg, Wo, bo))
+
+
+def test_componentwise_bar_separates_rounding_from_mistakes():
+    """The componentwise metric the block and LM GPU tests use: the f32 restatement sits under one
+    bf16 ulp of the output product's term magnitudes from its float64 twin, while a block that
+    drops the D skip, or a head fed the unnormalised stream, lands far outside CW_ULPS."""
+    from tests.util import CW_ULPS, block_inputs, cw_ulps, lm_params
+    p = block_inputs(2, 37, 64, 256, 16, 32, 4, seed=2037)
+    ref = oracle.mamba_block(**p, dt_rank=32)
+    ref64, terms = oracle.numpy_mamba_block(**p, dt_rank=32, return_terms=True)
+    assert cw_ulps(ref, ref64, terms) <= 1.0
+    bad = oracle.mamba_block(**dict(p, D=np.zeros_like(p["D"])), dt_rank=32)
+    assert cw_ulps(bad, ref64, terms) > 4 * CW_ULPS
+    P = lm_params(2, 32, 64, 16, 8, 4, 256, seed=47)
+    tok = np.random.default_rng(48).integers(0, 256, (2, 9))
+    lg, _ = oracle.lm_prefill(tok, P, 8)
+    lg64, _, lterms = oracle.numpy_lm_prefill(tok, P, 8, return_terms=True)
+    assert cw_ulps(lg, lg64, lterms) <= 1.0
+    bad = dict(P, norm_f=np.asarray(P["norm_f"]) * 1.5)
+    lgb, _ = oracle.lm_prefill(tok, bad, 8)
+    assert cw_ulps(lgb, lg64, lterms) > 4 * CW_ULPS

@@ -5,11 +5,18 @@ Tolerance metric (used by every parity test):
 i.e. elementwise relative error with a denominator floor at 1e-3 of the output's infinity
 norm, so near-zero outputs do not blow the ratio up. Bars: fp32 storage 1e-4, bf16 storage
 2e-2, both against the fp32 CPU oracle on identical inputs.
+
+Outputs of a bf16 product (the Mamba block's out_proj, the LM head) are held elementwise
+componentwise: |g_i - r_i| in bf16 ulps (2^-8) of terms_i = sum_j |a_ij| |b_j|, the magnitudes the
+product adds for output i (cw_ulps), at most CW_ULPS. A few one-ulp flips of bf16 intermediates
+move an output by a few ulps of its terms; where the terms cancel, the relative error above
+would divide that by a small result.
 """
 import numpy as np
 
 TOL_F32 = 1e-4
 TOL_BF16 = 2e-2
+CW_ULPS = 4.0
 
 
 def rel_err(g, r) -> float:
@@ -25,6 +32,16 @@ def norm_err(g, r) -> float:
     g = np.asarray(g, np.float64)
     r = np.asarray(r, np.float64)
     return float(np.abs(g - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+def cw_ulps(g, r, terms) -> float:
+    """max_i |g_i - r_i| / (2^-8 terms_i): the error in bf16 ulps of each output's term magnitudes."""
+    g = np.asarray(g, np.float64)
+    r = np.asarray(r, np.float64)
+    t = np.asarray(terms, np.float64)
+    if r.size == 0:
+        return 0.0
+    return float((np.abs(g - r) / np.maximum(2.0 ** -8 * t, 1e-30)).max())
 
 
 def bf16_round(x):
