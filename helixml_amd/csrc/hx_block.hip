@@ -47,8 +47,7 @@ struct ConvRow {
             uint32_t wds[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                wds[i] = (uint32_t)Storage<uint16_t>::round(v[2 * i]) |
-                         ((uint32_t)Storage<uint16_t>::round(v[2 * i + 1]) << 16);
+                wds[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
             *reinterpret_cast<uint4*>(p) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
         } else if constexpr (VEC && sizeof(T) == 4 && CPT == 4) {
             *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);

@@ -75,6 +75,14 @@ inline bool aligned(const void* p, size_t a) {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
+// fp32 -> bf16 on gfx950's converter (v_cvt_pk_bf16_f32): round to nearest even, a NaN stays a
+// quiet NaN, branch-free. Two values convert in one instruction; `a` lands in the low half.
+typedef float hx_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 hx_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(hx_f32x2{a, b}, hx_bf16x2));
+}
+
 // Storage <-> fp32. bf16 is stored as raw uint16 (upper half of an fp32); conversion to
 // storage rounds to nearest even.
 template <typename T> struct Storage;
@@ -87,11 +95,7 @@ template <> struct Storage<uint16_t> {
         return __uint_as_float(static_cast<uint32_t>(*p) << 16);
     }
     __device__ static inline uint16_t round(float v) {
-        uint32_t x = __float_as_uint(v);
-        if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x007fffffu))  // NaN stays NaN
-            return static_cast<uint16_t>((x >> 16) | 0x40u);
-        x += 0x7fffu + ((x >> 16) & 1u);
-        return static_cast<uint16_t>(x >> 16);
+        return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
     }
     __device__ static inline void store(uint16_t* p, float v) { *p = round(v); }
 };

@@ -307,8 +307,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_bf16_nt_skinny_kernel(int64_t M,
             }
 #pragma unroll
             for (int p = 0; p < PER; p += 2)
-                d[p / 2] = (uint32_t)Storage<uint16_t>::round(v[p]) |
-                           ((uint32_t)Storage<uint16_t>::round(v[p + 1]) << 16);
+                d[p / 2] = pack_bf16x2(v[p], v[p + 1]);
             vstore_bytes<PER * 2>(yb, d);
         } else {
             uint32_t d[PER];
@@ -391,14 +390,9 @@ __device__ inline void store_slab_fast(char* __restrict__ yb, int64_t ldb, const
                     f[2 * k + 1] += __uint_as_float(ow[k] & 0xffff0000u);
                 }
             }
-            // v_cvt_pk_bf16_f32: round to nearest even, as Storage<uint16_t>::round for every
-            // finite normal value
-            typedef float f32v2 __attribute__((ext_vector_type(2)));
-            typedef __bf16 bf16v2 __attribute__((ext_vector_type(2)));
             uint32_t wv[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                wv[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32v2{f[2 * k], f[2 * k + 1]}, bf16v2));
+            for (int k = 0; k < 4; ++k) wv[k] = pack_bf16x2(f[2 * k], f[2 * k + 1]);
             __builtin_nontemporal_store(u32v4{wv[0], wv[1], wv[2], wv[3]}, (g_u32v4*)q);
         } else {
             f32v4 f = v[p][0];
@@ -462,8 +456,7 @@ __device__ inline void store_tile_rows(const GemmOut& o, const float* __restrict
                     uint32_t wv[4];
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
-                        wv[q] = (uint32_t)Storage<uint16_t>::round(v[2 * q]) |
-                                ((uint32_t)Storage<uint16_t>::round(v[2 * q + 1]) << 16);
+                        wv[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
                     *reinterpret_cast<uint4*>(yp) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
                 } else {
                     float* yp = (float*)o.yp(seg) + off;

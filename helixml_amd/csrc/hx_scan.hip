@@ -559,13 +559,10 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
         return acc;
     };
     auto stage_dt = [&](const f32x4_t& acc, int buf) __attribute__((always_inline)) {
-        // round to bf16 with v_cvt_pk_bf16_f32 (round to nearest even, as Storage<uint16_t>::round
-        // for every non-NaN value) and widen back: branch-free
-        typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32v2_t;
-        typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16v2_t;
+        // round to bf16 (pack_bf16x2: round to nearest even) and widen back
 #pragma unroll
         for (int j = 0; j < 4; j += 2) {
-            const uint32_t pk = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32v2_t{acc[j], acc[j + 1]}, bf16v2_t));
+            const uint32_t pk = pack_bf16x2(acc[j], acc[j + 1]);
             s_in[w][buf][1][4 * r + j][c] = __uint_as_float(pk << 16);
             s_in[w][buf][1][4 * r + j + 1][c] = __uint_as_float(pk & 0xffff0000u);
         }

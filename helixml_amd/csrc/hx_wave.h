@@ -46,10 +46,9 @@ template <> struct Vec4<uint16_t> {
                            __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
     }
     __device__ static inline void store(uint16_t* p, float4 v) {
-        using S = Storage<uint16_t>;
         uint2 r;
-        r.x = (uint32_t)S::round(v.x) | ((uint32_t)S::round(v.y) << 16);
-        r.y = (uint32_t)S::round(v.z) | ((uint32_t)S::round(v.w) << 16);
+        r.x = pack_bf16x2(v.x, v.y);
+        r.y = pack_bf16x2(v.z, v.w);
         *reinterpret_cast<uint2*>(p) = r;
     }
 };

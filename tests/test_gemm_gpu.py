@@ -265,3 +265,27 @@ def test_gemm_empty_k_is_bias(dev, gemm_kernel):
     with pytest.raises(UnsupportedOperation):
         _ffi.call("hx_gemm_bf16_splitk", M, N, 0, X.data_ptr(), 8, W.data_ptr(), 8, None, 0, _ffi.HX_F32,
                   Y.data_ptr(), N, N, None, 0, N, None, 0, 2, ws.data_ptr(), ws.numel() * 4, s)
+
+
+@pytest.mark.parametrize("gemm_kernel", [0, 1, 3, 4, 5, 6, 7], indirect=True)
+@pytest.mark.parametrize("scale", [0, -130])
+def test_gemm_bf16_output_rounds_to_nearest_even(dev, gemm_kernel, scale):
+    """bf16 outputs are the round-to-nearest-even of the f32 sums, ties to even included, bit for
+    bit. Integer operands in [-3, 3] make every product and partial sum exact in f32 (|sum| <=
+    9216), whatever the summation order, so the sums are known exactly; most need rounding to 8
+    significant bits and many sit on a tie. Scaled by 2^-130 (each operand by 2^-65) the sums below
+    16 in magnitude become f32 subnormals, which must round the same way."""
+    g = torch.Generator().manual_seed(11)
+    M, N, K = 256, 128, 1024
+    Xi = torch.randint(-3, 4, (M, K), generator=g).float()
+    Wi = torch.randint(-3, 4, (N, K), generator=g).float()
+    exact = (Xi.double() @ Wi.double().T) * 2.0 ** scale  # exact: integer sums below 2^24
+    s = 2.0 ** (scale // 2)
+    X = (Xi * s).to(torch.bfloat16).to(dev)
+    W = (Wi * s).to(torch.bfloat16).to(dev)
+    y = ssm.gemm_bf16(X, W, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    want = bf16_round(exact.float().numpy())
+    got = y.float().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+        f"{int((got != want).sum())} of {got.size} outputs differ from round-to-nearest-even"
