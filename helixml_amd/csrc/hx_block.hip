@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void conv1d_silu_kernel(int L, int Dm, int nru
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ bias,
                                                           T* __restrict__ y) {
-    const int d0 = (blockIdx.y * 256 + threadIdx.x) * CPT;
+    const int d0 = (blockIdx.y * blockDim.x + threadIdx.x) * CPT;
     if (d0 >= Dm) return;
     const int b = blockIdx.x / nruns;
     const int t0 = (blockIdx.x - b * nruns) * TT;
@@ -77,6 +77,36 @@ __global__ __launch_bounds__(256) void conv1d_silu_kernel(int L, int Dm, int nru
     }
     const T* xb = x + (int64_t)b * L * ldx + d0;
     T* yb = y + (int64_t)b * L * Dm + d0;
+    if constexpr (VEC && sizeof(T) == 2 && CPT == 8) {
+        if (t0 + TT <= L) {
+            // a whole run: every input row of it (and the halo) is loaded up front, raw, so the
+            // thread has all its loads in flight at once; then the same arithmetic as below
+            uint4 raw[TT + KW - 1];
+#pragma unroll
+            for (int j = 0; j < TT + KW - 1; ++j) {
+                const int tt = t0 - (KW - 1) + j;
+                raw[j] = tt >= 0 ? *reinterpret_cast<const uint4*>(xb + (int64_t)tt * ldx) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int s = 0; s < TT; ++s) {
+                float o[CPT];
+#pragma unroll
+                for (int i = 0; i < CPT; ++i) {
+                    float acc = bv[i];
+#pragma unroll
+                    for (int j = 0; j < KW; ++j) {
+                        const uint4 q = raw[s + j];
+                        const uint32_t wd = (i >> 1) == 0 ? q.x : (i >> 1) == 1 ? q.y : (i >> 1) == 2 ? q.z : q.w;
+                        const float xv = __uint_as_float((i & 1) ? (wd & 0xffff0000u) : (wd << 16));
+                        acc = fmaf(wk[j][i], xv, acc);
+                    }
+                    o[i] = silu(acc);
+                }
+                ConvRow<T, CPT, VEC>::store(yb + (int64_t)(t0 + s) * Dm, o);
+            }
+            return;
+        }
+    }
     float win[KW][CPT];  // win[KW-1] = row t, win[KW-2] = row t-1, ...
 #pragma unroll
     for (int j = 0; j < KW - 1; ++j) {
@@ -109,14 +139,28 @@ __global__ __launch_bounds__(256) void conv1d_silu_kernel(int L, int Dm, int nru
     }
 }
 
+template <typename T, int KW, int CPT, bool VEC, int TT>
+void launch_conv_tt(int64_t Bt, int64_t L, int64_t Dm, int64_t groups, int nthr, const void* x,
+                    int64_t ldx, const float* w, const float* b, void* y, hipStream_t s) {
+    const int nruns = (int)((L + TT - 1) / TT);
+    dim3 grid((unsigned)(Bt * nruns), (unsigned)((groups + nthr - 1) / nthr));
+    hipLaunchKernelGGL((conv1d_silu_kernel<T, KW, CPT, VEC, TT>), grid, dim3(nthr), 0, s, (int)L,
+                       (int)Dm, nruns, (const T*)x, ldx, w, b, (T*)y);
+}
+
 template <typename T, int KW, int CPT, bool VEC>
 void launch_conv_k(int64_t Bt, int64_t L, int64_t Dm, const void* x, int64_t ldx, const float* w,
                    const float* b, void* y, hipStream_t s) {
-    constexpr int TT = 16;
-    const int nruns = (int)((L + TT - 1) / TT);
-    dim3 grid((unsigned)(Bt * nruns), (unsigned)((Dm / CPT + 255) / 256));
-    hipLaunchKernelGGL((conv1d_silu_kernel<T, KW, CPT, VEC, TT>), grid, dim3(256), 0, s, (int)L,
-                       (int)Dm, nruns, (const T*)x, ldx, w, b, (T*)y);
+    // threads per block: the row's channel groups rounded up to whole waves, at most 256
+    const int64_t groups = (Dm + CPT - 1) / CPT;
+    const int nthr = groups >= 256 ? 256 : (int)((groups + 63) / 64 * 64);
+    // runs of 32 steps (half the halo re-reads of 16) where they still give every SIMD 8 waves;
+    // measured: config 5 (16 x 8192 x 1024) 32-step runs faster, config 3 (4 x 4096 x 4096) 16
+    const int64_t waves32 = Bt * ((L + 31) / 32) * ((groups + nthr - 1) / nthr) * (nthr / 64);
+    if (waves32 >= 32 * (int64_t)device_cus())
+        launch_conv_tt<T, KW, CPT, VEC, 32>(Bt, L, Dm, groups, nthr, x, ldx, w, b, y, s);
+    else
+        launch_conv_tt<T, KW, CPT, VEC, 16>(Bt, L, Dm, groups, nthr, x, ldx, w, b, y, s);
 }
 
 template <typename T, int CPT, bool VEC>

@@ -60,6 +60,28 @@ def test_conv1d_silu_bf16_strided_rows(dev):
     assert e2 < TOL_BF16, e2
 
 
+def test_conv1d_silu_bf16_long_runs(dev):
+    """At config-5 size (16 x 8197 x 1024, a ragged last run) the kernel takes 32-step runs with
+    every input row loaded up front; one sequence alone takes 16-step runs. Both give the same
+    bits, and stay within the bf16 output rounding of the oracle."""
+    rng = np.random.default_rng(8)
+    bt, L, dim = 16, 8197, 1024
+    x = torch.randn((bt, L, dim), generator=torch.Generator().manual_seed(8)).to(dev, BF)
+    w = (rng.standard_normal((dim, 4)) * 0.5).astype(np.float32)
+    b = rng.standard_normal(dim).astype(np.float32)
+    wd, bd = torch.from_numpy(w).to(dev), torch.from_numpy(b).to(dev)
+    y = ssm.conv1d_silu(x, wd, bd)
+    for s in (0, bt - 1):
+        ys = ssm.conv1d_silu(x[s:s + 1].contiguous(), wd, bd)
+        assert torch.equal(ys[0], y[s]), f"sequence {s}: 32-step and 16-step runs differ"
+    xs = x[bt - 1].float().cpu().numpy()[None]
+    r = oracle.conv1d_silu(xs, w, b)
+    g = y[bt - 1:].float().cpu().numpy()
+    e1, e2 = norm_err(g, r), rel_err(g, bf16_round(r))
+    assert e1 <= 2.0 ** -8, e1
+    assert e2 < TOL_BF16, e2
+
+
 def test_conv1d_rejects_bad_width_and_dim(dev):
     x = torch.zeros((1, 4, 8), device=dev)
     with pytest.raises(UnsupportedOperation):
