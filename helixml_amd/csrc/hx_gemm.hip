@@ -347,9 +347,32 @@ __global__ __launch_bounds__(NW * 64) void gemm_bf16_nt_skinny_kernel(int64_t M,
 // `yb` points at the slab's first output element, `ldb` is the output row pitch in bytes, both
 // 16-byte aligned. bf16: 8 lanes x 8 columns per row, 8 rows per pass; fp32: 16 lanes x 4
 // columns, 4 rows per pass.
-// ACC adds the existing output (Y += X W^T), in the same order as the general path.
-template <bool BF16, bool ACC>
-__device__ inline void store_slab_fast(char* __restrict__ yb, int64_t ldb, const float* st, int lane) {
+// ACC adds the existing output (Y += X W^T), in the same order as the general path; the caller
+// loads it (load_slab_old) ahead of time.
+typedef uint32_t slab_u32v4 __attribute__((ext_vector_type(4)));
+template <bool BF16, int ROWS = 32> struct SlabGeom {  // a slab: ROWS x 64 columns
+    static constexpr int LPR = BF16 ? 8 : 16;  // lanes per row
+    static constexpr int RPP = 64 / LPR;       // rows per pass
+    static constexpr int NP = ROWS / RPP;      // passes
+    static constexpr int VW = BF16 ? 8 : 4;    // columns per lane
+};
+
+// The existing outputs of a slab, as store_slab_fast's lane reads them (global loads: a flat
+// access also counts in lgkmcnt and would hold up the LDS waits).
+template <bool BF16, int ROWS = 32>
+__device__ inline void load_slab_old(const char* __restrict__ yb, int64_t ldb, int lane,
+                                     slab_u32v4 (&old)[SlabGeom<BF16, ROWS>::NP]) {
+    using G = SlabGeom<BF16, ROWS>;
+    typedef __attribute__((address_space(1))) const slab_u32v4 g_u32v4;
+    const int rl = lane / G::LPR, cl = (lane % G::LPR) * G::VW;
+    const char* yp = yb + rl * ldb + cl * (BF16 ? 2 : 4);
+#pragma unroll
+    for (int p = 0; p < G::NP; ++p) old[p] = *(g_u32v4*)(yp + p * G::RPP * ldb);
+}
+
+template <bool BF16, bool ACC, int ROWS = 32>
+__device__ inline void store_slab_fast(char* __restrict__ yb, int64_t ldb, const float* st, int lane,
+                                       const slab_u32v4 (&old)[SlabGeom<BF16, ROWS>::NP]) {
     // explicit address spaces: LDS reads, and global (not flat) output accesses, since a flat
     // access also counts in lgkmcnt and would hold up the next slab's LDS waits until it completes
     typedef uint32_t u32v4 __attribute__((ext_vector_type(4)));
@@ -357,21 +380,13 @@ __device__ inline void store_slab_fast(char* __restrict__ yb, int64_t ldb, const
     typedef __attribute__((address_space(1))) u32v4 g_u32v4;
     typedef __attribute__((address_space(1))) f32v4 g_f32v4;
     typedef __attribute__((address_space(3))) const f32v4 l_f32v4;
-    constexpr int LPR = BF16 ? 8 : 16;    // lanes per row
-    constexpr int RPP = 64 / LPR;         // rows per pass
-    constexpr int NP = 32 / RPP;          // passes
-    constexpr int VW = BF16 ? 8 : 4;      // columns per lane
-    const int rl = lane / LPR, cl = (lane % LPR) * VW;
+    using G = SlabGeom<BF16, ROWS>;
+    constexpr int RPP = G::RPP, NP = G::NP, VW = G::VW;
+    const int rl = lane / G::LPR, cl = (lane % G::LPR) * VW;
     l_f32v4* sp = (l_f32v4*)(st + rl * 68 + cl);
     char* yp = yb + rl * ldb + cl * (BF16 ? 2 : 4);
-    // all of the slab's loads first (the outputs read for ACC, then the staged values), so their
-    // latencies overlap instead of each store waiting on the next load
+    // all of the slab's LDS reads first, so their latencies overlap
     f32v4 v[NP][VW / 4];
-    u32v4 old[ACC ? NP : 1];
-    if constexpr (ACC) {
-#pragma unroll
-        for (int p = 0; p < NP; ++p) old[p] = *(const g_u32v4*)(yp + p * RPP * ldb);
-    }
 #pragma unroll
     for (int p = 0; p < NP; ++p)
 #pragma unroll
@@ -407,19 +422,19 @@ __device__ inline void store_slab_fast(char* __restrict__ yb, int64_t ldb, const
     }
 }
 
-// Writes a wave's staged 32 x 64 fp32 tile (st, row stride 68) to the outputs: rows of 64
+// Writes a wave's staged nrows x 64 fp32 tile (st, row stride 68) to the outputs: rows of 64
 // columns as 16-byte vectors (8 bf16 or 4 fp32 per lane) with bias, SiLU and accumulate; a
 // vector that would straddle a column split or the N edge falls back to element stores.
 __device__ inline void store_tile_rows(const GemmOut& o, const float* __restrict__ bias,
                                        const float* st, int64_t M, int64_t N, int64_t row0,
-                                       int64_t col0, int lane) {
+                                       int64_t col0, int lane, int nrows = 32) {
         // rows of 64 columns: o.out_bf16 -> 8 lanes x 8 columns per row (8 rows per pass),
         // fp32 -> 16 lanes x 4 columns per row (4 rows per pass)
         const int vw = o.out_bf16 ? 8 : 4;
         const int lpr = 64 / vw;             // lanes per row
         const int rpp = 64 / lpr;            // rows per pass
         const int rl = lane / lpr, cl = (lane % lpr) * vw;
-        for (int rr = rl; rr < 32; rr += rpp) {
+        for (int rr = rl; rr < nrows; rr += rpp) {
             const int64_t row = row0 + rr;
             const int64_t col = col0 + cl;
             if (row >= M || col >= N) continue;
@@ -787,24 +802,31 @@ __device__ inline int xswz(int row) {  // XOR applied to the 16-byte chunk index
 // Epilogue of one wave's 128 x 128 sub-tile when it lies inside one output with aligned rows and
 // neither bias nor SiLU applies: 8 slabs of 32 x 64, each staged through the wave's LDS slab and
 // written with store_slab_fast. `yb` points at the sub-tile's first output element.
+// ACC: the existing outputs of each slab are loaded one slab ahead, so their latency overlaps the
+// previous slab's staging and stores instead of stalling every slab.
 template <bool BF16, bool ACC>
 __device__ __forceinline__ void d256_epilogue_fast(f32x16 (&acc)[4][4], float* st, char* yb, int64_t ldb,
                                                    int lane) {
+    constexpr int NP = SlabGeom<BF16>::NP;
+    auto slab_ptr = [&](int sl) { return yb + (sl >> 1) * 32 * ldb + (sl & 1) * 64 * (BF16 ? 2 : 4); };
+    slab_u32v4 old[2][NP];
+    if constexpr (ACC) load_slab_old<BF16>(slab_ptr(0), ldb, lane, old[0]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    st[row * 68 + j * 32 + (lane & 31)] = acc[i][2 * jj + j][r];
-                }
-            __builtin_amdgcn_wave_barrier();
-            store_slab_fast<BF16, ACC>(yb + i * 32 * ldb + jj * 64 * (BF16 ? 2 : 4), ldb, st, lane);
-            __builtin_amdgcn_wave_barrier();
+    for (int sl = 0; sl < 8; ++sl) {  // slab (i, jj) = (sl / 2, sl % 2)
+        const int i = sl >> 1, jj = sl & 1;
+        if constexpr (ACC) {
+            if (sl + 1 < 8) load_slab_old<BF16>(slab_ptr(sl + 1), ldb, lane, old[(sl + 1) & 1]);
         }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                st[row * 68 + j * 32 + (lane & 31)] = acc[i][2 * jj + j][r];
+            }
+        __builtin_amdgcn_wave_barrier();
+        store_slab_fast<BF16, ACC>(slab_ptr(sl), ldb, st, lane, old[sl & 1]);
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -903,7 +925,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
         else if (after == 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(QPW) : "memory");
         else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
-    static_assert(NST >= 2 && NST <= 4 && (SUB == 2 || SUB == 4) && 3 * QPW <= 63, "ring depth / K tile");
+    static_assert(NST >= 2 && NST <= 4 && (SUB == 2 || SUB == 4) && 3 * QPW <= 63 && QPW % 8 == 0,
+                  "ring depth / K tile");
     bf16x8 fg[2][8];  // [buffer][A rows 0..3, B rows 0..3] (32-row fragments)
 #pragma unroll
     for (int t = 0; t < NST; ++t)
@@ -917,10 +940,11 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
 #pragma unroll
         for (int s = 0; s < SUB; ++s) {
             const int cur = s & 1, nxt = cur ^ 1;
-            if (s == SUB - 1) {
-                if (kt + 1 < nk) wait_barrier(nk - 2 - kt < NST - 2 ? nk - 2 - kt : NST - 2);
-                if (kt + NST < nk) issue(kt + NST);
-            }
+            // the last sub-step issues tile kt + NST's loads between its MFMAs, QPW / 8 after each
+            // pair, rather than in one burst before them (measured: config 3 in_proj 493 -> 468 us,
+            // out_proj 231 -> 223 us, same bits)
+            const bool ilv = s == SUB - 1 && kt + NST < nk;  // uniform
+            if (s == SUB - 1 && kt + 1 < nk) wait_barrier(nk - 2 - kt < NST - 2 ? nk - 2 - kt : NST - 2);
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
 #pragma unroll
@@ -932,13 +956,23 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
                 // (the last tile's last sub-step reads unused fragments of the next stage, which
                 // no load targets any more, so that no sub-step branches)
                 fg[nxt][q] = s < SUB - 1 ? frag(stg, s + 1, q) : frag(nstg, 0, q);
+                if (ilv) {
+                    char* stage = sbase + (int)((kt + NST) % NST) * STB;
+#pragma unroll
+                    for (int u = 0; u < QPW / 8; ++u) {
+                        const int j = q * (QPW / 8) + u;
+                        __builtin_amdgcn_global_load_lds((gvoid_t*)(src[j] + (kt + NST) * KB),
+                                                         (lvoid_t*)(stage + (wave * QPW + j) * 1024), 16, 0, 0);
+                    }
+                }
             }
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+                __builtin_amdgcn_sched_group_barrier(0x020, QPW / 8, 0);  // loads (last sub-step)
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
         stg = nstg;
@@ -988,6 +1022,250 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
 
 
 
+// Epilogue of the persistent kernel for one wave's 128 x 128 sub-tile inside one output with
+// aligned rows and no bias/SiLU: 16 slabs of 16 x 64 through the wave's own 16-row LDS slab
+// (the K-tile ring keeps filling meanwhile); ACC loads each slab's existing outputs a slab ahead.
+template <bool BF16, bool ACC>
+__device__ __forceinline__ void d256p_epilogue_fast(f32x16 (&acc)[4][4], float* st, char* yb, int64_t ldb,
+                                                    int lane) {
+    constexpr int NP = SlabGeom<BF16, 16>::NP;
+    // slab sl: 32-row block i = sl / 4, 16-row half h = (sl / 2) % 2, 64-column half jj = sl % 2
+    auto slab_ptr = [&](int sl) {
+        return yb + ((sl >> 2) * 32 + ((sl >> 1) & 1) * 16) * ldb + (sl & 1) * 64 * (BF16 ? 2 : 4);
+    };
+    slab_u32v4 old[2][NP];
+    if constexpr (ACC) load_slab_old<BF16, 16>(slab_ptr(0), ldb, lane, old[0]);
+#pragma unroll
+    for (int sl = 0; sl < 16; ++sl) {
+        const int i = sl >> 2, h = (sl >> 1) & 1, jj = sl & 1;
+        if constexpr (ACC) {
+            if (sl + 1 < 16) load_slab_old<BF16, 16>(slab_ptr(sl + 1), ldb, lane, old[(sl + 1) & 1]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                const int r = 8 * h + rr;  // the accumulator rows of this half
+                const int row = 8 * ((r >> 2) - 2 * h) + 4 * (lane >> 5) + (r & 3);
+                st[row * 68 + j * 32 + (lane & 31)] = acc[i][2 * jj + j][r];
+            }
+        __builtin_amdgcn_wave_barrier();
+        store_slab_fast<BF16, ACC, 16>(slab_ptr(sl), ldb, st, lane, old[sl & 1]);
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// Persistent form of the 256 x 256 kernel: one block per CU walks its tiles (block b takes tile
+// ids b, b + gridDim.x, ... in tile_of's order, so each tile stays on the XCD the one-tile-per-
+// block launch gives it), and the K-tile ring runs on across tiles: the loads of the next tile's
+// first K tiles are issued during this tile's last ones, so they are in flight while this tile's
+// epilogue stores, and the next tile starts without a pipeline fill. The epilogue stages 16-row
+// slabs in an LDS region of its own (NST stages + 4 x 16 x 68 floats). Each tile's arithmetic is
+// the 256 x 256 kernel's: the same MFMA products, K ascending.
+template <int KB, int NST>
+__global__ __launch_bounds__(256) void gemm_bf16_nt_d256p_kernel(int64_t M, int64_t N, int64_t K,
+                                                                 const uint16_t* __restrict__ X,
+                                                                 int64_t ldx,
+                                                                 const uint16_t* __restrict__ W,
+                                                                 int64_t ldw,
+                                                                 const float* __restrict__ bias,
+                                                                 GemmOut o) {
+    constexpr int RB = KB * 2;              // bytes per tile row
+    constexpr int CPR = KB / 8;             // 16-byte chunks per row
+    constexpr int RPK = 1024 / RB;          // rows per KiB (one load instruction)
+    constexpr int STB = (XBM + XBN) * RB;   // stage bytes
+    constexpr int QPW = STB / 1024 / 4;     // load instructions per wave per tile
+    constexpr int QA = XBM * RB / 1024;     // KiB regions of A
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    char* sbase = reinterpret_cast<char*>(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nbx = (int)((N + XBN - 1) / XBN);
+    const int nb = nbx * (int)((M + XBM - 1) / XBM);
+    const int nblk = gridDim.x;  // <= nb
+    const int ntl = (nb - (int)blockIdx.x + nblk - 1) / nblk;  // this block's tiles
+    const int64_t nk = K / KB;
+    const int64_t total = (int64_t)ntl * nk;  // K tiles over all of this block's tiles
+    float* st = reinterpret_cast<float*>(sbase + NST * STB) + wave * (16 * 68);
+
+    // the global sources of the tile whose K tiles are being issued (set when the issue moves to
+    // the next tile): wave w issues KiB regions q = QPW*w .. of a stage, as in the 256 x 256 kernel
+    const uint16_t* src[QPW];
+    int src_tile = -1;
+    auto set_src = [&](int i) __attribute__((always_inline)) {
+        int tm, tn;
+        tile_of(nbx, nb, (int)blockIdx.x + i * nblk, tm, tn);
+        const int64_t m0 = (int64_t)tm * XBM, n0 = (int64_t)tn * XBN;
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const int q = wave * QPW + j;
+            const bool isA = q < QA;
+            const int row = (isA ? q : q - QA) * RPK + lane / CPR;
+            const int chunk = (lane % CPR) ^ xswz<KB>(row);
+            if (isA) {
+                const int64_t gr = m0 + row < M ? m0 + row : M - 1;
+                src[j] = X + gr * ldx + chunk * 8;
+            } else {
+                const int64_t gr = n0 + row < N ? n0 + row : N - 1;
+                src[j] = W + gr * ldw + chunk * 8;
+            }
+        }
+        src_tile = i;
+    };
+    // global K tile p of this block: its offset along K in the tile and its stage (the sources
+    // move on to p's tile first)
+    auto prep = [&](int64_t p, int64_t& koff, char*& stage) __attribute__((always_inline)) {
+        const int i = (int)(p / nk);
+        koff = (p - (int64_t)i * nk) * KB;
+        if (i != src_tile) set_src(i);
+        stage = sbase + (int)(p % NST) * STB;
+    };
+    auto load = [&](int j, int64_t koff, char* stage) __attribute__((always_inline)) {
+        __builtin_amdgcn_global_load_lds((gvoid_t*)(src[j] + koff), (lvoid_t*)(stage + (wave * QPW + j) * 1024),
+                                         16, 0, 0);
+    };
+    auto issue = [&](int64_t p) __attribute__((always_inline)) {
+        int64_t koff;
+        char* stage;
+        prep(p, koff, stage);
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) load(j, koff, stage);
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int fr = lane & 31;
+    const int fc = lane >> 5;
+    constexpr int SUB = KB / 16;
+    auto frag = [&](int stg, int s, int q) __attribute__((always_inline)) {
+        const char* stage = sbase + stg * STB;
+        const int off = ((2 * s + fc) ^ xswz<KB>(fr)) << 4;
+        return q < 4 ? *reinterpret_cast<const bf16x8*>(stage + (wm * 128 + fr) * RB + q * 32 * RB + off)
+                     : *reinterpret_cast<const bf16x8*>(stage + XBM * RB + (wn * 128 + fr) * RB +
+                                                        (q - 4) * 32 * RB + off);
+    };
+    // wait until at most `after` K tiles' loads are in flight (this wave's), then the barrier;
+    // the epilogue's stores count in vmcnt too, so the first wait of a tile also covers them
+    auto wait_barrier = [&](int64_t after) __attribute__((always_inline)) {
+        if (after >= 3) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(3 * QPW) : "memory");
+        else if (after == 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * QPW) : "memory");
+        else if (after == 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(QPW) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    static_assert(NST >= 2 && NST <= 4 && (SUB == 2 || SUB == 4) && 3 * QPW <= 63 && QPW % 8 == 0,
+                  "ring depth / K tile");
+    bf16x8 fg[2][8];
+#pragma unroll
+    for (int t = 0; t < NST; ++t)
+        if (t < total) issue(t);
+    wait_barrier((total < NST ? total : NST) - 1);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) fg[0][q] = frag(0, 0, q);
+    int stg = 0;
+    int64_t p = 0;
+    for (int i = 0; i < ntl; ++i) {
+        int tm, tn;
+        tile_of(nbx, nb, (int)blockIdx.x + i * nblk, tm, tn);
+        for (int64_t kt = 0; kt < nk; ++kt, ++p) {
+            const int nstg = stg + 1 == NST ? 0 : stg + 1;
+#pragma unroll
+            for (int s = 0; s < SUB; ++s) {
+                const int cur = s & 1, nxt = cur ^ 1;
+                // the last sub-step issues K tile p + NST's loads between its MFMAs, QPW / 8
+                // after each pair (uniform condition)
+                const bool ld = s == SUB - 1 && p + NST < total;
+                int64_t koff = 0;
+                char* lstage = sbase;
+                if (s == SUB - 1) {
+                    if (p + 1 < total) wait_barrier(total - 2 - p < NST - 2 ? total - 2 - p : NST - 2);
+                    if (ld) prep(p + NST, koff, lstage);
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+#pragma unroll
+                    for (int jj = 0; jj < 2; ++jj) {
+                        const int a = q >> 1, b = (q & 1) * 2 + jj;
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fg[cur][a], fg[cur][4 + b],
+                                                                            acc[a][b], 0, 0, 0);
+                    }
+                    // the last sub-step reads the next K tile's first fragments (the next tile's,
+                    // after a tile's last K tile; past the block's last K tile, unused stage data)
+                    fg[nxt][q] = s < SUB - 1 ? frag(stg, s + 1, q) : frag(nstg, 0, q);
+                    if (ld) {
+#pragma unroll
+                        for (int u = 0; u < QPW / 8; ++u) load(q * (QPW / 8) + u, koff, lstage);
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+                    __builtin_amdgcn_sched_group_barrier(0x020, QPW / 8, 0);  // loads
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            stg = nstg;
+        }
+
+        // epilogue of tile i; then its accumulators restart at zero
+        const int64_t m0 = (int64_t)tm * XBM, n0 = (int64_t)tn * XBN;
+        const int64_t r0 = m0 + wm * 128, c0 = n0 + wn * 128;
+        int seg = 0;
+        int64_t cc = c0;
+        if (c0 >= o.split2) { seg = 2; cc = c0 - o.split2; }
+        else if (c0 >= o.split1) { seg = 1; cc = c0 - o.split1; }
+        const int64_t seg_end = seg == 0 ? o.split1 : seg == 1 ? o.split2 : N;
+        const int64_t es = o.out_bf16 ? 2 : 4;
+        char* yb = (char*)o.yp(seg) + (r0 * o.ldp(seg) + cc) * es;
+        const int64_t ldb = o.ldp(seg) * es;
+        if (!bias && !(o.act & 1) && r0 + 128 <= M && c0 + 128 <= seg_end &&
+            (((uintptr_t)yb | (uint64_t)ldb) & 15) == 0) {
+            const int kind = (o.out_bf16 ? 0 : 2) + ((o.act & 2) ? 1 : 0);
+            if (kind == 0) d256p_epilogue_fast<true, false>(acc, st, yb, ldb, lane);
+            else if (kind == 1) d256p_epilogue_fast<true, true>(acc, st, yb, ldb, lane);
+            else if (kind == 2) d256p_epilogue_fast<false, false>(acc, st, yb, ldb, lane);
+            else d256p_epilogue_fast<false, true>(acc, st, yb, ldb, lane);
+        } else {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                    for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+#pragma unroll
+                            for (int rr = 0; rr < 8; ++rr) {
+                                const int r = 8 * h + rr;
+                                const int row = 8 * ((r >> 2) - 2 * h) + 4 * (lane >> 5) + (r & 3);
+                                st[row * 68 + j * 32 + (lane & 31)] = acc[a][2 * jj + j][r];
+                            }
+                        __builtin_amdgcn_wave_barrier();
+                        store_tile_rows(o, bias, st, M, N, r0 + a * 32 + h * 16, c0 + jj * 64, lane, 16);
+                        __builtin_amdgcn_wave_barrier();
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+    }
+}
+
 // Sum of the S split-K partials P[z][M][N] (fp32, row stride N) in slice order, then bias, SiLU,
 // accumulate and the column split of o, one element per thread (consecutive threads take
 // consecutive columns).
@@ -1035,6 +1313,29 @@ int launch_d256(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, con
     dim3 lg((unsigned)((N + XBN - 1) / XBN), (unsigned)((M + XBM - 1) / XBM));
     hipLaunchKernelGGL((gemm_bf16_nt_d256_kernel<KB, NST>), lg, dim3(256), bytes, as_stream(stream), M, N, K,
                        (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o, (int64_t)0);
+    HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+
+template <int KB, int NST>
+size_t d256p_bytes() {
+    return (size_t)NST * (hx::XBM + hx::XBN) * KB * 2 + 4 * 16 * 68 * sizeof(float);
+}
+
+template <int KB, int NST>
+bool d256p_ok() {
+    return hx::grant_dynamic_lds((const void*)hx::gemm_bf16_nt_d256p_kernel<KB, NST>, d256p_bytes<KB, NST>(), 0);
+}
+
+template <int KB, int NST>
+int launch_d256p(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* W, int64_t ldw,
+                 const float* bias, const hx::GemmOut& o, void* stream) {
+    using namespace hx;
+    const int64_t nb = ((N + XBN - 1) / XBN) * ((M + XBM - 1) / XBM);
+    const int64_t cus = device_cus();
+    const unsigned grid = (unsigned)(nb < cus ? nb : cus);  // one block per CU (the LDS allows one)
+    const size_t bytes = d256p_bytes<KB, NST>();
+    hipLaunchKernelGGL((gemm_bf16_nt_d256p_kernel<KB, NST>), dim3(grid), dim3(256), bytes, as_stream(stream), M, N, K, (const uint16_t*)X, ldx, (const uint16_t*)W, ldw, bias, o);
     HX_LAUNCH_CHECK();
     return HX_OK;
 }
@@ -1108,6 +1409,12 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     // the 32-wide K tile where K is not a multiple of 64 (config 5 dt_proj, K = 32)
     const bool d256_auto = g_gemm_kernel == 0 && N >= 256 && M >= 256 &&
                            ((M + XBM - 1) / XBM) * ((N + XBN - 1) / XBN) >= 256;
+    // the persistent form only when forced: alone it is ahead where K is short (config 5 in_proj
+    // 309 -> 291 us, head 45 -> 42 us; behind for long K, config 3 in_proj 458 vs 451 us), but
+    // the 12-layer config-5 prefill measured slower with it (17.97 vs 17.79 ms, same box). Both
+    // forms give the same bits.
+    if (vec && K > 0 && K % 64 == 0 && g_gemm_kernel == 8 && d256p_ok<64, 2>())
+        return launch_d256p<64, 2>(M, N, K, X, ldx, W, ldw, bias, o, stream);
     if (vec && K > 0 && K % 64 == 0 && (g_gemm_kernel == 5 || d256_auto) && d256_ok<64, 2>())
         return launch_d256<64, 2>(M, N, K, X, ldx, W, ldw, bias, o, stream);
     if (vec && K > 0 && K % 32 == 0 && (g_gemm_kernel == 6 || (d256_auto && K % 64 != 0)) && d256_ok<32, 4>())
@@ -1222,8 +1529,8 @@ extern "C" int hx_gemm_bf16_splitk(int64_t M, int64_t N, int64_t K, const void* 
 
 extern "C" int hx_set_gemm_kernel(int k) {
     using namespace hx;
-    HX_REQUIRE(k >= 0 && k <= 7 && k != 2, HX_ERR_INVALID_INPUT,
-               "hx_set_gemm_kernel: %d (0 auto, 1, 3, 4, 5, 6, 7)", k);
+    HX_REQUIRE(k >= 0 && k <= 8 && k != 2, HX_ERR_INVALID_INPUT,
+               "hx_set_gemm_kernel: %d (0 auto, 1, 3, 4, 5, 6, 7, 8)", k);
     g_gemm_kernel = k;
     return HX_OK;
 }

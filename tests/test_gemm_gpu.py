@@ -68,7 +68,7 @@ def gemm_kernel(dev, request):
     ssm.set_gemm_kernel(0)
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6, 7], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6, 7, 8], indirect=True)
 @pytest.mark.parametrize("M,N,K", [(512, 256, 512), (300, 200, 136), (257, 129, 64), (1024, 2048, 1024),
                                    (100, 72, 1000), (256, 64, 1024), (33, 40, 24), (300, 260, 192),
                                    (600, 136, 128)])
@@ -88,7 +88,7 @@ def test_gemm_tile_kernels_fp32_out(dev, gemm_kernel, M, N, K, act):
     assert err <= 1e-5, err
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6, 7], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6, 7, 8], indirect=True)
 @pytest.mark.parametrize("splits", [(128, 144), (100, 133), (8, 16)])
 def test_gemm_tile_kernels_splits_bf16(dev, gemm_kernel, splits):
     """Column splits on vector boundaries and straddling them (100, 133 are not multiples of 8)."""
@@ -103,7 +103,7 @@ def test_gemm_tile_kernels_splits_bf16(dev, gemm_kernel, splits):
     assert err <= 2 ** -7, err  # within one bf16 ulp of the rounded reference
 
 
-@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6, 7], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [1, 3, 4, 5, 6, 7, 8], indirect=True)
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 def test_gemm_accumulate_into_output(dev, gemm_kernel, out_dtype):
     """act bit 1: Y += X . W^T (the residual add of a pre-norm layer)."""
@@ -123,7 +123,7 @@ def test_gemm_accumulate_into_output(dev, gemm_kernel, out_dtype):
     assert err <= (1e-5 if out_dtype == torch.float32 else 2 ** -8), err
 
 
-@pytest.mark.parametrize("gemm_kernel", [0, 5, 6], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [0, 5, 6, 8], indirect=True)
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", [(512, 512, 256), (700, 520, 64), (1024, 768, 1088)])
 def test_gemm_whole_tile_stores(dev, gemm_kernel, out_dtype, M, N, K):
@@ -177,7 +177,7 @@ def test_gemm_splitk_rejects(dev):
                   _ffi.HX_F32, Y.data_ptr(), 32, 32, None, 0, 32, None, 0, 2, ws.data_ptr(), 64, None)
 
 
-@pytest.mark.parametrize("gemm_kernel", [4, 5], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [4, 5, 8], indirect=True)
 @pytest.mark.parametrize("M,N,K", [(2048, 512, 64), (8192, 1024, 256), (12288, 512, 128)])
 def test_gemm_grouped_tile_order(dev, gemm_kernel, M, N, K):
     """Grids whose tiles split evenly into whole row panels per XCD take the grouped tile order
@@ -246,7 +246,7 @@ def test_gemm_narrow_kernel(dev, out_dtype, M, N, K):
     assert err <= (1e-5 if out_dtype == torch.float32 else 2 ** -8), err
 
 
-@pytest.mark.parametrize("gemm_kernel", [0, 4, 5, 6, 7], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [0, 4, 5, 6, 7, 8], indirect=True)
 def test_gemm_empty_k_is_bias(dev, gemm_kernel):
     """K == 0 gives Y = bias (zeros without one) on every kernel choice: the tile kernels, which
     load whole K tiles, hand it to the guarded 128 x 128 kernel; split-K rejects it."""
@@ -267,7 +267,7 @@ def test_gemm_empty_k_is_bias(dev, gemm_kernel):
                   Y.data_ptr(), N, N, None, 0, N, None, 0, 2, ws.data_ptr(), ws.numel() * 4, s)
 
 
-@pytest.mark.parametrize("gemm_kernel", [0, 1, 3, 4, 5, 6, 7], indirect=True)
+@pytest.mark.parametrize("gemm_kernel", [0, 1, 3, 4, 5, 6, 7, 8], indirect=True)
 @pytest.mark.parametrize("scale", [0, -130])
 def test_gemm_bf16_output_rounds_to_nearest_even(dev, gemm_kernel, scale):
     """bf16 outputs are the round-to-nearest-even of the f32 sums, ties to even included, bit for
@@ -289,3 +289,40 @@ def test_gemm_bf16_output_rounds_to_nearest_even(dev, gemm_kernel, scale):
     got = y.float().cpu().numpy()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
         f"{int((got != want).sum())} of {got.size} outputs differ from round-to-nearest-even"
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4300, 64), (2304, 8192, 192), (3000, 6000, 1088)])
+def test_gemm_persistent_matches_one_tile_per_block(dev, M, N, K):
+    """The persistent 256 x 256 kernel (kernel 8: one block per CU walks its tiles, the K-tile ring
+    runs on across tiles) gives the one-tile-per-block kernel's bits on grids with more tiles than
+    CUs (1, 3 and 17 K tiles per tile, ragged edges): fp32 out with bias and SiLU, bf16 column
+    splits, and accumulation into fp32 and bf16 outputs."""
+    from helixml_amd import _ffi
+    g = torch.Generator().manual_seed(M + N + K)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
+    b = torch.randn(N, generator=g).to(dev)
+    Y0 = {dt: torch.randn(M, N, generator=g).to(dev).to(dt) for dt in (torch.float32, torch.bfloat16)}
+    s = torch.cuda.current_stream().cuda_stream
+
+    def run(kernel):
+        ssm.set_gemm_kernel(kernel)
+        try:
+            out = [ssm.gemm_bf16(X, W, b, act=1, out_dtype=torch.float32),
+                   ssm.gemm_bf16(X, W, out_dtype=torch.float32)]
+            out += list(ssm.gemm_bf16(X, W, splits=(N // 3 // 8 * 8, N // 2)))
+            for dt, y0 in Y0.items():
+                y = y0.clone()
+                od = _ffi.HX_F32 if dt == torch.float32 else _ffi.HX_BF16
+                _ffi.call("hx_gemm_bf16", M, N, K, X.data_ptr(), K, W.data_ptr(), K, None, 2, od,
+                          y.data_ptr(), N, N, None, 0, N, None, 0, s)
+                out.append(y)
+            torch.cuda.synchronize()
+            return out
+        finally:
+            ssm.set_gemm_kernel(0)
+
+    got, want = run(8), run(5)
+    for i, (a, c) in enumerate(zip(got, want)):
+        assert torch.equal(a, c), f"output {i} differs from the one-tile-per-block kernel"
+    assert norm_err(got[0].cpu().numpy(), ref(X, W, b, 1)) <= 1e-5
