@@ -700,14 +700,20 @@ def test_reference_execution_shape_restatement_is_bit_identical():
 def test_componentwise_bar_separates_rounding_from_mistakes():
     """The componentwise metric the block and LM GPU tests use: the f32 restatement sits under one
     bf16 ulp of the output product's term magnitudes from its float64 twin, while a block that
-    drops the D skip, or a head fed the unnormalised stream, lands far outside CW_ULPS."""
+    drops the D skip (about 180 ulps here), swaps the x and z halves of in_proj (about 940) or
+    drops dt_bias (about 700), or a head with a mis-scaled final norm weight, lands far outside
+    CW_ULPS."""
     from tests.util import CW_ULPS, block_inputs, cw_ulps, lm_params
     p = block_inputs(2, 37, 64, 256, 16, 32, 4, seed=2037)
     ref = oracle.mamba_block(**p, dt_rank=32)
     ref64, terms = oracle.numpy_mamba_block(**p, dt_rank=32, return_terms=True)
     assert cw_ulps(ref, ref64, terms) <= 1.0
-    bad = oracle.mamba_block(**dict(p, D=np.zeros_like(p["D"])), dt_rank=32)
-    assert cw_ulps(bad, ref64, terms) > 4 * CW_ULPS
+    di = p["w_in"].shape[0] // 2
+    for bad_p in (dict(p, D=np.zeros_like(p["D"])),
+                  dict(p, w_in=np.concatenate([p["w_in"][di:], p["w_in"][:di]], 0)),
+                  dict(p, dt_bias=np.zeros_like(p["dt_bias"]))):
+        bad = oracle.mamba_block(**bad_p, dt_rank=32)
+        assert cw_ulps(bad, ref64, terms) > 4 * CW_ULPS
     P = lm_params(2, 32, 64, 16, 8, 4, 256, seed=47)
     tok = np.random.default_rng(48).integers(0, 256, (2, 9))
     lg, _ = oracle.lm_prefill(tok, P, 8)
