@@ -2046,13 +2046,13 @@ int scan_fwd_dtproj(int64_t batch, int64_t seqlen, int64_t dim, const uint16_t* 
     HX_REQUIRE(scan_dtproj_ok(batch, seqlen, dim, rank), HX_ERR_UNSUPPORTED,
                "selective scan with dt_proj: sizes outside the fused path (batch %lld, seqlen %lld, "
                "dim %lld, dt_rank %lld)", (long long)batch, (long long)seqlen, (long long)dim, (long long)rank);
+    if (seqlen == 0)  // no steps (the empty operands may be NULL): the final state is the zero initial state
+        return last_state ? hx_fill_f32(batch * dim * 16, 0.0f, last_state, stream) : (int)HX_OK;
     HX_REQUIRE(u && dtlo && w_dt && A && B && C && z && out, HX_ERR_INVALID_INPUT,
                "selective scan with dt_proj: a required pointer is NULL");
     HX_REQUIRE(aligned(u, 16) && aligned(z, 16) && aligned(out, 16) && aligned(dtlo, 16) && aligned(w_dt, 16) &&
                    aligned(B, 32) && aligned(C, 32) && (!D || aligned(D, 16)) && (!dt_bias || aligned(dt_bias, 16)),
                HX_ERR_UNSUPPORTED, "selective scan with dt_proj: operands not 16-byte aligned");
-    if (seqlen == 0)  // no steps: the final state is the zero initial state
-        return last_state ? hx_fill_f32(batch * dim * 16, 0.0f, last_state, stream) : (int)HX_OK;
     constexpr int WPB = 4;
     const int64_t ntiles = (dim + 16 * WPB - 1) / (16 * WPB);
     WaveSeg sg{seqlen, 1, nullptr, nullptr, nullptr};

@@ -12,6 +12,7 @@ import torch
 
 import oracle
 from helixml_amd import ssm
+from helixml_amd._ffi import InvalidInput, UnsupportedOperation
 from tests.util import TOL_BF16, TOL_F32, bf16_round, norm_err, rel_err, scan_inputs
 
 pytestmark = pytest.mark.gpu
@@ -367,3 +368,38 @@ def test_scan_dtproj_matches_separate_steps(dev, bt, L, dim, r):
     e_ref = norm_err(f, ref)
     print(f"normwise: vs separate steps {e_sep:.3e}, vs oracle {e_ref:.3e}", flush=True)
     assert e_sep <= 4e-3 and e_ref <= 1e-2, (e_sep, e_ref)
+
+
+def test_scan_dtproj_errors_and_empty(dev):
+    """hx_selective_scan_dtproj_fwd takes dt_rank 32, 64, 96 or 128 and dim % 4 == 0 (else
+    UnsupportedOperation, nothing launched), needs every operand but D, dt_bias and last_state
+    (else InvalidInput), and with no steps sets the final state to zero."""
+    from helixml_amd import _ffi
+    bf = torch.bfloat16
+    bt, L, dim = 2, 16, 64
+
+    def args(r, d=dim, seq=L):
+        t = {"u": torch.zeros(bt, seq, d, device=dev, dtype=bf), "dt_lo": torch.zeros(bt, seq, r, device=dev, dtype=bf),
+             "w_dt": torch.zeros(d, r, device=dev, dtype=bf), "A": -torch.ones(d, 16, device=dev),
+             "B": torch.zeros(bt, seq, 16, device=dev, dtype=bf), "C": torch.zeros(bt, seq, 16, device=dev, dtype=bf),
+             "z": torch.zeros(bt, seq, d, device=dev, dtype=bf), "out": torch.zeros(bt, seq, d, device=dev, dtype=bf)}
+        return t
+
+    def call(t, r, d=dim, seq=L, last=None, drop=None):
+        p = {k: (None if k == drop else v.data_ptr()) for k, v in t.items()}
+        _ffi.call("hx_selective_scan_dtproj_fwd", bt, seq, d, r, p["u"], p["dt_lo"], p["w_dt"], p["A"], p["B"],
+                  p["C"], None, p["z"], None, p["out"], None if last is None else last.data_ptr(),
+                  torch.cuda.current_stream().cuda_stream)
+
+    for r in (16, 48, 160):
+        with pytest.raises(UnsupportedOperation):
+            call(args(r), r)
+    with pytest.raises(UnsupportedOperation):
+        call(args(32, d=66), 32, d=66)
+    for k in ("u", "dt_lo", "w_dt", "A", "B", "C", "z", "out"):
+        with pytest.raises(InvalidInput):
+            call(args(32), 32, drop=k)
+    last = torch.full((bt, dim, 16), float("nan"), device=dev)
+    call(args(64, seq=0), 64, seq=0, last=last)
+    torch.cuda.synchronize()
+    assert torch.equal(last, torch.zeros_like(last))
