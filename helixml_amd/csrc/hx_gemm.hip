@@ -1163,6 +1163,16 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256p_kernel(int64_t M, int6
     };
     static_assert(NST >= 2 && NST <= 4 && (SUB == 2 || SUB == 4) && 3 * QPW <= 63 && QPW % 8 == 0,
                   "ring depth / K tile");
+    // the first barrier after an epilogue: the loads it waits for were issued before the
+    // epilogue's stores, so `sprev` (the stores this wave's epilogue issued: 32 for bf16, 64 for
+    // fp32, capped at 63; 0 when unknown) may stay in flight (vector memory completes in order)
+    static_assert(NST == 2, "the epilogue wait assumes no other K tile's loads in flight");
+    auto wait_barrier_after_stores = [&](int sprev) __attribute__((always_inline)) {
+        if (sprev >= 63) asm volatile("s_waitcnt vmcnt(63) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else if (sprev >= 32) asm volatile("s_waitcnt vmcnt(32) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    int sprev = 0;
     bf16x8 fg[2][8];
 #pragma unroll
     for (int t = 0; t < NST; ++t)
@@ -1186,7 +1196,10 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256p_kernel(int64_t M, int6
                 int64_t koff = 0;
                 char* lstage = sbase;
                 if (s == SUB - 1) {
-                    if (p + 1 < total) wait_barrier(total - 2 - p < NST - 2 ? total - 2 - p : NST - 2);
+                    if (p + 1 < total) {
+                        if (kt == 0 && i > 0) wait_barrier_after_stores(sprev);
+                        else wait_barrier(total - 2 - p < NST - 2 ? total - 2 - p : NST - 2);
+                    }
                     if (ld) prep(p + NST, koff, lstage);
                 }
 #pragma unroll
@@ -1235,7 +1248,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256p_kernel(int64_t M, int6
             else if (kind == 1) d256p_epilogue_fast<true, true>(acc, st, yb, ldb, lane);
             else if (kind == 2) d256p_epilogue_fast<false, false>(acc, st, yb, ldb, lane);
             else d256p_epilogue_fast<false, true>(acc, st, yb, ldb, lane);
+            sprev = o.out_bf16 ? 16 * SlabGeom<true, 16>::NP : 16 * SlabGeom<false, 16>::NP;
         } else {
+            sprev = 0;
 #pragma unroll
             for (int a = 0; a < 4; ++a) {
 #pragma unroll
@@ -1409,11 +1424,14 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     // the 32-wide K tile where K is not a multiple of 64 (config 5 dt_proj, K = 32)
     const bool d256_auto = g_gemm_kernel == 0 && N >= 256 && M >= 256 &&
                            ((M + XBM - 1) / XBM) * ((N + XBN - 1) / XBN) >= 256;
-    // the persistent form only when forced: alone it is ahead where K is short (config 5 in_proj
-    // 309 -> 291 us, head 45 -> 42 us; behind for long K, config 3 in_proj 458 vs 451 us), but
-    // the 12-layer config-5 prefill measured slower with it (17.97 vs 17.79 ms, same box). Both
-    // forms give the same bits.
-    if (vec && K > 0 && K % 64 == 0 && g_gemm_kernel == 8 && d256p_ok<64, 2>())
+    // the persistent form where K is short (<= 1024) and every block gets at least two tiles:
+    // there a tile's epilogue (its output drain, which every CU reaches at once in the one-tile
+    // form) is a large share and overlaps the next tile's K loop (config 5 prefill 18.16 ->
+    // 18.02 ms on one box; config 3's K = 2048 / 4096 projections measured 1% slower with it).
+    // Both forms give the same bits.
+    const bool d256p_auto = d256_auto && K <= 1024 &&
+                            ((M + XBM - 1) / XBM) * ((N + XBN - 1) / XBN) >= 2 * (int64_t)device_cus();
+    if (vec && K > 0 && K % 64 == 0 && (g_gemm_kernel == 8 || d256p_auto) && d256p_ok<64, 2>())
         return launch_d256p<64, 2>(M, N, K, X, ldx, W, ldw, bias, o, stream);
     if (vec && K > 0 && K % 64 == 0 && (g_gemm_kernel == 5 || d256_auto) && d256_ok<64, 2>())
         return launch_d256<64, 2>(M, N, K, X, ldx, W, ldw, bias, o, stream);

@@ -392,8 +392,8 @@ int hx_set_scan_variant(int variant);
  * 4 direct-to-LDS 256x128 tiles (K % 64 == 0), 5 direct-to-LDS 256x256 tiles with 64-wide K tiles
  * (K % 64 == 0), 6 the same with 32-wide K tiles in a 4-stage ring (K % 32 == 0), 7 the narrow
  * kernel: 64-row tiles holding every column (N <= 256, K % 64 == 0), 8 the persistent form of 5
- * (one block per CU walks its tiles, the K-tile ring runs on across them; same bits as 5; never
- * chosen automatically). A shape a forced kernel cannot take goes to the 128x128 kernel (the
+ * (one block per CU walks its tiles, the K-tile ring runs on across them; same bits as 5; the
+ * automatic choice where K <= 1024 and there are at least two tiles per CU). A shape a forced kernel cannot take goes to the 128x128 kernel (the
  * small-M one for small shapes). A measurement knob. */
 int hx_set_gemm_kernel(int k);
 /* S4D knobs for later calls on the calling thread: path 0 auto (wave path for dstate 16), 1 the
