@@ -116,6 +116,12 @@ __device__ inline void lds_barrier() {
 typedef __attribute__((address_space(1))) void gvoid_t;
 typedef __attribute__((address_space(3))) void lvoid_t;
 
+// The long-sequence scans' end-state passes stop where every state's decay to its segment's end
+// is below 2^-kDecayDropBits: what they leave out is that decay times the state there, 2^-8 of
+// the fp32 rounding (2^-24) of that state.
+constexpr int kDecayDropBits = 32;
+constexpr float kDecayDrop = 0x1p-32f;  // 2^-kDecayDropBits
+
 // exp2 on the transcendental unit (v_exp_f32). Inputs here are finite; underflow flushes to 0.
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }

@@ -606,12 +606,13 @@ __global__ __launch_bounds__(256) void s4d_wave_kernel(
     }
     const float Dd = Dv ? Dv[dc] : 0.0f;
 
-    // END_ONLY: the system is time-invariant, so the steps after which |Abar|^k < 2^-48 for every
-    // state of the block's channels are known up front (k >= 48 / -(dt a_re log2 e), with half a
-    // bit of margin for expf's rounding of |Abar|); the end state from zero then starts that many
-    // steps (whole chunks) before the segment's end. What is left out is |Abar|^k times the
-    // state at that step, 2^-48 of quantities the fp32 recurrence holds to 2^-24. The carry
-    // still applies the segment's own transfer Abar^seg_len, which is smaller still.
+    // END_ONLY: the system is time-invariant, so the steps after which |Abar|^k < 2^-32
+    // (kDecayDropBits) for every state of the block's channels are known up front
+    // (k >= 32 / -(dt a_re log2 e), with half a bit of margin for expf's rounding of |Abar|); the
+    // end state from zero then starts that many steps (whole chunks) before the segment's end.
+    // What is left out is |Abar|^k times the state at that step, 2^-32 of quantities the fp32
+    // recurrence holds to 2^-24. The carry still applies the segment's own transfer
+    // Abar^seg_len, which is smaller still.
     int64_t tstart = tbeg;
     if constexpr (END_ONLY) {
         __shared__ int s_win;
@@ -621,7 +622,7 @@ __global__ __launch_bounds__(256) void s4d_wave_kernel(
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const float l2 = dt * a_re[dc * NS + 4 * r + k] * kLog2e;  // log2 |Abar|
-            const float wf = 48.5f / -l2;
+            const float wf = ((float)kDecayDropBits + 0.5f) / -l2;
             wl = max(wl, l2 < 0.0f && wf < 1.0e9f ? (int)ceilf(wf) : 0x7fffffff);
         }
         atomicMax(&s_win, dvalid ? wl : 0);

@@ -682,9 +682,9 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
     // END_ONLY: the segment's chunks from the last back to the first (all whole: segment lengths
     // are multiples of 16 and the last, possibly partial, segment has no end-state pass). It
     // stops after the first chunk at which every state of the wave's channels has decayed below
-    // 2^-48 on its way to the segment's end: what is left out is that decay times the state at
-    // that step (and times the entry state, whose decay over the whole segment is smaller
-    // still), 2^-48 of values the recurrence holds to 2^-24 (a NaN or growing decay never
+    // 2^-32 (kDecayDrop) on its way to the segment's end: what is left out is that decay times
+    // the state at that step (and times the entry state, whose decay over the whole segment is
+    // smaller still), 2^-32 of values the recurrence holds to 2^-24 (a NaN or growing decay never
     // stops it). The segment then publishes a decay of 0, so its entry state is not carried.
     bool dropped = false;
     if constexpr (END_ONLY) {
@@ -707,7 +707,7 @@ __global__ __launch_bounds__(64 * WPB) void scan_wave3_kernel(
                 B4 = Bn;
                 __builtin_amdgcn_wave_barrier();
                 const float qm = fmaxf(fmaxf(Q[0], Q[1]), fmaxf(Q[2], Q[3]));
-                if (__ballot(dvalid && !(qm < 0x1p-48f)) == 0) {
+                if (__ballot(dvalid && !(qm < kDecayDrop)) == 0) {
                     stop = true;
                     dropped = t0 > tbeg;
                 }

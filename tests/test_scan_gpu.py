@@ -256,7 +256,7 @@ def test_scan_segmented_long_sequence_path(dev, _reset_segments, nseg, shape, va
 @pytest.mark.parametrize("zero_a", [False, True])
 def test_scan_segmented_decay_window(dev, _reset_segments, zero_a):
     """Segments long enough that the end-state pass starts late: delta_raw ~ N(0, 0.5) (dt about
-    0.7) and A = -(n+1), so the decay to a 2048-step segment's end falls below 2^-48 within ~50
+    0.7) and A = -(n+1), so the decay to a 2048-step segment's end falls below 2^-32 within ~32
     steps and the end states come from that window alone (the carry takes no decay from such a
     segment). With one state's A = 0 in one channel no window applies to that channel's wave;
     that state then sums 8192 undamped terms, whose f32 rounding (in either summation order)
