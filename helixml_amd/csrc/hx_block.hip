@@ -9,6 +9,7 @@
 // (crates/nn/src/lib.rs:888-906) and allocates A/B/C/D/delta_proj/B_proj/C_proj it never uses
 // (lib.rs:851-867); this is the block those parameters describe. bf16 storage, fp32 arithmetic.
 #include "hx_common.h"
+#include "hx_wave.h"
 
 extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
                             const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
@@ -259,23 +260,249 @@ using namespace ::hx;
 // rounded to bf16 where that path stores them), so the two differ only in the order of the
 // x_proj and dt_proj sums.
 //   pass 1: xc = silu(conv_b + sum_j conv_w[c][j] * window[j]) -> LDS; window advanced
-//           (a thread owns channel pairs c = 2 tid + 1024 i)
-//   x_proj: 64 outputs at a time; thread (quad q = tid % 256, group g = tid / 256) sums
-//           w_x[j][4q..4q+3] * xc over its channels for 32 outputs j, a butterfly reduce-scatter
-//           leaves one output per lane pair, the 4 waves of a group add through LDS
+//   x_proj: dt_lo | B | C = W_x . xc (J = dt_rank + 32 outputs)
 //   pass 2: dt[c] = sum_r w_dt[c][r] * dt_lo[r]; dl = softplus(dt + dt_bias); per state n:
 //           h = exp(dl * A[c][n]) * h + dl * xc * B[n]; y = (sum_n C[n] * h + D * xc) * silu(z)
-// The step is a chain of dependent phases, so its time is load latency, not bandwidth: the
-// global loads of the first pass-1 pair, the first x_proj chunk and the first pass-2 round's
-// state are issued at the start, in the order the phases use them (a wait for one load also
-// waits for every memory operation issued before it); A and the dt_proj rows, read by every
-// block and so L2-hot, follow once the x_proj products are done (fewer live registers); the
-// stores all come after those loads.
 // State [batch][d_inner][16] fp32 and conv window [batch][d_conv-1][d_inner] fp32 in place.
 constexpr int kDecThreads = 512;
 
 __device__ inline float bf16r(float v) { return bf16_bits_to_f32(Storage<uint16_t>::round(v)); }
 
+// Pass 2 of both decode kernels for one channel ch of the sequence b: k4 = lane % 4 holds states
+// 4 k4 .. 4 k4 + 3 (hq, aq), dt_proj partial d over ranks 8 k4 .. 8 k4 + 7 (and beyond, looping)
+// summed across the 4 lanes; the state is stored, and the lane with k4 = 0 stores y.
+__device__ __attribute__((always_inline)) inline void decode_state_step(int64_t b, int d_inner, int ch, int k4, float d,
+                                         float4 hq, float4 aq, const float (&bk)[4],
+                                         const float (&ck)[4], const float* s_xc,
+                                         const float* s_aux, const float* Dv,
+                                         float* __restrict__ ssm_state, uint16_t* __restrict__ y) {
+    d += __shfl_xor(d, 1, 64);
+    d += __shfl_xor(d, 2, 64);
+    if (ch >= d_inner) return;  // uniform per lane group
+    float dl = bf16r(d) + s_aux[ch];
+    dl = softplus(dl);
+    const float uv = s_xc[ch];
+    const float du = dl * uv;
+    float h4[4] = {hq.x, hq.y, hq.z, hq.w};
+    const float a4[4] = {aq.x, aq.y, aq.z, aq.w};
+    float yy = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float ab = fast_exp2(dl * (a4[i] * kLog2e));
+        h4[i] = fmaf(ab, h4[i], du * bk[i]);
+        yy = fmaf(ck[i], h4[i], yy);
+    }
+    reinterpret_cast<float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4] =
+        make_float4(h4[0], h4[1], h4[2], h4[3]);
+    yy += __shfl_xor(yy, 1, 64);
+    yy += __shfl_xor(yy, 2, 64);
+    if (k4 == 0) {
+        if (Dv) yy = fmaf(s_aux[d_inner + ch], uv, yy);
+        y[b * (int64_t)d_inner + ch] = Storage<uint16_t>::round(yy * silu(s_aux[2 * d_inner + ch]));
+    }
+}
+
+// Row kernel, for d_inner <= 1024 and dt_rank <= 32 (one channel pair per thread in pass 1, at
+// most 64 x_proj outputs, 8 pass-2 channels per thread), straight-line code. The step is a chain
+// of dependent phases whose time is load latency and the CU's load port (every block reads all
+// of W_x, A and W_dt, 256 KB at config 5), so:
+//   * x_proj: wave w owns outputs 8w .. 8w+7 over every channel; lane l sums channel chunks
+//     8l + 512q (XV4: 16-byte loads, d_inner % 8 == 0) or 4l + 256q (8-byte loads), so each load
+//     instruction reads 1 KB or 512 B of a W_x row contiguously; the 8 per-lane sums meet by a
+//     register reduce-scatter (lane halves swapped, 16-lane rows swapped, DPP row rotate by 8:
+//     lane bits 5, 4, 3 pick the output 4 b5 + 2 b4 + b3) and a DPP sum over lane bits 0-2, with
+//     no LDS round trip and one barrier;
+//   * the loads are issued in the order the phases use them: pass-1 operands, W_x, then, once
+//     the pass-1 operands are in (they would otherwise queue behind 16 MB of state reads), this
+//     thread's state; A and the dt_proj rows (L2-hot) after the x_proj products.
+template <int KC, bool XV4>
+__global__ __launch_bounds__(kDecThreads) void ssm_decode_row_kernel(
+    int d_inner, int dt_rank, const uint16_t* __restrict__ xpart, const uint16_t* __restrict__ z,
+    const float* __restrict__ conv_w, const float* __restrict__ conv_b,
+    float* __restrict__ conv_state, const uint16_t* __restrict__ w_x,
+    const uint16_t* __restrict__ w_dt, const float* __restrict__ dt_bias,
+    const float* __restrict__ A, const float* __restrict__ Dv, float* __restrict__ ssm_state,
+    uint16_t* __restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) float s_dec[];
+    const int J = dt_rank + 32;
+    float* s_xc = s_dec;                 // [d_inner]
+    float* s_aux = s_xc + d_inner;       // [3][d_inner]: dt_bias, D, z (staged in pass 1)
+    float* s_dbc = s_aux + 3 * d_inner;  // [64]: dt_lo | B | C, bf16-rounded
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint16_t* xr = xpart + b * (int64_t)d_inner;
+    const uint16_t* zr = z + b * (int64_t)d_inner;
+    float* cst = conv_state + b * (int64_t)(KC - 1) * d_inner;
+
+    // pass-1 operands of channel pair (c, c + 1) (c clamped into range: values then unused)
+    const int c = 2 * tid < d_inner ? 2 * tid : d_inner - 2;
+    const uint32_t p_xw = *reinterpret_cast<const uint32_t*>(xr + c);
+    const uint32_t p_zw = *reinterpret_cast<const uint32_t*>(zr + c);
+    float2 p_prev[KC > 1 ? KC - 1 : 1];
+#pragma unroll
+    for (int j = 0; j < KC - 1; ++j) p_prev[j] = *reinterpret_cast<const float2*>(cst + (int64_t)j * d_inner + c);
+    float p_wk[2][KC];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        if constexpr (KC == 4) {
+            const float4 w4 = reinterpret_cast<const float4*>(conv_w)[c + e];
+            p_wk[e][0] = w4.x; p_wk[e][1] = w4.y; p_wk[e][2] = w4.z; p_wk[e][3] = w4.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < KC; ++j) p_wk[e][j] = conv_w[(c + e) * KC + j];
+        }
+    }
+    // (prvalue selects: an lvalue conditional would select an address, one arm on the stack)
+    const float2 p_cb = conv_b ? *reinterpret_cast<const float2*>(conv_b + c) : make_float2(0.0f, 0.0f);
+    const float2 p_dtb = dt_bias ? *reinterpret_cast<const float2*>(dt_bias + c) : make_float2(0.0f, 0.0f);
+    const float2 p_dv = Dv ? *reinterpret_cast<const float2*>(Dv + c) : make_float2(0.0f, 0.0f);
+    // x_proj operands: rows 8 wave + r (clamped to J - 1: sums never stored), chunks past
+    // d_inner clamped to chunk 0 (not summed)
+    constexpr int CW = XV4 ? 8 : 4;  // channels per chunk
+    constexpr int NQ = 1024 / (64 * CW);
+    using WChunk = std::conditional_t<XV4, uint4, uint2>;
+    WChunk wx[8][NQ];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const int jr = 8 * wave + r < J ? 8 * wave + r : J - 1;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int ch = CW * lane + 64 * CW * q < d_inner ? CW * lane + 64 * CW * q : 0;
+            wx[r][q] = *reinterpret_cast<const WChunk*>(w_x + (int64_t)jr * d_inner + ch);
+        }
+    }
+
+    // pass 1: conv window step
+    const float xv[2] = {__uint_as_float(p_xw << 16), __uint_as_float(p_xw & 0xffff0000u)};
+    float xcv[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        float acc = e ? p_cb.y : p_cb.x;
+#pragma unroll
+        for (int j = 0; j < KC - 1; ++j) acc = fmaf(p_wk[e][j], e ? p_prev[j].y : p_prev[j].x, acc);
+        acc = fmaf(p_wk[e][KC - 1], xv[e], acc);
+        xcv[e] = bf16r(silu(acc));
+    }
+    // the state loads follow the pass-1 operands' arrival (no memory access moves above this)
+    asm volatile("" ::"v"(xcv[0]), "v"(xcv[1]) : "memory");
+    constexpr int UC = 8;
+    constexpr int CSTEP = kDecThreads / 4;
+    const int k4 = tid & 3;
+    float4 hq[UC];
+#pragma unroll
+    for (int u = 0; u < UC; ++u) {
+        const int ch = (tid >> 2) + u * CSTEP < d_inner ? (tid >> 2) + u * CSTEP : d_inner - 1;  // clamped: unused
+        hq[u] = reinterpret_cast<const float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4];
+    }
+    if (2 * tid < d_inner) {
+        *reinterpret_cast<float2*>(s_xc + c) = make_float2(xcv[0], xcv[1]);
+        *reinterpret_cast<float2*>(s_aux + c) = p_dtb;
+        *reinterpret_cast<float2*>(s_aux + d_inner + c) = p_dv;
+        *reinterpret_cast<float2*>(s_aux + 2 * d_inner + c) =
+            make_float2(__uint_as_float(p_zw << 16), __uint_as_float(p_zw & 0xffff0000u));
+    }
+    __syncthreads();
+
+    // x_proj: this lane's share of the wave's 8 outputs
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int c0 = CW * lane + 64 * CW * q;
+        if (c0 < d_inner) {
+            float xs[CW];
+#pragma unroll
+            for (int i = 0; i < CW; i += 4) {
+                const float4 x4 = *reinterpret_cast<const float4*>(s_xc + c0 + i);
+                xs[i] = x4.x; xs[i + 1] = x4.y; xs[i + 2] = x4.z; xs[i + 3] = x4.w;
+            }
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                uint32_t wv[CW / 2];
+                if constexpr (XV4) {
+                    wv[0] = wx[r][q].x; wv[1] = wx[r][q].y; wv[2] = wx[r][q].z; wv[3] = wx[r][q].w;
+                } else {
+                    wv[0] = wx[r][q].x; wv[1] = wx[r][q].y;
+                }
+#pragma unroll
+                for (int i = 0; i < CW / 2; ++i) {
+                    acc[r] = fmaf(__uint_as_float(wv[i] << 16), xs[2 * i], acc[r]);
+                    acc[r] = fmaf(__uint_as_float(wv[i] & 0xffff0000u), xs[2 * i + 1], acc[r]);
+                }
+            }
+        }
+    }
+    // A and the dt_proj rows (read by every block: L2-hot), under the reduction
+    const bool vec_dt = (dt_rank & 31) == 0;
+    float4 aq[UC];
+    uint4 wq[UC];
+#pragma unroll
+    for (int u = 0; u < UC; ++u) {
+        const int ch = (tid >> 2) + u * CSTEP < d_inner ? (tid >> 2) + u * CSTEP : d_inner - 1;
+        aq[u] = reinterpret_cast<const float4*>(A + (int64_t)ch * 16)[k4];
+        if (vec_dt) wq[u] = *reinterpret_cast<const uint4*>(w_dt + (int64_t)ch * dt_rank + 8 * k4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { swap32(acc[i], acc[i + 4]); acc[i] += acc[i + 4]; }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) { swap16(acc[i], acc[i + 2]); acc[i] += acc[i + 2]; }
+    {
+        const bool up = (lane & 8) != 0;
+        const float send = up ? acc[0] : acc[1];
+        const float keep = up ? acc[1] : acc[0];
+        acc[0] = keep + dpp<kDppRor8>(send);
+    }
+    acc[0] += dpp<kDppXor1>(acc[0]);
+    acc[0] += dpp<kDppXor2>(acc[0]);
+    acc[0] += dpp<kDppHalfMirror>(acc[0]);
+    {
+        const int jrow = 8 * wave + 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1);
+        if ((lane & 7) == 0 && jrow < J) s_dbc[jrow] = bf16r(acc[0]);
+    }
+    __syncthreads();
+
+    // pass 2: dt_proj, state update, skip and gate
+    const float* dtlo = s_dbc;
+    const float* Bn = s_dbc + dt_rank;
+    const float* Cn = Bn + 16;
+    float bk[4], ck[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { bk[i] = Bn[4 * k4 + i]; ck[i] = Cn[4 * k4 + i]; }
+#pragma unroll
+    for (int u = 0; u < UC; ++u) {
+        const int ch = (tid >> 2) + u * CSTEP;
+        float d = 0.0f;
+        if (vec_dt) {
+            const uint32_t ws[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                d = fmaf(__uint_as_float(ws[i] << 16), dtlo[8 * k4 + 2 * i], d);
+                d = fmaf(__uint_as_float(ws[i] & 0xffff0000u), dtlo[8 * k4 + 2 * i + 1], d);
+            }
+        } else {
+            const uint16_t* wr = w_dt + (int64_t)(ch < d_inner ? ch : d_inner - 1) * dt_rank;
+            for (int r = k4; r < dt_rank; r += 4) d = fmaf(bf16_bits_to_f32(wr[r]), dtlo[r], d);
+        }
+        decode_state_step(b, d_inner, ch, k4, d, hq[u], aq[u], bk, ck, s_xc, s_aux, Dv, ssm_state, y);
+    }
+    // the advanced conv window, stored last: a store issued before a wait counts in it, and
+    // these are under a branch, so the compiler's waits for W_x would also wait for the state
+    if (2 * tid < d_inner) {
+#pragma unroll
+        for (int j = 0; j + 1 < KC - 1; ++j)
+            *reinterpret_cast<float2*>(cst + (int64_t)j * d_inner + c) = p_prev[j + 1];
+        if (KC > 1) *reinterpret_cast<float2*>(cst + (int64_t)(KC - 2) * d_inner + c) = make_float2(xv[0], xv[1]);
+    }
+}
+
+// General kernel (any d_inner % 4 == 0, any dt_rank): the same phases in loops.
+//   pass 1: a thread owns channel pairs c = 2 tid + 1024 i
+//   x_proj: 64 outputs at a time; thread (quad q = tid % 256, group g = tid / 256) sums
+//           w_x[j][4q..4q+3] * xc over its channels for 32 outputs j, a butterfly reduce-scatter
+//           leaves one output per lane pair, the 4 waves of a group add through LDS
+//   pass 2: rounds of 8 channels per group of four lanes, each round's operands loaded at its
+//           start
 // One level of a butterfly reduce-scatter across the wave: K values in acc[0..K) become K / 2,
 // the lanes with bit K set keeping the upper half of the pairwise sums (K a template argument so
 // every index is a constant and acc stays in registers).
@@ -290,11 +517,7 @@ __device__ inline void rs_level(float* acc, int lane) {
     }
 }
 
-// ONE: d_inner <= 1024 and dt_rank <= 32, so each thread has one channel pair in pass 1, one
-// x_proj chunk and one pass-2 round: straight-line code with the loads placed as above. Other
-// shapes loop, and load each pass-2 round's operands at the start of the round (the registers
-// the early loads would hold across the loops are not there).
-template <int KC, bool ONE>
+template <int KC>
 __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
     int d_inner, int dt_rank, const uint16_t* __restrict__ xpart, const uint16_t* __restrict__ z,
     const float* __restrict__ conv_w, const float* __restrict__ conv_b,
@@ -315,93 +538,31 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
     const uint16_t* zr = z + b * (int64_t)d_inner;
     float* cst = conv_state + b * (int64_t)(KC - 1) * d_inner;
 
-    // pass-1 operands of channel pair (c, c + 1) (c clamped into range: values then unused)
-    uint32_t p_xw, p_zw;
-    float p_wk[2][KC], p_cb[2], p_prev[KC > 1 ? KC - 1 : 1][2], p_dtb[2], p_dv[2];
-    auto load_p1 = [&](int c) __attribute__((always_inline)) {
-        c = c < d_inner ? c : d_inner - 2;
-        p_xw = *reinterpret_cast<const uint32_t*>(xr + c);
-        p_zw = *reinterpret_cast<const uint32_t*>(zr + c);
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            if constexpr (KC == 4) {
-                const float4 w4 = reinterpret_cast<const float4*>(conv_w)[c + e];
-                p_wk[e][0] = w4.x; p_wk[e][1] = w4.y; p_wk[e][2] = w4.z; p_wk[e][3] = w4.w;
-            } else {
-#pragma unroll
-                for (int j = 0; j < KC; ++j) p_wk[e][j] = conv_w[(c + e) * KC + j];
-            }
-            p_cb[e] = conv_b ? conv_b[c + e] : 0.0f;
-#pragma unroll
-            for (int j = 0; j < KC - 1; ++j) p_prev[j][e] = cst[(int64_t)j * d_inner + c + e];
-            p_dtb[e] = dt_bias ? dt_bias[c + e] : 0.0f;
-            p_dv[e] = Dv ? Dv[c + e] : 0.0f;
-        }
-    };
-    // x_proj operands: rows j0 + 32 g + jj (clamped to J - 1: sums never stored) of channels
-    // cb + 4q .. +3 (clamped into range: not summed)
-    const int xq = tid & 255, xg = tid >> 8;
-    uint2 wxq[32];
-    auto load_wx = [&](int j0, int cb) __attribute__((always_inline)) {
-        const int c = cb + 4 * xq < d_inner ? cb + 4 * xq : d_inner - 4;
-#pragma unroll
-        for (int jj = 0; jj < 32; ++jj) {
-            const int jr = j0 + 32 * xg + jj < J ? j0 + 32 * xg + jj : J - 1;
-            wxq[jj] = *reinterpret_cast<const uint2*>(w_x + (int64_t)jr * d_inner + c);
-        }
-    };
-    // Pass-2 operands of a round of UC channels per group of four lanes (lane part k4 = states
-    // 4k4..4k4+3 and dt_proj ranks 8k4..8k4+7 of the first 32): state, A and the first 16 bytes
-    // of the dt_proj row.
-    constexpr int UC = 8;
-    constexpr int CSTEP = kDecThreads / 4;
-    const int k4 = tid & 3;
-    const bool vec_dt = (dt_rank & 31) == 0;
-    float4 hq[UC], aq[UC];
-    uint4 wq[UC];
-    auto load_state = [&](int ch0) __attribute__((always_inline)) {
-#pragma unroll
-        for (int u = 0; u < UC; ++u) {
-            const int ch = ch0 + u * CSTEP < d_inner ? ch0 + u * CSTEP : d_inner - 1;  // clamped: unused
-            hq[u] = reinterpret_cast<const float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4];
-        }
-    };
-    auto load_aw = [&](int ch0) __attribute__((always_inline)) {  // shared by all blocks: L2-hot
-#pragma unroll
-        for (int u = 0; u < UC; ++u) {
-            const int ch = ch0 + u * CSTEP < d_inner ? ch0 + u * CSTEP : d_inner - 1;
-            aq[u] = reinterpret_cast<const float4*>(A + (int64_t)ch * 16)[k4];
-            if (vec_dt) wq[u] = *reinterpret_cast<const uint4*>(w_dt + (int64_t)ch * dt_rank + 8 * k4);
-        }
-    };
-    load_p1(2 * tid);
-    load_wx(0, 0);
-    if constexpr (ONE) load_state(tid >> 2);
-
     // pass 1: conv window step
     for (int c = 2 * tid; c < d_inner; c += 2 * kDecThreads) {
-        if (!ONE && c != 2 * tid) load_p1(c);
+        const uint32_t p_xw = *reinterpret_cast<const uint32_t*>(xr + c);
+        const uint32_t p_zw = *reinterpret_cast<const uint32_t*>(zr + c);
         const float xv[2] = {__uint_as_float(p_xw << 16), __uint_as_float(p_xw & 0xffff0000u)};
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            float acc = p_cb[e];
+            float acc = conv_b ? conv_b[c + e] : 0.0f;
 #pragma unroll
-            for (int j = 0; j < KC - 1; ++j) acc = fmaf(p_wk[e][j], p_prev[j][e], acc);
-            acc = fmaf(p_wk[e][KC - 1], xv[e], acc);
+            for (int j = 0; j < KC - 1; ++j) acc = fmaf(conv_w[(c + e) * KC + j], cst[(int64_t)j * d_inner + c + e], acc);
+            acc = fmaf(conv_w[(c + e) * KC + KC - 1], xv[e], acc);
 #pragma unroll
-            for (int j = 0; j + 1 < KC - 1; ++j) cst[(int64_t)j * d_inner + c + e] = p_prev[j + 1][e];
+            for (int j = 0; j + 1 < KC - 1; ++j) cst[(int64_t)j * d_inner + c + e] = cst[(int64_t)(j + 1) * d_inner + c + e];
             if (KC > 1) cst[(int64_t)(KC - 2) * d_inner + c + e] = xv[e];
             s_xc[c + e] = bf16r(silu(acc));
-            s_aux[c + e] = p_dtb[e];
-            s_aux[d_inner + c + e] = p_dv[e];
+            s_aux[c + e] = dt_bias ? dt_bias[c + e] : 0.0f;
+            s_aux[d_inner + c + e] = Dv ? Dv[c + e] : 0.0f;
         }
         s_aux[2 * d_inner + c] = __uint_as_float(p_zw << 16);
         s_aux[2 * d_inner + c + 1] = __uint_as_float(p_zw & 0xffff0000u);
-        if constexpr (ONE) break;
     }
     __syncthreads();
 
     // x_proj: 64 outputs at a time
+    const int xq = tid & 255, xg = tid >> 8;
     const int jj_lane = (((lane >> 5) & 1) << 4) | (((lane >> 4) & 1) << 3) | (((lane >> 3) & 1) << 2) |
                         (((lane >> 2) & 1) << 1) | ((lane >> 1) & 1);
     for (int j0 = 0; j0 < J; j0 += 64) {
@@ -409,21 +570,20 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
 #pragma unroll
         for (int jj = 0; jj < 32; ++jj) acc[jj] = 0.0f;
         for (int cb = 0; cb < d_inner; cb += 1024) {
-            if (!ONE && (j0 != 0 || cb != 0)) load_wx(j0, cb);
             const int c = cb + 4 * xq;
             if (c < d_inner) {
                 const float4 x4 = *reinterpret_cast<const float4*>(s_xc + c);
 #pragma unroll
                 for (int jj = 0; jj < 32; ++jj) {
-                    acc[jj] = fmaf(__uint_as_float(wxq[jj].x << 16), x4.x, acc[jj]);
-                    acc[jj] = fmaf(__uint_as_float(wxq[jj].x & 0xffff0000u), x4.y, acc[jj]);
-                    acc[jj] = fmaf(__uint_as_float(wxq[jj].y << 16), x4.z, acc[jj]);
-                    acc[jj] = fmaf(__uint_as_float(wxq[jj].y & 0xffff0000u), x4.w, acc[jj]);
+                    const int jr = j0 + 32 * xg + jj < J ? j0 + 32 * xg + jj : J - 1;  // clamped: never stored
+                    const uint2 w = *reinterpret_cast<const uint2*>(w_x + (int64_t)jr * d_inner + c);
+                    acc[jj] = fmaf(__uint_as_float(w.x << 16), x4.x, acc[jj]);
+                    acc[jj] = fmaf(__uint_as_float(w.x & 0xffff0000u), x4.y, acc[jj]);
+                    acc[jj] = fmaf(__uint_as_float(w.y << 16), x4.z, acc[jj]);
+                    acc[jj] = fmaf(__uint_as_float(w.y & 0xffff0000u), x4.w, acc[jj]);
                 }
             }
-            if constexpr (ONE) break;
         }
-        if constexpr (ONE) load_aw(tid >> 2);  // under the reductions and barriers that follow
         // butterfly reduce-scatter across the wave: the lane pair (2i, 2i + 1) ends with the
         // wave's sum for output jj_lane
         rs_level<32>(acc, lane);
@@ -442,11 +602,13 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
             s_dbc[j0 + tid] = bf16r(t);
         }
         __syncthreads();
-        if constexpr (ONE) break;
     }
 
-    // pass 2: dt_proj, state update, skip and gate (the first round's operands were loaded at
-    // the start of the kernel, under pass 1 and x_proj).
+    // pass 2: dt_proj, state update, skip and gate, in rounds of UC channels per lane group
+    constexpr int UC = 8;
+    constexpr int CSTEP = kDecThreads / 4;
+    const int k4 = tid & 3;
+    const bool vec_dt = (dt_rank & 31) == 0;
     const float* dtlo = s_dbc;
     const float* Bn = s_dbc + dt_rank;
     const float* Cn = Bn + 16;
@@ -454,24 +616,21 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) { bk[i] = Bn[4 * k4 + i]; ck[i] = Cn[4 * k4 + i]; }
     for (int ch0 = tid >> 2; ch0 < d_inner; ch0 += UC * CSTEP) {
-        if constexpr (!ONE) {  // general shapes: each round's operands at its start
-            load_state(ch0);
-            load_aw(ch0);
+        float4 hq[UC], aq[UC];
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int ch = ch0 + u * CSTEP < d_inner ? ch0 + u * CSTEP : d_inner - 1;  // clamped: unused
+            hq[u] = reinterpret_cast<const float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4];
+            aq[u] = reinterpret_cast<const float4*>(A + (int64_t)ch * 16)[k4];
         }
 #pragma unroll
         for (int u = 0; u < UC; ++u) {
             const int ch = ch0 + u * CSTEP;
             const int chc = ch < d_inner ? ch : d_inner - 1;
+            const uint16_t* wr = w_dt + (int64_t)chc * dt_rank;
             float d = 0.0f;
             if (vec_dt) {
-                const uint32_t ws[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    d = fmaf(__uint_as_float(ws[i] << 16), dtlo[8 * k4 + 2 * i], d);
-                    d = fmaf(__uint_as_float(ws[i] & 0xffff0000u), dtlo[8 * k4 + 2 * i + 1], d);
-                }
-                const uint16_t* wr = w_dt + (int64_t)chc * dt_rank;
-                for (int r0 = 8 * k4 + 32; !ONE && r0 < dt_rank; r0 += 32) {
+                for (int r0 = 8 * k4; r0 < dt_rank; r0 += 32) {
                     const uint4 wv = *reinterpret_cast<const uint4*>(wr + r0);
                     const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
@@ -481,35 +640,10 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
                     }
                 }
             } else {
-                const uint16_t* wr = w_dt + (int64_t)chc * dt_rank;
                 for (int r = k4; r < dt_rank; r += 4) d = fmaf(bf16_bits_to_f32(wr[r]), dtlo[r], d);
             }
-            d += __shfl_xor(d, 1, 64);
-            d += __shfl_xor(d, 2, 64);
-            if (ch >= d_inner) continue;  // uniform per lane group
-            float dl = bf16r(d) + s_aux[ch];
-            dl = softplus(dl);
-            const float uv = s_xc[ch];
-            const float du = dl * uv;
-            float h4[4] = {hq[u].x, hq[u].y, hq[u].z, hq[u].w};
-            const float a4[4] = {aq[u].x, aq[u].y, aq[u].z, aq[u].w};
-            float yy = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float ab = fast_exp2(dl * (a4[i] * kLog2e));
-                h4[i] = fmaf(ab, h4[i], du * bk[i]);
-                yy = fmaf(ck[i], h4[i], yy);
-            }
-            reinterpret_cast<float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4] =
-                make_float4(h4[0], h4[1], h4[2], h4[3]);
-            yy += __shfl_xor(yy, 1, 64);
-            yy += __shfl_xor(yy, 2, 64);
-            if (k4 == 0) {
-                if (Dv) yy = fmaf(s_aux[d_inner + ch], uv, yy);
-                y[b * (int64_t)d_inner + ch] = Storage<uint16_t>::round(yy * silu(s_aux[2 * d_inner + ch]));
-            }
+            decode_state_step(b, d_inner, ch, k4, d, hq[u], aq[u], bk, ck, s_xc, s_aux, Dv, ssm_state, y);
         }
-        if constexpr (ONE) break;
     }
 }
 
@@ -522,9 +656,14 @@ int launch_ssm_decode(int64_t batch, int64_t d_inner, int64_t dt_rank, int64_t d
                       const void* xpart, const void* z, const float* conv_w, const float* conv_b,
                       float* conv_state, const void* w_x, const void* w_dt, const float* dt_bias,
                       const float* A, const float* D, float* ssm_state, void* y, void* stream) {
-    const size_t lds = ssm_decode_lds(d_inner, dt_rank);
     HX_REQUIRE(batch <= 0x7fffffff, HX_ERR_UNSUPPORTED, "mamba_layer_decode: batch %lld too large",
                (long long)batch);
+    // the row kernel's float2 loads of the conv window, conv_b, dt_bias and D, and 16-byte W_x
+    // chunks, need those alignments; otherwise the general kernel runs
+    const bool row = d_inner <= 2 * kDecThreads && dt_rank <= 32 && aligned(conv_state, 8) &&
+                     aligned(conv_b, 8) && aligned(dt_bias, 8) && aligned(D, 8);
+    const bool xv4 = d_inner % 8 == 0 && aligned(w_x, 16);
+    const size_t lds = row ? (size_t)(4 * d_inner + 64) * sizeof(float) : ssm_decode_lds(d_inner, dt_rank);
     auto go = [&](auto kern) {
         if (lds > 64 * 1024 &&
             hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
@@ -536,19 +675,27 @@ int launch_ssm_decode(int64_t batch, int64_t d_inner, int64_t dt_rank, int64_t d
         HX_LAUNCH_CHECK();
         return (int)HX_OK;
     };
-    if (d_inner <= 2 * kDecThreads && dt_rank <= 32) {
+    if (row && xv4) {
         switch (d_conv) {
-            case 1: return go(ssm_decode_kernel<1, true>);
-            case 2: return go(ssm_decode_kernel<2, true>);
-            case 3: return go(ssm_decode_kernel<3, true>);
-            default: return go(ssm_decode_kernel<4, true>);
+            case 1: return go(ssm_decode_row_kernel<1, true>);
+            case 2: return go(ssm_decode_row_kernel<2, true>);
+            case 3: return go(ssm_decode_row_kernel<3, true>);
+            default: return go(ssm_decode_row_kernel<4, true>);
+        }
+    }
+    if (row) {
+        switch (d_conv) {
+            case 1: return go(ssm_decode_row_kernel<1, false>);
+            case 2: return go(ssm_decode_row_kernel<2, false>);
+            case 3: return go(ssm_decode_row_kernel<3, false>);
+            default: return go(ssm_decode_row_kernel<4, false>);
         }
     }
     switch (d_conv) {
-        case 1: return go(ssm_decode_kernel<1, false>);
-        case 2: return go(ssm_decode_kernel<2, false>);
-        case 3: return go(ssm_decode_kernel<3, false>);
-        default: return go(ssm_decode_kernel<4, false>);
+        case 1: return go(ssm_decode_kernel<1>);
+        case 2: return go(ssm_decode_kernel<2>);
+        case 3: return go(ssm_decode_kernel<3>);
+        default: return go(ssm_decode_kernel<4>);
     }
 }
 

@@ -190,6 +190,32 @@ def test_lm_decode_general_shapes(dev, dm, di, r, K):
     assert err <= 1e-2, err
 
 
+@pytest.mark.parametrize("dm,di,r,K", [(132, 132, 12, 2), (100, 200, 16, 1), (1020, 1020, 32, 3),
+                                       (512, 1024, 20, 4)])
+def test_lm_decode_row_kernel_shapes(dev, dm, di, r, K):
+    """The decode step's row kernel (d_inner <= 1024, dt_rank <= 32) off config 5's shape:
+    8-byte W_x chunks (d_inner % 8 != 0: 132, 1020), 16-byte chunks with lanes past d_inner
+    (200), conv widths 1 to 3, x_proj outputs past dt_rank + 32 on the last waves, element
+    dt_proj rows (dt_rank 12, 16, 20) and the 16-byte ones (32). Two decode steps against the
+    oracle; decode continues the prefill."""
+    P = lm_params(2, dm, di, 16, r, K, 256, seed=di + r)
+    m = model_from(P, dev, dt_rank=r, K=K)
+    tok = np.random.default_rng(di + 1).integers(0, 256, (3, 8)).astype(np.int32)
+    td = torch.from_numpy(tok).to(dev)
+    print(f"case row decode d_model {dm} d_inner {di} dt_rank {r} conv {K}", flush=True)
+    _, state = m.prefill(td[:, :6])
+    _, rstate = oracle.lm_prefill(tok[:, :6], P, r)
+    for t in (6, 7):
+        lg = m.decode_step(td[:, t].contiguous(), state)
+        torch.cuda.synchronize()
+        rl, rstate = oracle.lm_decode_step(tok[:, t], P, rstate, r)
+        err = norm_err(lg.cpu().numpy(), rl)
+        assert err <= 1e-2, (t, err)
+    full, _ = m.prefill(td)
+    err = norm_err(lg.cpu().numpy(), full[:, 7].cpu().numpy())
+    assert err <= 1e-2, err
+
+
 def test_lm_config5_full_size(dev):
     """12 layers, d_model 512, d_inner 1024, N 16, dt_rank 32, conv 4, vocab
     256, batch 16 x L 8192 prefill, then one decode step for all 16 sequences. The oracle checks
