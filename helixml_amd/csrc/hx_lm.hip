@@ -1,6 +1,7 @@
 // hx_lm.hip — the byte-level SSM LM pieces around the Mamba block: token
 // embedding gather, RMSNorm, and the single-step causal conv of recurrent decode.
 #include "hx_common.h"
+#include "hx_wave.h"
 
 namespace hx {
 namespace {
@@ -33,9 +34,26 @@ __device__ inline float wave_sum(float v) {
     return v;
 }
 
+// Sum over the wave, the same value in every lane: DPP within each 16-lane row (quad permutes,
+// the half-row mirror, the row rotate by 8), then the rows and the halves by register swaps. Every
+// level adds a lane's value to its partner's, so all lanes form the identical sum.
+__device__ inline float wave_allsum(float v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppRor8>(v);
+    float a = v, b = v;
+    swap16(a, b);
+    v = a + b;
+    a = v; b = v;
+    swap32(a, b);
+    return a + b;
+}
+
 // nn::RMSNorm::forward (crates/nn/src/lib.rs:258-285): ms = mean(x^2 over the row);
-// y = x / sqrt(ms + eps) * w. One wave per row; the row is read once (kept in registers when
-// dim <= 64 * 4 * RPL).
+// y = x / sqrt(ms + eps) * w. One wave per row, dim <= 64 * 4 * RPL: the row and the weight
+// are loaded together in one round (the weight is L2-hot), kept in registers, and each lane
+// writes its 4 outputs with one 8-byte (bf16) or 16-byte (fp32) store.
 template <typename TO, int RPL>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int64_t dim,
                                                       const float* __restrict__ x,
@@ -45,29 +63,35 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(int64_t rows, int64_t dim,
     if (r >= rows) return;
     const int lane = threadIdx.x & 63;
     const float* xr = x + r * dim;
-    float4 v[RPL];
-    float ss = 0.0f;
+    float4 v[RPL], wv[RPL];
 #pragma unroll
     for (int i = 0; i < RPL; ++i) {
         const int64_t c = (int64_t)(i * 64 + lane) * 4;
         v[i] = c < dim ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0, 0, 0, 0);
+        wv[i] = c < dim ? *reinterpret_cast<const float4*>(w + c) : make_float4(0, 0, 0, 0);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) {
         ss = fmaf(v[i].x, v[i].x, ss);
         ss = fmaf(v[i].y, v[i].y, ss);
         ss = fmaf(v[i].z, v[i].z, ss);
         ss = fmaf(v[i].w, v[i].w, ss);
     }
-    ss = wave_sum(ss);
+    ss = wave_allsum(ss);
     const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
     TO* yr = y + r * dim;
 #pragma unroll
     for (int i = 0; i < RPL; ++i) {
         const int64_t c = (int64_t)(i * 64 + lane) * 4;
         if (c < dim) {
-            const float4 wv = *reinterpret_cast<const float4*>(w + c);
-            Storage<TO>::store(yr + c, v[i].x * inv * wv.x);
-            Storage<TO>::store(yr + c + 1, v[i].y * inv * wv.y);
-            Storage<TO>::store(yr + c + 2, v[i].z * inv * wv.z);
-            Storage<TO>::store(yr + c + 3, v[i].w * inv * wv.w);
+            const float4 o = make_float4(v[i].x * inv * wv[i].x, v[i].y * inv * wv[i].y,
+                                         v[i].z * inv * wv[i].z, v[i].w * inv * wv[i].w);
+            if constexpr (std::is_same_v<TO, float>) {
+                *reinterpret_cast<float4*>(yr + c) = o;
+            } else {
+                *reinterpret_cast<uint2*>(yr + c) = make_uint2(pack_bf16x2(o.x, o.y), pack_bf16x2(o.z, o.w));
+            }
         }
     }
 }
@@ -169,7 +193,8 @@ extern "C" int hx_rmsnorm_fwd(int64_t rows, int64_t dim, const float* x, const f
     HX_REQUIRE(x && weight && y, HX_ERR_INVALID_INPUT, "rmsnorm: NULL pointer");
     hipStream_t s = as_stream(stream);
     dim3 grid((unsigned)((rows + 3) / 4));
-    const bool vec = dim % 4 == 0 && aligned(x, 16) && aligned(weight, 16);
+    const bool vec = dim % 4 == 0 && aligned(x, 16) && aligned(weight, 16) &&
+                     aligned(y, out_dtype == HX_BF16 ? 8 : 16);
     if (vec && dim <= 512) {
         if (out_dtype == HX_BF16)
             hipLaunchKernelGGL((rmsnorm_kernel<uint16_t, 2>), grid, dim3(256), 0, s, rows, dim, x,
