@@ -794,6 +794,22 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_narrow_kernel(int64_t M, int
 // discarded).
 constexpr int XBM = 256, XBN = 256;
 
+// The loads of a K tile into the ring, QPW instructions per wave, go out over a window of LW
+// sub-steps: the last sub-step of the K tile NST before it (right after the barrier that frees its
+// stage) and the first LW - 1 sub-steps of the next K tile. Issued as one burst, a block's 64 load
+// instructions of a 64-wide K tile arrive at the load path in a quarter of the tile's MFMA time,
+// twice what it accepts, and the waves stall on issue while their MFMAs drain. Without any loads
+// in the loop (a timing copy multiplying stale stage data) config 3 in_proj takes 410 us against
+// 485-506; with a 3-sub-step window 460-490 (2-5% faster in five A/B runs on different boxes,
+// out_proj 3-4%, same bits); a 2-sub-step window gains less, and a 4-sub-step window, whose last
+// loads have one sub-step before the barrier that waits for them, nothing. Slot w of the window
+// issues loads lw_base .. + lw_cnt. (The persistent kernel keeps the one-sub-step form: the
+// window measured slower there.)
+template <int QPW, int LW>
+__device__ constexpr int lw_cnt(int w) { return QPW / LW + (w < QPW % LW ? 1 : 0); }
+template <int QPW, int LW>
+__device__ constexpr int lw_base(int w) { return w * (QPW / LW) + (w < QPW % LW ? w : QPW % LW); }
+
 template <int KB>
 __device__ inline int xswz(int row) {  // XOR applied to the 16-byte chunk index of a row
     return KB == 64 ? (row & 7) : ((row >> 1) & 3);
@@ -927,6 +943,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
     };
     static_assert(NST >= 2 && NST <= 4 && (SUB == 2 || SUB == 4) && 3 * QPW <= 63 && QPW % 8 == 0,
                   "ring depth / K tile");
+    // window of LW sub-steps with two stages: its slots precede the barrier that waits for them
+    // (vmcnt(0): no other K tile's loads are in flight there); deeper rings keep one sub-step
+    constexpr int LW = (NST == 2 && SUB == 4) ? 3 : 1;
     bf16x8 fg[2][8];  // [buffer][A rows 0..3, B rows 0..3] (32-row fragments)
 #pragma unroll
     for (int t = 0; t < NST; ++t)
@@ -940,10 +959,13 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
 #pragma unroll
         for (int s = 0; s < SUB; ++s) {
             const int cur = s & 1, nxt = cur ^ 1;
-            // the last sub-step issues tile kt + NST's loads between its MFMAs, QPW / 8 after each
-            // pair, rather than in one burst before them (measured: config 3 in_proj 493 -> 468 us,
-            // out_proj 231 -> 223 us, same bits)
-            const bool ilv = s == SUB - 1 && kt + NST < nk;  // uniform
+            // loads between the MFMAs (one burst before them measured config 3 in_proj 493 vs 468
+            // us), over a window of LW sub-steps: slot w = 0 is this tile's last sub-step (starts
+            // tile kt + NST), slot w >= 1 sub-step w - 1 (continues tile kt + NST - 1)
+            const int w = s == SUB - 1 ? 0 : (s + 1 < LW ? s + 1 : -1);
+            const int64_t tl = w == 0 ? kt + NST : kt + NST - 1;
+            const bool ilv = w == 0 ? tl < nk : (w > 0 && kt >= 1 && tl < nk);  // uniform
+            const int jb = w < 0 ? 0 : lw_base<QPW, LW>(w), jc = w < 0 ? 0 : lw_cnt<QPW, LW>(w);
             if (s == SUB - 1 && kt + 1 < nk) wait_barrier(nk - 2 - kt < NST - 2 ? nk - 2 - kt : NST - 2);
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
@@ -957,11 +979,11 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
                 // no load targets any more, so that no sub-step branches)
                 fg[nxt][q] = s < SUB - 1 ? frag(stg, s + 1, q) : frag(nstg, 0, q);
                 if (ilv) {
-                    char* stage = sbase + (int)((kt + NST) % NST) * STB;
+                    char* stage = sbase + (int)(tl % NST) * STB;
 #pragma unroll
-                    for (int u = 0; u < QPW / 8; ++u) {
-                        const int j = q * (QPW / 8) + u;
-                        __builtin_amdgcn_global_load_lds((gvoid_t*)(src[j] + (kt + NST) * KB),
+                    for (int u = q * jc / 8; u < (q + 1) * jc / 8; ++u) {
+                        const int j = jb + u;
+                        __builtin_amdgcn_global_load_lds((gvoid_t*)(src[j] + tl * KB),
                                                          (lvoid_t*)(stage + (wave * QPW + j) * 1024), 16, 0, 0);
                     }
                 }
@@ -970,7 +992,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
             for (int q = 0; q < 8; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-                __builtin_amdgcn_sched_group_barrier(0x020, QPW / 8, 0);  // loads (last sub-step)
+                __builtin_amdgcn_sched_group_barrier(0x020, (lw_cnt<QPW, LW>(0) + 7) / 8, 0);  // loads
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -1191,7 +1213,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256p_kernel(int64_t M, int6
             for (int s = 0; s < SUB; ++s) {
                 const int cur = s & 1, nxt = cur ^ 1;
                 // the last sub-step issues K tile p + NST's loads between its MFMAs, QPW / 8
-                // after each pair (uniform condition)
+                // after each pair (uniform condition); spread over a window of sub-steps as in the
+                // one-tile kernel they measured slower here (config 5 in_proj 308 -> 320 us)
                 const bool ld = s == SUB - 1 && p + NST < total;
                 int64_t koff = 0;
                 char* lstage = sbase;
