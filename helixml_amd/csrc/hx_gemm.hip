@@ -1481,24 +1481,40 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
     if (vec && K % 8 == 0 && K >= 8 && g_gemm_kernel != 1 && g_gemm_kernel != 4 &&
         (g_gemm_kernel == 3 || tiles128 < 128) && (M + 31) / 32 <= 65535) {
         // 64-wide tiles where they still give the GPU 256 blocks (decode in_proj), else 32-wide;
-        // SP covers a wave's whole share of K where it can (one round of loads)
+        // SP covers a wave's whole share of K where it can (one round of loads). Where the grid
+        // has at most one block per CU, blocks of 8 waves: each wave loads half the share, and two
+        // waves per SIMD overlap their load rounds (config 5 decode at batch 256: 403 -> 394 us
+        // per step, the same with only out_proj's 128 blocks so; the sums over the waves' K
+        // slices then meet in 8 parts)
         const bool wide = ((N + 63) / 64) * ((M + 31) / 32) >= 256;
-        const int64_t spw = ((K + 15) / 16 + 3) / 4;  // K-steps per wave
-        auto launch = [&](auto kern, int tn) {
+        const int tn = wide ? 64 : 32;
+        const bool w8 = ((N + tn - 1) / tn) * ((M + 31) / 32) <= device_cus();
+        const int64_t spw = ((K + 15) / 16 + (w8 ? 7 : 3)) / (w8 ? 8 : 4);  // K-steps per wave
+        auto launch = [&](auto kern, int nw) {
             dim3 sg((unsigned)((N + tn - 1) / tn), (unsigned)((M + 31) / 32));
-            hipLaunchKernelGGL(kern, sg, dim3(256), 0, as_stream(stream), M, N, K, (const uint16_t*)X,
+            hipLaunchKernelGGL(kern, sg, dim3(64 * nw), 0, as_stream(stream), M, N, K, (const uint16_t*)X,
                                ldx, (const uint16_t*)W, ldw, bias, o);
         };
-        if (wide) {
-            if (spw <= 2) launch(gemm_bf16_nt_skinny_kernel<64, 4, 2>, 64);
-            else if (spw <= 4) launch(gemm_bf16_nt_skinny_kernel<64, 4, 4>, 64);
-            else if (spw <= 8) launch(gemm_bf16_nt_skinny_kernel<64, 4, 8>, 64);
-            else launch(gemm_bf16_nt_skinny_kernel<64, 4, 16>, 64);
+        if (wide && w8) {
+            if (spw <= 2) launch(gemm_bf16_nt_skinny_kernel<64, 8, 2>, 8);
+            else if (spw <= 4) launch(gemm_bf16_nt_skinny_kernel<64, 8, 4>, 8);
+            else if (spw <= 8) launch(gemm_bf16_nt_skinny_kernel<64, 8, 8>, 8);
+            else launch(gemm_bf16_nt_skinny_kernel<64, 8, 16>, 8);
+        } else if (wide) {
+            if (spw <= 2) launch(gemm_bf16_nt_skinny_kernel<64, 4, 2>, 4);
+            else if (spw <= 4) launch(gemm_bf16_nt_skinny_kernel<64, 4, 4>, 4);
+            else if (spw <= 8) launch(gemm_bf16_nt_skinny_kernel<64, 4, 8>, 4);
+            else launch(gemm_bf16_nt_skinny_kernel<64, 4, 16>, 4);
+        } else if (w8) {
+            if (spw <= 2) launch(gemm_bf16_nt_skinny_kernel<32, 8, 2>, 8);
+            else if (spw <= 4) launch(gemm_bf16_nt_skinny_kernel<32, 8, 4>, 8);
+            else if (spw <= 8) launch(gemm_bf16_nt_skinny_kernel<32, 8, 8>, 8);
+            else launch(gemm_bf16_nt_skinny_kernel<32, 8, 16>, 8);
         } else {
-            if (spw <= 2) launch(gemm_bf16_nt_skinny_kernel<32, 4, 2>, 32);
-            else if (spw <= 4) launch(gemm_bf16_nt_skinny_kernel<32, 4, 4>, 32);
-            else if (spw <= 8) launch(gemm_bf16_nt_skinny_kernel<32, 4, 8>, 32);
-            else launch(gemm_bf16_nt_skinny_kernel<32, 4, 16>, 32);
+            if (spw <= 2) launch(gemm_bf16_nt_skinny_kernel<32, 4, 2>, 4);
+            else if (spw <= 4) launch(gemm_bf16_nt_skinny_kernel<32, 4, 4>, 4);
+            else if (spw <= 8) launch(gemm_bf16_nt_skinny_kernel<32, 4, 8>, 4);
+            else launch(gemm_bf16_nt_skinny_kernel<32, 4, 16>, 4);
         }
         HX_LAUNCH_CHECK();
         return HX_OK;
