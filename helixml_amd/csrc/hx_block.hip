@@ -265,6 +265,10 @@ using namespace ::hx;
 //           h = exp(dl * A[c][n]) * h + dl * xc * B[n]; y = (sum_n C[n] * h + D * xc) * silu(z)
 // State [batch][d_inner][16] fp32 and conv window [batch][d_conv-1][d_inner] fp32 in place.
 constexpr int kDecThreads = 512;
+// The state is read and written once per step: non-temporal (streaming) accesses keep its
+// 16.8 MB per layer at config 5 from evicting the data the step reuses (the layer's weights, the
+// activations the next launch reads) from the caches; the config-5 decode step 0.391 -> 0.348 ms.
+typedef float hx_f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline float bf16r(float v) { return bf16_bits_to_f32(Storage<uint16_t>::round(v)); }
 
@@ -292,8 +296,8 @@ __device__ __attribute__((always_inline)) inline void decode_state_step(int64_t 
         h4[i] = fmaf(ab, h4[i], du * bk[i]);
         yy = fmaf(ck[i], h4[i], yy);
     }
-    reinterpret_cast<float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4] =
-        make_float4(h4[0], h4[1], h4[2], h4[3]);
+    __builtin_nontemporal_store(hx_f32x4{h4[0], h4[1], h4[2], h4[3]},
+                                reinterpret_cast<hx_f32x4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16) + k4);
     yy += __shfl_xor(yy, 1, 64);
     yy += __shfl_xor(yy, 2, 64);
     if (k4 == 0) {
@@ -392,7 +396,8 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_row_kernel(
 #pragma unroll
     for (int u = 0; u < UC; ++u) {
         const int ch = (tid >> 2) + u * CSTEP < d_inner ? (tid >> 2) + u * CSTEP : d_inner - 1;  // clamped: unused
-        hq[u] = reinterpret_cast<const float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4];
+        const hx_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const hx_f32x4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16) + k4);
+        hq[u] = make_float4(v[0], v[1], v[2], v[3]);
     }
     if (2 * tid < d_inner) {
         *reinterpret_cast<float2*>(s_xc + c) = make_float2(xcv[0], xcv[1]);
