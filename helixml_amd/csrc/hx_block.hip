@@ -265,9 +265,10 @@ using namespace ::hx;
 //           h = exp(dl * A[c][n]) * h + dl * xc * B[n]; y = (sum_n C[n] * h + D * xc) * silu(z)
 // State [batch][d_inner][16] fp32 and conv window [batch][d_conv-1][d_inner] fp32 in place.
 constexpr int kDecThreads = 512;
-// The state is read and written once per step: non-temporal (streaming) accesses keep its
-// 16.8 MB per layer at config 5 from evicting the data the step reuses (the layer's weights, the
-// activations the next launch reads) from the caches; the config-5 decode step 0.391 -> 0.348 ms.
+// The state is read and written once per step: non-temporal (streaming) accesses keep its 16.8 MB
+// per layer at config 5 from evicting the data the step reuses (the layer's weights, the
+// activations the next launch reads) from the caches; the config-5 decode step 0.391 -> 0.348
+// ms. (The conv window, 3 MB per layer, measured 2 us per step slower streamed so.)
 typedef float hx_f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline float bf16r(float v) { return bf16_bits_to_f32(Storage<uint16_t>::round(v)); }
@@ -625,7 +626,8 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_kernel(
 #pragma unroll
         for (int u = 0; u < UC; ++u) {
             const int ch = ch0 + u * CSTEP < d_inner ? ch0 + u * CSTEP : d_inner - 1;  // clamped: unused
-            hq[u] = reinterpret_cast<const float4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16)[k4];
+            const hx_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const hx_f32x4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16) + k4);
+            hq[u] = make_float4(v[0], v[1], v[2], v[3]);
             aq[u] = reinterpret_cast<const float4*>(A + (int64_t)ch * 16)[k4];
         }
 #pragma unroll

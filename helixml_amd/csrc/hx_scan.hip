@@ -991,11 +991,14 @@ template <bool HZ, int OPS> struct HandoverRead {
 
 // One element stored through a raw buffer resource: offsets at or past the resource's size are
 // dropped by the hardware, so a store needs no branch (and the compiler's wait counts stay exact).
+// Cache policy of the split-state kernel's input loads and of the wave kernels' output stores:
+// non-temporal (each element is read or written once; config 2 132.0 -> 130.3 us).
+constexpr int kStream = 2;
 __device__ inline void buf_store(float v, __amdgpu_buffer_rsrc_t rs, uint32_t off, float*) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, off, 0, kStream);
 }
 __device__ inline void buf_store(float v, __amdgpu_buffer_rsrc_t rs, uint32_t off, uint16_t*) {
-    __builtin_amdgcn_raw_buffer_store_b16(Storage<uint16_t>::round(v), rs, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(Storage<uint16_t>::round(v), rs, off, 0, kStream);
 }
 constexpr int kBufRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
 
@@ -1462,10 +1465,10 @@ __global__ __launch_bounds__(512) void scan_ws2_kernel(
             const uint32_t cb = (uint32_t)qc * chunk_bytes;
 #pragma unroll
             for (int i = 0; i < NLD; ++i) {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lvoid_t*)(dst + 1024 * i), 16, loff[i] + cb, 0, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_d, (lvoid_t*)(dst + OPB + 1024 * i), 16, loff[i] + cb, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lvoid_t*)(dst + 1024 * i), 16, loff[i] + cb, 0, 0, kStream);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_d, (lvoid_t*)(dst + OPB + 1024 * i), 16, loff[i] + cb, 0, 0, kStream);
                 if (HAS_Z)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_z, (lvoid_t*)(dst + 2 * OPB + 1024 * i), 16, loff[i] + cb, 0, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_z, (lvoid_t*)(dst + 2 * OPB + 1024 * i), 16, loff[i] + cb, 0, 0, kStream);
             }
         };
         const int c = lane & 15, s2 = lane >> 4;
