@@ -991,8 +991,11 @@ template <bool HZ, int OPS> struct HandoverRead {
 
 // One element stored through a raw buffer resource: offsets at or past the resource's size are
 // dropped by the hardware, so a store needs no branch (and the compiler's wait counts stay exact).
-// Cache policy of the split-state kernel's input loads and of the wave kernels' output stores:
-// non-temporal (each element is read or written once; config 2 132.0 -> 130.3 us).
+// Cache policy of the split-state kernel's input loads and of the warp-specialised kernels'
+// output stores: non-temporal (each element is read or written once; config 2 132.0 -> 130.3
+// us). The wave kernel keeps the default: streaming its loads and stores measured config 4
+// 0.70 -> 0.80 ms (the end-state pass's reads are read again by the full pass) and config 3
+// slower.
 constexpr int kStream = 2;
 __device__ inline void buf_store(float v, __amdgpu_buffer_rsrc_t rs, uint32_t off, float*) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, off, 0, kStream);
