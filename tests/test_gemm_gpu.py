@@ -326,3 +326,29 @@ def test_gemm_persistent_matches_one_tile_per_block(dev, M, N, K):
     for i, (a, c) in enumerate(zip(got, want)):
         assert torch.equal(a, c), f"output {i} differs from the one-tile-per-block kernel"
     assert norm_err(got[0].cpu().numpy(), ref(X, W, b, 1)) <= 1e-5
+
+
+@pytest.mark.parametrize("kernel", [5, 8])
+def test_gemm_pointer_loads_past_2gib(dev, kernel):
+    """The 256 x 256 kernels load their tiles with 32-bit buffer offsets where every byte offset
+    into X and W stays below 2^31, and with 64-bit pointer loads otherwise. X here is exactly 2 GiB
+    (131072 x 8192 bf16), so the whole product takes the pointer form; its first and last 256 rows
+    must be the bits of the same kernel run on those rows alone (the buffer form: the same MFMA
+    products in the same order)."""
+    M, N, K = 131072, 256, 8192
+    g = torch.Generator(device=dev).manual_seed(kernel)
+    X = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, device=dev, generator=g) / np.sqrt(K)).to(torch.bfloat16)
+    print(f"case gemm {M}x{N}x{K} kernel {kernel} (2 GiB X)", flush=True)
+    ssm.set_gemm_kernel(kernel)
+    try:
+        Y = ssm.gemm_bf16(X, W, out_dtype=torch.float32)
+        head = ssm.gemm_bf16(X[:256].contiguous(), W, out_dtype=torch.float32)
+        tail = ssm.gemm_bf16(X[M - 256:].contiguous(), W, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+    finally:
+        ssm.set_gemm_kernel(0)
+    assert torch.equal(Y[:256], head)
+    assert torch.equal(Y[M - 256:], tail)
+    assert norm_err(tail.cpu().numpy(), ref(X[M - 256:], W)) <= 1e-5
+    del X, Y
