@@ -801,11 +801,11 @@ constexpr int kGemmBufRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data f
 // instructions of a 64-wide K tile arrive at the load path in a quarter of the tile's MFMA time,
 // twice what it accepts, and the waves stall on issue while their MFMAs drain. Without any loads
 // in the loop (a timing copy multiplying stale stage data) config 3 in_proj takes 410 us against
-// 485-506; with a 3-sub-step window 460-490 (2-5% faster in five A/B runs on different boxes,
-// out_proj 3-4%, same bits); a 2-sub-step window gains less, and a 4-sub-step window, whose last
-// loads have one sub-step before the barrier that waits for them, nothing. Slot w of the window
-// issues loads lw_base .. + lw_cnt. (The persistent kernel keeps the one-sub-step form: the
-// window measured slower there.)
+// 485-506. With the buffer loads below, one box, three rounds: one sub-step 474-478 us, a
+// 2-sub-step window 456-459 (out_proj 259-268 against 275-282), 3 sub-steps 461-463, 4 (whose
+// last loads have one sub-step before the barrier that waits for them) 484-490; the same bits.
+// Slot w of the window issues loads lw_base .. + lw_cnt. (The persistent kernel keeps the
+// one-sub-step form: a window measured slower there.)
 template <int QPW, int LW>
 __device__ constexpr int lw_cnt(int w) { return QPW / LW + (w < QPW % LW ? 1 : 0); }
 template <int QPW, int LW>
@@ -960,7 +960,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_d256_kernel(int64_t M, int64
                   "ring depth / K tile");
     // window of LW sub-steps with two stages: its slots precede the barrier that waits for them
     // (vmcnt(0): no other K tile's loads are in flight there); deeper rings keep one sub-step
-    constexpr int LW = (NST == 2 && SUB == 4) ? 3 : 1;
+    constexpr int LW = (NST == 2 && SUB == 4) ? 2 : 1;
     bf16x8 fg[2][8];  // [buffer][A rows 0..3, B rows 0..3] (32-row fragments)
 #pragma unroll
     for (int t = 0; t < NST; ++t)
