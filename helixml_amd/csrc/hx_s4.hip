@@ -13,6 +13,10 @@
 #include "hx_common.h"
 #include "hx_wave.h"
 
+// The outputs of the S4D wave kernel and the time-parallel output kernel are written once:
+// non-temporal stores (config 4: S4 time-parallel 392.9 -> 388.3 us, S4D about 1.5% faster).
+typedef float hx_f32x4s __attribute__((ext_vector_type(4)));
+
 namespace hx {
 namespace {
 
@@ -646,9 +650,11 @@ __global__ __launch_bounds__(256) void s4d_wave_kernel(
     auto store_out = [&](int64_t t0, int buf) __attribute__((always_inline)) {
         if constexpr (!END_ONLY) {
             const int64_t t = t0 + mrow;
-            if (mvalid && t < tend)
-                *reinterpret_cast<float4*>(y + rowbase + t * Dm + mch) =
-                    *reinterpret_cast<const float4*>(&s_out[buf][mrow][mcl]);
+            if (mvalid && t < tend) {
+                const float4 v = *reinterpret_cast<const float4*>(&s_out[buf][mrow][mcl]);
+                __builtin_nontemporal_store(hx_f32x4s{v.x, v.y, v.z, v.w},
+                                            reinterpret_cast<hx_f32x4s*>(y + rowbase + t * Dm + mch));
+            }
         }
     };
     // one chunk: FULL = all 16 steps inside the segment (no per-step guard)
@@ -1007,7 +1013,7 @@ __global__ __launch_bounds__(256) void s4p_output_kernel(int64_t M, int64_t L, i
         float acc = dd * sx[mm][tt];
 #pragma unroll
         for (int n = 0; n < 16; ++n) acc = fmaf(c[n], sh[tt][n], acc);
-        y[t * M + m] = acc * g;
+        __builtin_nontemporal_store(acc * g, y + t * M + m);
     }
 }
 
