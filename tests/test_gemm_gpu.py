@@ -21,9 +21,13 @@ def ref(X, W, bias=None, act=0):
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 32), (256, 384, 512), (100, 70, 40), (1, 1, 8),
-                                   (300, 160, 4096), (512, 2048, 256), (129, 257, 264)])
+                                   (300, 160, 4096), (512, 2048, 256), (129, 257, 264),
+                                   (256, 2048, 512), (96, 96, 4104)])
 @pytest.mark.parametrize("act", [0, 1])
 def test_gemm_fp32_out(dev, M, N, K, act):
+    """Default kernel choice. (256, 2048, 512) is the decode in_proj shape: the small-M kernel's
+    64-wide tiles with 8-wave blocks (256 blocks, one per CU); (96, 96, 4104) its 32-wide 8-wave
+    form with K past one round of loads per wave and a last piece past K (masked)."""
     g = torch.Generator().manual_seed(M * 7 + N)
     X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
     W = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(torch.bfloat16).to(dev)
