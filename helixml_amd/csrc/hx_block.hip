@@ -276,11 +276,10 @@ __device__ inline float bf16r(float v) { return bf16_bits_to_f32(Storage<uint16_
 // Pass 2 of both decode kernels for one channel ch of the sequence b: k4 = lane % 4 holds states
 // 4 k4 .. 4 k4 + 3 (hq, aq), dt_proj partial d over ranks 8 k4 .. 8 k4 + 7 (and beyond, looping)
 // summed across the 4 lanes; the state is stored, and the lane with k4 = 0 stores y.
-__device__ __attribute__((always_inline)) inline void decode_state_step(int64_t b, int d_inner, int ch, int k4, float d,
-                                         float4 hq, float4 aq, const float (&bk)[4],
-                                         const float (&ck)[4], const float* s_xc,
-                                         const float* s_aux, const float* Dv,
-                                         float* __restrict__ ssm_state, uint16_t* __restrict__ y) {
+__device__ __attribute__((always_inline)) inline void decode_state_step(
+    int64_t b, int d_inner, int ch, int k4, float d, float4 hq, float4 aq, const float (&bk)[4],
+    const float (&ck)[4], const float* s_xc, const float* s_aux, const float* Dv,
+    float* __restrict__ ssm_state, uint16_t* __restrict__ y) {
     d += __shfl_xor(d, 1, 64);
     d += __shfl_xor(d, 2, 64);
     if (ch >= d_inner) return;  // uniform per lane group
