@@ -253,7 +253,7 @@ struct BlockWeights {
 // ----------------------------------------------------------------------------- fused decode
 using namespace ::hx;
 
-// The SSM half of one recurrent decode step of a layer, one block of 512 threads per sequence:
+// The SSM half of one recurrent decode step of a layer, one block per sequence:
 // the conv window step, x_proj (dt_lo | B | C), dt_proj, the state update with the D skip and
 // the SiLU(z) gate — four launches of the unfused step in one, with every intermediate in LDS or
 // registers instead of HBM. Rounding points are the unfused path's (xc, dt_lo, B, C and dt are
@@ -264,7 +264,8 @@ using namespace ::hx;
 //   pass 2: dt[c] = sum_r w_dt[c][r] * dt_lo[r]; dl = softplus(dt + dt_bias); per state n:
 //           h = exp(dl * A[c][n]) * h + dl * xc * B[n]; y = (sum_n C[n] * h + D * xc) * silu(z)
 // State [batch][d_inner][16] fp32 and conv window [batch][d_conv-1][d_inner] fp32 in place.
-constexpr int kDecThreads = 512;
+constexpr int kDecThreads = 512;   // the general kernel's block
+constexpr int kRowThreads = 1024;  // the row kernel's block (16 waves)
 // The state is read and written once per step: non-temporal (streaming) accesses keep its 16.8 MB
 // per layer at config 5 from evicting the data the step reuses (the layer's weights, the
 // activations the next launch reads) from the caches; the config-5 decode step 0.391 -> 0.348
@@ -306,21 +307,25 @@ __device__ __attribute__((always_inline)) inline void decode_state_step(
     }
 }
 
-// Row kernel, for d_inner <= 1024 and dt_rank <= 32 (one channel pair per thread in pass 1, at
-// most 64 x_proj outputs, 8 pass-2 channels per thread), straight-line code. The step is a chain
-// of dependent phases whose time is load latency and the CU's load port (every block reads all
-// of W_x, A and W_dt, 256 KB at config 5), so:
-//   * x_proj: wave w owns outputs 8w .. 8w+7 over every channel; lane l sums channel chunks
+// Row kernel, for d_inner <= 1024 and dt_rank <= 32: 16 waves (1024 threads), one conv channel
+// per thread in pass 1, 4 x_proj outputs per wave, 4 pass-2 channels per thread, straight-line
+// code. The step is a chain of dependent phases whose time is load latency, the CU's load port
+// (every block reads all of W_x, A and W_dt, 256 KB at config 5) and the state's 16.8 MB read
+// and write, so:
+//   * x_proj: wave w owns outputs 4w .. 4w+3 over every channel; lane l sums channel chunks
 //     8l + 512q (XV4: 16-byte loads, d_inner % 8 == 0) or 4l + 256q (8-byte loads), so each load
-//     instruction reads 1 KB or 512 B of a W_x row contiguously; the 8 per-lane sums meet by a
-//     register reduce-scatter (lane halves swapped, 16-lane rows swapped, DPP row rotate by 8:
-//     lane bits 5, 4, 3 pick the output 4 b5 + 2 b4 + b3) and a DPP sum over lane bits 0-2, with
-//     no LDS round trip and one barrier;
+//     instruction reads 1 KB or 512 B of a W_x row contiguously; the 4 per-lane sums meet by a
+//     register reduce-scatter (lane halves swapped, then 16-lane rows: lane bits 5, 4 pick the
+//     output 2 b5 + b4) and a DPP sum over the 16 lanes of a row, with no LDS round trip;
 //   * the loads are issued in the order the phases use them: pass-1 operands, W_x, then, once
 //     the pass-1 operands are in (they would otherwise queue behind 16 MB of state reads), this
-//     thread's state; A and the dt_proj rows (L2-hot) after the x_proj products.
+//     thread's state; A and the dt_proj rows (L2-hot) after the x_proj products; the conv-window
+//     stores come last (stores under a branch would make the compiler's waits for W_x also wait
+//     for the state).
+// 16 waves instead of 8 (each loading half the W_x rows and half the state): config 5 decode
+// 0.347 -> 0.332 ms per step.
 template <int KC, bool XV4>
-__global__ __launch_bounds__(kDecThreads) void ssm_decode_row_kernel(
+__global__ __launch_bounds__(kRowThreads) void ssm_decode_row_kernel(
     int d_inner, int dt_rank, const uint16_t* __restrict__ xpart, const uint16_t* __restrict__ z,
     const float* __restrict__ conv_w, const float* __restrict__ conv_b,
     float* __restrict__ conv_state, const uint16_t* __restrict__ w_x,
@@ -329,89 +334,68 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_row_kernel(
     uint16_t* __restrict__ y) {
     extern __shared__ __attribute__((aligned(16))) float s_dec[];
     const int J = dt_rank + 32;
-    float* s_xc = s_dec;                 // [d_inner]
-    float* s_aux = s_xc + d_inner;       // [3][d_inner]: dt_bias, D, z (staged in pass 1)
-    float* s_dbc = s_aux + 3 * d_inner;  // [64]: dt_lo | B | C, bf16-rounded
+    float* s_xc = s_dec;
+    float* s_aux = s_xc + d_inner;
+    float* s_dbc = s_aux + 3 * d_inner;
     const int64_t b = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint16_t* xr = xpart + b * (int64_t)d_inner;
-    const uint16_t* zr = z + b * (int64_t)d_inner;
     float* cst = conv_state + b * (int64_t)(KC - 1) * d_inner;
 
-    // pass-1 operands of channel pair (c, c + 1) (c clamped into range: values then unused)
-    const int c = 2 * tid < d_inner ? 2 * tid : d_inner - 2;
-    const uint32_t p_xw = *reinterpret_cast<const uint32_t*>(xr + c);
-    const uint32_t p_zw = *reinterpret_cast<const uint32_t*>(zr + c);
-    float2 p_prev[KC > 1 ? KC - 1 : 1];
+    const int c = tid < d_inner ? tid : d_inner - 1;
+    const float p_x = bf16_bits_to_f32(xpart[b * (int64_t)d_inner + c]);
+    const float p_z = bf16_bits_to_f32(z[b * (int64_t)d_inner + c]);
+    float p_prev[KC > 1 ? KC - 1 : 1];
 #pragma unroll
-    for (int j = 0; j < KC - 1; ++j) p_prev[j] = *reinterpret_cast<const float2*>(cst + (int64_t)j * d_inner + c);
-    float p_wk[2][KC];
+    for (int j = 0; j < KC - 1; ++j) p_prev[j] = cst[(int64_t)j * d_inner + c];
+    float p_wk[KC];
+    if constexpr (KC == 4) {
+        const float4 w4 = reinterpret_cast<const float4*>(conv_w)[c];
+        p_wk[0] = w4.x; p_wk[1] = w4.y; p_wk[2] = w4.z; p_wk[3] = w4.w;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        if constexpr (KC == 4) {
-            const float4 w4 = reinterpret_cast<const float4*>(conv_w)[c + e];
-            p_wk[e][0] = w4.x; p_wk[e][1] = w4.y; p_wk[e][2] = w4.z; p_wk[e][3] = w4.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < KC; ++j) p_wk[e][j] = conv_w[(c + e) * KC + j];
-        }
+        for (int j = 0; j < KC; ++j) p_wk[j] = conv_w[c * KC + j];
     }
-    // (prvalue selects: an lvalue conditional would select an address, one arm on the stack)
-    const float2 p_cb = conv_b ? *reinterpret_cast<const float2*>(conv_b + c) : make_float2(0.0f, 0.0f);
-    const float2 p_dtb = dt_bias ? *reinterpret_cast<const float2*>(dt_bias + c) : make_float2(0.0f, 0.0f);
-    const float2 p_dv = Dv ? *reinterpret_cast<const float2*>(Dv + c) : make_float2(0.0f, 0.0f);
-    // x_proj operands: rows 8 wave + r (clamped to J - 1: sums never stored), chunks past
-    // d_inner clamped to chunk 0 (not summed)
-    constexpr int CW = XV4 ? 8 : 4;  // channels per chunk
+    const float p_cb = conv_b ? conv_b[c] : 0.0f;
+    const float p_dtb = dt_bias ? dt_bias[c] : 0.0f;
+    const float p_dv = Dv ? Dv[c] : 0.0f;
+    constexpr int CW = XV4 ? 8 : 4;
     constexpr int NQ = 1024 / (64 * CW);
     using WChunk = std::conditional_t<XV4, uint4, uint2>;
-    WChunk wx[8][NQ];
+    WChunk wx[4][NQ];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        const int jr = 8 * wave + r < J ? 8 * wave + r : J - 1;
+    for (int r = 0; r < 4; ++r) {
+        const int jr = 4 * wave + r < J ? 4 * wave + r : J - 1;
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
             const int ch = CW * lane + 64 * CW * q < d_inner ? CW * lane + 64 * CW * q : 0;
             wx[r][q] = *reinterpret_cast<const WChunk*>(w_x + (int64_t)jr * d_inner + ch);
         }
     }
-
-    // pass 1: conv window step
-    const float xv[2] = {__uint_as_float(p_xw << 16), __uint_as_float(p_xw & 0xffff0000u)};
-    float xcv[2];
+    float acc0 = p_cb;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        float acc = e ? p_cb.y : p_cb.x;
-#pragma unroll
-        for (int j = 0; j < KC - 1; ++j) acc = fmaf(p_wk[e][j], e ? p_prev[j].y : p_prev[j].x, acc);
-        acc = fmaf(p_wk[e][KC - 1], xv[e], acc);
-        xcv[e] = bf16r(silu(acc));
-    }
-    // the state loads follow the pass-1 operands' arrival (no memory access moves above this)
-    asm volatile("" ::"v"(xcv[0]), "v"(xcv[1]) : "memory");
-    constexpr int UC = 8;
-    constexpr int CSTEP = kDecThreads / 4;
+    for (int j = 0; j < KC - 1; ++j) acc0 = fmaf(p_wk[j], p_prev[j], acc0);
+    acc0 = fmaf(p_wk[KC - 1], p_x, acc0);
+    const float xcv = bf16r(silu(acc0));
+    asm volatile("" ::"v"(xcv) : "memory");
+    constexpr int UC = 4;
+    constexpr int CSTEP = kRowThreads / 4;
     const int k4 = tid & 3;
     float4 hq[UC];
 #pragma unroll
     for (int u = 0; u < UC; ++u) {
-        const int ch = (tid >> 2) + u * CSTEP < d_inner ? (tid >> 2) + u * CSTEP : d_inner - 1;  // clamped: unused
+        const int ch = (tid >> 2) + u * CSTEP < d_inner ? (tid >> 2) + u * CSTEP : d_inner - 1;
         const hx_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const hx_f32x4*>(ssm_state + (b * (int64_t)d_inner + ch) * 16) + k4);
         hq[u] = make_float4(v[0], v[1], v[2], v[3]);
     }
-    if (2 * tid < d_inner) {
-        *reinterpret_cast<float2*>(s_xc + c) = make_float2(xcv[0], xcv[1]);
-        *reinterpret_cast<float2*>(s_aux + c) = p_dtb;
-        *reinterpret_cast<float2*>(s_aux + d_inner + c) = p_dv;
-        *reinterpret_cast<float2*>(s_aux + 2 * d_inner + c) =
-            make_float2(__uint_as_float(p_zw << 16), __uint_as_float(p_zw & 0xffff0000u));
+    if (tid < d_inner) {
+        s_xc[c] = xcv;
+        s_aux[c] = p_dtb;
+        s_aux[d_inner + c] = p_dv;
+        s_aux[2 * d_inner + c] = p_z;
     }
     __syncthreads();
 
-    // x_proj: this lane's share of the wave's 8 outputs
-    float acc[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
         const int c0 = CW * lane + 64 * CW * q;
@@ -423,7 +407,7 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_row_kernel(
                 xs[i] = x4.x; xs[i + 1] = x4.y; xs[i + 2] = x4.z; xs[i + 3] = x4.w;
             }
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
+            for (int r = 0; r < 4; ++r) {
                 uint32_t wv[CW / 2];
                 if constexpr (XV4) {
                     wv[0] = wx[r][q].x; wv[1] = wx[r][q].y; wv[2] = wx[r][q].z; wv[3] = wx[r][q].w;
@@ -438,7 +422,6 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_row_kernel(
             }
         }
     }
-    // A and the dt_proj rows (read by every block: L2-hot), under the reduction
     const bool vec_dt = (dt_rank & 31) == 0;
     float4 aq[UC];
     uint4 wq[UC];
@@ -449,25 +432,19 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_row_kernel(
         if (vec_dt) wq[u] = *reinterpret_cast<const uint4*>(w_dt + (int64_t)ch * dt_rank + 8 * k4);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { swap32(acc[i], acc[i + 4]); acc[i] += acc[i + 4]; }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) { swap16(acc[i], acc[i + 2]); acc[i] += acc[i + 2]; }
-    {
-        const bool up = (lane & 8) != 0;
-        const float send = up ? acc[0] : acc[1];
-        const float keep = up ? acc[1] : acc[0];
-        acc[0] = keep + dpp<kDppRor8>(send);
-    }
+    for (int i = 0; i < 2; ++i) { swap32(acc[i], acc[i + 2]); acc[i] += acc[i + 2]; }
+    swap16(acc[0], acc[1]);
+    acc[0] += acc[1];
     acc[0] += dpp<kDppXor1>(acc[0]);
     acc[0] += dpp<kDppXor2>(acc[0]);
     acc[0] += dpp<kDppHalfMirror>(acc[0]);
+    acc[0] += dpp<kDppRor8>(acc[0]);
     {
-        const int jrow = 8 * wave + 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1);
-        if ((lane & 7) == 0 && jrow < J) s_dbc[jrow] = bf16r(acc[0]);
+        const int jrow = 4 * wave + 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1);
+        if ((lane & 15) == 0 && jrow < J) s_dbc[jrow] = bf16r(acc[0]);
     }
     __syncthreads();
 
-    // pass 2: dt_proj, state update, skip and gate
     const float* dtlo = s_dbc;
     const float* Bn = s_dbc + dt_rank;
     const float* Cn = Bn + 16;
@@ -491,13 +468,10 @@ __global__ __launch_bounds__(kDecThreads) void ssm_decode_row_kernel(
         }
         decode_state_step(b, d_inner, ch, k4, d, hq[u], aq[u], bk, ck, s_xc, s_aux, Dv, ssm_state, y);
     }
-    // the advanced conv window, stored last: a store issued before a wait counts in it, and
-    // these are under a branch, so the compiler's waits for W_x would also wait for the state
-    if (2 * tid < d_inner) {
+    if (tid < d_inner) {
 #pragma unroll
-        for (int j = 0; j + 1 < KC - 1; ++j)
-            *reinterpret_cast<float2*>(cst + (int64_t)j * d_inner + c) = p_prev[j + 1];
-        if (KC > 1) *reinterpret_cast<float2*>(cst + (int64_t)(KC - 2) * d_inner + c) = make_float2(xv[0], xv[1]);
+        for (int j = 0; j + 1 < KC - 1; ++j) cst[(int64_t)j * d_inner + c] = p_prev[j + 1];
+        if (KC > 1) cst[(int64_t)(KC - 2) * d_inner + c] = p_x;
     }
 }
 
@@ -664,17 +638,14 @@ int launch_ssm_decode(int64_t batch, int64_t d_inner, int64_t dt_rank, int64_t d
                       const float* A, const float* D, float* ssm_state, void* y, void* stream) {
     HX_REQUIRE(batch <= 0x7fffffff, HX_ERR_UNSUPPORTED, "mamba_layer_decode: batch %lld too large",
                (long long)batch);
-    // the row kernel's float2 loads of the conv window, conv_b, dt_bias and D, and 16-byte W_x
-    // chunks, need those alignments; otherwise the general kernel runs
-    const bool row = d_inner <= 2 * kDecThreads && dt_rank <= 32 && aligned(conv_state, 8) &&
-                     aligned(conv_b, 8) && aligned(dt_bias, 8) && aligned(D, 8);
-    const bool xv4 = d_inner % 8 == 0 && aligned(w_x, 16);
+    const bool row = d_inner <= kRowThreads && dt_rank <= 32;
+    const bool xv4 = d_inner % 8 == 0 && aligned(w_x, 16);  // 16-byte W_x chunks
     const size_t lds = row ? (size_t)(4 * d_inner + 64) * sizeof(float) : ssm_decode_lds(d_inner, dt_rank);
-    auto go = [&](auto kern) {
+    auto go = [&](auto kern, int threads) {
         if (lds > 64 * 1024 &&
             hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
             return set_error(HX_ERR_UNSUPPORTED, "mamba_layer_decode: %zu bytes of LDS unavailable", lds);
-        hipLaunchKernelGGL(kern, dim3((unsigned)batch), dim3(kDecThreads), lds, as_stream(stream),
+        hipLaunchKernelGGL(kern, dim3((unsigned)batch), dim3(threads), lds, as_stream(stream),
                            (int)d_inner, (int)dt_rank, (const uint16_t*)xpart, (const uint16_t*)z,
                            conv_w, conv_b, conv_state, (const uint16_t*)w_x, (const uint16_t*)w_dt,
                            dt_bias, A, D, ssm_state, (uint16_t*)y);
@@ -683,25 +654,25 @@ int launch_ssm_decode(int64_t batch, int64_t d_inner, int64_t dt_rank, int64_t d
     };
     if (row && xv4) {
         switch (d_conv) {
-            case 1: return go(ssm_decode_row_kernel<1, true>);
-            case 2: return go(ssm_decode_row_kernel<2, true>);
-            case 3: return go(ssm_decode_row_kernel<3, true>);
-            default: return go(ssm_decode_row_kernel<4, true>);
+            case 1: return go(ssm_decode_row_kernel<1, true>, kRowThreads);
+            case 2: return go(ssm_decode_row_kernel<2, true>, kRowThreads);
+            case 3: return go(ssm_decode_row_kernel<3, true>, kRowThreads);
+            default: return go(ssm_decode_row_kernel<4, true>, kRowThreads);
         }
     }
     if (row) {
         switch (d_conv) {
-            case 1: return go(ssm_decode_row_kernel<1, false>);
-            case 2: return go(ssm_decode_row_kernel<2, false>);
-            case 3: return go(ssm_decode_row_kernel<3, false>);
-            default: return go(ssm_decode_row_kernel<4, false>);
+            case 1: return go(ssm_decode_row_kernel<1, false>, kRowThreads);
+            case 2: return go(ssm_decode_row_kernel<2, false>, kRowThreads);
+            case 3: return go(ssm_decode_row_kernel<3, false>, kRowThreads);
+            default: return go(ssm_decode_row_kernel<4, false>, kRowThreads);
         }
     }
     switch (d_conv) {
-        case 1: return go(ssm_decode_kernel<1>);
-        case 2: return go(ssm_decode_kernel<2>);
-        case 3: return go(ssm_decode_kernel<3>);
-        default: return go(ssm_decode_kernel<4>);
+        case 1: return go(ssm_decode_kernel<1>, kDecThreads);
+        case 2: return go(ssm_decode_kernel<2>, kDecThreads);
+        case 3: return go(ssm_decode_kernel<3>, kDecThreads);
+        default: return go(ssm_decode_kernel<4>, kDecThreads);
     }
 }
 
