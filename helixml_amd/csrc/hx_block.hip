@@ -840,11 +840,20 @@ extern "C" int hx_mamba_layer_decode(int64_t batch, int64_t d_model, int64_t d_i
     char* p = (char*)workspace;
     void* xn = p;
     const BlockBufs b = carve(p + align256((size_t)batch * d_model * 2), batch, d_inner, dt_rank, dstate);
-    if ((rc = hx_rmsnorm_fwd(batch, d_model, resid, norm_w, eps, HX_BF16, xn, stream))) return rc;
-    if ((rc = hx_gemm_bf16(batch, 2 * d_inner, d_model, xn, d_model, w.w_in, d_model, nullptr, 0,
-                           HX_BF16, b.xpart, d_inner, d_inner, b.z, d_inner, 2 * d_inner, nullptr,
-                           0, stream)))
-        return rc;
+    // the pre-norm inside in_proj's operand load where the small-M GEMM holds whole rows
+    // (d_model <= 512: config 5's decode), else RMSNorm to bf16 then in_proj
+    if (gemm_rmsnorm_small_ok(batch, 2 * d_inner, d_model, resid, d_model, norm_w, w.w_in, d_model)) {
+        if ((rc = gemm_rmsnorm_small(batch, 2 * d_inner, d_model, resid, d_model, norm_w, eps, w.w_in,
+                                     d_model, HX_BF16, b.xpart, d_inner, d_inner, b.z, d_inner,
+                                     2 * d_inner, nullptr, 0, as_stream(stream))))
+            return rc;
+    } else {
+        if ((rc = hx_rmsnorm_fwd(batch, d_model, resid, norm_w, eps, HX_BF16, xn, stream))) return rc;
+        if ((rc = hx_gemm_bf16(batch, 2 * d_inner, d_model, xn, d_model, w.w_in, d_model, nullptr, 0,
+                               HX_BF16, b.xpart, d_inner, d_inner, b.z, d_inner, 2 * d_inner,
+                               nullptr, 0, stream)))
+            return rc;
+    }
     // conv step, x_proj, dt_proj, state update and gate in one launch (ssm_decode_kernel)
     HX_REQUIRE(aligned(ssm_state, 16) && aligned(w.A, 16) && aligned(w.w_x, 8) &&
                    aligned(w.w_dt, 16) && aligned(w.conv_w, 16),

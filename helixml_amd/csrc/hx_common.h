@@ -33,6 +33,17 @@ int device_cus();
 // column: N <= 192, K >= 1024, K % 64 == 0). It depends on the weight shape only, so every M
 // gets the same arithmetic per row.
 bool gemm_narrow_auto(int64_t N, int64_t K);
+// Y = bf16(rmsnorm(X) * nw) . W^T in one launch: hx_rmsnorm_fwd's bf16 output (X fp32 [M, ldx],
+// nw fp32 [K]) fed to hx_gemm_bf16 (no bias, no activation; the same output arguments), with the
+// normalisation done in the small-M GEMM kernel's operand load. gemm_rmsnorm_small_ok tells
+// whether the sizes and alignment fit: the automatic GEMM choice, the small-M kernel for M x N
+// (fewer than 128 tiles of 128 x 128) and K <= 512 in 8-wide pieces (16-byte aligned rows).
+bool gemm_rmsnorm_small_ok(int64_t M, int64_t N, int64_t K, const float* X, int64_t ldx,
+                           const float* nw, const void* W, int64_t ldw);
+int gemm_rmsnorm_small(int64_t M, int64_t N, int64_t K, const float* X, int64_t ldx, const float* nw,
+                       float eps, const void* W, int64_t ldw, int out_dtype, void* Y0, int64_t ld0,
+                       int64_t split1, void* Y1, int64_t ld1, int64_t split2, void* Y2, int64_t ld2,
+                       hipStream_t stream);
 
 // The Mamba block's dt_proj and selective scan in one launch (bf16 storage, dstate 16, softplus,
 // z gate, zero initial state): delta = bf16(dt_lo . w_dt^T) is formed per 16-step chunk on the

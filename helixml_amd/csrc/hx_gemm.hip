@@ -9,7 +9,7 @@
 // are 16-byte and issued one K-step ahead. The epilogue can split the N columns over up to three
 // outputs with their own row strides (in_proj -> x | z, x_proj -> dt | B | C) so later kernels read
 // contiguous operands.
-#include "hx_common.h"
+#include "hx_wave.h"
 
 namespace hx {
 namespace {
@@ -215,22 +215,32 @@ __device__ inline void vstore_bytes(char* p, const uint32_t* d) {
     }
 }
 
-template <int TN, int NW, int SP>
+// XT = uint16_t: X is bf16. XT = float: X is the fp32 rows of an RMSNorm whose output is the
+// GEMM's left operand, bf16(x / sqrt(mean(x^2) + eps) * nw) (nn::RMSNorm::forward,
+// crates/nn/src/lib.rs:258-285, rounded to bf16 as hx_rmsnorm_fwd's bf16 output): the block
+// holds all K of its 32 rows in one round (K <= 16 * NW * SP), so each row's sum of squares is
+// formed from the loaded pieces (the two lanes of a row in a wave, then the waves in order) and
+// the pieces are normalised and packed to bf16 in registers. nw and eps are unused for bf16 X.
+template <int TN, int NW, int SP, typename XT = uint16_t>
 __global__ __launch_bounds__(NW * 64) void gemm_bf16_nt_skinny_kernel(int64_t M, int64_t N, int64_t K,
-                                                                      const uint16_t* __restrict__ X,
+                                                                      const XT* __restrict__ X,
                                                                       int64_t ldx,
                                                                       const uint16_t* __restrict__ W,
                                                                       int64_t ldw,
                                                                       const float* __restrict__ bias,
-                                                                      GemmOut o) {
+                                                                      GemmOut o,
+                                                                      const float* __restrict__ nw,
+                                                                      float eps) {
     constexpr int NT = TN / 32;
     constexpr int PER = 32 * TN / (NW * 64);  // outputs per thread in the epilogue
+    constexpr bool NORM = std::is_same_v<XT, float>;
     static_assert(PER >= 2 && (PER & (PER - 1)) == 0 && TN % PER == 0, "epilogue groups");
     __shared__ float part[NW][32][TN + 1];
+    __shared__ float rss[NORM ? NW : 1][32];  // per wave: its pieces' sum of squares of each row
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * 32, n0 = (int64_t)blockIdx.x * TN;
     const int fr = lane & 31, fk = (lane >> 5) * 8;
-    const uint16_t* xr = X + (m0 + fr < M ? m0 + fr : M - 1) * ldx;
+    const XT* xr = X + (m0 + fr < M ? m0 + fr : M - 1) * ldx;
     const uint16_t* wr[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -248,6 +258,64 @@ __global__ __launch_bounds__(NW * 64) void gemm_bf16_nt_skinny_kernel(int64_t M,
     for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+    if constexpr (NORM) {
+        // one straight-line round that every wave runs (the barrier is block-wide); pieces past
+        // K load the row's first piece and are masked to zero, so they add nothing to the sums
+        float4 xv[SP][2], gv[SP][2];
+        bf16x8 b[NT][SP];
+        float ss = 0.0f;
+#pragma unroll
+        for (int q = 0; q < SP; ++q) {
+            const int64_t kk = (int64_t)(w + NW * q) * 16 + fk;
+            const bool in = kk + 8 <= K;
+            const int64_t kc = in ? kk : 0;
+            uint32_t msk = in ? 0xffffffffu : 0u;
+            asm volatile("" : "+v"(msk));
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint4 v = *reinterpret_cast<const uint4*>(xr + kc + 4 * h);
+                v.x &= msk; v.y &= msk; v.z &= msk; v.w &= msk;
+                xv[q][h] = __builtin_bit_cast(float4, v);
+                gv[q][h] = *reinterpret_cast<const float4*>(nw + kc + 4 * h);
+            }
+#pragma unroll
+            for (int j = 0; j < NT; ++j) b[j][q] = piece(wr[j], kc, msk);
+        }
+#pragma unroll
+        for (int q = 0; q < SP; ++q)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                ss = fmaf(xv[q][h].x, xv[q][h].x, ss);
+                ss = fmaf(xv[q][h].y, xv[q][h].y, ss);
+                ss = fmaf(xv[q][h].z, xv[q][h].z, ss);
+                ss = fmaf(xv[q][h].w, xv[q][h].w, ss);
+            }
+        {  // lanes fr and fr + 32 hold the two halves of row fr's pieces: both form lo + hi
+            float lo = ss, hi = ss;
+            swap32(lo, hi);
+            ss = lo + hi;
+        }
+        if (lane < 32) rss[w][fr] = ss;
+        __syncthreads();
+        float tot = rss[0][fr];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) tot += rss[w2][fr];
+        const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+#pragma unroll
+        for (int q = 0; q < SP; ++q) {
+            uint32_t d[4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float4 x4 = xv[q][h], g4 = gv[q][h];
+                d[2 * h] = pack_bf16x2(x4.x * inv * g4.x, x4.y * inv * g4.y);
+                d[2 * h + 1] = pack_bf16x2(x4.z * inv * g4.z, x4.w * inv * g4.w);
+            }
+            const bf16x8 a = __builtin_bit_cast(bf16x8, make_uint4(d[0], d[1], d[2], d[3]));
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j][q], acc[j], 0, 0, 0);
+        }
+    } else
     for (int64_t s0 = w; s0 < nsteps; s0 += (int64_t)NW * SP) {  // wave-uniform rounds
         bf16x8 a[SP], b[NT][SP];
 #pragma unroll
@@ -1451,6 +1519,77 @@ namespace hx {
 bool gemm_narrow_auto(int64_t N, int64_t K) { return N >= 1 && N <= 192 && K >= 1024 && K % 64 == 0; }
 }  // namespace hx
 
+namespace hx {
+namespace {
+// The small-M kernel's tiling for an M x N x K product: 64-wide tiles where they still give the
+// GPU 256 blocks (decode in_proj), else 32-wide; blocks of 8 waves where the grid has at most one
+// block per CU, else 4; spw = the K-steps (16 wide) each wave covers.
+struct SkinnyShape {
+    bool wide, w8;
+    int tn;
+    int64_t spw;
+};
+SkinnyShape skinny_shape(int64_t M, int64_t N, int64_t K) {
+    SkinnyShape sh;
+    sh.wide = ((N + 63) / 64) * ((M + 31) / 32) >= 256;
+    sh.tn = sh.wide ? 64 : 32;
+    sh.w8 = ((N + sh.tn - 1) / sh.tn) * ((M + 31) / 32) <= device_cus();
+    sh.spw = ((K + 15) / 16 + (sh.w8 ? 7 : 3)) / (sh.w8 ? 8 : 4);
+    return sh;
+}
+}  // namespace
+
+bool gemm_rmsnorm_small_ok(int64_t M, int64_t N, int64_t K, const float* X, int64_t ldx,
+                           const float* nw, const void* W, int64_t ldw) {
+    if (g_gemm_kernel != 0 || M <= 0 || N <= 0 || K < 8 || K % 8 != 0 || ldx < K || ldw < K)
+        return false;
+    if (ldx % 4 != 0 || ldw % 8 != 0 || !aligned(X, 16) || !aligned(nw, 16) || !aligned(W, 16))
+        return false;
+    // hx_gemm_bf16 takes the small-M kernel for these sizes (its other forms need K >= 1024 or
+    // at least 128 tiles of 128 x 128)
+    if (((M + BM - 1) / BM) * ((N + BN - 1) / BN) >= 128 || (M + 31) / 32 > 65535) return false;
+    return skinny_shape(M, N, K).spw <= 4;  // one round of at most 4 pieces per lane
+}
+
+int gemm_rmsnorm_small(int64_t M, int64_t N, int64_t K, const float* X, int64_t ldx, const float* nw,
+                       float eps, const void* W, int64_t ldw, int out_dtype, void* Y0, int64_t ld0,
+                       int64_t split1, void* Y1, int64_t ld1, int64_t split2, void* Y2, int64_t ld2,
+                       hipStream_t stream) {
+    HX_REQUIRE(gemm_rmsnorm_small_ok(M, N, K, X, ldx, nw, W, ldw), HX_ERR_UNSUPPORTED,
+               "gemm_rmsnorm_small: sizes or alignment outside the fused form");
+    HX_REQUIRE(out_dtype == HX_F32 || out_dtype == HX_BF16, HX_ERR_DTYPE_MISMATCH,
+               "gemm_rmsnorm_small: out_dtype %d", out_dtype);
+    HX_REQUIRE(Y0 && ld0 >= 0, HX_ERR_INVALID_INPUT, "gemm_rmsnorm_small: Y0 is NULL");
+    if (split1 <= 0 || split1 > N) split1 = N;
+    if (split2 < split1 || split2 > N) split2 = N;
+    HX_REQUIRE(split1 == N || Y1, HX_ERR_INVALID_INPUT, "gemm_rmsnorm_small: Y1 is NULL but split1 < N");
+    HX_REQUIRE(split2 == N || Y2, HX_ERR_INVALID_INPUT, "gemm_rmsnorm_small: Y2 is NULL but split2 < N");
+    const GemmOut o{{Y0, Y1, Y2}, {ld0, ld1, ld2}, split1, split2, out_dtype == HX_BF16, 0};
+    const SkinnyShape sh = skinny_shape(M, N, K);
+    auto launch = [&](auto kern, int nwv) {
+        dim3 sg((unsigned)((N + sh.tn - 1) / sh.tn), (unsigned)((M + 31) / 32));
+        hipLaunchKernelGGL(kern, sg, dim3(64 * nwv), 0, stream, M, N, K, X, ldx, (const uint16_t*)W,
+                           ldw, (const float*)nullptr, o, nw, eps);
+    };
+    const bool two = sh.spw <= 2;
+    if (sh.wide && sh.w8) {
+        if (two) launch(gemm_bf16_nt_skinny_kernel<64, 8, 2, float>, 8);
+        else launch(gemm_bf16_nt_skinny_kernel<64, 8, 4, float>, 8);
+    } else if (sh.wide) {
+        if (two) launch(gemm_bf16_nt_skinny_kernel<64, 4, 2, float>, 4);
+        else launch(gemm_bf16_nt_skinny_kernel<64, 4, 4, float>, 4);
+    } else if (sh.w8) {
+        if (two) launch(gemm_bf16_nt_skinny_kernel<32, 8, 2, float>, 8);
+        else launch(gemm_bf16_nt_skinny_kernel<32, 8, 4, float>, 8);
+    } else {
+        if (two) launch(gemm_bf16_nt_skinny_kernel<32, 4, 2, float>, 4);
+        else launch(gemm_bf16_nt_skinny_kernel<32, 4, 4, float>, 4);
+    }
+    HX_LAUNCH_CHECK();
+    return HX_OK;
+}
+}  // namespace hx
+
 extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
                             const void* W, int64_t ldw, const float* bias, int act, int out_dtype,
                             void* Y0, int64_t ld0, int64_t split1, void* Y1, int64_t ld1,
@@ -1525,14 +1664,14 @@ extern "C" int hx_gemm_bf16(int64_t M, int64_t N, int64_t K, const void* X, int6
         // waves per SIMD overlap their load rounds (config 5 decode at batch 256: 403 -> 394 us
         // per step, the same with only out_proj's 128 blocks so; the sums over the waves' K
         // slices then meet in 8 parts)
-        const bool wide = ((N + 63) / 64) * ((M + 31) / 32) >= 256;
-        const int tn = wide ? 64 : 32;
-        const bool w8 = ((N + tn - 1) / tn) * ((M + 31) / 32) <= device_cus();
-        const int64_t spw = ((K + 15) / 16 + (w8 ? 7 : 3)) / (w8 ? 8 : 4);  // K-steps per wave
+        const SkinnyShape sh = skinny_shape(M, N, K);
+        const bool wide = sh.wide, w8 = sh.w8;
+        const int tn = sh.tn;
+        const int64_t spw = sh.spw;
         auto launch = [&](auto kern, int nw) {
             dim3 sg((unsigned)((N + tn - 1) / tn), (unsigned)((M + 31) / 32));
             hipLaunchKernelGGL(kern, sg, dim3(64 * nw), 0, as_stream(stream), M, N, K, (const uint16_t*)X,
-                               ldx, (const uint16_t*)W, ldw, bias, o);
+                               ldx, (const uint16_t*)W, ldw, bias, o, (const float*)nullptr, 0.0f);
         };
         if (wide && w8) {
             if (spw <= 2) launch(gemm_bf16_nt_skinny_kernel<64, 8, 2>, 8);

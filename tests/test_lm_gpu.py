@@ -216,6 +216,44 @@ def test_lm_decode_row_kernel_shapes(dev, dm, di, r, K):
     assert err <= 1e-2, err
 
 
+@pytest.mark.parametrize("bt,dm,di", [(512, 256, 1024), (64, 256, 2560), (256, 512, 1024), (3, 64, 128)])
+def test_lm_decode_fused_prenorm_tilings(dev, bt, dm, di):
+    """The decode step's pre-norm folded into in_proj's operand load, in each tiling of the
+    small-M GEMM it rides on: 64-wide tiles with 4 waves (batch 512, in_proj N 2048 K 256),
+    32-wide with 4 waves (batch 64, N 5120), 64-wide with 8 waves (config 5's batch 256) and
+    32-wide with 8 waves and two pieces per lane (batch 3, K 64). One decode step of a 1-layer
+    model against the same step with the separate RMSNorm launch (a forced GEMM kernel takes the
+    unfused form: the two differ only in the order of the rows' sums of squares, normwise <= 1e-3)
+    and against the oracle on the first and last sequences."""
+    from helixml_amd import ssm
+    r = 16
+    P = lm_params(1, dm, di, 16, r, 4, 256, seed=bt + di)
+    m = model_from(P, dev, dt_rank=r)
+    rng = np.random.default_rng(bt * 7 + dm)
+    tok = rng.integers(0, 256, (bt, 5)).astype(np.int32)
+    td = torch.from_numpy(tok).to(dev)
+    print(f"case fused pre-norm decode batch {bt} d_model {dm} d_inner {di}", flush=True)
+    _, state = m.prefill(td[:, :4].contiguous())
+    st_sep = [(s_.clone(), c.clone()) for s_, c in state]
+    lg = m.decode_step(td[:, 4].contiguous(), state)
+    ssm.set_gemm_kernel(3)
+    try:
+        lg_sep = m.decode_step(td[:, 4].contiguous(), st_sep)
+    finally:
+        ssm.set_gemm_kernel(0)
+    torch.cuda.synchronize()
+    err = norm_err(lg.cpu().numpy(), lg_sep.cpu().numpy())
+    assert err <= 1e-3, err
+    for (a, b), (c, d) in zip(state, st_sep):
+        assert norm_err(a.cpu().numpy(), c.cpu().numpy()) <= 1e-3
+        assert torch.equal(b, d)  # the conv window holds copied inputs
+    sub = tok[[0, bt - 1]]
+    _, rst = oracle.lm_prefill(sub[:, :4], P, r)
+    rl, _ = oracle.lm_decode_step(sub[:, 4], P, rst, r)
+    err = norm_err(lg.cpu().numpy()[[0, bt - 1]], rl)
+    assert err <= 1e-2, err
+
+
 def test_lm_config5_full_size(dev):
     """12 layers, d_model 512, d_inner 1024, N 16, dt_rank 32, conv 4, vocab
     256, batch 16 x L 8192 prefill, then one decode step for all 16 sequences. The oracle checks
