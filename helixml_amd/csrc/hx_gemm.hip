@@ -734,15 +734,20 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_dlds_kernel(int64_t M, int64
 // and every column, so the grid is M / 64 blocks and no K split is needed. Block tile 64 x NB
 // (NB = 64 CB, N <= NB): 4 waves in 2 x 2, each 32 rows x 32 CB columns (CB
 // v_mfma_f32_32x32x16_bf16 per 16-wide K step, K ascending as in the other kernels, so each
-// output is the same sum). K tiles of 64 move straight into a 3-stage LDS ring with
+// output is the same sum). K tiles of 64 move straight into a 3- or 4-stage LDS ring with
 // global_load_lds_dwordx4 (A rows 0..63, then W rows 0..NB-1, 128-byte rows with the 16-byte
-// chunks XOR-swizzled by row); the loads of tile kt+2 are issued while tile kt is multiplied.
+// chunks XOR-swizzled by row); the loads of tile kt+2 (kt+3) are issued while tile kt is multiplied.
 // W (at most NB x K) is read by every block and stays in L2. Requires K % 64 == 0 and 16-byte
 // aligned rows; rows past M or N are clamped (their outputs are discarded).
-constexpr int NBM = 64, NST3 = 3;
+constexpr int NBM = 64;
 
 template <int CB>
 constexpr int narrow_stage_bytes() { return (NBM + 64 * CB) * 128; }
+// Ring depth: 4 stages (loads 3 K tiles ahead) where a CU holds one block either way (CB = 3:
+// 128 KB against 96 KB), else 3, which keeps 2 or 3 blocks per CU (measured on MI355X: config 3
+// x_proj, CB = 3, 52.7 -> 49.7 us with 4 stages; config 5 x_proj, CB = 1, 50.8 -> 54.3 us).
+template <int CB>
+constexpr int narrow_stages() { return CB >= 3 ? 4 : 3; }
 
 template <int CB>
 __global__ __launch_bounds__(256) void gemm_bf16_nt_narrow_kernel(int64_t M, int64_t N, int64_t K,
@@ -755,6 +760,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_narrow_kernel(int64_t M, int
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     char* sbase = reinterpret_cast<char*>(smem);
     constexpr int SB = narrow_stage_bytes<CB>();
+    constexpr int NST3 = narrow_stages<CB>();
     constexpr int QW = (NBM + 64 * CB) / 8 / 4;  // 1-KiB load regions per wave per tile
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -795,14 +801,20 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_narrow_kernel(int64_t M, int
     const int fr = lane & 31;
     const int fc = lane >> 5;
     const int64_t nk = K / 64;
-    issue(0);
-    if (nk > 1) issue(1);
+#pragma unroll
+    for (int t = 0; t < NST3 - 1; ++t)
+        if (t < nk) issue(t);
+    static_assert(NST3 == 3 || NST3 == 4, "ring depth");
     for (int64_t kt = 0; kt < nk; ++kt) {
-        // this wave's loads of tile kt are done when at most the QW of tile kt+1 remain; wait and
-        // barrier in one statement so the compiler adds no wait for tile kt+1's loads
-        if (kt + 1 < nk) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(QW) : "memory");
+        // this wave's loads of tile kt are done when at most the QW of each later tile already
+        // issued (up to NST3 - 2 of them) remain; wait and barrier in one statement so the
+        // compiler adds no wait for the later tiles' loads
+        if (NST3 == 4 && kt + 2 < nk)
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * QW) : "memory");
+        else if (kt + 1 < nk) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(QW) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-        if (kt + 2 < nk) issue(kt + 2);  // stage (kt+2)%3 was last read in iteration kt-1
+        // stage (kt + NST3 - 1) % NST3 was last read in iteration kt - 1
+        if (kt + NST3 - 1 < nk) issue(kt + NST3 - 1);
         const char* stage = sbase + (int)(kt % NST3) * SB;
         const char* aw = stage + (wm * 32 + fr) * 128;
         const char* bw = stage + (NBM + wn * 32 * CB + fr) * 128;
@@ -1491,7 +1503,7 @@ template <int CB>
 int launch_narrow_cb(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* W,
                      int64_t ldw, const float* bias, const hx::GemmOut& o, void* stream) {
     using namespace hx;
-    const size_t bytes = (size_t)NST3 * narrow_stage_bytes<CB>();
+    const size_t bytes = (size_t)narrow_stages<CB>() * narrow_stage_bytes<CB>();
     HX_REQUIRE(grant_dynamic_lds((const void*)gemm_bf16_nt_narrow_kernel<CB>, bytes, 0), HX_ERR_UNSUPPORTED,
                "gemm_bf16: the device does not grant %zu bytes of LDS", bytes);
     HX_REQUIRE((M + NBM - 1) / NBM <= 0x7fffffff, HX_ERR_UNSUPPORTED, "gemm_bf16: M=%lld too large",
