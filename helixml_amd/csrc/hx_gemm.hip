@@ -745,7 +745,8 @@ template <int CB>
 constexpr int narrow_stage_bytes() { return (NBM + 64 * CB) * 128; }
 // Ring depth: 4 stages (loads 3 K tiles ahead) where a CU holds one block either way (CB = 3:
 // 128 KB against 96 KB), else 3, which keeps 2 or 3 blocks per CU (measured on MI355X: config 3
-// x_proj, CB = 3, 52.7 -> 49.7 us with 4 stages; config 5 x_proj, CB = 1, 50.8 -> 54.3 us).
+// x_proj, CB = 3, 52.7 -> 49.7 us with 4 stages, 54 us with 5 (160 KiB); config 5 x_proj,
+// CB = 1, 50.8 -> 54.3 us with 4).
 template <int CB>
 constexpr int narrow_stages() { return CB >= 3 ? 4 : 3; }
 
