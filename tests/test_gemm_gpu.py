@@ -203,11 +203,12 @@ def test_gemm_grouped_tile_order(dev, gemm_kernel, M, N, K):
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", [(2000, 160, 4096), (333, 64, 1024), (64, 192, 2048), (7, 1, 1024),
-                                   (130, 250, 1088)])
+                                   (130, 250, 1088), (97, 150, 1024)])
 def test_gemm_narrow_kernel(dev, out_dtype, M, N, K):
     """The narrow kernel (64-row tiles holding every column, the x_proj shapes) on its own
     (kernel 7) and as the automatic choice: the block's dt_lo | B | C splits, bias, accumulate,
-    ragged M and N; its fp32 sums are the 256 x 128 direct-to-LDS kernel's bit for bit (both add
+    ragged M and N (N 150 within a 192-column tile); its fp32 sums are the 256 x 128
+    direct-to-LDS kernel's bit for bit (both add
     the same 32 x 32 x 16 MFMA products with K ascending)."""
     g = torch.Generator().manual_seed(M + N + K)
     X = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
